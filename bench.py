@@ -1,0 +1,317 @@
+"""Benchmark of the MI355X quantized-linear backend for janis.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline] [--quick]
+
+Workload (the configuration the headline metric is quoted on): the decode
+linears of a Qwen3-8B-shaped model at batch 1 -- 36 layers of
+    qkv  4096 -> 4096+1024+1024   (q_proj, k_proj, v_proj as one launch; they share x)
+    o    4096 -> 4096
+    gate+up 4096 -> 2 x 12288     (one launch)
+    down 12288 -> 4096
+plus lm_head 4096 -> 151936, 4-bit affine group 64, bf16 scales/biases/x/y,
+synthetic random weights resident in HBM (4.26 GB of packed weights). One
+"step" is one token: the 145 launches in order, replayed from a HIP graph.
+
+Printed: one JSON line with
+    value     aggregate algorithmic HBM GB/s over the step
+    tok_s     decode tok/s of the linears (1 / step time)
+    roofline  for the dominant kernel, from HIP events on the launch stream
+    cpu_baseline  janis's AVX2 per-channel kernel (restated in oracle/) on the
+              host cores, on a bounded sample of the same workload
+and per-shape, prefill (MFMA) and MoE-gather figures under "extra".
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+HIDDEN, INTER, VOCAB, LAYERS, GS = 4096, 12288, 151936, 36, 64
+
+
+def qbytes(n: int, k: int) -> int:
+    """Algorithmic bytes of one 4-bit g64 qmv: codes + bf16 scales/biases + x + y."""
+    return n * k // 2 + 4 * n * (k // GS) + 2 * k + 2 * n
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="skip the extra per-config figures")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this backend is measured on one GPU; --gpus N > 1 is not "
+                                   "supported (the path would shard by output rows / experts, "
+                                   "see DESIGN.md)"}))
+        return 2
+
+    import torch
+
+    from janis_amd.engine import BF16, I32, U32, HipBackend
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(1234)
+    hip = HipBackend(0)
+    log("device:", hip.EngineInfo())
+
+    def qweight(n, k, lead=()):
+        shape = (*lead, n, k // 8)
+        w = torch.randint(-2**31, 2**31 - 1, shape, dtype=torch.int32, device=dev)
+        s = (torch.randn((*lead, n, k // GS), device=dev).abs() * 0.02).to(torch.bfloat16)
+        b = (-8.0 * s.float() + torch.randn((*lead, n, k // GS), device=dev) * 1e-3).to(torch.bfloat16)
+        return (hip.Wrap(w.data_ptr(), shape, U32, keep=w),
+                hip.Wrap(s.data_ptr(), s.shape, BF16, keep=s),
+                hip.Wrap(b.data_ptr(), b.shape, BF16, keep=b))
+
+    def bf16(shape, randn=True):
+        t = torch.randn(shape, device=dev).to(torch.bfloat16) if randn else \
+            torch.empty(shape, device=dev, dtype=torch.bfloat16)
+        return hip.Wrap(t.data_ptr(), shape, BF16, keep=t)
+
+    # ---- weights and activations of the 36-layer sequence ---------------------------
+    t0 = time.time()
+    shapes = {"qkv": (HIDDEN + 2 * 1024, HIDDEN), "o": (HIDDEN, HIDDEN),
+              "gate_up": (2 * INTER, HIDDEN), "down": (HIDDEN, INTER)}
+    layers = [{name: qweight(n, k) for name, (n, k) in shapes.items()} for _ in range(LAYERS)]
+    head = qweight(VOCAB, HIDDEN)
+    x_h, x_attn, x_ffn = bf16((1, HIDDEN)), bf16((1, HIDDEN)), bf16((1, INTER))
+    ys = {name: bf16((1, n), randn=False) for name, (n, k) in shapes.items()}
+    y_head = bf16((1, VOCAB), randn=False)
+    torch.cuda.synchronize()
+    log(f"weights ready in {time.time() - t0:.1f}s")
+    xin = {"qkv": x_h, "o": x_attn, "gate_up": x_h, "down": x_ffn}
+
+    def launch(name, wsb, x, y):
+        w, s, b = wsb
+        hip.QuantMatmul(x, w, s, b, True, GS, 4, out=y)
+
+    def sequence():
+        for L in layers:
+            for name in ("qkv", "o", "gate_up", "down"):
+                launch(name, L[name], xin[name], ys[name])
+        launch("lm_head", head, x_h, y_head)
+
+    bytes_layer = sum(qbytes(n, k) for n, k in shapes.values())
+    bytes_token = LAYERS * bytes_layer + qbytes(VOCAB, HIDDEN)
+    n_launch = LAYERS * 4 + 1
+
+    def capture(fn):
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            hip.SetStream(s.cuda_stream)
+            fn()  # warm the launch path outside the graph
+            torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            hip.SetStream(torch.cuda.current_stream().cuda_stream)
+            fn()
+        hip.SetStream(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        return g
+
+    def time_graph(g, steps, warmup):
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(steps):
+            g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps  # ms per replay
+
+    # ---- headline: the whole token ------------------------------------------------------
+    g_seq = capture(sequence)
+    ms_step = time_graph(g_seq, args.steps, args.warmup)
+    gbs = bytes_token / (ms_step * 1e-3) / 1e9
+    tok_s = 1000.0 / ms_step
+    log(f"sequence: {ms_step * 1e3:.1f} us/token, {gbs:.0f} GB/s, {tok_s:.0f} tok/s")
+
+    # ---- per shape, rotating through the 36 layer copies (defeats the 256 MB cache) -------
+    per_shape = {}
+    for name, (n, k) in shapes.items():
+        g = capture(lambda name=name: [launch(name, L[name], xin[name], ys[name]) for L in layers])
+        ms = time_graph(g, max(5, args.steps // 2), 3) / LAYERS
+        per_shape[name] = {"N": n, "K": k, "us": round(ms * 1e3, 2),
+                           "GB_s": round(qbytes(n, k) / (ms * 1e-3) / 1e9, 1)}
+        del g
+    g = capture(lambda: launch("lm_head", head, x_h, y_head))
+    ms = time_graph(g, max(5, args.steps // 2), 3)
+    per_shape["lm_head"] = {"N": VOCAB, "K": HIDDEN, "us": round(ms * 1e3, 2),
+                            "GB_s": round(qbytes(VOCAB, HIDDEN) / (ms * 1e-3) / 1e9, 1)}
+    del g
+    log("per shape:", per_shape)
+
+    # ---- dominant kernel: the K=4096 GEMV instantiation (qkv, o, gate_up, lm_head) ----------
+    # Events bracket a graph of exactly that kernel's launches, back to back, in the
+    # sequence's order; achieved = their algorithmic bytes / their time per launch.
+    def k4096_only():
+        for L in layers:
+            for name in ("qkv", "o", "gate_up"):
+                launch(name, L[name], xin[name], ys[name])
+        launch("lm_head", head, x_h, y_head)
+
+    g = capture(k4096_only)
+    ms_dom = time_graph(g, args.steps, args.warmup)
+    del g
+    n_dom = LAYERS * 3 + 1
+    bytes_dom = LAYERS * sum(qbytes(*shapes[n]) for n in ("qkv", "o", "gate_up")) + qbytes(VOCAB, HIDDEN)
+    dom_gbs = bytes_dom / (ms_dom * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "qmv_bf16x_kernel<64,2,4> (K=4096 decode GEMV)",
+                "launches_per_step": n_dom, "avg_launch_us": round(ms_dom * 1e3 / n_dom, 3),
+                "algorithmic_bytes_per_launch": bytes_dom // n_dom}
+
+    extra = {"per_shape": per_shape, "launches_per_token": n_launch, "bytes_per_token": bytes_token}
+
+    if not args.quick:
+        extra.update(prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args))
+
+    # ---- CPU baseline --------------------------------------------------------------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args.cpu_seconds, bytes_token)
+
+    out = {
+        "metric": "4-bit qmv HBM GB/s (% of peak) + Qwen3-8B-shape decode tok/s, 1 MI355X",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4 codes, bf16 act, fp32 acc",
+        "data": "synthetic (random 4-bit codes, |N(0,1)|*0.02 bf16 scales, N(0,1) bf16 x)",
+        "config": {"workload": "qwen3_8b_decode_linears_36L_plus_lm_head", "batch": 1,
+                   "hidden": HIDDEN, "intermediate": INTER, "vocab": VOCAB, "layers": LAYERS,
+                   "bits": 4, "group_size": GS, "launches": n_launch, "graph": True},
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "tok_s": round(tok_s, 1),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+    hip.Close()
+    return 0
+
+
+def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
+    """Config 2 (prefill qmm, MFMA) and config 3 (MoE gather) figures."""
+    from janis_amd import synth
+    from janis_amd.engine import I32
+
+    res = {}
+    # prefill: gate_up 4096->12288 and down 12288->4096 at M in {128, 512, 2048}
+    pre = {}
+    for name, (n, k) in {"gate_up": (12288, 4096), "down": (4096, 12288)}.items():
+        copies = [qweight(n, k) for _ in range(4)]
+        for m in (128, 512, 2048):
+            x = bf16((m, k))
+            y = bf16((m, n), randn=False)
+            g = capture(lambda: [hip.QuantMatmul(x, *c, True, GS, 4, out=y) for c in copies])
+            ms = time_graph(g, 5, 2) / len(copies)
+            fl = 2.0 * m * n * k
+            pre[f"{name}_M{m}"] = {"us": round(ms * 1e3, 1), "TFLOP_s": round(fl / (ms * 1e-3) / 1e12, 1),
+                                   "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)}
+            del g
+        del copies
+    res["prefill_qmm"] = pre
+    log("prefill:", pre)
+
+    # MoE: Qwen3-30B-A3B experts (E=128, hidden 2048, inter 768), top-8
+    E, H, I, K = 128, 2048, 768, 8
+    moe = {}
+    nl = 8  # rotate 8 layers of experts (8 x 340 MB) to defeat the cache
+    stacks = [{"gate": qweight(I, H, (E,)), "up": qweight(I, H, (E,)), "down": qweight(H, I, (E,))}
+              for _ in range(nl)]
+    for T in (1, 16):
+        idx_np, _ = synth.route(77 + T, T, E, K)
+        U = len(set(idx_np.reshape(-1).tolist()))
+        it = torch.from_numpy(idx_np).to(dev)
+        idx = hip.Wrap(it.data_ptr(), tuple(idx_np.shape), I32, keep=it)
+        xg = bf16((T, 1, 1, H))
+        hg = bf16((T, K, 1, I))
+        yg, yu = bf16((T, K, 1, I), randn=False), bf16((T, K, 1, I), randn=False)
+        yd = bf16((T, K, 1, H), randn=False)
+
+        def moe_layers():
+            for st in stacks:
+                hip.GatherQuantMatmul(xg, *st["gate"], idx, True, GS, 4, out=yg)
+                hip.GatherQuantMatmul(xg, *st["up"], idx, True, GS, 4, out=yu)
+                hip.GatherQuantMatmul(hg, *st["down"], idx, True, GS, 4, out=yd)
+
+        g = capture(moe_layers)
+        ms = time_graph(g, 10, 3) / nl
+        per_expert = 3 * (I * H // 2 + 4 * I * (H // GS))  # packed codes + scales/biases of one expert
+        byt = U * per_expert + 2 * T * H + 2 * T * K * (2 * I + H) + 2 * T * K * I
+        moe[f"T{T}"] = {"unique_experts": U, "us_per_layer": round(ms * 1e3, 2),
+                        "GB_s": round(byt / (ms * 1e-3) / 1e9, 1), "launches_per_layer": 6}
+        del g
+    res["moe_gather"] = moe
+    log("moe:", moe)
+    del stacks
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(seconds: float, bytes_token: int):
+    """janis's amd64 decode path -- the AVX2 per-channel kernel over parallelFor
+    chunks (cpu/qmv_amd64.s, cpu/cpu.go:37-79), restated in oracle/ -- timed on all
+    host cores over one layer of the same shapes plus a 1/8 slice of lm_head."""
+    import numpy as np
+
+    from janis_amd import synth
+    from oracle import oracle
+
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = min(cores, 16)  # the GPU box's CPU share
+    shapes = [(6144, HIDDEN), (HIDDEN, HIDDEN), (2 * INTER, HIDDEN), (HIDDEN, INTER), (VOCAB // 8, HIDDEN)]
+    mats = [synth.quant_linear(500 + i, n, k) for i, (n, k) in enumerate(shapes)]
+    xs = {k: synth.activations(900 + k, (k,))[1] for k in (HIDDEN, INTER)}
+    sb = [(q.w, q.s, q.b) for q in mats]
+    byt = sum(qbytes(n, k) for n, k in shapes)
+    # one untimed pass, then as many passes as fit in `seconds`
+    for (w, s, b), (n, k) in zip(sb, shapes):
+        oracle.qmv_avx2_parallel(xs[k], w, s, b, GS, cores)
+    t0 = time.perf_counter()
+    passes = 0
+    while True:
+        for (w, s, b), (n, k) in zip(sb, shapes):
+            _, used = oracle.qmv_avx2_parallel(xs[k], w, s, b, GS, cores)
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or passes >= 1000:
+            break
+    gbs = byt * passes / el / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": int(used), "kind": "port",
+            "avx2": bool(oracle.have_avx2_fma()),
+            "tok_s_equiv": round(gbs * 1e9 / bytes_token, 2),
+            "sample": f"{passes} passes over one layer (qkv, o, gate_up, down) + 1/8 of lm_head "
+                      f"({byt / 1e6:.0f} MB), fp32 x, {el:.1f}s"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,162 @@
+/*
+ * janis_hip.h -- C ABI of the MI355X (gfx950) quantized-linear backend for
+ * janis (github.com/guregodevo/janis).
+ *
+ * This is the boundary a cgo package would bind: plain pointers, sizes and
+ * enums, no C++ or torch types. Each entry point names the method of janis's
+ * engine.Backend interface (engine/backend.go) it implements. All tensor
+ * pointers passed to the operator entry points are DEVICE pointers (from
+ * jh_alloc or any other HIP allocation on the context's device), row-major and
+ * contiguous. Operators are enqueued on the context's stream and return
+ * without waiting; jh_d2h and jh_sync wait.
+ *
+ * Every function returns JH_OK (0) or a non-zero status; the message of the
+ * last failure on a context is jh_last_error(ctx). The reference backends
+ * panic on bad input (cpu/cpu_misc.go:137, ggml/ggml.go:439); a Go wrapper
+ * turns a non-zero status into that panic.
+ *
+ * Threading: one context is used by one thread at a time, as janis drives its
+ * backend from one engine thread (serve/serve.go:94-105). Distinct contexts are
+ * independent.
+ */
+#ifndef JANIS_HIP_H
+#define JANIS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__) || defined(__clang__)
+#define JH_API __attribute__((visibility("default")))
+#else
+#define JH_API
+#endif
+
+/* Element types; values equal engine.DType (engine/backend.go:11-21). */
+typedef enum {
+    JH_F32 = 0,
+    JH_F16 = 1,
+    JH_BF16 = 2,
+    JH_I32 = 3,
+    JH_U32 = 4,
+    JH_U8 = 5
+} jh_dtype;
+
+/* Status codes. */
+enum {
+    JH_OK = 0,
+    JH_ERR_INVALID = 1,     /* bad shape, dtype, pointer or argument */
+    JH_ERR_UNSUPPORTED = 2, /* valid for the reference, not implemented here */
+    JH_ERR_HIP = 3,         /* the HIP runtime reported an error */
+    JH_ERR_OOM = 4          /* device allocation failed */
+};
+
+typedef struct jh_ctx jh_ctx;
+
+/* ---- context, memory, streams --------------------------------------------- */
+
+/* Backend.Version (engine/backend.go:145): library name and version. */
+JH_API const char *jh_version(void);
+
+/* Creates a context on HIP device `device` with a stream of its own at the
+ * default priority. Replaces the backend constructors ggml.New()
+ * (ggml/ggml.go) and cpu.New() (cpu/cpu.go:84). */
+JH_API int jh_create(int device, jh_ctx **out);
+
+/* Backend.Close (engine/backend.go:286): waits for queued work, releases the
+ * context's stream and workspace. Safe on NULL. */
+JH_API void jh_destroy(jh_ctx *ctx);
+
+/* Message of the last failure on ctx ("" if none). Valid until the next call
+ * on ctx. With ctx == NULL, the last failure of jh_create. */
+JH_API const char *jh_last_error(const jh_ctx *ctx);
+
+/* Device name and compute-unit count, for EngineInfo (backend_cpu.go:27-30). */
+JH_API int jh_device_info(jh_ctx *ctx, char *name, size_t name_len, int *compute_units);
+
+/* Enqueue on a caller-owned hipStream_t instead of the context's own stream
+ * (NULL restores the context's stream). The caller keeps the stream alive. */
+JH_API int jh_set_stream(jh_ctx *ctx, void *hip_stream);
+
+/* The hipStream_t operators are enqueued on. */
+JH_API void *jh_get_stream(const jh_ctx *ctx);
+
+/* When on, jh_gather_quant_matmul copies the expert indices to the host and
+ * rejects out-of-range ones with JH_ERR_INVALID before launching, as
+ * JANIS_GGML_CHECK turns on read-back checks (ggml/ggml.go:622-677). When off
+ * (default) an out-of-range index yields a row of NaN and no memory outside
+ * the expert stack is read. */
+JH_API int jh_set_checks(jh_ctx *ctx, int on);
+
+/* Waits for every operator enqueued on the context's stream. */
+JH_API int jh_sync(jh_ctx *ctx);
+
+/* Device memory (hipMalloc / hipFree). jh_free(NULL) is a no-op. */
+JH_API int jh_alloc(jh_ctx *ctx, size_t bytes, void **out);
+JH_API int jh_free(jh_ctx *ctx, void *ptr);
+
+/* Host -> device copy of `bytes`; returns once the source may be reused, as
+ * FromRaw/FromFloats copy (engine/backend.go:147-154, mlxc/mlxc.go:27-31). */
+JH_API int jh_h2d(jh_ctx *ctx, void *dst_device, const void *src_host, size_t bytes);
+
+/* Device -> host copy after all queued work; the tail of Floats/Ints
+ * (engine/backend.go:276-283). */
+JH_API int jh_d2h(jh_ctx *ctx, void *dst_host, const void *src_device, size_t bytes);
+
+/* ---- MLX affine-quantized operators ---------------------------------------- *
+ * Layout (MLX, cpu/cpu_misc.go:124-130): a quantized matrix of `rows` rows and
+ * `in_features` columns is
+ *   w       uint32 [rows, in_features * bits / 32], 32/bits codes per word,
+ *           least-significant first;
+ *   scales  [rows, in_features / group_size] of sb_dtype (JH_BF16, JH_F16 or JH_F32);
+ *   biases  same shape and dtype as scales;
+ * and element (r, j) is  scale * code + bias  with the group's scale and bias.
+ * Supported here: bits == 4 (other widths return JH_ERR_UNSUPPORTED) and any
+ * group_size that divides in_features; group sizes 32, 64 and 128 with bf16
+ * activations take the fast kernels, the rest a slower generic kernel.
+ * w, x and y must be 16-byte aligned (jh_alloc gives 256). */
+
+/* Backend.Dequantize (engine/backend.go:261-263; cpu/cpu_misc.go:134-161):
+ * out[r, j] = fl32(code(r, j) * scale + bias), bit-identical to the CPU
+ * backend, written as out_dtype (JH_F32, or JH_BF16 rounded to nearest-even). */
+JH_API int jh_dequantize(jh_ctx *ctx, const uint32_t *w, const void *scales, const void *biases,
+                  jh_dtype sb_dtype, int64_t rows, int64_t in_features, int group_size, int bits,
+                  void *out, jh_dtype out_dtype);
+
+/* Backend.QuantMatmul (engine/backend.go:265-267; cpu/cpu_misc.go:232-400)
+ * with transpose != 0 (the QuantizedLinear convention, the only one the models
+ * use; transpose == 0 returns JH_ERR_UNSUPPORTED):
+ *   y[rows, out_features] = x[rows, in_features] . W^T
+ * x_dtype and y_dtype are JH_BF16 or JH_F32; accumulation is fp32. rows == 1
+ * runs the decode GEMV, rows > 1 the MFMA prefill GEMM. rows == 0 is a no-op. */
+JH_API int jh_quant_matmul(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t rows, const uint32_t *w,
+                    const void *scales, const void *biases, jh_dtype sb_dtype, int64_t out_features,
+                    int64_t in_features, int transpose, int group_size, int bits, void *y,
+                    jh_dtype y_dtype);
+
+/* Backend.GatherQuantMatmul (engine/backend.go:269-274; cpu/cpu_misc.go:178-230),
+ * the MoE expert product, with transpose != 0:
+ *   x            [n_lead, a_vectors, in_features]  (the reference's [lead.., A, 1, in]);
+ *                a_vectors == 1 shares one vector across the k_slots experts,
+ *                a_vectors == k_slots gives each slot its own vector;
+ *   w/scales/biases stacked over experts: [n_experts, out_features, .];
+ *   rhs_indices  int32 [n_lead, k_slots], device memory;
+ *   y            [n_lead, k_slots, out_features]   (the reference's [lead.., K, 1, out]).
+ * Slots are bucketed by expert on the device, so each routed expert's packed
+ * weights are read once per call whatever the number of slots routed to it,
+ * and experts nobody routed to are not read. One call = one bucketing launch
+ * plus one product launch. */
+JH_API int jh_gather_quant_matmul(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t n_lead,
+                           int64_t a_vectors, const uint32_t *w, const void *scales,
+                           const void *biases, jh_dtype sb_dtype, int64_t n_experts,
+                           int64_t out_features, int64_t in_features, const int32_t *rhs_indices,
+                           int64_t k_slots, int transpose, int group_size, int bits, void *y,
+                           jh_dtype y_dtype);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* JANIS_HIP_H */

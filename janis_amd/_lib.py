@@ -1,0 +1,87 @@
+"""ctypes binding of libjanis_hip.so (the C ABI in include/janis_hip.h).
+
+The library is the product: there is no CPU fallback. Loading fails loudly when
+the shared object has not been built (python -m janis_amd.build).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libjanis_hip.so")
+
+# engine.DType (engine/backend.go:11-21)
+F32, F16, BF16, I32, U32, U8 = range(6)
+JH_OK, JH_ERR_INVALID, JH_ERR_UNSUPPORTED, JH_ERR_HIP, JH_ERR_OOM = range(5)
+
+EXPORTS = [
+    "jh_version", "jh_create", "jh_destroy", "jh_last_error", "jh_device_info",
+    "jh_set_stream", "jh_get_stream", "jh_set_checks", "jh_sync", "jh_alloc", "jh_free",
+    "jh_h2d", "jh_d2h", "jh_dequantize", "jh_quant_matmul", "jh_gather_quant_matmul",
+]
+
+_lib = None
+
+
+class JanisHipError(RuntimeError):
+    """A non-zero status from the C ABI (the reference backends panic here)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run `python -m janis_amd.build` "
+                           "(there is no CPU fallback for this backend)")
+    L = ctypes.CDLL(LIB_PATH)
+    c_ctx = ctypes.c_void_p
+    p = ctypes.c_void_p
+    i64 = ctypes.c_int64
+    i = ctypes.c_int
+    L.jh_version.restype = ctypes.c_char_p
+    L.jh_version.argtypes = []
+    L.jh_create.argtypes = [i, ctypes.POINTER(c_ctx)]
+    L.jh_create.restype = i
+    L.jh_destroy.argtypes = [c_ctx]
+    L.jh_destroy.restype = None
+    L.jh_last_error.argtypes = [c_ctx]
+    L.jh_last_error.restype = ctypes.c_char_p
+    L.jh_device_info.argtypes = [c_ctx, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(i)]
+    L.jh_device_info.restype = i
+    L.jh_set_stream.argtypes = [c_ctx, p]
+    L.jh_set_stream.restype = i
+    L.jh_get_stream.argtypes = [c_ctx]
+    L.jh_get_stream.restype = p
+    L.jh_set_checks.argtypes = [c_ctx, i]
+    L.jh_set_checks.restype = i
+    L.jh_sync.argtypes = [c_ctx]
+    L.jh_sync.restype = i
+    L.jh_alloc.argtypes = [c_ctx, ctypes.c_size_t, ctypes.POINTER(p)]
+    L.jh_alloc.restype = i
+    L.jh_free.argtypes = [c_ctx, p]
+    L.jh_free.restype = i
+    L.jh_h2d.argtypes = [c_ctx, p, p, ctypes.c_size_t]
+    L.jh_h2d.restype = i
+    L.jh_d2h.argtypes = [c_ctx, p, p, ctypes.c_size_t]
+    L.jh_d2h.restype = i
+    L.jh_dequantize.argtypes = [c_ctx, p, p, p, i, i64, i64, i, i, p, i]
+    L.jh_dequantize.restype = i
+    L.jh_quant_matmul.argtypes = [c_ctx, p, i, i64, p, p, p, i, i64, i64, i, i, i, p, i]
+    L.jh_quant_matmul.restype = i
+    L.jh_gather_quant_matmul.argtypes = [c_ctx, p, i, i64, i64, p, p, p, i, i64, i64, i64, p,
+                                         i64, i, i, i, p, i]
+    L.jh_gather_quant_matmul.restype = i
+    _lib = L
+    return L
+
+
+def check(ctx, rc: int) -> None:
+    if rc != JH_OK:
+        msg = load().jh_last_error(ctx)
+        raise JanisHipError(rc, msg.decode() if msg else "")

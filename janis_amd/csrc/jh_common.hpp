@@ -1,0 +1,103 @@
+// Internal declarations shared by the HIP sources of libjanis_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "../../include/janis_hip.h"
+
+namespace jh {
+
+// ---- element conversions --------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// float -> bfloat16, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+// Two floats -> packed bf16x2 (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load of packed weights (read once per call: non-temporal).
+__device__ __forceinline__ uint4 load_stream16(const uint32_t* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Load element i of a scale/bias array of the given dtype as fp32 (exact).
+__device__ __forceinline__ float load_sb(const void* p, int64_t i, int dt) {
+    if (dt == JH_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    if (dt == JH_F16) return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    return static_cast<const float*>(p)[i];
+}
+
+__device__ __forceinline__ void store_y(void* y, int64_t i, float v, int dt) {
+    if (dt == JH_BF16)
+        static_cast<uint16_t*>(y)[i] = f32_to_bf16(v);
+    else
+        static_cast<float*>(y)[i] = v;
+}
+
+// ---- launch descriptors ------------------------------------------------------
+
+struct QuantMatrix {
+    const uint32_t* w;   // [rows, P]
+    const void* scales;  // [rows, G]
+    const void* biases;  // [rows, G]
+    int sb_dtype;
+    int64_t rows;        // out_features
+    int64_t in;          // in_features (K)
+    int group_size;
+};
+
+struct Status {
+    int code = JH_OK;
+    std::string msg;
+    static Status ok() { return {}; }
+    static Status fail(int c, std::string m) {
+        Status s;
+        s.code = c;
+        s.msg = std::move(m);
+        return s;
+    }
+};
+
+// Launchers (return a failure only for launch-time errors).
+Status launch_dequantize(const QuantMatrix& m, void* out, int out_dtype, hipStream_t st);
+Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int y_dtype,
+                  int num_cus, hipStream_t st);
+Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y,
+                  int y_dtype, int num_cus, hipStream_t st);
+
+struct GatherArgs {
+    QuantMatrix m;        // one expert's shape; w/scales/biases point at expert 0
+    int64_t n_experts;
+    const void* x;
+    int x_dtype;
+    int64_t n_lead, a_vectors, k_slots;
+    const int32_t* idx;
+    void* y;
+    int y_dtype;
+    void* workspace;      // gather_workspace_bytes(n_experts, n_lead*k_slots)
+};
+size_t gather_workspace_bytes(int64_t n_experts, int64_t n_pairs);
+Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st);
+
+}  // namespace jh

@@ -1,0 +1,328 @@
+// C ABI of libjanis_hip.so (include/janis_hip.h): context, memory, argument
+// checking and dispatch of the quantized-linear operators to their kernels.
+//
+// Dispatch mirrors the reference's QuantMatmul (cpu/cpu_misc.go:232-400):
+// rows == 1 is the decode GEMV (qmv.hip), rows > 1 the prefill GEMM (qmm.hip);
+// GatherQuantMatmul buckets by expert on the device (gather.hip).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "jh_common.hpp"
+
+struct jh_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    int num_cus = 256;
+    int checks = 0;
+    char name[256] = {0};
+    std::string err;
+    void* ws = nullptr;  // gather bucketing workspace, grown on demand
+    size_t ws_bytes = 0;
+};
+
+namespace {
+
+thread_local std::string g_create_error;
+
+int fail(jh_ctx* c, int code, const std::string& msg) {
+    if (c) c->err = msg;
+    return code;
+}
+
+int hip_fail(jh_ctx* c, hipError_t e, const char* what) {
+    return fail(c, JH_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define JH_HIP(ctx, call)                                      \
+    do {                                                       \
+        hipError_t e_ = (call);                                \
+        if (e_ != hipSuccess) return hip_fail((ctx), e_, #call); \
+    } while (0)
+
+// Makes ctx's device current on this thread (hipSetDevice is per thread).
+int enter(jh_ctx* c) {
+    if (!c) return JH_ERR_INVALID;
+    c->err.clear();
+    JH_HIP(c, hipSetDevice(c->device));
+    return JH_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_quant(jh_ctx* c, const char* op, const uint32_t* w, const void* s, const void* b,
+                int sb_dtype, int64_t rows, int64_t in, int group_size, int bits) {
+    if (bits != 4)
+        return fail(c, JH_ERR_UNSUPPORTED,
+                    std::string(op) + ": only 4-bit weights are implemented (bits=" +
+                        std::to_string(bits) + ")");
+    if (sb_dtype != JH_BF16 && sb_dtype != JH_F16 && sb_dtype != JH_F32)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": scales/biases must be bf16, f16 or f32");
+    if (rows < 0 || in <= 0)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape");
+    if (in % 8 != 0)
+        return fail(c, JH_ERR_INVALID,
+                    std::string(op) + ": in_features must be a multiple of 8 for 4-bit words");
+    if (group_size <= 0 || in % group_size != 0)
+        return fail(c, JH_ERR_INVALID,
+                    std::string(op) + ": group_size " + std::to_string(group_size) +
+                        " does not divide in_features " + std::to_string(in));
+    if (rows > 0 && (!w || !s || !b))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": null weight pointer");
+    if (!aligned16(w))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": weight pointer not 16-byte aligned");
+    return JH_OK;
+}
+
+int check_act_dtype(jh_ctx* c, const char* op, const char* what, int dt) {
+    if (dt != JH_BF16 && dt != JH_F32)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": " + what + " must be bf16 or f32");
+    return JH_OK;
+}
+
+int finish(jh_ctx* c, const jh::Status& s, const char* op) {
+    if (s.code != JH_OK) return fail(c, s.code, s.msg);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(c, e, op);
+    return JH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* jh_version(void) { return "janis-hip-gfx950 0.1.0"; }
+
+int jh_create(int device, jh_ctx** out) {
+    g_create_error.clear();
+    if (!out) {
+        g_create_error = "jh_create: out is NULL";
+        return JH_ERR_INVALID;
+    }
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) {
+        g_create_error = std::string("jh_create: no HIP device: ") + hipGetErrorString(e);
+        return JH_ERR_HIP;
+    }
+    if (device < 0 || device >= n) {
+        g_create_error = "jh_create: device " + std::to_string(device) + " out of range";
+        return JH_ERR_INVALID;
+    }
+    jh_ctx* c = new jh_ctx();
+    c->device = device;
+    hipDeviceProp_t prop;
+    if ((e = hipSetDevice(device)) != hipSuccess || (e = hipGetDeviceProperties(&prop, device)) != hipSuccess ||
+        (e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking)) != hipSuccess) {
+        g_create_error = std::string("jh_create: ") + hipGetErrorString(e);
+        delete c;
+        return JH_ERR_HIP;
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        g_create_error = std::string("jh_create: device is ") + prop.gcnArchName +
+                         ", this library is built for gfx950 only";
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return JH_ERR_UNSUPPORTED;
+    }
+    c->stream = c->own_stream;
+    c->num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    std::snprintf(c->name, sizeof(c->name), "%s (%s, %d CUs)", prop.name, prop.gcnArchName, c->num_cus);
+    *out = c;
+    return JH_OK;
+}
+
+void jh_destroy(jh_ctx* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->own_stream) (void)hipStreamSynchronize(c->own_stream);
+    if (c->stream && c->stream != c->own_stream) (void)hipStreamSynchronize(c->stream);
+    if (c->ws) (void)hipFree(c->ws);
+    if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+    delete c;
+}
+
+const char* jh_last_error(const jh_ctx* c) { return c ? c->err.c_str() : g_create_error.c_str(); }
+
+int jh_device_info(jh_ctx* c, char* name, size_t name_len, int* compute_units) {
+    if (int r = enter(c)) return r;
+    if (name && name_len) {
+        std::strncpy(name, c->name, name_len - 1);
+        name[name_len - 1] = 0;
+    }
+    if (compute_units) *compute_units = c->num_cus;
+    return JH_OK;
+}
+
+int jh_set_stream(jh_ctx* c, void* s) {
+    if (int r = enter(c)) return r;
+    c->stream = s ? static_cast<hipStream_t>(s) : c->own_stream;
+    return JH_OK;
+}
+
+void* jh_get_stream(const jh_ctx* c) { return c ? static_cast<void*>(c->stream) : nullptr; }
+
+int jh_set_checks(jh_ctx* c, int on) {
+    if (int r = enter(c)) return r;
+    c->checks = on != 0;
+    return JH_OK;
+}
+
+int jh_sync(jh_ctx* c) {
+    if (int r = enter(c)) return r;
+    JH_HIP(c, hipStreamSynchronize(c->stream));
+    return JH_OK;
+}
+
+int jh_alloc(jh_ctx* c, size_t bytes, void** out) {
+    if (int r = enter(c)) return r;
+    if (!out) return fail(c, JH_ERR_INVALID, "jh_alloc: out is NULL");
+    *out = nullptr;
+    if (bytes == 0) bytes = 1;
+    hipError_t e = hipMalloc(out, bytes);
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) {
+        (void)hipGetLastError();
+        return fail(c, JH_ERR_OOM, "jh_alloc: out of device memory for " + std::to_string(bytes) + " bytes");
+    }
+    if (e != hipSuccess) return hip_fail(c, e, "hipMalloc");
+    return JH_OK;
+}
+
+int jh_free(jh_ctx* c, void* p) {
+    if (int r = enter(c)) return r;
+    if (!p) return JH_OK;
+    JH_HIP(c, hipFree(p));
+    return JH_OK;
+}
+
+int jh_h2d(jh_ctx* c, void* dst, const void* src, size_t bytes) {
+    if (int r = enter(c)) return r;
+    if (bytes == 0) return JH_OK;
+    if (!dst || !src) return fail(c, JH_ERR_INVALID, "jh_h2d: null pointer");
+    JH_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+    JH_HIP(c, hipStreamSynchronize(c->stream));
+    return JH_OK;
+}
+
+int jh_d2h(jh_ctx* c, void* dst, const void* src, size_t bytes) {
+    if (int r = enter(c)) return r;
+    if (bytes == 0) return JH_OK;
+    if (!dst || !src) return fail(c, JH_ERR_INVALID, "jh_d2h: null pointer");
+    JH_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+    JH_HIP(c, hipStreamSynchronize(c->stream));
+    return JH_OK;
+}
+
+int jh_dequantize(jh_ctx* c, const uint32_t* w, const void* scales, const void* biases,
+                  jh_dtype sb_dtype, int64_t rows, int64_t in_features, int group_size, int bits,
+                  void* out, jh_dtype out_dtype) {
+    if (int r = enter(c)) return r;
+    if (int r = check_quant(c, "jh_dequantize", w, scales, biases, sb_dtype, rows, in_features,
+                            group_size, bits))
+        return r;
+    if (out_dtype != JH_F32 && out_dtype != JH_BF16)
+        return fail(c, JH_ERR_INVALID, "jh_dequantize: out_dtype must be f32 or bf16");
+    if (rows == 0) return JH_OK;
+    if (!out || !aligned16(out)) return fail(c, JH_ERR_INVALID, "jh_dequantize: out must be 16-byte aligned");
+    jh::QuantMatrix m{w, scales, biases, sb_dtype, rows, in_features, group_size};
+    return finish(c, jh::launch_dequantize(m, out, out_dtype, c->stream), "dequant4_kernel");
+}
+
+int jh_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, const uint32_t* w,
+                    const void* scales, const void* biases, jh_dtype sb_dtype, int64_t out_features,
+                    int64_t in_features, int transpose, int group_size, int bits, void* y,
+                    jh_dtype y_dtype) {
+    if (int r = enter(c)) return r;
+    if (!transpose)
+        return fail(c, JH_ERR_UNSUPPORTED,
+                    "jh_quant_matmul: transpose=false (x @ Dequantize(w)) is not implemented; "
+                    "the models only use transpose=true");
+    if (int r = check_quant(c, "jh_quant_matmul", w, scales, biases, sb_dtype, out_features,
+                            in_features, group_size, bits))
+        return r;
+    if (int r = check_act_dtype(c, "jh_quant_matmul", "x", x_dtype)) return r;
+    if (int r = check_act_dtype(c, "jh_quant_matmul", "y", y_dtype)) return r;
+    if (rows < 0) return fail(c, JH_ERR_INVALID, "jh_quant_matmul: rows < 0");
+    if (rows == 0 || out_features == 0) return JH_OK;
+    if (!x || !y || !aligned16(x) || !aligned16(y))
+        return fail(c, JH_ERR_INVALID, "jh_quant_matmul: x and y must be non-null and 16-byte aligned");
+    jh::QuantMatrix m{w, scales, biases, sb_dtype, out_features, in_features, group_size};
+    if (rows == 1)
+        return finish(c, jh::launch_qmv(m, x, x_dtype, y, y_dtype, c->num_cus, c->stream), "qmv");
+    return finish(c, jh::launch_qmm(m, x, x_dtype, rows, y, y_dtype, c->num_cus, c->stream), "qmm");
+}
+
+int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n_lead,
+                           int64_t a_vectors, const uint32_t* w, const void* scales,
+                           const void* biases, jh_dtype sb_dtype, int64_t n_experts,
+                           int64_t out_features, int64_t in_features, const int32_t* rhs_indices,
+                           int64_t k_slots, int transpose, int group_size, int bits, void* y,
+                           jh_dtype y_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_gather_quant_matmul";
+    if (!transpose) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": transpose=false is not implemented");
+    if (int r = check_quant(c, op, w, scales, biases, sb_dtype, out_features, in_features,
+                            group_size, bits))
+        return r;
+    if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "y", y_dtype)) return r;
+    if (n_lead < 0 || k_slots < 0 || n_experts <= 0)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad n_lead / k_slots / n_experts");
+    if (a_vectors != 1 && a_vectors != k_slots)
+        return fail(c, JH_ERR_INVALID,
+                    std::string(op) + ": a_vectors must be 1 or k_slots (x is [lead, A, 1, in])");
+    const int64_t n_pairs = n_lead * k_slots;
+    if (n_pairs == 0 || out_features == 0) return JH_OK;
+    if (n_pairs > (int64_t)1 << 30) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": too many slots");
+    if (!x || !y || !rhs_indices || !aligned16(x) || !aligned16(y))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": null or unaligned x / y / indices");
+    if (c->checks) {
+        std::vector<int32_t> h((size_t)n_pairs);
+        JH_HIP(c, hipMemcpyAsync(h.data(), rhs_indices, h.size() * sizeof(int32_t),
+                                 hipMemcpyDeviceToHost, c->stream));
+        JH_HIP(c, hipStreamSynchronize(c->stream));
+        for (size_t i = 0; i < h.size(); i++)
+            if (h[i] < 0 || h[i] >= n_experts)
+                return fail(c, JH_ERR_INVALID,
+                            std::string(op) + ": expert index " + std::to_string(h[i]) +
+                                " at slot " + std::to_string(i) + " outside [0, " +
+                                std::to_string(n_experts) + ")");
+    }
+    const size_t need = jh::gather_workspace_bytes(n_experts, n_pairs);
+    if (need > c->ws_bytes) {
+        if (c->ws) {
+            JH_HIP(c, hipStreamSynchronize(c->stream));
+            JH_HIP(c, hipFree(c->ws));
+            c->ws = nullptr;
+            c->ws_bytes = 0;
+        }
+        size_t cap = 4096;
+        while (cap < need) cap *= 2;
+        if (hipMalloc(&c->ws, cap) != hipSuccess) {
+            (void)hipGetLastError();
+            c->ws = nullptr;
+            return fail(c, JH_ERR_OOM, std::string(op) + ": workspace allocation failed");
+        }
+        c->ws_bytes = cap;
+    }
+    jh::GatherArgs a;
+    a.m = jh::QuantMatrix{w, scales, biases, sb_dtype, out_features, in_features, group_size};
+    a.n_experts = n_experts;
+    a.x = x;
+    a.x_dtype = x_dtype;
+    a.n_lead = n_lead;
+    a.a_vectors = a_vectors;
+    a.k_slots = k_slots;
+    a.idx = rhs_indices;
+    a.y = y;
+    a.y_dtype = y_dtype;
+    a.workspace = c->ws;
+    return finish(c, jh::launch_gather(a, c->num_cus, c->stream), "gather");
+}
+
+}  // extern "C"

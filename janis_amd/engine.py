@@ -1,0 +1,237 @@
+"""Host-side mirror of janis's engine.Backend for the quantized-linear path.
+
+HipBackend offers the methods of engine.Backend (engine/backend.go:142-287)
+that this backend implements -- FromRaw, FromFloats, FromInt32, Dequantize,
+QuantMatmul, GatherQuantMatmul, Floats, Ints, Bytes/DTypeOf (RawReader),
+Version, Close -- with the reference's names, argument meaning and result
+shapes, each a thin call into the C ABI of libjanis_hip.so (include/janis_hip.h).
+It is what a Go `hip` package would do over cgo, written in Python so the parity
+tests read like the reference's own backend tests. Bad input raises
+JanisHipError where the reference panics.
+
+Tensors live in device memory owned by the backend (jh_alloc) and are freed
+when the handle is collected, like the Go finalizers of the ggml backend
+(ggml/ggml.go:451-465).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import BF16, F16, F32, I32, U32, U8, JanisHipError, check
+
+DTYPE_SIZE = {F32: 4, F16: 2, BF16: 2, I32: 4, U32: 4, U8: 1}
+DTYPE_NAME = {F32: "F32", F16: "F16", BF16: "BF16", I32: "I32", U32: "U32", U8: "U8"}
+
+
+class Tensor:
+    """Device tensor: shape, dtype, device pointer. engine.Tensor (engine/backend.go:24-26)."""
+
+    def __init__(self, backend: "HipBackend", ptr: int, shape, dtype: int, owned: bool = True, keep=None):
+        self._b = backend
+        self.ptr = int(ptr) if ptr else 0
+        self.shape = tuple(int(d) for d in shape)
+        self.dtype = dtype
+        self._owned = owned
+        self._keep = keep  # an object whose lifetime covers the memory (non-owned views)
+
+    def Shape(self) -> list:
+        return list(self.shape)
+
+    @property
+    def numel(self) -> int:
+        return int(np.prod(self.shape, dtype=np.int64)) if self.shape else 1
+
+    @property
+    def nbytes(self) -> int:
+        return self.numel * DTYPE_SIZE[self.dtype]
+
+    def __del__(self):
+        try:
+            if self._owned and self.ptr and self._b._ctx:
+                _lib.load().jh_free(self._b._ctx, ctypes.c_void_p(self.ptr))
+        except Exception:
+            pass
+        self.ptr = 0
+
+    def __repr__(self):
+        return f"Tensor({DTYPE_NAME[self.dtype]}, {list(self.shape)})"
+
+
+class HipBackend:
+    """engine.Backend subset on one MI355X (gfx950)."""
+
+    def __init__(self, device: int = 0):
+        L = _lib.load()
+        ctx = ctypes.c_void_p()
+        rc = L.jh_create(device, ctypes.byref(ctx))
+        if rc != 0:
+            raise JanisHipError(rc, (L.jh_last_error(None) or b"").decode())
+        self._L = L
+        self._ctx = ctx
+
+    # -- lifecycle / info ------------------------------------------------------
+    def Version(self) -> str:
+        return self._L.jh_version().decode()
+
+    def EngineInfo(self) -> str:
+        buf = ctypes.create_string_buffer(256)
+        cus = ctypes.c_int()
+        check(self._ctx, self._L.jh_device_info(self._ctx, buf, 256, ctypes.byref(cus)))
+        return f"HIP backend on {buf.value.decode()}"
+
+    def Close(self) -> None:
+        if self._ctx:
+            self._L.jh_destroy(self._ctx)
+            self._ctx = None
+
+    def Sync(self) -> None:
+        check(self._ctx, self._L.jh_sync(self._ctx))
+
+    def SetStream(self, stream_handle: int | None) -> None:
+        """Enqueue on a caller's hipStream_t (e.g. torch.cuda.current_stream().cuda_stream)."""
+        check(self._ctx, self._L.jh_set_stream(self._ctx, ctypes.c_void_p(stream_handle or 0)))
+
+    def SetChecks(self, on: bool) -> None:
+        check(self._ctx, self._L.jh_set_checks(self._ctx, int(bool(on))))
+
+    # -- creation ----------------------------------------------------------------
+    def empty(self, dtype: int, *shape) -> Tensor:
+        n = int(np.prod(shape, dtype=np.int64)) if shape else 1
+        p = ctypes.c_void_p()
+        check(self._ctx, self._L.jh_alloc(self._ctx, max(1, n * DTYPE_SIZE[dtype]), ctypes.byref(p)))
+        return Tensor(self, p.value, shape, dtype)
+
+    def FromRaw(self, dt: int, raw, *shape) -> Tensor:
+        """Copies packed little-endian bytes of dtype dt (engine/backend.go:152-154)."""
+        buf = np.frombuffer(raw, dtype=np.uint8) if isinstance(raw, (bytes, bytearray, memoryview)) \
+            else np.ascontiguousarray(raw).view(np.uint8).reshape(-1)
+        t = self.empty(dt, *shape)
+        if buf.size != t.nbytes:
+            raise JanisHipError(_lib.JH_ERR_INVALID,
+                                f"FromRaw: {buf.size} bytes for shape {list(shape)} of {DTYPE_NAME[dt]}")
+        check(self._ctx, self._L.jh_h2d(self._ctx, ctypes.c_void_p(t.ptr),
+                                        buf.ctypes.data_as(ctypes.c_void_p), buf.size))
+        return t
+
+    def FromFloats(self, data, *shape) -> Tensor:
+        a = np.ascontiguousarray(data, dtype=np.float32)
+        return self.FromRaw(F32, a, *(shape or a.shape))
+
+    def FromInt32(self, data, *shape) -> Tensor:
+        a = np.ascontiguousarray(data, dtype=np.int32)
+        return self.FromRaw(I32, a, *(shape or a.shape))
+
+    def FromBF16Bits(self, bits, *shape) -> Tensor:
+        a = np.ascontiguousarray(bits, dtype=np.uint16)
+        return self.FromRaw(BF16, a, *(shape or a.shape))
+
+    def Wrap(self, ptr: int, shape, dtype: int, keep=None) -> Tensor:
+        """A non-owning handle over existing device memory (e.g. a torch tensor)."""
+        return Tensor(self, ptr, shape, dtype, owned=False, keep=keep)
+
+    # -- read back -------------------------------------------------------------------
+    def Bytes(self, t: Tensor) -> bytes:
+        out = np.empty(t.nbytes, dtype=np.uint8)
+        check(self._ctx, self._L.jh_d2h(self._ctx, out.ctypes.data_as(ctypes.c_void_p),
+                                        ctypes.c_void_p(t.ptr), t.nbytes))
+        return out.tobytes()
+
+    def DTypeOf(self, t: Tensor) -> int:
+        return t.dtype
+
+    def Floats(self, t: Tensor) -> np.ndarray:
+        """engine/backend.go:276-277: evaluates and copies out as float32."""
+        raw = np.frombuffer(self.Bytes(t), dtype=np.uint8)
+        if t.dtype == F32:
+            a = raw.view(np.float32)
+        elif t.dtype == BF16:
+            a = (raw.view(np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+        elif t.dtype == F16:
+            a = raw.view(np.float16).astype(np.float32)
+        elif t.dtype in (I32,):
+            a = raw.view(np.int32).astype(np.float32)
+        else:
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"Floats: unsupported dtype {DTYPE_NAME[t.dtype]}")
+        return a.reshape(t.shape).copy()
+
+    def Ints(self, t: Tensor) -> np.ndarray:
+        raw = np.frombuffer(self.Bytes(t), dtype=np.uint8)
+        if t.dtype not in (I32, U32):
+            raise JanisHipError(_lib.JH_ERR_INVALID, "Ints: tensor is not I32/U32")
+        return raw.view(np.int32).reshape(t.shape).copy()
+
+    # -- quantized operators ------------------------------------------------------------
+    @staticmethod
+    def _sb_dtype(scales: Tensor, biases: Tensor) -> int:
+        if scales.dtype != biases.dtype:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "scales and biases differ in dtype")
+        return scales.dtype
+
+    def Dequantize(self, w: Tensor, scales: Tensor, biases: Tensor, groupSize: int, bits: int,
+                   out_dtype: int = F32) -> Tensor:
+        """engine/backend.go:261-263: w [..., P] U32 -> [..., P*32/bits] (cpu/cpu_misc.go:134-161)."""
+        if w.dtype != U32:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "Dequantize: weight tensor is not packed U32")
+        P = w.shape[-1]
+        k = P * (32 // bits)
+        rows = w.numel // P
+        out = self.empty(out_dtype, *w.shape[:-1], k)
+        check(self._ctx, self._L.jh_dequantize(self._ctx, w.ptr, scales.ptr, biases.ptr,
+                                               self._sb_dtype(scales, biases), rows, k, groupSize,
+                                               bits, out.ptr, out_dtype))
+        return out
+
+    def QuantMatmul(self, x: Tensor, w: Tensor, scales: Tensor, biases: Tensor, transpose: bool,
+                    groupSize: int, bits: int, out: Tensor | None = None, out_dtype: int | None = None) -> Tensor:
+        """engine/backend.go:265-267: x [..., in] -> [..., out] with W [out, P]
+        (transpose=true, cpu/cpu_misc.go:232-400). The result has x's dtype
+        unless out_dtype says otherwise; `out` may supply the result buffer."""
+        if w.dtype != U32:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatmul: weight tensor is not packed U32")
+        n, P = w.shape[-2], w.shape[-1]
+        k = P * (32 // bits)
+        if x.shape[-1] != k:
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"QuantMatmul: x has {x.shape[-1]} features, W has {k}")
+        rows = x.numel // k
+        yd = out_dtype if out_dtype is not None else (out.dtype if out is not None else x.dtype)
+        y = out if out is not None else self.empty(yd, *x.shape[:-1], n)
+        check(self._ctx, self._L.jh_quant_matmul(self._ctx, x.ptr, x.dtype, rows, w.ptr, scales.ptr,
+                                                 biases.ptr, self._sb_dtype(scales, biases), n, k,
+                                                 int(bool(transpose)), groupSize, bits, y.ptr, y.dtype))
+        return y
+
+    def GatherQuantMatmul(self, x: Tensor, w: Tensor, scales: Tensor, biases: Tensor, rhsIndices: Tensor,
+                          transpose: bool, groupSize: int, bits: int, out: Tensor | None = None,
+                          out_dtype: int | None = None) -> Tensor:
+        """engine/backend.go:269-274: x [lead.., A, 1, in], stacks [E, out, .],
+        rhsIndices [lead.., K] -> [lead.., K, 1, out] (cpu/cpu_misc.go:178-230)."""
+        if w.dtype != U32 or len(w.shape) != 3:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "GatherQuantMatmul: w must be U32 [E, out, P]")
+        if rhsIndices.dtype != I32:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "GatherQuantMatmul: indices must be I32")
+        E, n, P = w.shape
+        k = P * (32 // bits)
+        rs = rhsIndices.shape
+        K = rs[-1]
+        n_lead = int(np.prod(rs[:-1], dtype=np.int64)) if len(rs) > 1 else 1
+        if x.shape[-1] != k or len(x.shape) < 3:
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"GatherQuantMatmul: x {list(x.shape)} vs in={k}")
+        A = x.shape[-3]
+        if x.numel != n_lead * A * k:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "GatherQuantMatmul: x lead dims do not match indices")
+        yd = out_dtype if out_dtype is not None else (out.dtype if out is not None else x.dtype)
+        y = out if out is not None else self.empty(yd, *rs, 1, n)
+        check(self._ctx, self._L.jh_gather_quant_matmul(
+            self._ctx, x.ptr, x.dtype, n_lead, A, w.ptr, scales.ptr, biases.ptr,
+            self._sb_dtype(scales, biases), E, n, k, rhsIndices.ptr, K, int(bool(transpose)),
+            groupSize, bits, y.ptr, y.dtype))
+        return y
+
+    def __del__(self):
+        try:
+            self.Close()
+        except Exception:
+            pass

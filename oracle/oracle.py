@@ -1,0 +1,171 @@
+"""ctypes view of the CPU oracle (liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, always as the checker or the CPU baseline, never as the product.
+It restates janis's CPU quantized-linear arithmetic; see janis_oracle.h for the
+reference file:line each function follows.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+
+_lib = None
+
+
+def build() -> None:
+    """Compile liboracle.so from the C sources next to this file."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        L.or_dequantize.argtypes = [_u32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _int, _int]
+        L.or_dequantize.restype = None
+        for name in ("or_qchannel4_ref", "or_qchannel4_avx2_order", "or_qchannel4_avx2"):
+            fn = getattr(L, name)
+            fn.argtypes = [_u32p, _f32p, _f32p, _f32p, _int, _int]
+            fn.restype = ctypes.c_float
+        L.or_have_avx2_fma.argtypes = []
+        L.or_have_avx2_fma.restype = _int
+        L.or_qmv_blocked_go.argtypes = [_f32p, _u32p, _f32p, _f32p, _f32p, _i64, _i64, _int, _int]
+        L.or_qmv_blocked_go.restype = None
+        L.or_qmv_generic.argtypes = [_f32p, _u32p, _f32p, _f32p, _f32p, _i64, _i64, _int, _int]
+        L.or_qmv_generic.restype = None
+        L.or_qmm_wbuf.argtypes = [_f32p, _i64, _u32p, _f32p, _f32p, _f32p, _i64, _i64, _int, _int]
+        L.or_qmm_wbuf.restype = None
+        L.or_quant_matmul.argtypes = [_f32p, _i64, _u32p, _f32p, _f32p, _f32p, _i64, _i64, _int, _int, _int]
+        L.or_quant_matmul.restype = None
+        L.or_gather_quant_matmul.argtypes = [_f32p, _i64, _i64, _u32p, _f32p, _f32p, _i64, _i32p, _i64,
+                                             _f32p, _i64, _i64, _int, _int, _int]
+        L.or_gather_quant_matmul.restype = _int
+        L.or_qmv_avx2_parallel.argtypes = [_f32p, _u32p, _f32p, _f32p, _f32p, _i64, _i64, _int, _int]
+        L.or_qmv_avx2_parallel.restype = _int
+        L.or_topk.argtypes = [_f32p, _int, _int, _i32p, _f32p]
+        L.or_topk.restype = None
+        L.or_softmax_row.argtypes = [_f32p, _f32p, _int]
+        L.or_softmax_row.restype = None
+        _lib = L
+    return _lib
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _u32(a):
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+def dequantize(w, s, b, group_size: int, bits: int = 4) -> np.ndarray:
+    """cpu/cpu_misc.go:134-161. w [..., P] -> [..., P*32/bits] float32."""
+    w, s, b = _u32(w), _f32(s), _f32(b)
+    P = w.shape[-1]
+    rows = w.size // P
+    out = np.empty(w.shape[:-1] + (P * (32 // bits),), dtype=np.float32)
+    lib().or_dequantize(w, s, b, out, rows, P, s.shape[-1], group_size, bits)
+    return out
+
+
+def qchannel4(kind: str, w, x, s, b, groups: int, wpg: int) -> float:
+    fn = {"ref": lib().or_qchannel4_ref, "avx2_order": lib().or_qchannel4_avx2_order,
+          "avx2": lib().or_qchannel4_avx2}[kind]
+    return float(fn(_u32(w), _f32(x), _f32(s), _f32(b), groups, wpg))
+
+
+def have_avx2_fma() -> bool:
+    return bool(lib().or_have_avx2_fma())
+
+
+def quant_matmul(x, w, s, b, group_size: int, bits: int = 4, simd: bool = True) -> np.ndarray:
+    """cpu/cpu_misc.go:232-400 (transpose=true). x [..., K] -> [..., N]."""
+    x, w, s, b = _f32(x), _u32(w), _f32(s), _f32(b)
+    N, P = w.shape[-2], w.shape[-1]
+    K = P * (32 // bits)
+    assert x.shape[-1] == K, (x.shape, K)
+    rows = x.size // K
+    y = np.empty(x.shape[:-1] + (N,), dtype=np.float32)
+    lib().or_quant_matmul(x, rows, w, s, b, y, N, K, group_size, bits, int(simd))
+    return y
+
+
+def qmv_blocked_go(x, w, s, b, group_size: int, workers: int = 1) -> np.ndarray:
+    x, w, s, b = _f32(x), _u32(w), _f32(s), _f32(b)
+    N, K = w.shape[-2], w.shape[-1] * 8
+    y = np.empty((N,), dtype=np.float32)
+    lib().or_qmv_blocked_go(x, w, s, b, y, N, K, group_size, workers)
+    return y
+
+
+def qmv_generic(x, w, s, b, group_size: int, bits: int) -> np.ndarray:
+    x, w, s, b = _f32(x), _u32(w), _f32(s), _f32(b)
+    N, K = w.shape[-2], w.shape[-1] * (32 // bits)
+    y = np.empty((N,), dtype=np.float32)
+    lib().or_qmv_generic(x, w, s, b, y, N, K, group_size, bits)
+    return y
+
+
+def qmm_wbuf(x, w, s, b, group_size: int, bits: int = 4) -> np.ndarray:
+    x, w, s, b = _f32(x), _u32(w), _f32(s), _f32(b)
+    N, K = w.shape[-2], w.shape[-1] * (32 // bits)
+    rows = x.size // K
+    y = np.empty(x.shape[:-1] + (N,), dtype=np.float32)
+    lib().or_qmm_wbuf(x, rows, w, s, b, y, N, K, group_size, bits)
+    return y
+
+
+def gather_quant_matmul(x, w, s, b, idx, group_size: int, bits: int = 4, simd: bool = True) -> np.ndarray:
+    """cpu/cpu_misc.go:178-230. x [n_lead, A, 1, K] (or [n_lead, A, K]),
+    w [E, N, P], idx [n_lead, k] -> y [n_lead, k, 1, N]."""
+    x, w, s, b = _f32(x), _u32(w), _f32(s), _f32(b)
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    E, N, P = w.shape
+    K = P * (32 // bits)
+    n_lead = int(np.prod(idx.shape[:-1], dtype=np.int64))
+    k_slots = idx.shape[-1]
+    A = x.size // (n_lead * K)
+    y = np.zeros(idx.shape + (1, N), dtype=np.float32)
+    rc = lib().or_gather_quant_matmul(x, n_lead, A, w, s, b, E, idx, k_slots, y, N, K,
+                                      group_size, bits, int(simd))
+    if rc != 0:
+        raise IndexError("expert index out of range")
+    return y
+
+
+def qmv_avx2_parallel(x, w, s, b, group_size: int, workers: int) -> tuple[np.ndarray, int]:
+    x, w, s, b = _f32(x), _u32(w), _f32(s), _f32(b)
+    N, K = w.shape[-2], w.shape[-1] * 8
+    y = np.empty((N,), dtype=np.float32)
+    used = lib().or_qmv_avx2_parallel(x, w, s, b, y, N, K, group_size, workers)
+    return y, used
+
+
+def topk(row, k: int) -> tuple[np.ndarray, np.ndarray]:
+    row = _f32(row)
+    idx = np.empty(k, dtype=np.int32)
+    val = np.empty(k, dtype=np.float32)
+    lib().or_topk(row, row.size, k, idx, val)
+    return idx, val
+
+
+def softmax_row(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().or_softmax_row(x, out, x.size)
+    return out

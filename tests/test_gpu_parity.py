@@ -1,0 +1,306 @@
+"""GPU parity of the HIP backend against the CPU oracle, through the C ABI.
+
+Bar (as stated for this path): bf16 outputs within 1e-2 * max|y_oracle| of the
+oracle (the relOK convention of ggml/ggml_test.go:56-65, fp32 accumulation on
+both sides); dequantized weights bit-exact. fp32 outputs are held to 1e-3.
+At full model sizes the oracle is run on a random subset of output rows (each
+output depends only on its own weight row), and size-independent properties
+(one-hot columns, linearity) cover the whole matrix.
+"""
+import numpy as np
+import pytest
+
+from janis_amd import synth
+from janis_amd.engine import BF16, F16, F32, I32, U32, JanisHipError
+from tests.conftest import rel_ok, step, upload_quant
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+F32_TOL = 1e-3
+
+
+def _oracle_rows(oracle, x, q, rows):
+    """Oracle QuantMatmul restricted to output rows `rows` (decode or prefill path)."""
+    return oracle.quant_matmul(x, q.w[rows], q.s[rows], q.b[rows], q.group_size)
+
+
+# -- Dequantize ----------------------------------------------------------------
+
+def test_dequantize_known_answer(hip):
+    """cpu/cpu_test.go:121-149 through the C ABI."""
+    step("jh_dequantize word 0x87654321 gs=4")
+    w = hip.FromRaw(U32, np.array([0x87654321], np.uint32), 1, 1)
+    s = hip.FromFloats(np.array([2.0, 0.1], np.float32), 1, 2)
+    b = hip.FromFloats(np.array([0.5, -1.0], np.float32), 1, 2)
+    got = hip.Floats(hip.Dequantize(w, s, b, 4, 4))[0]
+    want = np.array([2.5, 4.5, 6.5, 8.5, -0.5, -0.4, -0.3, -0.2], np.float32)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-6)
+    step("jh_quant_matmul ones gs=4 (generic kernel)")
+    x = hip.FromFloats(np.ones(8, np.float32), 1, 8)
+    y = hip.Floats(hip.QuantMatmul(x, w, s, b, True, 4, 4))
+    assert abs(float(y[0, 0]) - 20.6) < 1e-5
+
+
+@pytest.mark.parametrize("sb", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("n,k,gs", [(64, 4096, 64), (33, 768, 32), (17, 1024, 128), (5, 64, 16)])
+def test_dequantize_bit_exact(hip, oracle, sb, n, k, gs):
+    q = synth.quant_linear(100 + n, n, k, gs)
+    w = hip.FromRaw(U32, q.w, n, k // 8)
+    if sb == "bf16":
+        s_np, b_np = q.s, q.b
+        s, b = hip.FromBF16Bits(q.s_bits, *q.s_bits.shape), hip.FromBF16Bits(q.b_bits, *q.b_bits.shape)
+    elif sb == "f16":
+        s_np = q.s.astype(np.float16).astype(np.float32)
+        b_np = q.b.astype(np.float16).astype(np.float32)
+        s = hip.FromRaw(F16, q.s.astype(np.float16), *q.s.shape)
+        b = hip.FromRaw(F16, q.b.astype(np.float16), *q.b.shape)
+    else:  # arbitrary fp32 scales: q*s is not exact, so the rounding order matters
+        rng = np.random.default_rng(n)
+        s_np = (q.s * (1 + rng.random(q.s.shape, dtype=np.float32) * 1e-3)).astype(np.float32)
+        b_np = (q.b + rng.random(q.b.shape, dtype=np.float32) * 1e-4).astype(np.float32)
+        s, b = hip.FromFloats(s_np), hip.FromFloats(b_np)
+    step(f"jh_dequantize {n}x{k} gs={gs} scales={sb}")
+    got = hip.Floats(hip.Dequantize(w, s, b, gs, 4))
+    want = oracle.dequantize(q.w, s_np, b_np, gs)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    got16 = hip.Floats(hip.Dequantize(w, s, b, gs, 4, out_dtype=BF16))
+    assert np.array_equal(got16, synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(want)))
+
+
+@pytest.mark.parametrize("name,tol", [("f32", 2e-4), ("bf16", 5e-2)])
+def test_inkling2_embed_golden(hip, name, tol):
+    """The MLX golden embedding held by the reference (inkling2/testdata), with
+    the dequantization on the GPU and RMSNorm (cpu/cpu_ops.go:145-162) on the host."""
+    import os
+
+    from tests.test_oracle import GOLDEN, _rmsnorm_rows
+
+    fx = np.load(os.path.join(GOLDEN, f"inkling2_embed_{name}.npz"))
+    rows = fx["w"][fx["tokens"]]
+    w = hip.FromRaw(U32, rows, *rows.shape)
+    if str(fx["s_dtype"]) == "BF16":
+        s = hip.FromBF16Bits(fx["s"][fx["tokens"]])
+        b = hip.FromBF16Bits(fx["b"][fx["tokens"]])
+        norm = synth.bf16_bits_to_f32(fx["norm"])
+    else:
+        s, b, norm = hip.FromFloats(fx["s"][fx["tokens"]]), hip.FromFloats(fx["b"][fx["tokens"]]), fx["norm"]
+    step(f"jh_dequantize inkling2 embed {name}")
+    deq = hip.Floats(hip.Dequantize(w, s, b, int(fx["group_size"]), int(fx["bits"])))
+    got = _rmsnorm_rows(deq, norm, float(fx["eps"]))
+    ok, d, sc = rel_ok(got, fx["embed"], tol)
+    assert ok, (d, sc)
+
+
+# -- decode qmv ---------------------------------------------------------------
+
+QMV_SHAPES = [
+    # (N, K, gs): every fast-kernel instantiation, group sizes, ragged N, the generic path
+    (4096, 4096, 64), (1024, 4096, 64), (33, 2048, 64), (1000, 6144, 64), (257, 8192, 64),
+    (4096, 12288, 64), (100, 16384, 64), (129, 1024, 64), (70, 3072, 64), (65, 512, 64),
+    (48, 1536, 64), (31, 256, 64), (768, 768, 64), (300, 4096, 32), (300, 4096, 128),
+    (50, 2048, 32), (40, 768, 128), (24, 1032, 8), (9, 96, 32),
+]
+
+
+@pytest.mark.parametrize("n,k,gs", QMV_SHAPES)
+def test_qmv_matches_oracle(hip, oracle, n, k, gs):
+    q = synth.quant_linear(1000 + n + k, n, k, gs)
+    xb, x = synth.activations(2000 + k, (1, k))
+    w, s, b = upload_quant(hip, q)
+    xt = hip.FromBF16Bits(xb, 1, k)
+    want = oracle.quant_matmul(x, q.w, q.s, q.b, gs)  # AVX2-kernel order (cpu/qmv_amd64.s)
+    step(f"jh_quant_matmul rows=1 N={n} K={k} gs={gs} y=bf16")
+    y16 = hip.Floats(hip.QuantMatmul(xt, w, s, b, True, gs, 4))
+    ok, d, sc = rel_ok(y16, want, BF16_TOL)
+    assert ok, ("bf16", d, sc)
+    step(f"jh_quant_matmul rows=1 N={n} K={k} gs={gs} y=f32")
+    y32 = hip.Floats(hip.QuantMatmul(xt, w, s, b, True, gs, 4, out_dtype=F32))
+    ok, d, sc = rel_ok(y32, want, F32_TOL)
+    assert ok, ("f32", d, sc)
+
+
+def test_qmv_f32_activations(hip, oracle):
+    """x in fp32 (the CPU backend's activation type) takes the generic kernel."""
+    q = synth.quant_linear(7, 200, 4096)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, 4096)).astype(np.float32)
+    w, s, b = upload_quant(hip, q)
+    step("jh_quant_matmul rows=1 x=f32")
+    y = hip.Floats(hip.QuantMatmul(hip.FromFloats(x), w, s, b, True, 64, 4))
+    ok, d, sc = rel_ok(y, oracle.quant_matmul(x, q.w, q.s, q.b, 64), F32_TOL)
+    assert ok, (d, sc)
+
+
+@pytest.mark.parametrize("name,n,k", [("q_proj", 4096, 4096), ("k_proj", 1024, 4096),
+                                      ("gate_up", 24576, 4096), ("down", 4096, 12288),
+                                      ("lm_head", 151936, 4096)])
+def test_qwen3_8b_decode_shapes(hip, oracle, name, n, k):
+    """Config-1 shapes at full size: oracle on 384 random rows, plus one-hot
+    columns over the whole matrix (bit-exact with fp32 output)."""
+    q = synth.quant_linear(3000 + n, n, k)
+    xb, x = synth.activations(4000 + k, (1, k))
+    w, s, b = upload_quant(hip, q)
+    step(f"jh_quant_matmul {name} {n}x{k}")
+    y = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, 1, k), w, s, b, True, 64, 4))
+    rows = np.sort(np.random.default_rng(n).choice(n, size=min(n, 384), replace=False))
+    want = _oracle_rows(oracle, x, q, rows)
+    ok, d, sc = rel_ok(y[0, rows], want[0], BF16_TOL)
+    assert ok, (d, sc)
+    for j in (0, 31, k // 2 + 5, k - 1):
+        e = np.zeros((1, k), np.uint16)
+        e[0, j] = 0x3F80  # bf16 1.0
+        step(f"jh_quant_matmul {name} one-hot column {j}")
+        yc = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(e, 1, k), w, s, b, True, 64, 4, out_dtype=F32))[0]
+        col = oracle.dequantize(q.w[rows], q.s[rows], q.b[rows], 64)[:, j]
+        assert np.array_equal(yc[rows].view(np.uint32), col.copy().view(np.uint32))
+
+
+def test_qmv_linearity_full_lm_head(hip):
+    """y(a + b) == y(a) + y(b) over all 151936 rows (fp32 output), with b = a
+    with random signs so that a + b (0 or 2a) is exact in bf16."""
+    n, k = 151936, 4096
+    q = synth.quant_linear(77, n, k)
+    w, s, b = upload_quant(hip, q)
+    ab, a = synth.activations(78, (1, k))
+    sign = np.random.default_rng(79).integers(0, 2, (1, k)).astype(np.uint16) << np.uint16(15)
+    bb = (ab ^ sign).astype(np.uint16)
+    cb = synth.f32_to_bf16_bits((a + synth.bf16_bits_to_f32(bb)).astype(np.float32))
+    assert np.array_equal(synth.bf16_bits_to_f32(cb), a + synth.bf16_bits_to_f32(bb))
+    run = lambda xb: hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, 1, k), w, s, b, True, 64, 4,
+                                                out_dtype=F32))[0].astype(np.float64)
+    step("jh_quant_matmul lm_head linearity")
+    ya, yb, yc = run(ab), run(bb), run(cb)
+    ok, d, sc = rel_ok(yc, ya + yb, F32_TOL)
+    assert ok, (d, sc)
+
+
+# -- prefill qmm ------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k,gs", [(2, 64, 512, 64), (3, 130, 1024, 64), (13, 256, 2048, 64),
+                                      (128, 384, 4096, 64), (77, 200, 1024, 32), (40, 96, 768, 128),
+                                      (5, 24, 1032, 8)])
+def test_qmm_matches_oracle(hip, oracle, m, n, k, gs):
+    q = synth.quant_linear(5000 + m + n, n, k, gs)
+    xb, x = synth.activations(6000 + m, (m, k))
+    w, s, b = upload_quant(hip, q)
+    want = oracle.quant_matmul(x, q.w, q.s, q.b, gs)  # wbuf order (cpu/cpu_misc.go:378-399)
+    step(f"jh_quant_matmul rows={m} N={n} K={k} gs={gs}")
+    y = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, m, k), w, s, b, True, gs, 4))
+    ok, d, sc = rel_ok(y, want, BF16_TOL)
+    assert ok, (d, sc)
+    y32 = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, m, k), w, s, b, True, gs, 4, out_dtype=F32))
+    ok, d, sc = rel_ok(y32, want, 5e-3)
+    assert ok, ("f32 out", d, sc)
+
+
+@pytest.mark.parametrize("m", [128, 512, 2048])
+@pytest.mark.parametrize("name,n,k", [("gate_up", 12288, 4096), ("down", 4096, 12288)])
+def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
+    """Config-2 shapes: the oracle on a random 48x96 block of the output."""
+    q = synth.quant_linear(7000 + n, n, k)
+    xb, x = synth.activations(8000 + m, (m, k))
+    w, s, b = upload_quant(hip, q)
+    step(f"jh_quant_matmul prefill {name} M={m}")
+    y = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, m, k), w, s, b, True, 64, 4))
+    rng = np.random.default_rng(m + n)
+    rs = np.sort(rng.choice(m, size=min(m, 48), replace=False))
+    cs = np.sort(rng.choice(n, size=96, replace=False))
+    want = oracle.quant_matmul(x[rs], q.w[cs], q.s[cs], q.b[cs], 64)
+    ok, d, sc = rel_ok(y[np.ix_(rs, cs)], want, BF16_TOL)
+    assert ok, (d, sc)
+
+
+def test_qmm_rows_are_independent(hip):
+    """Row r of a prefill product equals the decode product of x[r] (fp32 out, 1e-3)."""
+    q = synth.quant_linear(11, 512, 4096)
+    xb, _ = synth.activations(12, (37, 4096))
+    w, s, b = upload_quant(hip, q)
+    step("jh_quant_matmul rows=37 vs rows=1")
+    y = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, 37, 4096), w, s, b, True, 64, 4, out_dtype=F32))
+    for r in (0, 17, 36):
+        yr = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb[r:r + 1], 1, 4096), w, s, b, True, 64, 4,
+                                        out_dtype=F32))
+        ok, d, sc = rel_ok(y[r], yr[0], 5e-3)
+        assert ok, (r, d, sc)
+
+
+# -- MoE gather ------------------------------------------------------------------
+
+@pytest.mark.parametrize("n_tok", [1, 16])
+@pytest.mark.parametrize("proj", ["gate", "down"])
+def test_gather_qwen3_30b_a3b(hip, oracle, n_tok, proj):
+    """Config 3: 128 experts, hidden 2048, moe_intermediate 768, top-8 of a
+    seeded router. gate: x [T,1,1,2048] shared by the 8 slots (A=1);
+    down: x [T,8,1,768] one vector per slot (A=K)."""
+    E, K = 128, 8
+    n, k = (768, 2048) if proj == "gate" else (2048, 768)
+    A = 1 if proj == "gate" else K
+    q = synth.quant_linear(9000 + n, n, k, lead=(E,))
+    idx, _ = synth.route(9100 + n_tok, n_tok, E, K)
+    xb, x = synth.activations(9200 + n_tok, (n_tok, A, 1, k))
+    w, s, b = upload_quant(hip, q)
+    it = hip.FromInt32(idx)
+    step(f"jh_gather_quant_matmul {proj} T={n_tok} U={len(np.unique(idx))}")
+    y = hip.Floats(hip.GatherQuantMatmul(hip.FromBF16Bits(xb, n_tok, A, 1, k), w, s, b, it, True, 64, 4))
+    assert y.shape == (n_tok, K, 1, n)
+    want = oracle.gather_quant_matmul(x, q.w, q.s, q.b, idx, 64)
+    ok, d, sc = rel_ok(y, want, BF16_TOL)
+    assert ok, (d, sc)
+
+
+@pytest.mark.parametrize("E,n,k,gs,A", [(6, 40, 512, 64, 1), (6, 40, 512, 64, 8), (3, 100, 4096, 32, 1),
+                                         (5, 64, 1032, 8, 8)])
+def test_gather_small_with_collisions(hip, oracle, E, n, k, gs, A):
+    """Many slots per expert (R > 1 buckets), ragged rows, generic kernel."""
+    K, T = 8, 4
+    q = synth.quant_linear(50 + E + k, n, k, gs, lead=(E,))
+    idx = np.random.default_rng(E * k).integers(0, E, (T, K)).astype(np.int32)
+    xb, x = synth.activations(60 + A, (T, A, 1, k))
+    w, s, b = upload_quant(hip, q)
+    step(f"jh_gather_quant_matmul E={E} n={n} k={k} gs={gs} A={A}")
+    y = hip.Floats(hip.GatherQuantMatmul(hip.FromBF16Bits(xb, T, A, 1, k), w, s, b, hip.FromInt32(idx),
+                                         True, gs, 4, out_dtype=F32))
+    want = oracle.gather_quant_matmul(x, q.w, q.s, q.b, idx, gs)
+    ok, d, sc = rel_ok(y, want, F32_TOL)
+    assert ok, (d, sc)
+    # f32 activations take the generic gather kernel
+    yf = hip.Floats(hip.GatherQuantMatmul(hip.FromFloats(x), w, s, b, hip.FromInt32(idx), True, gs, 4))
+    ok, d, sc = rel_ok(yf, want, F32_TOL)
+    assert ok, ("f32 x", d, sc)
+
+
+def test_gather_out_of_range_index(hip):
+    q = synth.quant_linear(1, 32, 512, lead=(4,))
+    w, s, b = upload_quant(hip, q)
+    xb, _ = synth.activations(2, (1, 1, 1, 512))
+    idx = hip.FromInt32(np.array([[0, 7, 3, -1]], np.int32))
+    step("jh_gather_quant_matmul bad index, checks off")
+    y = hip.Floats(hip.GatherQuantMatmul(hip.FromBF16Bits(xb, 1, 1, 1, 512), w, s, b, idx, True, 64, 4,
+                                         out_dtype=F32))
+    assert np.isfinite(y[0, 0]).all() and np.isfinite(y[0, 2]).all()
+    assert np.isnan(y[0, 1]).all() and np.isnan(y[0, 3]).all()
+    hip.SetChecks(True)
+    try:
+        step("jh_gather_quant_matmul bad index, checks on")
+        with pytest.raises(JanisHipError):
+            hip.GatherQuantMatmul(hip.FromBF16Bits(xb, 1, 1, 1, 512), w, s, b, idx, True, 64, 4)
+    finally:
+        hip.SetChecks(False)
+
+
+# -- errors (the reference panics) ---------------------------------------------------
+
+def test_bad_arguments_raise(hip):
+    q = synth.quant_linear(1, 16, 256)
+    w, s, b = upload_quant(hip, q)
+    xb, _ = synth.activations(1, (1, 256))
+    x = hip.FromBF16Bits(xb, 1, 256)
+    with pytest.raises(JanisHipError):  # 8-bit not implemented
+        hip.QuantMatmul(x, w, s, b, True, 64, 8)
+    with pytest.raises(JanisHipError):  # transpose=false
+        hip.QuantMatmul(x, w, s, b, False, 64, 4)
+    with pytest.raises(JanisHipError):  # group does not divide K
+        hip.QuantMatmul(x, w, s, b, True, 96, 4)
+    with pytest.raises(JanisHipError):  # feature mismatch
+        hip.QuantMatmul(hip.FromBF16Bits(np.zeros((1, 128), np.uint16)), w, s, b, True, 64, 4)

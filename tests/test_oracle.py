@@ -1,0 +1,254 @@
+"""Pins the CPU oracle (oracle/) before anything is compared against it.
+
+Every oracle function is checked against at least one of: the reference's own
+known answer (cpu/cpu_test.go:121-149), the MLX-produced golden embedding held
+by the reference (inkling2/testdata, via tests/golden/), closed forms
+(one-hot and all-ones inputs), float64 brute force, and bit-identity between
+two independent restatements of the same kernel (scalar lane order vs AVX2
+intrinsics).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from janis_amd import synth
+from tests.conftest import rel_ok
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def brute_f64(x, q):
+    """float64 brute force: dequantize exactly, then a dense product."""
+    from oracle import oracle as o
+
+    wd = o.dequantize(q.w, q.s, q.b, q.group_size).astype(np.float64)
+    return np.asarray(x, dtype=np.float64) @ wd.T
+
+
+# -- the reference's only numeric known answer -----------------------------
+
+def test_dequantize_known_answer(oracle):
+    """cpu/cpu_test.go:121-149: word 0x87654321, group 4, S={2,0.1}, B={0.5,-1}."""
+    w = np.array([[0x87654321]], dtype=np.uint32)
+    s = np.array([[2.0, 0.1]], dtype=np.float32)
+    b = np.array([[0.5, -1.0]], dtype=np.float32)
+    got = oracle.dequantize(w, s, b, 4, 4)
+    want = np.array([2.5, 4.5, 6.5, 8.5, -0.5, -0.4, -0.3, -0.2], dtype=np.float32)
+    np.testing.assert_allclose(got[0], want, rtol=0, atol=1e-6)
+    y = oracle.quant_matmul(np.ones((1, 8), np.float32), w, s, b, 4, 4)
+    assert abs(float(y[0, 0]) - 20.6) < 1e-5
+
+
+def test_dequantize_is_fl32_q_times_s_plus_b(oracle):
+    q = synth.quant_linear(11, 16, 256)
+    got = oracle.dequantize(q.w, q.s, q.b, 64)
+    codes = ((q.w[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(16, 256)
+    g = np.arange(256) // 64
+    want = (codes.astype(np.float32) * q.s[:, g]).astype(np.float32) + q.b[:, g]
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+
+
+# -- MLX goldens held by the reference -------------------------------------
+
+def _rmsnorm_rows(x, w, eps):
+    """cpu/cpu_ops.go:145-162 order in float32."""
+    x = x.astype(np.float32)
+    out = np.empty_like(x)
+    for r in range(x.shape[0]):
+        ss = np.float32(0)
+        for v in x[r]:
+            ss = np.float32(ss + np.float32(v * v))
+        inv = np.float32(1.0) / np.float32(np.sqrt(np.float64(np.float32(ss / np.float32(x.shape[1])) + np.float32(eps))))
+        out[r] = (x[r] * inv).astype(np.float32) * w
+    return out
+
+
+@pytest.mark.parametrize("name,tol", [("f32", 2e-4), ("bf16", 5e-2)])
+def test_inkling2_embed_golden(oracle, name, tol):
+    """inkling2/reference_test.go:100-122: embed = RMSNorm(Dequantize(rows))."""
+    fx = np.load(os.path.join(GOLDEN, f"inkling2_embed_{name}.npz"))
+    wide = (lambda a, dt: synth.bf16_bits_to_f32(a) if str(dt) == "BF16" else a.astype(np.float32))
+    s, b = wide(fx["s"], fx["s_dtype"]), wide(fx["b"], fx["b_dtype"])
+    norm = wide(fx["norm"], fx["norm_dtype"])
+    rows = fx["w"][fx["tokens"]]
+    deq = oracle.dequantize(rows, s[fx["tokens"]], b[fx["tokens"]], int(fx["group_size"]), int(fx["bits"]))
+    got = _rmsnorm_rows(deq, norm, float(fx["eps"]))
+    ok, d, scale = rel_ok(got, fx["embed"], tol)
+    assert ok, (d, scale)
+
+
+def test_golden_catches_reversed_nibble_order(oracle):
+    """A plausible mistake (most-significant nibble first), planted on the CPU
+    side, must fail the golden: the fixture pins the code order."""
+    fx = np.load(os.path.join(GOLDEN, "inkling2_embed_f32.npz"))
+    rows = fx["w"][fx["tokens"]]
+    rev = np.zeros_like(rows)
+    for l in range(8):
+        rev |= ((rows >> np.uint32(4 * l)) & np.uint32(0xF)) << np.uint32(4 * (7 - l))
+    deq = oracle.dequantize(rev, fx["s"][fx["tokens"]], fx["b"][fx["tokens"]], 64, 4)
+    got = _rmsnorm_rows(deq, fx["norm"], float(fx["eps"]))
+    ok, _, _ = rel_ok(got, fx["embed"], 2e-4)
+    assert not ok
+
+
+# -- the per-channel kernel -------------------------------------------------
+
+SHAPES = [(1, 1), (1, 8), (2, 8), (4, 8), (32, 8), (16, 2), (8, 16), (3, 4)]  # cpu/qmv_test.go:40-42
+
+
+@pytest.mark.parametrize("groups,wpg", SHAPES)
+def test_avx2_intrinsics_bit_identical_to_lane_order(oracle, groups, wpg):
+    if not oracle.have_avx2_fma():
+        pytest.skip("host has no AVX2+FMA")
+    rng = np.random.default_rng(groups * 100 + wpg)
+    for _ in range(20):
+        n = groups * wpg
+        w = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+        x = (rng.random(n * 8, dtype=np.float32) * 2 - 1).astype(np.float32)
+        s = (rng.random(groups, dtype=np.float32) * 0.1 + 0.01).astype(np.float32)
+        b = (rng.random(groups, dtype=np.float32) * 0.2 - 0.1).astype(np.float32)
+        a = np.float32(oracle.qchannel4("avx2", w, x, s, b, groups, wpg))
+        o = np.float32(oracle.qchannel4("avx2_order", w, x, s, b, groups, wpg))
+        assert a.view(np.uint32) == o.view(np.uint32)
+
+
+@pytest.mark.parametrize("groups,wpg", SHAPES)
+def test_lane_order_matches_scalar_ref(oracle, groups, wpg):
+    """cpu/qmv_test.go:34-70 tolerance 1e-3*(1+|want|), against float64 too."""
+    rng = np.random.default_rng(42 + groups * 7 + wpg)
+    n = groups * wpg
+    w = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    x = (rng.random(n * 8, dtype=np.float32) * 2 - 1).astype(np.float32)
+    s = (rng.random(groups, dtype=np.float32) * 0.1 + 0.01).astype(np.float32)
+    b = (rng.random(groups, dtype=np.float32) * 0.2 - 0.1).astype(np.float32)
+    got = oracle.qchannel4("avx2_order", w, x, s, b, groups, wpg)
+    want = oracle.qchannel4("ref", w, x, s, b, groups, wpg)
+    assert abs(got - want) <= 1e-3 * (1 + abs(want))
+    codes = ((w[:, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(-1).astype(np.float64)
+    gi = np.arange(n * 8) // (wpg * 8)
+    exact = float(np.sum(x.astype(np.float64) * (codes * s[gi] + b[gi])))
+    assert abs(got - exact) <= 1e-4 * (1 + abs(exact))
+
+
+def test_one_hot_input_returns_dequantized_column_exactly(oracle):
+    """x = e_j: the factored decode kernel reduces to fl32(q*s+b) bit for bit,
+    and so does the prefill (wbuf) path. Pins lane mapping and nibble order."""
+    q = synth.quant_linear(5, 24, 512)
+    deq = oracle.dequantize(q.w, q.s, q.b, 64)
+    for j in (0, 1, 7, 8, 63, 64, 200, 511):
+        x = np.zeros((1, 512), np.float32)
+        x[0, j] = 1.0
+        for simd in (True, False):
+            y = oracle.quant_matmul(x, q.w, q.s, q.b, 64, simd=simd)[0]
+            assert np.array_equal(y.view(np.uint32), deq[:, j].copy().view(np.uint32)), (j, simd)
+        x2 = np.repeat(x, 2, axis=0)
+        y2 = oracle.quant_matmul(x2, q.w, q.s, q.b, 64)
+        assert np.array_equal(y2[1].view(np.uint32), deq[:, j].copy().view(np.uint32))
+
+
+def test_all_ones_input_closed_form(oracle):
+    q = synth.quant_linear(6, 32, 1024)
+    codes = ((q.w[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(32, 1024)
+    qsum = codes.reshape(32, 16, 64).sum(axis=2).astype(np.float64)
+    want = (q.s.astype(np.float64) * qsum + 64.0 * q.b.astype(np.float64)).sum(axis=1)
+    for simd in (True, False):
+        y = oracle.quant_matmul(np.ones((1, 1024), np.float32), q.w, q.s, q.b, 64, simd=simd)[0]
+        ok, d, sc = rel_ok(y, want, 1e-5)
+        assert ok, (d, sc)
+
+
+@pytest.mark.parametrize("rows", [1, 3, 13])
+def test_quant_matmul_matches_float64(oracle, rows):
+    q = synth.quant_linear(7, 96, 2048)
+    _, x = synth.activations(8, (rows, 2048))
+    for simd in (True, False):
+        y = oracle.quant_matmul(x, q.w, q.s, q.b, 64, simd=simd)
+        ok, d, sc = rel_ok(y, brute_f64(x, q), 1e-5)
+        assert ok, (rows, simd, d, sc)
+
+
+def test_quant_matmul_is_linear_in_x(oracle):
+    q = synth.quant_linear(9, 64, 1024)
+    _, x1 = synth.activations(10, (1, 1024))
+    _, x2 = synth.activations(11, (1, 1024))
+    y = oracle.quant_matmul((2.0 * x1 + x2).astype(np.float32), q.w, q.s, q.b, 64)
+    y1 = oracle.quant_matmul(x1, q.w, q.s, q.b, 64)
+    y2 = oracle.quant_matmul(x2, q.w, q.s, q.b, 64)
+    ok, d, sc = rel_ok(y, 2.0 * y1.astype(np.float64) + y2, 1e-5)
+    assert ok, (d, sc)
+
+
+@pytest.mark.parametrize("workers", [1, 3, 16])
+def test_blocked_go_path(oracle, workers):
+    """The 4-channel blocked decode loop (cpu/cpu_misc.go:277-347) with the
+    remainder lanes exercised by chunk sizes that are not multiples of 4."""
+    q = synth.quant_linear(12, 70, 1024)
+    _, x = synth.activations(13, (1, 1024))
+    y = oracle.qmv_blocked_go(x[0], q.w, q.s, q.b, 64, workers)
+    ok, d, sc = rel_ok(y, brute_f64(x, q)[0], 1e-5)
+    assert ok, (d, sc)
+
+
+def test_generic_width_path_8bit(oracle):
+    rng = np.random.default_rng(3)
+    N, K, gs = 16, 256, 64
+    w = rng.integers(0, 2**32, (N, K // 4), dtype=np.uint64).astype(np.uint32)
+    s = (rng.random((N, K // gs), dtype=np.float32) * 0.01).astype(np.float32)
+    b = (-rng.random((N, K // gs), dtype=np.float32)).astype(np.float32)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    y = oracle.quant_matmul(x, w, s, b, gs, bits=8)
+    wd = oracle.dequantize(w, s, b, gs, 8).astype(np.float64)
+    ok, d, sc = rel_ok(y[0], x[0].astype(np.float64) @ wd.T, 1e-5)
+    assert ok, (d, sc)
+    codes = ((w[:, :, None] >> (8 * np.arange(4, dtype=np.uint32))) & 0xFF).reshape(N, K)
+    g = np.arange(K) // gs
+    qs = (codes.astype(np.float32) * s[:, g]).astype(np.float32)  # rounded product, then the add
+    assert np.array_equal(wd.astype(np.float32), (qs + b[:, g]).astype(np.float32))
+
+
+# -- gather ------------------------------------------------------------------
+
+@pytest.mark.parametrize("n_lead,A", [(1, 1), (1, 8), (4, 1), (4, 8)])
+def test_gather_reduces_to_per_slot_quant_matmul(oracle, n_lead, A):
+    E, N, K, k = 6, 40, 512, 8
+    q = synth.quant_linear(14, N, K, lead=(E,))
+    idx = np.random.default_rng(n_lead * 10 + A).integers(0, E, (n_lead, k)).astype(np.int32)
+    _, x = synth.activations(15, (n_lead, A, 1, K))
+    y = oracle.gather_quant_matmul(x, q.w, q.s, q.b, idx, 64)
+    assert y.shape == (n_lead, k, 1, N)
+    for l in range(n_lead):
+        for j in range(k):
+            e = idx[l, j]
+            R = int((idx == e).sum())  # rows the reference batches for this expert
+            xv = x[l, 0 if A == 1 else j, 0][None]
+            want = oracle.quant_matmul(np.repeat(xv, R, 0), q.w[e], q.s[e], q.b[e], 64)[0]
+            assert np.array_equal(y[l, j, 0], want), (l, j, e, R)
+
+
+def test_gather_rejects_out_of_range_index(oracle):
+    q = synth.quant_linear(16, 8, 64, lead=(2,))
+    with pytest.raises(IndexError):
+        oracle.gather_quant_matmul(np.zeros((1, 1, 1, 64), np.float32), q.w, q.s, q.b,
+                                   np.array([[0, 2]], np.int32), 64)
+
+
+# -- router helpers ------------------------------------------------------------
+
+def test_topk_selection_sort_ties(oracle):
+    idx, val = oracle.topk(np.array([2, 2, 9], np.float32), 2)
+    assert list(idx) == [2, 1]  # the swap moves index 0 behind index 1
+    i2, _ = synth.topk_rows(np.array([[2, 2, 9]], np.float32), 2)
+    assert list(i2[0]) == [2, 1]
+
+
+def test_synth_router_matches_oracle(oracle):
+    idx, sc = synth.route(21, 16, 128, 8)
+    logits = synth.normal(synth.stream_seed(21, 4), 16 * 128).astype(np.float32).reshape(16, 128)
+    for t in range(16):
+        p = oracle.softmax_row(logits[t])
+        np.testing.assert_allclose(p.sum(), 1.0, rtol=1e-5)
+        oi, ov = oracle.topk(p, 8)
+        assert list(oi) == list(idx[t])
+        np.testing.assert_allclose(sc[t], ov / ov.sum(), rtol=1e-5)
+        assert list(oi) == list(np.argsort(-p.astype(np.float64), kind="stable")[:8])
