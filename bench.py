@@ -303,7 +303,7 @@ def cpu_baseline(seconds: float, bytes_token: int):
             _, used = oracle.qmv_avx2_parallel(xs[k], w, s, b, GS, cores)
         passes += 1
         el = time.perf_counter() - t0
-        if el >= seconds or passes >= 1000:
+        if el >= seconds:
             break
     gbs = byt * passes / el / 1e9
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": int(used), "kind": "port",

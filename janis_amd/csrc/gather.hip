@@ -79,8 +79,9 @@ __global__ __launch_bounds__(1024) void moe_bucket_kernel(const int32_t* __restr
     }
 }
 
-constexpr uint32_t kNibPair = 0x000F000Fu;
-constexpr uint32_t kBf16Base = 0x43004300u;
+constexpr uint32_t kBf16Bytes = 0x43434343u;
+constexpr uint32_t kSelB0B2 = 0x04020400u;
+constexpr uint32_t kSelB1B3 = 0x04030401u;
 constexpr float kCodeOffset = 128.0f;
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
@@ -88,17 +89,21 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
+// acc + sum_l (128 + q_l) * x_l over the 8 codes of `word`; xa = x0..x7 as bf16
+// pairs (x0,x1) (x2,x3) (x4,x5) (x6,x7). Codes become bf16 128 + q by placing
+// them under the high byte 0x43 with v_perm_b32 (see qmv.hip); x is regrouped
+// to (x_p, x_{p+4}) to match.
 __device__ __forceinline__ float word_dot(uint32_t word, uint4 xa, float acc) {
-    // xa = x0..x7 of this word as 4 dwords (bf16 pairs (x0,x1) (x2,x3) (x4,x5) (x6,x7));
-    // regroup to (x_p, x_{p+4}).
-    const uint32_t p0 = (xa.x & 0xFFFFu) | (xa.z << 16);
-    const uint32_t p1 = (xa.x >> 16) | (xa.z & 0xFFFF0000u);
-    const uint32_t p2 = (xa.y & 0xFFFFu) | (xa.w << 16);
-    const uint32_t p3 = (xa.y >> 16) | (xa.w & 0xFFFF0000u);
-    acc = dot2_bf16((word & kNibPair) | kBf16Base, p0, acc);
-    acc = dot2_bf16(((word >> 4) & kNibPair) | kBf16Base, p1, acc);
-    acc = dot2_bf16(((word >> 8) & kNibPair) | kBf16Base, p2, acc);
-    acc = dot2_bf16(((word >> 12) & kNibPair) | kBf16Base, p3, acc);
+    const uint32_t x04 = __builtin_amdgcn_perm(xa.z, xa.x, 0x05040100u);
+    const uint32_t x15 = __builtin_amdgcn_perm(xa.z, xa.x, 0x07060302u);
+    const uint32_t x26 = __builtin_amdgcn_perm(xa.w, xa.y, 0x05040100u);
+    const uint32_t x37 = __builtin_amdgcn_perm(xa.w, xa.y, 0x07060302u);
+    const uint32_t lo = word & 0x0F0F0F0Fu;
+    const uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB0B2), x04, acc);
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB0B2), x15, acc);
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB1B3), x26, acc);
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB1B3), x37, acc);
     return acc;
 }
 
@@ -110,22 +115,24 @@ __device__ __forceinline__ float sum8_bf16(uint4 v) {
     return (a + b) + (c + d);
 }
 
-template <int LPR>
-__device__ __forceinline__ float slice_sum(float v) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+template <bool SB_F16>
+__device__ __forceinline__ float sb_at(const uint16_t* p, uint32_t i) {
+    if constexpr (SB_F16)
+        return f16_to_f32(p[i]);
+    else
+        return bf16_to_f32(p[i]);
 }
 
-// Rows per block = 4 waves * (64/LPR) slices * RPW rows.
-template <int LPR, int ITERS, int RPW>
+// Rows per block = 4 waves * (64/LPR) slices * RPW rows. Loads use clamped row
+// indices (always in bounds) and are issued back to back; stores are predicated.
+template <int LPR, int ITERS, int RPW, bool SB_F16>
 __global__ __launch_bounds__(256) void gather_qmv_kernel(
-    const uint32_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ B,
-    int sb_dt, const uint16_t* __restrict__ X, void* __restrict__ Y, int y_dt, int64_t N,
-    int gs_log2, const int* __restrict__ ws, int64_t E, int64_t k_slots, int64_t a_vectors) {
+    const uint32_t* __restrict__ W, const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
+    const uint16_t* __restrict__ X, void* __restrict__ Y, int y_dt, uint32_t N, int gs_log2,
+    const int* __restrict__ ws, int64_t E, int64_t k_slots, int64_t a_vectors) {
     constexpr int SLICES = 64 / LPR;
-    constexpr int64_t P = 4 * LPR * ITERS;
-    constexpr int64_t K = 8 * P;
+    constexpr uint32_t P = 4 * LPR * ITERS;
+    constexpr uint32_t K = 8 * P;
     const int U = ws[0];
     if ((int)blockIdx.y >= U) return;
     const int64_t e = ws[1 + blockIdx.y];
@@ -134,32 +141,31 @@ __global__ __launch_bounds__(256) void gather_qmv_kernel(
 
     const int lane = threadIdx.x & 63;
     const int sl = lane % LPR, slice = lane / LPR;
-    const int64_t G = K >> gs_log2;
-    const int64_t row0 =
-        ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (SLICES * RPW) + (int64_t)slice * RPW;
-    const uint32_t* We = W + e * N * P;
-    const int64_t sb0 = e * N * G;
+    const uint32_t G = K >> gs_log2;
+    const uint32_t row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (SLICES * RPW) + slice * RPW;
+    const uint32_t* We = W + e * (int64_t)N * P;
+    const uint16_t* Se = S + e * (int64_t)N * G;
+    const uint16_t* Be = B + e * (int64_t)N * G;
 
     uint4 wv[RPW][ITERS];
     float sc[RPW][ITERS], bo[RPW][ITERS];
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
-        const int64_t row = row0 + r;
-        const bool ok = row < N;
+        const uint32_t row = min(row0 + r, N - 1);
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+            wv[r][it] = load_stream16(We + (row * P + it * 4 * LPR + 4 * sl));
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const uint32_t row = min(row0 + r, N - 1);
 #pragma unroll
         for (int it = 0; it < ITERS; it++) {
-            const int64_t g = (32 * (it * LPR + sl)) >> gs_log2;
-            if (ok) {
-                wv[r][it] = load_stream16(We + row * P + it * 4 * LPR + 4 * sl);
-                const float s = load_sb(S, sb0 + row * G + g, sb_dt);
-                const float b = load_sb(B, sb0 + row * G + g, sb_dt);
-                sc[r][it] = s;
-                bo[r][it] = fmaf(-kCodeOffset, s, b);
-            } else {
-                wv[r][it] = make_uint4(0, 0, 0, 0);
-                sc[r][it] = 0.0f;
-                bo[r][it] = 0.0f;
-            }
+            const uint32_t g = (32u * (it * LPR + sl)) >> gs_log2;
+            const float s = sb_at<SB_F16>(Se, row * G + g);
+            const float b = sb_at<SB_F16>(Be, row * G + g);
+            sc[r][it] = s;
+            bo[r][it] = fmaf(-kCodeOffset, s, b);
         }
     }
 
@@ -189,22 +195,29 @@ __global__ __launch_bounds__(256) void gather_qmv_kernel(
         }
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            const float v = slice_sum<LPR>(part[r]);
-            const int64_t row = row0 + r;
-            if (sl == 0 && row < N) store_y(Y, pair * N + row, v, y_dt);
+            const float v = slice_sum_last<LPR>(part[r]);
+            const uint32_t row = row0 + r;
+            if (sl == LPR - 1 && row < N) store_y(Y, pair * N + row, v, y_dt);
         }
     }
 }
 
-template <int LPR, int ITERS, int RPW>
-Status run_fast(const GatherArgs& a, int64_t max_u, int gs_log2, hipStream_t st) {
+template <int LPR, int ITERS, int RPW, bool SB_F16>
+Status run_fast_sb(const GatherArgs& a, int64_t max_u, int gs_log2, hipStream_t st) {
     constexpr int64_t rows_per_block = 4 * (64 / LPR) * RPW;
     const int64_t blocks = (a.m.rows + rows_per_block - 1) / rows_per_block;
-    hipLaunchKernelGGL((gather_qmv_kernel<LPR, ITERS, RPW>), dim3((unsigned)blocks, (unsigned)max_u),
-                       dim3(256), 0, st, a.m.w, a.m.scales, a.m.biases, a.m.sb_dtype,
-                       static_cast<const uint16_t*>(a.x), a.y, a.y_dtype, a.m.rows, gs_log2,
+    hipLaunchKernelGGL((gather_qmv_kernel<LPR, ITERS, RPW, SB_F16>), dim3((unsigned)blocks, (unsigned)max_u),
+                       dim3(256), 0, st, a.m.w, static_cast<const uint16_t*>(a.m.scales),
+                       static_cast<const uint16_t*>(a.m.biases), static_cast<const uint16_t*>(a.x),
+                       a.y, a.y_dtype, (uint32_t)a.m.rows, gs_log2,
                        static_cast<const int*>(a.workspace), a.n_experts, a.k_slots, a.a_vectors);
     return Status::ok();
+}
+
+template <int LPR, int ITERS, int RPW>
+Status run_fast(const GatherArgs& a, int64_t max_u, int gs_log2, hipStream_t st) {
+    if (a.m.sb_dtype == JH_F16) return run_fast_sb<LPR, ITERS, RPW, true>(a, max_u, gs_log2, st);
+    return run_fast_sb<LPR, ITERS, RPW, false>(a, max_u, gs_log2, st);
 }
 
 int log2_exact(int v) {
@@ -230,7 +243,9 @@ Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st) {
     if (max_u > 65535) return Status::fail(JH_ERR_UNSUPPORTED, "gather_quant_matmul: too many experts in one call");
     const int gl = log2_exact(a.m.group_size);
     const int64_t P = a.m.in / 8;
-    const bool fast_ok = a.x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (a.m.in % a.m.group_size) == 0;
+    const bool fast_ok = a.x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (a.m.in % a.m.group_size) == 0 &&
+                         (a.m.sb_dtype == JH_BF16 || a.m.sb_dtype == JH_F16) &&
+                         a.m.rows * (a.m.in / 8) < ((int64_t)1 << 32);
     if (fast_ok) {
         switch (P) {
             case 256 * 1: return run_fast<64, 1, 4>(a, max_u, gl, st);

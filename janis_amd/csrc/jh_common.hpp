@@ -5,6 +5,7 @@
 
 #include <cstdint>
 #include <string>
+#include <type_traits>
 
 #include "../../include/janis_hip.h"
 
@@ -39,6 +40,34 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 load_stream16(const uint32_t* p) {
     const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Sum of v over each slice of LPR consecutive lanes (LPR a power of two <= 64),
+// with DPP: an inclusive row_shr scan inside each row of 16 lanes, then
+// row_bcast15/row_bcast31 to carry row totals across rows. The slice total is
+// valid in the slice's LAST lane (lane % LPR == LPR - 1); other lanes hold
+// partial sums.
+template <int LPR>
+__device__ __forceinline__ float slice_sum_last(float v) {
+    auto dpp = [](float x, auto ctrl, auto row_mask) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                             0, __builtin_bit_cast(int, x), decltype(ctrl)::value,
+                                             decltype(row_mask)::value, 0xF, false));
+    };
+    using C1 = std::integral_constant<int, 0x111>;  // row_shr:1
+    using C2 = std::integral_constant<int, 0x112>;  // row_shr:2
+    using C4 = std::integral_constant<int, 0x114>;  // row_shr:4
+    using C8 = std::integral_constant<int, 0x118>;  // row_shr:8
+    using B15 = std::integral_constant<int, 0x142>; // row_bcast:15
+    using B31 = std::integral_constant<int, 0x143>; // row_bcast:31
+    using All = std::integral_constant<int, 0xF>;
+    if constexpr (LPR >= 2) v += dpp(v, C1{}, All{});
+    if constexpr (LPR >= 4) v += dpp(v, C2{}, All{});
+    if constexpr (LPR >= 8) v += dpp(v, C4{}, All{});
+    if constexpr (LPR >= 16) v += dpp(v, C8{}, All{});
+    if constexpr (LPR >= 32) v += dpp(v, B15{}, std::integral_constant<int, 0xA>{});
+    if constexpr (LPR >= 64) v += dpp(v, B31{}, std::integral_constant<int, 0xC>{});
+    return v;
 }
 
 // Load element i of a scale/bias array of the given dtype as fp32 (exact).

@@ -11,11 +11,13 @@
 //    into registers and reused for every row the wave visits.
 //  * Each lane streams its words with 128-bit loads; a slice reads LPR*16
 //    contiguous bytes per row and iteration (coalesced).
-//  * Nibbles become bf16 with one AND-OR: (w >> 4p) & 0x000F000F | 0x43004300 is
-//    the bf16 pair (128 + q_p, 128 + q_{p+4}), exact. v_dot2_f32_bf16 multiplies
-//    it with the bf16 pair (x_p, x_{p+4}) and accumulates in fp32, so 8 codes
-//    cost 7 integer ops and 4 dot2. The constant 128 is removed per group
-//    through the x-sum that the factorisation needs anyway:
+//  * Codes become bf16 without conversion instructions: a code q in the low 4
+//    mantissa bits of bf16(128.0) = 0x4300 is exactly 128 + q. Two masks split a
+//    word into its even and odd codes (one per byte) and v_perm_b32 assembles
+//    the pairs (128 + q_p, 128 + q_{p+4}). v_dot2_f32_bf16 multiplies a pair
+//    with the bf16 pair (x_p, x_{p+4}) and accumulates in fp32, so 8 codes cost
+//    7 integer ops and 4 dot2. The constant 128 is removed per group through
+//    the x-sum that the factorisation needs anyway:
 //      scale*sum(x*(128+q)) + (bias - 128*scale)*sum(x) = scale*sum(x*q) + bias*sum(x).
 //  * Partial sums are reduced across the slice with cross-lane adds; the
 //    slice's first lane writes y (fp32 or bf16).
@@ -26,8 +28,11 @@ namespace {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-constexpr uint32_t kNibPair = 0x000F000Fu;
-constexpr uint32_t kBf16Base = 0x43004300u;  // bf16(128.0) in both halves
+constexpr uint32_t kBf16Bytes = 0x43434343u;  // 0x43 = high byte of bf16(128.0)
+// v_perm_b32 selectors over {src0 = kBf16Bytes (bytes 4..7), src1 = codes (bytes 0..3)}:
+// result bytes (low to high) = code byte 0, 0x43, code byte 2, 0x43  /  byte 1, 0x43, byte 3, 0x43
+constexpr uint32_t kSelB0B2 = 0x04020400u;
+constexpr uint32_t kSelB1B3 = 0x04030401u;
 constexpr float kCodeOffset = 128.0f;
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
@@ -36,11 +41,17 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 }
 
 // acc + sum_l (128 + q_l) * x_l over the 8 codes of `word`; xp[p] = (x_p, x_{p+4}).
+// lo = word & 0x0F0F0F0F holds codes 0,2,4,6 one per byte, hi = (word >> 4) &
+// 0x0F0F0F0F codes 1,3,5,7; v_perm_b32 then builds each bf16 pair by taking two
+// code bytes and filling the high byte of each half with 0x43 from kBf16Bytes:
+// 7 integer ops and 4 dot2 per word.
 __device__ __forceinline__ float word_dot(uint32_t word, const uint32_t* xp, float acc) {
-    acc = dot2_bf16((word & kNibPair) | kBf16Base, xp[0], acc);
-    acc = dot2_bf16(((word >> 4) & kNibPair) | kBf16Base, xp[1], acc);
-    acc = dot2_bf16(((word >> 8) & kNibPair) | kBf16Base, xp[2], acc);
-    acc = dot2_bf16(((word >> 12) & kNibPair) | kBf16Base, xp[3], acc);
+    const uint32_t lo = word & 0x0F0F0F0Fu;
+    const uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB0B2), xp[0], acc);  // (q0, q4)
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB0B2), xp[1], acc);  // (q1, q5)
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB1B3), xp[2], acc);  // (q2, q6)
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB1B3), xp[3], acc);  // (q3, q7)
     return acc;
 }
 
@@ -58,67 +69,65 @@ __device__ __forceinline__ float pair_up(uint4 v, uint32_t* xp) {
     return (a + b) + (c + d);
 }
 
-template <int LPR>
-__device__ __forceinline__ float slice_sum(float v) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-// LPR lanes per row, ITERS 128-bit loads per lane per row (K = 256*LPR*ITERS/... ):
-//   words per row P = 4 * LPR * ITERS.  RPW rows per slice per pass.
-template <int LPR, int ITERS, int RPW>
+// LPR lanes per row; each lane issues ITERS 16-byte loads per row, so a row
+// has P = 4 * LPR * ITERS words (K = 32 * LPR * ITERS). A wave serves
+// 64 / LPR rows at a time, RPW consecutive rows per slice per pass; the grid
+// strides over passes. Loads use clamped row indices (always in bounds) so all
+// of a pass's loads are issued back to back; only the store is predicated.
+template <int LPR, int ITERS, int RPW, bool SB_F16>
 __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
-    const uint32_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ B,
-    int sb_dt, const uint16_t* __restrict__ X, void* __restrict__ Y, int y_dt, int64_t N,
-    int gs_log2) {
+    const uint32_t* __restrict__ W, const uint16_t* __restrict__ S,
+    const uint16_t* __restrict__ B, const uint16_t* __restrict__ X, void* __restrict__ Y,
+    int y_dt, uint32_t N, int gs_log2) {
     constexpr int SLICES = 64 / LPR;
-    constexpr int64_t P = 4 * LPR * ITERS;
+    constexpr uint32_t P = 4 * LPR * ITERS;
+    constexpr int ROWS_PER_WAVE = SLICES * RPW;
     const int lane = threadIdx.x & 63;
     const int sl = lane % LPR;
     const int slice = lane / LPR;
-    const int64_t G = (P * 8) >> gs_log2;
+    const uint32_t G = (P * 8) >> gs_log2;
 
+    // this lane's part of x, as (x_p, x_{p+4}) bf16 pairs, and its sums
     uint32_t xp[ITERS][16];
     float xs[ITERS];
-    int gi[ITERS];
+    uint32_t gi[ITERS];
 #pragma unroll
     for (int it = 0; it < ITERS; it++) {
-        const int e0 = 32 * (it * LPR + sl);
+        const uint32_t e0 = 32u * (it * LPR + sl);
         const uint4* xv = reinterpret_cast<const uint4*>(X + e0);
-        float s = 0.0f;
+        float sum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) s += pair_up(xv[j], &xp[it][4 * j]);
-        xs[it] = s;
+        for (int j = 0; j < 4; j++) sum += pair_up(xv[j], &xp[it][4 * j]);
+        xs[it] = sum;
         gi[it] = e0 >> gs_log2;
     }
 
-    const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
-    constexpr int ROWS_PER_WAVE = SLICES * RPW;
+    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
 
-    for (int64_t base = wave * ROWS_PER_WAVE; base < N; base += nwaves * ROWS_PER_WAVE) {
-        const int64_t row0 = base + (int64_t)slice * RPW;
+    for (uint32_t base = wave * ROWS_PER_WAVE; base < N; base += nwaves * ROWS_PER_WAVE) {
+        const uint32_t row0 = base + (uint32_t)slice * RPW;
+        // Rows are clamped to N-1 so every load is in bounds and the pass's
+        // loads issue back to back; only the stores are predicated.
         uint4 wv[RPW][ITERS];
         float sc[RPW][ITERS], bo[RPW][ITERS];
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            const int64_t row = row0 + r;
-            const bool ok = row < N;
-            const uint32_t* wr = W + row * P + 4 * sl;
+            const uint32_t row = min(row0 + r, N - 1);
+#pragma unroll
+            for (int it = 0; it < ITERS; it++)
+                wv[r][it] = load_stream16(W + (row * P + it * 4 * LPR + 4 * sl));
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            const uint32_t row = min(row0 + r, N - 1);
 #pragma unroll
             for (int it = 0; it < ITERS; it++) {
-                if (ok) {
-                    wv[r][it] = load_stream16(wr + it * 4 * LPR);
-                    const float s = load_sb(S, row * G + gi[it], sb_dt);
-                    const float b = load_sb(B, row * G + gi[it], sb_dt);
-                    sc[r][it] = s;
-                    bo[r][it] = fmaf(-kCodeOffset, s, b);
-                } else {
-                    wv[r][it] = make_uint4(0, 0, 0, 0);
-                    sc[r][it] = 0.0f;
-                    bo[r][it] = 0.0f;
-                }
+                const uint16_t sh = S[row * G + gi[it]], bh = B[row * G + gi[it]];
+                const float s = SB_F16 ? f16_to_f32(sh) : bf16_to_f32(sh);
+                const float b = SB_F16 ? f16_to_f32(bh) : bf16_to_f32(bh);
+                sc[r][it] = s;
+                bo[r][it] = fmaf(-kCodeOffset, s, b);
             }
         }
 #pragma unroll
@@ -134,9 +143,9 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
                 part = fmaf(sc[r][it], d, part);
                 part = fmaf(bo[r][it], xs[it], part);
             }
-            part = slice_sum<LPR>(part);
-            const int64_t row = row0 + r;
-            if (sl == 0 && row < N) store_y(Y, row, part, y_dt);
+            part = slice_sum_last<LPR>(part);
+            const uint32_t row = row0 + r;
+            if (sl == LPR - 1 && row < N) store_y(Y, row, part, y_dt);
         }
     }
 }
@@ -206,18 +215,36 @@ __global__ __launch_bounds__(256) void qmv_generic_kernel(
 
 namespace {
 
+template <int LPR, int ITERS, int RPW, bool SB_F16>
+Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gs_log2,
+                   int num_cus, hipStream_t st) {
+    constexpr int64_t rows_per_block = 4 * (64 / LPR) * RPW;
+    auto kern = qmv_bf16x_kernel<LPR, ITERS, RPW, SB_F16>;
+    // persistent-style grid: at most what is resident at once, so multi-pass
+    // shapes reuse the x registers instead of queueing more waves
+    static int resident = 0;
+    if (resident == 0) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) != hipSuccess || per_cu < 1)
+            per_cu = 2;
+        resident = per_cu;
+    }
+    int64_t blocks = (m.rows + rows_per_block - 1) / rows_per_block;
+    const int64_t cap = (int64_t)num_cus * resident;
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, st, m.w,
+                       static_cast<const uint16_t*>(m.scales), static_cast<const uint16_t*>(m.biases),
+                       static_cast<const uint16_t*>(x), y, y_dtype, (uint32_t)m.rows, gs_log2);
+    return Status::ok();
+}
+
 template <int LPR, int ITERS, int RPW>
 Status run_fast(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gs_log2,
                 int num_cus, hipStream_t st) {
-    constexpr int64_t rows_per_block = 4 * (64 / LPR) * RPW;
-    int64_t blocks = (m.rows + rows_per_block - 1) / rows_per_block;
-    const int64_t cap = (int64_t)num_cus * 8;
-    if (blocks > cap) blocks = cap;
-    if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL((qmv_bf16x_kernel<LPR, ITERS, RPW>), dim3((unsigned)blocks), dim3(256), 0,
-                       st, m.w, m.scales, m.biases, m.sb_dtype,
-                       static_cast<const uint16_t*>(x), y, y_dtype, m.rows, gs_log2);
-    return Status::ok();
+    if (m.sb_dtype == JH_F16)
+        return run_fast_sb<LPR, ITERS, RPW, true>(m, x, y, y_dtype, gs_log2, num_cus, st);
+    return run_fast_sb<LPR, ITERS, RPW, false>(m, x, y, y_dtype, gs_log2, num_cus, st);
 }
 
 int log2_exact(int v) {
@@ -244,7 +271,9 @@ Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int
                   int num_cus, hipStream_t st) {
     const int gl = log2_exact(m.group_size);
     const int64_t P = m.in / 8;
-    const bool fast_ok = x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0;
+    const bool fast_ok = x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0 &&
+                         (m.sb_dtype == JH_BF16 || m.sb_dtype == JH_F16) &&
+                         m.rows * (m.in / 8) < ((int64_t)1 << 32);
     if (fast_ok) {
         switch (P) {
             case 256 * 1: return run_fast<64, 1, 4>(m, x, y, y_dtype, gl, num_cus, st);
