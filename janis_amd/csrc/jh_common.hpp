@@ -36,6 +36,28 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// Raw buffer resources (gfx9 descriptor word 3 = 0x00020000: 32-bit dwords,
+// no swizzle). A buffer load outside [0, bytes) returns 0 instead of faulting,
+// and takes a 32-bit byte offset, so kernels address rows with 32-bit math and
+// need no clamping. `bytes` must be below 2^31 (checked by the launchers).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+constexpr int kAuxNT = 2;  // non-temporal: streamed data, read once
+
+__device__ __forceinline__ uint4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAuxNT);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
+// fp32 -> bf16 bits with the hardware's round-to-nearest-even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint16_t f32_to_bf16_hw(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
 // 16-byte streaming load of packed weights (read once per call: non-temporal).
 __device__ __forceinline__ uint4 load_stream16(const uint32_t* p) {
     const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));

@@ -69,31 +69,104 @@ __device__ __forceinline__ float pair_up(uint4 v, uint32_t* xp) {
     return (a + b) + (c + d);
 }
 
-// LPR lanes per row; each lane issues ITERS 16-byte loads per row, so a row
-// has P = 4 * LPR * ITERS words (K = 32 * LPR * ITERS). A wave serves
-// 64 / LPR rows at a time, RPW consecutive rows per slice per pass; the grid
-// strides over passes. Loads use clamped row indices (always in bounds) so all
-// of a pass's loads are issued back to back; only the store is predicated.
-template <int LPR, int ITERS, int RPW, bool SB_F16>
+// The slice sums of RPW values at once: each DPP step is applied to all RPW
+// values before the next, so the DPP read-after-write waits are filled with
+// useful work. Totals land in the last lane of each slice (see slice_sum_last).
+template <int LPR, int RPW>
+__device__ __forceinline__ void slice_sums_last(float (&v)[RPW]) {
+    auto step = [&](auto ctrl, auto row_mask) {
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+            v[r] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                  0, __builtin_bit_cast(int, v[r]), decltype(ctrl)::value,
+                                                  decltype(row_mask)::value, 0xF, false));
+    };
+    using All = std::integral_constant<int, 0xF>;
+    if constexpr (LPR >= 2) step(std::integral_constant<int, 0x111>{}, All{});
+    if constexpr (LPR >= 4) step(std::integral_constant<int, 0x112>{}, All{});
+    if constexpr (LPR >= 8) step(std::integral_constant<int, 0x114>{}, All{});
+    if constexpr (LPR >= 16) step(std::integral_constant<int, 0x118>{}, All{});
+    if constexpr (LPR >= 32) step(std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xA>{});
+    if constexpr (LPR >= 64) step(std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xC>{});
+}
+
+// Stores RPW consecutive outputs from one lane (vector store when all are in
+// range and RPW is 2 or 4).
+template <int RPW>
+__device__ __forceinline__ void store_rows(void* Y, int y_dt, uint32_t row0, uint32_t N,
+                                           const float (&v)[RPW]) {
+    if constexpr (RPW == 2 || RPW == 4) {
+        if (row0 + RPW <= N) {
+            if (y_dt == JH_BF16) {
+                uint32_t pk[RPW / 2];
+#pragma unroll
+                for (int r = 0; r < RPW; r += 2)
+                    pk[r / 2] = (uint32_t)f32_to_bf16_hw(v[r]) | ((uint32_t)f32_to_bf16_hw(v[r + 1]) << 16);
+                if constexpr (RPW == 4)
+                    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(Y) + row0) = make_uint2(pk[0], pk[1]);
+                else
+                    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(Y) + row0) = pk[0];
+            } else {
+                float* yf = static_cast<float*>(Y) + row0;
+                if constexpr (RPW == 4)
+                    *reinterpret_cast<float4*>(yf) = make_float4(v[0], v[1], v[2], v[3]);
+                else
+                    *reinterpret_cast<float2*>(yf) = make_float2(v[0], v[1]);
+            }
+            return;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
+        if (row0 + r < N) {
+            if (y_dt == JH_BF16)
+                static_cast<uint16_t*>(Y)[row0 + r] = f32_to_bf16_hw(v[r]);
+            else
+                static_cast<float*>(Y)[row0 + r] = v[r];
+        }
+}
+
+// Decode GEMV tile:
+//   LPR    lanes per row slice (64 / LPR row slices per wave)
+//   ITERS  16-byte weight loads per lane per row and K part
+//   RPW    consecutive rows per slice per pass
+//   KSPLIT waves sharing one row (each takes 1/KSPLIT of K); their partial sums
+//          meet in LDS. A block has 4 waves = 4 / KSPLIT row groups.
+// Words per row P = 4 * LPR * ITERS * KSPLIT (K = 32 * LPR * ITERS * KSPLIT).
+// The grid strides over passes of whole blocks (block-uniform loop, so the
+// LDS barriers are reached by all waves). Weights and scales are read through
+// buffer resources: rows past N read as zero, so every load is unconditional
+// and issues back to back; only the stores are predicated.
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16>
 __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     const uint32_t* __restrict__ W, const uint16_t* __restrict__ S,
     const uint16_t* __restrict__ B, const uint16_t* __restrict__ X, void* __restrict__ Y,
     int y_dt, uint32_t N, int gs_log2) {
     constexpr int SLICES = 64 / LPR;
-    constexpr uint32_t P = 4 * LPR * ITERS;
+    constexpr int RGROUPS = 4 / KSPLIT;                 // row groups per block
+    constexpr uint32_t PK = 4 * LPR * ITERS;            // words per K part
+    constexpr uint32_t P = PK * KSPLIT;
     constexpr int ROWS_PER_WAVE = SLICES * RPW;
+    constexpr int ROWS_PER_BLOCK = RGROUPS * ROWS_PER_WAVE;
     const int lane = threadIdx.x & 63;
+    const int wv_id = threadIdx.x >> 6;
+    const int ks = wv_id % KSPLIT, rg = wv_id / KSPLIT;
     const int sl = lane % LPR;
     const int slice = lane / LPR;
     const uint32_t G = (P * 8) >> gs_log2;
+    const auto rw = make_rsrc(W, N * P * 4);
+    const auto rs = make_rsrc(S, N * G * 2);
+    const auto rb = make_rsrc(B, N * G * 2);
+    __shared__ float red[(KSPLIT > 1) ? (KSPLIT - 1) * RGROUPS * ROWS_PER_WAVE : 1];
 
     // this lane's part of x, as (x_p, x_{p+4}) bf16 pairs, and its sums
     uint32_t xp[ITERS][16];
     float xs[ITERS];
-    uint32_t gi[ITERS];
+    uint32_t gi[ITERS], wo[ITERS];
 #pragma unroll
     for (int it = 0; it < ITERS; it++) {
-        const uint32_t e0 = 32u * (it * LPR + sl);
+        wo[it] = ks * PK + it * 4 * LPR + 4 * sl;   // word offset inside a row
+        const uint32_t e0 = 8u * wo[it];
         const uint4* xv = reinterpret_cast<const uint4*>(X + e0);
         float sum = 0.0f;
 #pragma unroll
@@ -102,51 +175,58 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
         gi[it] = e0 >> gs_log2;
     }
 
-    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
-
-    for (uint32_t base = wave * ROWS_PER_WAVE; base < N; base += nwaves * ROWS_PER_WAVE) {
-        const uint32_t row0 = base + (uint32_t)slice * RPW;
-        // Rows are clamped to N-1 so every load is in bounds and the pass's
-        // loads issue back to back; only the stores are predicated.
+    for (uint32_t bbase = blockIdx.x * ROWS_PER_BLOCK; bbase < N; bbase += gridDim.x * ROWS_PER_BLOCK) {
+        const uint32_t row0 = bbase + rg * ROWS_PER_WAVE + (uint32_t)slice * RPW;
         uint4 wv[RPW][ITERS];
-        float sc[RPW][ITERS], bo[RPW][ITERS];
+        uint16_t sh[RPW][ITERS], bh[RPW][ITERS];
 #pragma unroll
-        for (int r = 0; r < RPW; r++) {
-            const uint32_t row = min(row0 + r, N - 1);
+        for (int r = 0; r < RPW; r++)
 #pragma unroll
             for (int it = 0; it < ITERS; it++)
-                wv[r][it] = load_stream16(W + (row * P + it * 4 * LPR + 4 * sl));
-        }
+                wv[r][it] = buf_load16_nt(rw, ((row0 + r) * P + wo[it]) * 4);
 #pragma unroll
-        for (int r = 0; r < RPW; r++) {
-            const uint32_t row = min(row0 + r, N - 1);
+        for (int r = 0; r < RPW; r++)
 #pragma unroll
             for (int it = 0; it < ITERS; it++) {
-                const uint16_t sh = S[row * G + gi[it]], bh = B[row * G + gi[it]];
-                const float s = SB_F16 ? f16_to_f32(sh) : bf16_to_f32(sh);
-                const float b = SB_F16 ? f16_to_f32(bh) : bf16_to_f32(bh);
-                sc[r][it] = s;
-                bo[r][it] = fmaf(-kCodeOffset, s, b);
+                const uint32_t off = ((row0 + r) * G + gi[it]) * 2;
+                sh[r][it] = buf_load2(rs, off);
+                bh[r][it] = buf_load2(rb, off);
             }
-        }
+        float part[RPW];
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            float part = 0.0f;
+            part[r] = 0.0f;
 #pragma unroll
             for (int it = 0; it < ITERS; it++) {
+                const float sc = SB_F16 ? f16_to_f32(sh[r][it]) : bf16_to_f32(sh[r][it]);
+                const float bi = SB_F16 ? f16_to_f32(bh[r][it]) : bf16_to_f32(bh[r][it]);
                 float d = 0.0f;
                 d = word_dot(wv[r][it].x, &xp[it][0], d);
                 d = word_dot(wv[r][it].y, &xp[it][4], d);
                 d = word_dot(wv[r][it].z, &xp[it][8], d);
                 d = word_dot(wv[r][it].w, &xp[it][12], d);
-                part = fmaf(sc[r][it], d, part);
-                part = fmaf(bo[r][it], xs[it], part);
+                part[r] = fmaf(sc, d, part[r]);
+                part[r] = fmaf(fmaf(-kCodeOffset, sc, bi), xs[it], part[r]);
             }
-            part = slice_sum_last<LPR>(part);
-            const uint32_t row = row0 + r;
-            if (sl == LPR - 1 && row < N) store_y(Y, row, part, y_dt);
         }
+        slice_sums_last<LPR, RPW>(part);
+        if constexpr (KSPLIT > 1) {
+            // K parts 1.. hand their slice totals to part 0 through LDS
+            const int slot = (rg * SLICES + slice) * RPW;
+            if (ks > 0 && sl == LPR - 1)
+#pragma unroll
+                for (int r = 0; r < RPW; r++)
+                    red[((ks - 1) * RGROUPS * SLICES * RPW) + slot + r] = part[r];
+            __syncthreads();
+            if (ks == 0 && sl == LPR - 1)
+#pragma unroll
+                for (int k = 1; k < KSPLIT; k++)
+#pragma unroll
+                    for (int r = 0; r < RPW; r++)
+                        part[r] += red[((k - 1) * RGROUPS * SLICES * RPW) + slot + r];
+            __syncthreads();
+        }
+        if (ks == 0 && sl == LPR - 1) store_rows<RPW>(Y, y_dt, row0, N, part);
     }
 }
 
@@ -215,13 +295,13 @@ __global__ __launch_bounds__(256) void qmv_generic_kernel(
 
 namespace {
 
-template <int LPR, int ITERS, int RPW, bool SB_F16>
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16>
 Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gs_log2,
                    int num_cus, hipStream_t st) {
-    constexpr int64_t rows_per_block = 4 * (64 / LPR) * RPW;
-    auto kern = qmv_bf16x_kernel<LPR, ITERS, RPW, SB_F16>;
+    constexpr int64_t rows_per_block = (4 / KSPLIT) * (64 / LPR) * RPW;
+    auto kern = qmv_bf16x_kernel<LPR, ITERS, RPW, KSPLIT, SB_F16>;
     // persistent-style grid: at most what is resident at once, so multi-pass
-    // shapes reuse the x registers instead of queueing more waves
+    // shapes reuse the x registers instead of queueing more blocks
     static int resident = 0;
     if (resident == 0) {
         int per_cu = 0;
@@ -239,12 +319,12 @@ Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, in
     return Status::ok();
 }
 
-template <int LPR, int ITERS, int RPW>
+template <int LPR, int ITERS, int RPW, int KSPLIT = 1>
 Status run_fast(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gs_log2,
                 int num_cus, hipStream_t st) {
     if (m.sb_dtype == JH_F16)
-        return run_fast_sb<LPR, ITERS, RPW, true>(m, x, y, y_dtype, gs_log2, num_cus, st);
-    return run_fast_sb<LPR, ITERS, RPW, false>(m, x, y, y_dtype, gs_log2, num_cus, st);
+        return run_fast_sb<LPR, ITERS, RPW, KSPLIT, true>(m, x, y, y_dtype, gs_log2, num_cus, st);
+    return run_fast_sb<LPR, ITERS, RPW, KSPLIT, false>(m, x, y, y_dtype, gs_log2, num_cus, st);
 }
 
 int log2_exact(int v) {
@@ -273,21 +353,25 @@ Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int
     const int64_t P = m.in / 8;
     const bool fast_ok = x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0 &&
                          (m.sb_dtype == JH_BF16 || m.sb_dtype == JH_F16) &&
-                         m.rows * (m.in / 8) < ((int64_t)1 << 32);
+                         (m.rows + 64) * (m.in / 2) < ((int64_t)1 << 31);
     if (fast_ok) {
+        // Tile per row length, from a sweep of the Qwen3-8B shapes on MI355X:
+        // splitting K over 2-4 waves per row beats one wave per row at every
+        // shape (more waves in flight, shorter per-wave dependency chains).
+        if (P == 512 && m.rows >= 65536) return run_fast<64, 1, 8, 2>(m, x, y, y_dtype, gl, num_cus, st);
         switch (P) {
-            case 256 * 1: return run_fast<64, 1, 4>(m, x, y, y_dtype, gl, num_cus, st);
-            case 256 * 2: return run_fast<64, 2, 4>(m, x, y, y_dtype, gl, num_cus, st);
-            case 256 * 3: return run_fast<64, 3, 2>(m, x, y, y_dtype, gl, num_cus, st);
-            case 256 * 4: return run_fast<64, 4, 2>(m, x, y, y_dtype, gl, num_cus, st);
-            case 256 * 6: return run_fast<64, 6, 1>(m, x, y, y_dtype, gl, num_cus, st);
-            case 256 * 8: return run_fast<64, 8, 1>(m, x, y, y_dtype, gl, num_cus, st);
-            case 128 * 1: return run_fast<32, 1, 4>(m, x, y, y_dtype, gl, num_cus, st);
-            case 128 * 3: return run_fast<32, 3, 2>(m, x, y, y_dtype, gl, num_cus, st);
-            case 64 * 1: return run_fast<16, 1, 4>(m, x, y, y_dtype, gl, num_cus, st);
-            case 64 * 3: return run_fast<16, 3, 2>(m, x, y, y_dtype, gl, num_cus, st);
-            case 32 * 1: return run_fast<8, 1, 4>(m, x, y, y_dtype, gl, num_cus, st);
-            case 32 * 3: return run_fast<8, 3, 2>(m, x, y, y_dtype, gl, num_cus, st);
+            case 512 * 1: return run_fast<32, 1, 4, 4>(m, x, y, y_dtype, gl, num_cus, st);
+            case 512 * 2: return run_fast<32, 2, 2, 4>(m, x, y, y_dtype, gl, num_cus, st);
+            case 512 * 3: return run_fast<32, 3, 2, 4>(m, x, y, y_dtype, gl, num_cus, st);
+            case 512 * 4: return run_fast<32, 4, 2, 4>(m, x, y, y_dtype, gl, num_cus, st);
+            case 256 * 1: return run_fast<32, 1, 4, 2>(m, x, y, y_dtype, gl, num_cus, st);
+            case 256 * 3: return run_fast<32, 3, 2, 2>(m, x, y, y_dtype, gl, num_cus, st);
+            case 128 * 1: return run_fast<16, 1, 4, 2>(m, x, y, y_dtype, gl, num_cus, st);
+            case 128 * 3: return run_fast<16, 3, 2, 2>(m, x, y, y_dtype, gl, num_cus, st);
+            case 64 * 1: return run_fast<16, 1, 4, 1>(m, x, y, y_dtype, gl, num_cus, st);
+            case 64 * 3: return run_fast<16, 3, 2, 1>(m, x, y, y_dtype, gl, num_cus, st);
+            case 32 * 1: return run_fast<8, 1, 4, 1>(m, x, y, y_dtype, gl, num_cus, st);
+            case 32 * 3: return run_fast<8, 3, 2, 1>(m, x, y, y_dtype, gl, num_cus, st);
             default: break;
         }
     }

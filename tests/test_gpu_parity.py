@@ -95,12 +95,12 @@ def test_inkling2_embed_golden(hip, name, tol):
 # -- decode qmv ---------------------------------------------------------------
 
 QMV_SHAPES = [
-    # (N, K, gs): every fast-kernel instantiation, group sizes, ragged N, the generic path
+    # (N, K, gs): every fast-kernel tile (K = 256..16384), group sizes 32/64/128,
+    # ragged N, the lm_head-size tile, and the generic kernel (K = 1032, gs = 8)
     (4096, 4096, 64), (1024, 4096, 64), (33, 2048, 64), (1000, 6144, 64), (257, 8192, 64),
     (4096, 12288, 64), (100, 16384, 64), (129, 1024, 64), (70, 3072, 64), (65, 512, 64),
     (48, 1536, 64), (31, 256, 64), (768, 768, 64), (300, 4096, 32), (300, 4096, 128),
-    (50, 2048, 32), (40, 768, 128), (24, 1032, 8), (9, 96, 32),
-]
+    (50, 2048, 32), (40, 768, 128), (24, 1032, 8), (9, 96, 32), (65539, 4096, 64)]
 
 
 @pytest.mark.parametrize("n,k,gs", QMV_SHAPES)
