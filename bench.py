@@ -294,7 +294,7 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
         per_expert = 3 * (I * H // 2 + 4 * I * (H // GS))  # packed codes + scales/biases of one expert
         byt = U * per_expert + 2 * T * H + 2 * T * K * (2 * I + H) + 2 * T * K * I
         moe[f"T{T}"] = {"unique_experts": U, "us_per_layer": round(ms * 1e3, 2),
-                        "GB_s": round(byt / (ms * 1e-3) / 1e9, 1), "launches_per_layer": 6}
+                        "GB_s": round(byt / (ms * 1e-3) / 1e9, 1), "launches_per_layer": 3}
         del g
     res["moe_gather"] = moe
     log("moe:", moe)

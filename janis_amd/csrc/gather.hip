@@ -1,23 +1,24 @@
 // MoE expert product (GatherQuantMatmul, cpu/cpu_misc.go:178-230) on gfx950.
 //
 // The reference buckets the (lead, slot) pairs by expert on the host and runs
-// one QuantMatmul per used expert. Here the bucketing runs on the device so the
-// routing never has to come back to the host:
+// one QuantMatmul per used expert. Here the bucketing runs on the device, so the
+// routing never comes back to the host, and each routed expert's packed weights
+// are read once per call whatever the number of slots routed to it:
 //
-//  1. moe_bucket_kernel (one workgroup): counts the pairs per expert, lists the
-//     used experts in ascending id order (the reference's iteration order),
-//     and writes each expert's pairs in (lead, slot) order into a workspace:
+//  * decode-sized calls (pairs <= kFusedMaxPairs): ONE launch. Every block
+//    stages the indices in LDS, marks the used experts in a bitmap, takes the
+//    u-th used expert (ascending id, the reference's iteration order) for
+//    blockIdx.y = u and collects that expert's pairs; then it loads its rows of
+//    the expert into registers and applies them to each pair.
+//  * larger calls: moe_bucket_kernel writes the buckets to a workspace
 //        ws[0]                  U, the number of used experts
-//        ws[1 .. 1+E)           used expert ids
+//        ws[1 .. 1+E)           used expert ids, ascending
 //        ws[1+E .. 2+2E)        bucket offsets (U+1 of them)
-//        ws[2+2E .. 2+2E+pairs) pair ids  (pair = lead * k_slots + slot)
-//     An out-of-range index gets a row of NaN and no bucket.
-//  2. gather_qmv_kernel: grid (row blocks, min(E, pairs)); block (rb, u) loads
-//     its rows of expert uniq[u] into registers ONCE and applies them to every
-//     pair routed to that expert, so each used expert's packed weights are
-//     read once per call and unused experts are never read. The inner product
-//     is the decode kernel's: bf16 pairs (128+q) against bf16 x pairs with
-//     v_dot2_f32_bf16, the 128 removed through the group's sum of x.
+//        ws[2+2E .. 2+2E+pairs) pair ids (pair = lead * k_slots + slot)
+//    and the product kernel reads them.
+// An out-of-range index gets a row of NaN and no bucket. The inner product is
+// the decode GEMV's: bf16 pairs (128+q) against bf16 x pairs with
+// v_dot2_f32_bf16, the 128 removed through the group's sum of x.
 #include "jh_common.hpp"
 
 namespace jh {
@@ -33,6 +34,14 @@ namespace {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 constexpr int kMaxExperts = 4096;
 
+constexpr int kFusedMaxPairs = 1024;
+
+__device__ __forceinline__ void nan_row(void* Y, int y_dt, int64_t p, int64_t N, int tid, int nthreads) {
+    const float nan = __uint_as_float(0x7fc00000u);
+    for (int64_t j = tid; j < N; j += nthreads) store_y(Y, p * N + j, nan, y_dt);
+}
+
+// Workspace bucketing for calls with many pairs (one workgroup of 1024).
 __global__ __launch_bounds__(1024) void moe_bucket_kernel(const int32_t* __restrict__ idx,
                                                           int64_t n_pairs, int64_t E,
                                                           int* __restrict__ ws,
@@ -47,12 +56,10 @@ __global__ __launch_bounds__(1024) void moe_bucket_kernel(const int32_t* __restr
     __syncthreads();
     for (int64_t p = threadIdx.x; p < n_pairs; p += blockDim.x) {
         const int e = idx[p];
-        if (e >= 0 && e < E) {
+        if (e >= 0 && e < E)
             atomicAdd(&cnt[e], 1);
-        } else {
-            const float nan = __uint_as_float(0x7fc00000u);
-            for (int64_t j = 0; j < N; j++) store_y(Y, p * N + j, nan, y_dt);
-        }
+        else
+            for (int64_t j = 0; j < N; j++) store_y(Y, p * N + j, __uint_as_float(0x7fc00000u), y_dt);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -65,6 +72,7 @@ __global__ __launch_bounds__(1024) void moe_bucket_kernel(const int32_t* __restr
                 off += cnt[e];
                 U++;
             }
+            cnt[e] = 0;  // reused as the fill cursor below
         }
         offs[U] = off;
         ws[0] = U;
@@ -73,10 +81,47 @@ __global__ __launch_bounds__(1024) void moe_bucket_kernel(const int32_t* __restr
     for (int64_t p = threadIdx.x; p < n_pairs; p += blockDim.x) {
         const int e = idx[p];
         if (e < 0 || e >= E) continue;
-        int rank = 0;
-        for (int64_t q = 0; q < p; q++) rank += (idx[q] == e);
-        pairs[start[e] + rank] = (int)p;
+        pairs[start[e] + atomicAdd(&cnt[e], 1)] = (int)p;
     }
+}
+
+// In-block bucketing for one expert (the fused path). Returns the expert id of
+// bucket u (ascending order) or -1 if fewer than u+1 experts are used; fills
+// plist[0..*np) with that expert's pairs. Block-wide: every thread calls it.
+__device__ int bucket_in_block(const int32_t* __restrict__ idx, int n_pairs, int E, int u,
+                               int* sidx, uint32_t* pres, int* plist, int* np, int* sel,
+                               void* Y, int y_dt, int64_t N) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int words = (E + 31) >> 5;
+    for (int w = tid; w < words; w += nt) pres[w] = 0u;
+    if (tid == 0) *np = 0;
+    __syncthreads();
+    for (int p = tid; p < n_pairs; p += nt) {
+        const int e = idx[p];
+        sidx[p] = e;
+        if (e >= 0 && e < E) atomicOr(&pres[e >> 5], 1u << (e & 31));
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int e_sel = -1, seen = 0;
+        for (int w = 0; w < words && e_sel < 0; w++) {
+            uint32_t bits = pres[w];
+            const int c = __popc(bits);
+            if (seen + c > u) {
+                for (int k = seen; k < u; k++) bits &= bits - 1;  // drop the lower set bits
+                e_sel = (w << 5) + __ffs(bits) - 1;
+            }
+            seen += c;
+        }
+        *sel = e_sel;
+    }
+    __syncthreads();
+    const int e = *sel;
+    if (e >= 0)
+        for (int p = tid; p < n_pairs; p += nt)
+            if (sidx[p] == e) plist[atomicAdd(np, 1)] = p;
+    __syncthreads();
+    return e;
 }
 
 constexpr uint32_t kBf16Bytes = 0x43434343u;
@@ -115,59 +160,73 @@ __device__ __forceinline__ float sum8_bf16(uint4 v) {
     return (a + b) + (c + d);
 }
 
-template <bool SB_F16>
-__device__ __forceinline__ float sb_at(const uint16_t* p, uint32_t i) {
-    if constexpr (SB_F16)
-        return f16_to_f32(p[i]);
-    else
-        return bf16_to_f32(p[i]);
-}
-
-// Rows per block = 4 waves * (64/LPR) slices * RPW rows. Loads use clamped row
-// indices (always in bounds) and are issued back to back; stores are predicated.
-template <int LPR, int ITERS, int RPW, bool SB_F16>
+// Rows per block = 4 waves * (64/LPR) slices * RPW rows. Weights and scales are
+// read through buffer resources (rows past N read 0), so loads are
+// unconditional and issue back to back; stores are predicated.
+template <int LPR, int ITERS, int RPW, bool SB_F16, bool FUSED>
 __global__ __launch_bounds__(256) void gather_qmv_kernel(
     const uint32_t* __restrict__ W, const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
     const uint16_t* __restrict__ X, void* __restrict__ Y, int y_dt, uint32_t N, int gs_log2,
-    const int* __restrict__ ws, int64_t E, int64_t k_slots, int64_t a_vectors) {
+    const int* __restrict__ ws, const int32_t* __restrict__ idx, int n_pairs, int64_t E,
+    int64_t k_slots, int64_t a_vectors) {
     constexpr int SLICES = 64 / LPR;
     constexpr uint32_t P = 4 * LPR * ITERS;
     constexpr uint32_t K = 8 * P;
-    const int U = ws[0];
-    if ((int)blockIdx.y >= U) return;
-    const int64_t e = ws[1 + blockIdx.y];
-    const int p_begin = ws[1 + E + blockIdx.y], p_end = ws[2 + E + blockIdx.y];
-    const int* pairs = ws + 2 + 2 * E;
+    __shared__ int sidx[FUSED ? kFusedMaxPairs : 1];
+    __shared__ int plist_s[FUSED ? kFusedMaxPairs : 1];
+    __shared__ uint32_t pres[FUSED ? kMaxExperts / 32 : 1];
+    __shared__ int np_s, sel_s;
+    int64_t e;
+    int p_begin, p_end;
+    const int* pairs;
+    if constexpr (FUSED) {
+        if (blockIdx.x == 0 && blockIdx.y == 0)
+            for (int p = 0; p < n_pairs; p++) {
+                const int ei = idx[p];
+                if (ei < 0 || ei >= E) nan_row(Y, y_dt, p, N, threadIdx.x, blockDim.x);
+            }
+        const int es = bucket_in_block(idx, n_pairs, (int)E, blockIdx.y, sidx, pres, plist_s, &np_s,
+                                       &sel_s, Y, y_dt, N);
+        if (es < 0) return;  // block-uniform
+        e = es;
+        p_begin = 0;
+        p_end = np_s;
+        pairs = plist_s;
+    } else {
+        const int U = ws[0];
+        if ((int)blockIdx.y >= U) return;
+        e = ws[1 + blockIdx.y];
+        p_begin = ws[1 + E + blockIdx.y];
+        p_end = ws[2 + E + blockIdx.y];
+        pairs = ws + 2 + 2 * E;
+    }
 
     const int lane = threadIdx.x & 63;
     const int sl = lane % LPR, slice = lane / LPR;
     const uint32_t G = K >> gs_log2;
     const uint32_t row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (SLICES * RPW) + slice * RPW;
-    const uint32_t* We = W + e * (int64_t)N * P;
-    const uint16_t* Se = S + e * (int64_t)N * G;
-    const uint16_t* Be = B + e * (int64_t)N * G;
+    const auto rw = make_rsrc(W + e * (int64_t)N * P, N * P * 4);
+    const auto rs = make_rsrc(S + e * (int64_t)N * G, N * G * 2);
+    const auto rb = make_rsrc(B + e * (int64_t)N * G, N * G * 2);
 
     uint4 wv[RPW][ITERS];
     float sc[RPW][ITERS], bo[RPW][ITERS];
 #pragma unroll
-    for (int r = 0; r < RPW; r++) {
-        const uint32_t row = min(row0 + r, N - 1);
+    for (int r = 0; r < RPW; r++)
 #pragma unroll
         for (int it = 0; it < ITERS; it++)
-            wv[r][it] = load_stream16(We + (row * P + it * 4 * LPR + 4 * sl));
-    }
+            wv[r][it] = buf_load16_nt(rw, ((row0 + r) * P + it * 4 * LPR + 4 * sl) * 4);
 #pragma unroll
-    for (int r = 0; r < RPW; r++) {
-        const uint32_t row = min(row0 + r, N - 1);
+    for (int r = 0; r < RPW; r++)
 #pragma unroll
         for (int it = 0; it < ITERS; it++) {
-            const uint32_t g = (32u * (it * LPR + sl)) >> gs_log2;
-            const float s = sb_at<SB_F16>(Se, row * G + g);
-            const float b = sb_at<SB_F16>(Be, row * G + g);
+            const uint32_t off = ((row0 + r) * G + ((32u * (it * LPR + sl)) >> gs_log2)) * 2;
+            const uint16_t sh = buf_load2(rs, off), bh = buf_load2(rb, off);
+            const float s = SB_F16 ? f16_to_f32(sh) : bf16_to_f32(sh);
+            const float b = SB_F16 ? f16_to_f32(bh) : bf16_to_f32(bh);
             sc[r][it] = s;
             bo[r][it] = fmaf(-kCodeOffset, s, b);
         }
-    }
 
     for (int pi = p_begin; pi < p_end; pi++) {
         const int64_t pair = pairs[pi];
@@ -197,27 +256,37 @@ __global__ __launch_bounds__(256) void gather_qmv_kernel(
         for (int r = 0; r < RPW; r++) {
             const float v = slice_sum_last<LPR>(part[r]);
             const uint32_t row = row0 + r;
-            if (sl == LPR - 1 && row < N) store_y(Y, pair * N + row, v, y_dt);
+            if (sl == LPR - 1 && row < N) {
+                if (y_dt == JH_BF16)
+                    static_cast<uint16_t*>(Y)[pair * N + row] = f32_to_bf16_hw(v);
+                else
+                    static_cast<float*>(Y)[pair * N + row] = v;
+            }
         }
     }
 }
 
-template <int LPR, int ITERS, int RPW, bool SB_F16>
+template <int LPR, int ITERS, int RPW, bool SB_F16, bool FUSED>
 Status run_fast_sb(const GatherArgs& a, int64_t max_u, int gs_log2, hipStream_t st) {
     constexpr int64_t rows_per_block = 4 * (64 / LPR) * RPW;
     const int64_t blocks = (a.m.rows + rows_per_block - 1) / rows_per_block;
-    hipLaunchKernelGGL((gather_qmv_kernel<LPR, ITERS, RPW, SB_F16>), dim3((unsigned)blocks, (unsigned)max_u),
-                       dim3(256), 0, st, a.m.w, static_cast<const uint16_t*>(a.m.scales),
-                       static_cast<const uint16_t*>(a.m.biases), static_cast<const uint16_t*>(a.x),
-                       a.y, a.y_dtype, (uint32_t)a.m.rows, gs_log2,
-                       static_cast<const int*>(a.workspace), a.n_experts, a.k_slots, a.a_vectors);
+    hipLaunchKernelGGL((gather_qmv_kernel<LPR, ITERS, RPW, SB_F16, FUSED>),
+                       dim3((unsigned)blocks, (unsigned)max_u), dim3(256), 0, st, a.m.w,
+                       static_cast<const uint16_t*>(a.m.scales), static_cast<const uint16_t*>(a.m.biases),
+                       static_cast<const uint16_t*>(a.x), a.y, a.y_dtype, (uint32_t)a.m.rows, gs_log2,
+                       static_cast<const int*>(a.workspace), a.idx, (int)(a.n_lead * a.k_slots),
+                       a.n_experts, a.k_slots, a.a_vectors);
     return Status::ok();
 }
 
 template <int LPR, int ITERS, int RPW>
-Status run_fast(const GatherArgs& a, int64_t max_u, int gs_log2, hipStream_t st) {
-    if (a.m.sb_dtype == JH_F16) return run_fast_sb<LPR, ITERS, RPW, true>(a, max_u, gs_log2, st);
-    return run_fast_sb<LPR, ITERS, RPW, false>(a, max_u, gs_log2, st);
+Status run_fast(const GatherArgs& a, int64_t max_u, int gs_log2, bool fused, hipStream_t st) {
+    if (fused) {
+        if (a.m.sb_dtype == JH_F16) return run_fast_sb<LPR, ITERS, RPW, true, true>(a, max_u, gs_log2, st);
+        return run_fast_sb<LPR, ITERS, RPW, false, true>(a, max_u, gs_log2, st);
+    }
+    if (a.m.sb_dtype == JH_F16) return run_fast_sb<LPR, ITERS, RPW, true, false>(a, max_u, gs_log2, st);
+    return run_fast_sb<LPR, ITERS, RPW, false, false>(a, max_u, gs_log2, st);
 }
 
 int log2_exact(int v) {
@@ -226,10 +295,28 @@ int log2_exact(int v) {
     return ((1 << l) == v) ? l : -1;
 }
 
+bool fast_tile_exists(int64_t P) {
+    switch (P) {
+        case 256: case 512: case 768: case 1024: case 1536: case 128: case 384:
+        case 64: case 192: case 32: case 96:
+            return true;
+        default:
+            return false;
+    }
+}
+
 }  // namespace
 
 size_t gather_workspace_bytes(int64_t n_experts, int64_t n_pairs) {
     return sizeof(int) * (size_t)(2 + 2 * n_experts + n_pairs);
+}
+
+bool gather_uses_workspace(const GatherArgs& a) {
+    const int gl = log2_exact(a.m.group_size);
+    const bool fast = a.x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (a.m.in % a.m.group_size) == 0 &&
+                      (a.m.sb_dtype == JH_BF16 || a.m.sb_dtype == JH_F16) &&
+                      (a.m.rows + 64) * (a.m.in / 2) < ((int64_t)1 << 31) && fast_tile_exists(a.m.in / 8);
+    return !(fast && a.n_lead * a.k_slots <= kFusedMaxPairs);
 }
 
 Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st) {
@@ -237,28 +324,30 @@ Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st) {
     if (n_pairs == 0) return Status::ok();
     if (a.n_experts > kMaxExperts)
         return Status::fail(JH_ERR_UNSUPPORTED, "gather_quant_matmul: more than 4096 experts");
-    hipLaunchKernelGGL(moe_bucket_kernel, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.n_experts,
-                       static_cast<int*>(a.workspace), a.y, a.y_dtype, a.m.rows);
     const int64_t max_u = n_pairs < a.n_experts ? n_pairs : a.n_experts;
     if (max_u > 65535) return Status::fail(JH_ERR_UNSUPPORTED, "gather_quant_matmul: too many experts in one call");
     const int gl = log2_exact(a.m.group_size);
+    const bool fused = !gather_uses_workspace(a);
+    if (!fused)
+        hipLaunchKernelGGL(moe_bucket_kernel, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.n_experts,
+                           static_cast<int*>(a.workspace), a.y, a.y_dtype, a.m.rows);
     const int64_t P = a.m.in / 8;
     const bool fast_ok = a.x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (a.m.in % a.m.group_size) == 0 &&
                          (a.m.sb_dtype == JH_BF16 || a.m.sb_dtype == JH_F16) &&
-                         a.m.rows * (a.m.in / 8) < ((int64_t)1 << 32);
+                         (a.m.rows + 64) * (a.m.in / 2) < ((int64_t)1 << 31);
     if (fast_ok) {
         switch (P) {
-            case 256 * 1: return run_fast<64, 1, 4>(a, max_u, gl, st);
-            case 256 * 2: return run_fast<64, 2, 2>(a, max_u, gl, st);
-            case 256 * 3: return run_fast<64, 3, 2>(a, max_u, gl, st);
-            case 256 * 4: return run_fast<64, 4, 1>(a, max_u, gl, st);
-            case 256 * 6: return run_fast<64, 6, 1>(a, max_u, gl, st);
-            case 128 * 1: return run_fast<32, 1, 4>(a, max_u, gl, st);
-            case 128 * 3: return run_fast<32, 3, 2>(a, max_u, gl, st);
-            case 64 * 1: return run_fast<16, 1, 4>(a, max_u, gl, st);
-            case 64 * 3: return run_fast<16, 3, 2>(a, max_u, gl, st);
-            case 32 * 1: return run_fast<8, 1, 4>(a, max_u, gl, st);
-            case 32 * 3: return run_fast<8, 3, 2>(a, max_u, gl, st);
+            case 256 * 1: return run_fast<64, 1, 4>(a, max_u, gl, fused, st);
+            case 256 * 2: return run_fast<64, 2, 2>(a, max_u, gl, fused, st);
+            case 256 * 3: return run_fast<64, 3, 2>(a, max_u, gl, fused, st);
+            case 256 * 4: return run_fast<64, 4, 1>(a, max_u, gl, fused, st);
+            case 256 * 6: return run_fast<64, 6, 1>(a, max_u, gl, fused, st);
+            case 128 * 1: return run_fast<32, 1, 4>(a, max_u, gl, fused, st);
+            case 128 * 3: return run_fast<32, 3, 2>(a, max_u, gl, fused, st);
+            case 64 * 1: return run_fast<16, 1, 4>(a, max_u, gl, fused, st);
+            case 64 * 3: return run_fast<16, 3, 2>(a, max_u, gl, fused, st);
+            case 32 * 1: return run_fast<8, 1, 4>(a, max_u, gl, fused, st);
+            case 32 * 3: return run_fast<8, 3, 2>(a, max_u, gl, fused, st);
             default: break;
         }
     }

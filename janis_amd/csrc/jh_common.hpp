@@ -149,6 +149,8 @@ struct GatherArgs {
     void* workspace;      // gather_workspace_bytes(n_experts, n_lead*k_slots)
 };
 size_t gather_workspace_bytes(int64_t n_experts, int64_t n_pairs);
+// False when the call buckets inside its product launch (no workspace needed).
+bool gather_uses_workspace(const GatherArgs& a);
 Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st);
 
 }  // namespace jh

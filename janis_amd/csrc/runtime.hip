@@ -293,23 +293,6 @@ int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n
                                 " at slot " + std::to_string(i) + " outside [0, " +
                                 std::to_string(n_experts) + ")");
     }
-    const size_t need = jh::gather_workspace_bytes(n_experts, n_pairs);
-    if (need > c->ws_bytes) {
-        if (c->ws) {
-            JH_HIP(c, hipStreamSynchronize(c->stream));
-            JH_HIP(c, hipFree(c->ws));
-            c->ws = nullptr;
-            c->ws_bytes = 0;
-        }
-        size_t cap = 4096;
-        while (cap < need) cap *= 2;
-        if (hipMalloc(&c->ws, cap) != hipSuccess) {
-            (void)hipGetLastError();
-            c->ws = nullptr;
-            return fail(c, JH_ERR_OOM, std::string(op) + ": workspace allocation failed");
-        }
-        c->ws_bytes = cap;
-    }
     jh::GatherArgs a;
     a.m = jh::QuantMatrix{w, scales, biases, sb_dtype, out_features, in_features, group_size};
     a.n_experts = n_experts;
@@ -321,7 +304,27 @@ int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n
     a.idx = rhs_indices;
     a.y = y;
     a.y_dtype = y_dtype;
-    a.workspace = c->ws;
+    a.workspace = nullptr;
+    if (jh::gather_uses_workspace(a)) {
+        const size_t need = jh::gather_workspace_bytes(n_experts, n_pairs);
+        if (need > c->ws_bytes) {
+            if (c->ws) {
+                JH_HIP(c, hipStreamSynchronize(c->stream));
+                JH_HIP(c, hipFree(c->ws));
+                c->ws = nullptr;
+                c->ws_bytes = 0;
+            }
+            size_t cap = 4096;
+            while (cap < need) cap *= 2;
+            if (hipMalloc(&c->ws, cap) != hipSuccess) {
+                (void)hipGetLastError();
+                c->ws = nullptr;
+                return fail(c, JH_ERR_OOM, std::string(op) + ": workspace allocation failed");
+            }
+            c->ws_bytes = cap;
+        }
+        a.workspace = c->ws;
+    }
     return finish(c, jh::launch_gather(a, c->num_cus, c->stream), "gather");
 }
 

@@ -270,6 +270,22 @@ def test_gather_small_with_collisions(hip, oracle, E, n, k, gs, A):
     assert ok, ("f32 x", d, sc)
 
 
+@pytest.mark.parametrize("n_tok,A", [(160, 1), (160, 8)])
+def test_gather_many_slots_workspace_path(hip, oracle, n_tok, A):
+    """More than 1024 (token, slot) pairs: the separate bucketing launch."""
+    E, K, n, k = 16, 8, 96, 512
+    q = synth.quant_linear(70 + A, n, k, lead=(E,))
+    idx, _ = synth.route(71, n_tok, E, K)
+    xb, x = synth.activations(72 + A, (n_tok, A, 1, k))
+    w, s, b = upload_quant(hip, q)
+    step(f"jh_gather_quant_matmul pairs={n_tok * K} A={A}")
+    y = hip.Floats(hip.GatherQuantMatmul(hip.FromBF16Bits(xb, n_tok, A, 1, k), w, s, b, hip.FromInt32(idx),
+                                         True, 64, 4, out_dtype=F32))
+    want = oracle.gather_quant_matmul(x, q.w, q.s, q.b, idx, 64)
+    ok, d, sc = rel_ok(y, want, F32_TOL)
+    assert ok, (d, sc)
+
+
 def test_gather_out_of_range_index(hip):
     q = synth.quant_linear(1, 32, 512, lead=(4,))
     w, s, b = upload_quant(hip, q)
