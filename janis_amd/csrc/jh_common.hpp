@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <string>
 #include <type_traits>
@@ -135,7 +136,9 @@ Status launch_dequantize(const QuantMatrix& m, void* out, int out_dtype, hipStre
 Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int y_dtype,
                   int num_cus, hipStream_t st);
 Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y,
-                  int y_dtype, int num_cus, hipStream_t st);
+                  int y_dtype, int num_cus, hipStream_t st, void* workspace);
+// fp32 accumulation buffer a split-K prefill needs (0 when none).
+size_t qmm_workspace_bytes(const QuantMatrix& m, int64_t rows, int x_dtype, int y_dtype, int num_cus);
 
 struct GatherArgs {
     QuantMatrix m;        // one expert's shape; w/scales/biases point at expert 0

@@ -54,6 +54,26 @@ int enter(jh_ctx* c) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Grows the context's workspace to at least `need` bytes (power of two, >= 4 KiB).
+int ensure_workspace(jh_ctx* c, size_t need, const char* op) {
+    if (need <= c->ws_bytes) return JH_OK;
+    if (c->ws) {
+        JH_HIP(c, hipStreamSynchronize(c->stream));
+        JH_HIP(c, hipFree(c->ws));
+        c->ws = nullptr;
+        c->ws_bytes = 0;
+    }
+    size_t cap = 4096;
+    while (cap < need) cap *= 2;
+    if (hipMalloc(&c->ws, cap) != hipSuccess) {
+        (void)hipGetLastError();
+        c->ws = nullptr;
+        return fail(c, JH_ERR_OOM, std::string(op) + ": workspace allocation failed");
+    }
+    c->ws_bytes = cap;
+    return JH_OK;
+}
+
 int check_quant(jh_ctx* c, const char* op, const uint32_t* w, const void* s, const void* b,
                 int sb_dtype, int64_t rows, int64_t in, int group_size, int bits) {
     if (bits != 4)
@@ -254,7 +274,10 @@ int jh_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, co
     jh::QuantMatrix m{w, scales, biases, sb_dtype, out_features, in_features, group_size};
     if (rows == 1)
         return finish(c, jh::launch_qmv(m, x, x_dtype, y, y_dtype, c->num_cus, c->stream), "qmv");
-    return finish(c, jh::launch_qmm(m, x, x_dtype, rows, y, y_dtype, c->num_cus, c->stream), "qmm");
+    const size_t need = jh::qmm_workspace_bytes(m, rows, x_dtype, y_dtype, c->num_cus);
+    if (need)
+        if (int r = ensure_workspace(c, need, "jh_quant_matmul")) return r;
+    return finish(c, jh::launch_qmm(m, x, x_dtype, rows, y, y_dtype, c->num_cus, c->stream, c->ws), "qmm");
 }
 
 int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n_lead,
@@ -306,23 +329,7 @@ int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n
     a.y_dtype = y_dtype;
     a.workspace = nullptr;
     if (jh::gather_uses_workspace(a)) {
-        const size_t need = jh::gather_workspace_bytes(n_experts, n_pairs);
-        if (need > c->ws_bytes) {
-            if (c->ws) {
-                JH_HIP(c, hipStreamSynchronize(c->stream));
-                JH_HIP(c, hipFree(c->ws));
-                c->ws = nullptr;
-                c->ws_bytes = 0;
-            }
-            size_t cap = 4096;
-            while (cap < need) cap *= 2;
-            if (hipMalloc(&c->ws, cap) != hipSuccess) {
-                (void)hipGetLastError();
-                c->ws = nullptr;
-                return fail(c, JH_ERR_OOM, std::string(op) + ": workspace allocation failed");
-            }
-            c->ws_bytes = cap;
-        }
+        if (int r = ensure_workspace(c, jh::gather_workspace_bytes(n_experts, n_pairs), op)) return r;
         a.workspace = c->ws;
     }
     return finish(c, jh::launch_gather(a, c->num_cus, c->stream), "gather");
