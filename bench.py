@@ -245,9 +245,9 @@ def main() -> int:
 
 
 def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
-    """Config 2 (prefill qmm, MFMA) and config 3 (MoE gather) figures."""
+    """Config 2 (prefill qmm, MFMA) and config 3 (MoE gather, whole expert MLP) figures."""
     from janis_amd import synth
-    from janis_amd.engine import I32
+    from janis_amd.engine import F32, I32
 
     res = {}
     # prefill: gate_up 4096->12288 and down 12288->4096 at M in {128, 512, 2048}
@@ -295,6 +295,26 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
         byt = U * per_expert + 2 * T * H + 2 * T * K * (2 * I + H) + 2 * T * K * I
         moe[f"T{T}"] = {"unique_experts": U, "us_per_layer": round(ms * 1e3, 2),
                         "GB_s": round(byt / (ms * 1e-3) / 1e9, 1), "launches_per_layer": 3}
+        del g
+
+        # the whole expert MLP (gate+up SwiGLU, down with the score-weighted sum)
+        _, sc_np = synth.route(77 + T, T, E, K)
+        sct = torch.from_numpy(sc_np).to(dev)
+        scores = hip.Wrap(sct.data_ptr(), tuple(sc_np.shape), F32, keep=sct)
+        xs = bf16((T, H))
+        ot = torch.empty((T, H), device=dev, dtype=torch.float32)
+        out = hip.Wrap(ot.data_ptr(), (T, H), F32, keep=ot)
+
+        def moe_fused():
+            for st in stacks:
+                hip.MoeSwiGLU(xs, st["gate"], st["up"], st["down"], idx, scores, GS, 4, out=out)
+
+        g = capture(moe_fused)
+        ms = time_graph(g, 10, 3) / nl
+        byt = U * per_expert + 2 * T * H + 2 * 2 * T * K * I + 4 * T * H
+        moe[f"T{T}_swiglu"] = {"unique_experts": U, "us_per_layer": round(ms * 1e3, 2),
+                               "GB_s": round(byt / (ms * 1e-3) / 1e9, 1), "launches_per_layer": 3,
+                               "note": "jh_moe_swiglu: out clear + gate/up SwiGLU + down combine"}
         del g
     res["moe_gather"] = moe
     log("moe:", moe)

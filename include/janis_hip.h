@@ -156,6 +156,39 @@ JH_API int jh_gather_quant_matmul(jh_ctx *ctx, const void *x, jh_dtype x_dtype, 
                            int64_t k_slots, int transpose, int group_size, int bits, void *y,
                            jh_dtype y_dtype);
 
+/* The expert MLP of moeApply (qwen/moe.go:501-511) in one call, for a backend
+ * that offers it (the engine's optional-capability pattern,
+ * engine/backend.go:38-112). The reference composes it from three
+ * GatherQuantMatmul calls and four element-wise operators:
+ *   g = gather(x, gate), u = gather(x, up)      one vector per token (A = 1)
+ *   h = SiLU(g) * u                              SiLU(v) = v / (1 + exp(-v))
+ *   d = gather(h, down)                          one vector per slot (A = k_slots)
+ *   out[t, :] = mean_k(d[t, k, :] * scores[t, k]) * k_slots
+ * Here it is two product launches (gate+up with the SiLU*mul epilogue; down with
+ * the score-weighted sum done as fp32 atomics into out) plus one clearing
+ * launch, and h stays on the device in bf16.
+ *   x            bf16 [n_tok, hidden] (x_dtype must be JH_BF16)
+ *   gate, up     stacked [n_experts, intermediate, hidden * bits / 32] with
+ *                scales/biases [n_experts, intermediate, hidden / group_size]
+ *   down         stacked [n_experts, hidden, intermediate * bits / 32] with
+ *                scales/biases [n_experts, hidden, intermediate / group_size]
+ *   rhs_indices  int32 [n_tok, k_slots] and scores fp32 [n_tok, k_slots], device memory
+ *   out          [n_tok, hidden] of out_dtype (JH_F32 or JH_BF16)
+ * The score-weighted sum is accumulated with atomics, so its fp32 rounding
+ * order varies from run to run. A token with an index outside [0, n_experts)
+ * gets a row of NaN (or JH_ERR_INVALID when jh_set_checks is on). Shapes
+ * outside the expert tiles (hidden and intermediate in {256, 512, 768, 1024,
+ * 1536, 2048, 3072, 4096, 6144, 8192, 12288}, group_size 32/64/128, 16-bit
+ * scales shared by the three stacks) return JH_ERR_UNSUPPORTED; callers then
+ * compose it from jh_gather_quant_matmul as the reference does. */
+JH_API int jh_moe_swiglu(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t n_tok,
+                  const uint32_t *w_gate, const void *s_gate, const void *b_gate,
+                  const uint32_t *w_up, const void *s_up, const void *b_up,
+                  const uint32_t *w_down, const void *s_down, const void *b_down,
+                  jh_dtype sb_dtype, int64_t n_experts, int64_t hidden, int64_t intermediate,
+                  const int32_t *rhs_indices, const float *scores, int64_t k_slots,
+                  int group_size, int bits, void *out, jh_dtype out_dtype);
+
 #ifdef __cplusplus
 }
 #endif

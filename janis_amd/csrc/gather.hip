@@ -1,24 +1,33 @@
-// MoE expert product (GatherQuantMatmul, cpu/cpu_misc.go:178-230) on gfx950.
+// MoE expert products on gfx950: GatherQuantMatmul (cpu/cpu_misc.go:178-230)
+// and the whole expert MLP of moeApply (qwen/moe.go:501-511).
 //
 // The reference buckets the (lead, slot) pairs by expert on the host and runs
 // one QuantMatmul per used expert. Here the bucketing runs on the device, so the
 // routing never comes back to the host, and each routed expert's packed weights
 // are read once per call whatever the number of slots routed to it:
 //
-//  * decode-sized calls (pairs <= kFusedMaxPairs): ONE launch. Every block
-//    stages the indices in LDS, marks the used experts in a bitmap, takes the
-//    u-th used expert (ascending id, the reference's iteration order) for
-//    blockIdx.y = u and collects that expert's pairs; then it loads its rows of
-//    the expert into registers and applies them to each pair.
+//  * decode-sized calls (pairs <= kFusedMaxPairs): every block stages the
+//    indices in LDS, marks the used experts in a bitmap, takes the u-th used
+//    expert (ascending id, the reference's iteration order) for blockIdx.y = u
+//    and collects that expert's pairs, inside the product launch;
 //  * larger calls: moe_bucket_kernel writes the buckets to a workspace
 //        ws[0]                  U, the number of used experts
 //        ws[1 .. 1+E)           used expert ids, ascending
 //        ws[1+E .. 2+2E)        bucket offsets (U+1 of them)
 //        ws[2+2E .. 2+2E+pairs) pair ids (pair = lead * k_slots + slot)
 //    and the product kernel reads them.
-// An out-of-range index gets a row of NaN and no bucket. The inner product is
-// the decode GEMV's: bf16 pairs (128+q) against bf16 x pairs with
-// v_dot2_f32_bf16, the 128 removed through the group's sum of x.
+// An out-of-range index gets a row of NaN and no bucket.
+//
+// moe_qmv_kernel is the decode GEMV of qmv.hip (codes become bf16 128+q through
+// v_perm_b32 and meet bf16 x pairs in v_dot2_f32_bf16; the 128 is removed
+// through the group's sum of x) run per expert bucket: block (rb, u) loads its
+// rows of expert u into registers once, then applies them to the x vector of
+// every pair in the bucket. Its epilogue is one of
+//    EPI_PLAIN    y[pair, row]    = dot                      (GatherQuantMatmul)
+//    EPI_SWIGLU   y[pair, row]    = SiLU(dot_gate) * dot_up  (two stacks, one launch)
+//    EPI_COMBINE  out[lead, row] += score[pair] * dot        (fp32 atomics)
+// so a whole moeApply is one SWIGLU launch over gate+up and one COMBINE launch
+// over down, with the hidden activations h kept in bf16 between them.
 #include "jh_common.hpp"
 
 namespace jh {
@@ -33,15 +42,16 @@ namespace {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 constexpr int kMaxExperts = 4096;
-
 constexpr int kFusedMaxPairs = 1024;
+enum { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_COMBINE = 2 };
 
 __device__ __forceinline__ void nan_row(void* Y, int y_dt, int64_t p, int64_t N, int tid, int nthreads) {
     const float nan = __uint_as_float(0x7fc00000u);
     for (int64_t j = tid; j < N; j += nthreads) store_y(Y, p * N + j, nan, y_dt);
 }
 
-// Workspace bucketing for calls with many pairs (one workgroup of 1024).
+// Workspace bucketing for calls with many pairs (one workgroup of 1024). Pairs
+// with an out-of-range index get a NaN row in Y when Y is given.
 __global__ __launch_bounds__(1024) void moe_bucket_kernel(const int32_t* __restrict__ idx,
                                                           int64_t n_pairs, int64_t E,
                                                           int* __restrict__ ws,
@@ -58,7 +68,7 @@ __global__ __launch_bounds__(1024) void moe_bucket_kernel(const int32_t* __restr
         const int e = idx[p];
         if (e >= 0 && e < E)
             atomicAdd(&cnt[e], 1);
-        else
+        else if (Y)
             for (int64_t j = 0; j < N; j++) store_y(Y, p * N + j, __uint_as_float(0x7fc00000u), y_dt);
     }
     __syncthreads();
@@ -89,8 +99,7 @@ __global__ __launch_bounds__(1024) void moe_bucket_kernel(const int32_t* __restr
 // bucket u (ascending order) or -1 if fewer than u+1 experts are used; fills
 // plist[0..*np) with that expert's pairs. Block-wide: every thread calls it.
 __device__ int bucket_in_block(const int32_t* __restrict__ idx, int n_pairs, int E, int u,
-                               int* sidx, uint32_t* pres, int* plist, int* np, int* sel,
-                               void* Y, int y_dt, int64_t N) {
+                               int* sidx, uint32_t* pres, int* plist, int* np, int* sel) {
     const int tid = threadIdx.x, nt = blockDim.x;
     const int words = (E + 31) >> 5;
     for (int w = tid; w < words; w += nt) pres[w] = 0u;
@@ -124,7 +133,7 @@ __device__ int bucket_in_block(const int32_t* __restrict__ idx, int n_pairs, int
     return e;
 }
 
-constexpr uint32_t kBf16Bytes = 0x43434343u;
+constexpr uint32_t kBf16Bytes = 0x43434343u;  // 0x43 = high byte of bf16(128.0)
 constexpr uint32_t kSelB0B2 = 0x04020400u;
 constexpr uint32_t kSelB1B3 = 0x04030401u;
 constexpr float kCodeOffset = 128.0f;
@@ -134,25 +143,26 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// acc + sum_l (128 + q_l) * x_l over the 8 codes of `word`; xa = x0..x7 as bf16
-// pairs (x0,x1) (x2,x3) (x4,x5) (x6,x7). Codes become bf16 128 + q by placing
-// them under the high byte 0x43 with v_perm_b32 (see qmv.hip); x is regrouped
-// to (x_p, x_{p+4}) to match.
-__device__ __forceinline__ float word_dot(uint32_t word, uint4 xa, float acc) {
-    const uint32_t x04 = __builtin_amdgcn_perm(xa.z, xa.x, 0x05040100u);
-    const uint32_t x15 = __builtin_amdgcn_perm(xa.z, xa.x, 0x07060302u);
-    const uint32_t x26 = __builtin_amdgcn_perm(xa.w, xa.y, 0x05040100u);
-    const uint32_t x37 = __builtin_amdgcn_perm(xa.w, xa.y, 0x07060302u);
+// acc + sum_l (128 + q_l) * x_l over the 8 codes of `word`, with
+// xp[p] = (x_p, x_{p+4}) as bf16 pairs (see pair_up). v_perm_b32 places code
+// bytes under the high byte 0x43, giving bf16 128 + q exactly.
+__device__ __forceinline__ float word_dot(uint32_t word, const uint32_t* xp, float acc) {
     const uint32_t lo = word & 0x0F0F0F0Fu;
     const uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB0B2), x04, acc);
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB0B2), x15, acc);
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB1B3), x26, acc);
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB1B3), x37, acc);
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB0B2), xp[0], acc);
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB0B2), xp[1], acc);
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB1B3), xp[2], acc);
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB1B3), xp[3], acc);
     return acc;
 }
 
-__device__ __forceinline__ float sum8_bf16(uint4 v) {
+// The 8 bf16 inputs (x0,x1) (x2,x3) (x4,x5) (x6,x7) of one word regrouped as
+// (x0,x4) (x1,x5) (x2,x6) (x3,x7); returns their fp32 sum.
+__device__ __forceinline__ float pair_up(uint4 v, uint32_t* xp) {
+    xp[0] = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+    xp[1] = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+    xp[2] = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+    xp[3] = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
     const float a = __uint_as_float(v.x << 16) + __uint_as_float(v.x & 0xFFFF0000u);
     const float b = __uint_as_float(v.y << 16) + __uint_as_float(v.y & 0xFFFF0000u);
     const float c = __uint_as_float(v.z << 16) + __uint_as_float(v.z & 0xFFFF0000u);
@@ -160,139 +170,252 @@ __device__ __forceinline__ float sum8_bf16(uint4 v) {
     return (a + b) + (c + d);
 }
 
-// Rows per block = 4 waves * (64/LPR) slices * RPW rows. Weights and scales are
-// read through buffer resources (rows past N read 0), so loads are
-// unconditional and issue back to back; stores are predicated.
-template <int LPR, int ITERS, int RPW, bool SB_F16, bool FUSED>
-__global__ __launch_bounds__(256) void gather_qmv_kernel(
-    const uint32_t* __restrict__ W, const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
-    const uint16_t* __restrict__ X, void* __restrict__ Y, int y_dt, uint32_t N, int gs_log2,
-    const int* __restrict__ ws, const int32_t* __restrict__ idx, int n_pairs, int64_t E,
-    int64_t k_slots, int64_t a_vectors) {
+// SiLU as the reference defines it (cpu/cpu.go:327-329): v / (1 + exp(-v)).
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+struct MoeArgs {
+    const uint32_t* w[2];  // stacks [E, N, P]: [0] the only stack or gate, [1] up (SWIGLU)
+    const uint16_t* s[2];  // [E, N, G] bf16 or f16
+    const uint16_t* b[2];
+    const uint16_t* x;     // bf16 rows of K
+    void* y;               // PLAIN/SWIGLU: [pairs, N] bf16 or f32; COMBINE: f32 [n_lead, N]
+    int y_dt;
+    uint32_t N;            // rows per expert
+    int gs_log2;
+    const int* ws;         // buckets (unfused path)
+    const int32_t* idx;    // [n_lead, k_slots]
+    int n_pairs;
+    int64_t E, k_slots, a_vectors;
+    const float* scores;   // COMBINE: [n_lead, k_slots]
+};
+
+// Expert-slot GEMV (see the file comment). LPR lanes per row, each lane ITERS
+// 16-byte words per K-part; K split over KSPLIT waves that meet in LDS. Rows per
+// block = (4 / KSPLIT) * (64 / LPR) * RPW.
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int EPI, bool FUSED>
+__global__ __launch_bounds__(256) void moe_qmv_kernel(MoeArgs a) {
+    constexpr int NSTK = EPI == EPI_SWIGLU ? 2 : 1;
     constexpr int SLICES = 64 / LPR;
-    constexpr uint32_t P = 4 * LPR * ITERS;
+    constexpr int RGROUPS = 4 / KSPLIT;
+    constexpr uint32_t PK = 4 * LPR * ITERS;  // words per K-part
+    constexpr uint32_t P = PK * KSPLIT;
     constexpr uint32_t K = 8 * P;
+    constexpr int ROWS_PER_WAVE = SLICES * RPW;
+    constexpr int ROWS_PER_BLOCK = RGROUPS * ROWS_PER_WAVE;
     __shared__ int sidx[FUSED ? kFusedMaxPairs : 1];
     __shared__ int plist_s[FUSED ? kFusedMaxPairs : 1];
     __shared__ uint32_t pres[FUSED ? kMaxExperts / 32 : 1];
     __shared__ int np_s, sel_s;
+    __shared__ float red[KSPLIT > 1 ? (KSPLIT - 1) * NSTK * ROWS_PER_BLOCK : 1];
+
     int64_t e;
     int p_begin, p_end;
     const int* pairs;
     if constexpr (FUSED) {
-        if (blockIdx.x == 0 && blockIdx.y == 0)
-            for (int p = 0; p < n_pairs; p++) {
-                const int ei = idx[p];
-                if (ei < 0 || ei >= E) nan_row(Y, y_dt, p, N, threadIdx.x, blockDim.x);
+        if (EPI != EPI_COMBINE && blockIdx.x == 0 && blockIdx.y == 0)
+            for (int p = 0; p < a.n_pairs; p++) {
+                const int ei = a.idx[p];
+                if (ei < 0 || ei >= a.E) nan_row(a.y, a.y_dt, p, a.N, threadIdx.x, blockDim.x);
             }
-        const int es = bucket_in_block(idx, n_pairs, (int)E, blockIdx.y, sidx, pres, plist_s, &np_s,
-                                       &sel_s, Y, y_dt, N);
+        const int es = bucket_in_block(a.idx, a.n_pairs, (int)a.E, blockIdx.y, sidx, pres, plist_s,
+                                       &np_s, &sel_s);
         if (es < 0) return;  // block-uniform
         e = es;
         p_begin = 0;
         p_end = np_s;
         pairs = plist_s;
     } else {
-        const int U = ws[0];
+        const int U = a.ws[0];
         if ((int)blockIdx.y >= U) return;
-        e = ws[1 + blockIdx.y];
-        p_begin = ws[1 + E + blockIdx.y];
-        p_end = ws[2 + E + blockIdx.y];
-        pairs = ws + 2 + 2 * E;
+        e = a.ws[1 + blockIdx.y];
+        p_begin = a.ws[1 + a.E + blockIdx.y];
+        p_end = a.ws[2 + a.E + blockIdx.y];
+        pairs = a.ws + 2 + 2 * a.E;
     }
 
     const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int ks = wave % KSPLIT, rg = wave / KSPLIT;
     const int sl = lane % LPR, slice = lane / LPR;
-    const uint32_t G = K >> gs_log2;
-    const uint32_t row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (SLICES * RPW) + slice * RPW;
-    const auto rw = make_rsrc(W + e * (int64_t)N * P, N * P * 4);
-    const auto rs = make_rsrc(S + e * (int64_t)N * G, N * G * 2);
-    const auto rb = make_rsrc(B + e * (int64_t)N * G, N * G * 2);
+    const uint32_t N = a.N;
+    const uint32_t G = K >> a.gs_log2;
+    const int slot = rg * ROWS_PER_WAVE + slice * RPW;  // first row inside the block
+    const uint32_t row0 = blockIdx.x * ROWS_PER_BLOCK + slot;
 
-    uint4 wv[RPW][ITERS];
-    float sc[RPW][ITERS], bo[RPW][ITERS];
+    uint32_t wo[ITERS];  // word offset inside a row
 #pragma unroll
-    for (int r = 0; r < RPW; r++)
+    for (int it = 0; it < ITERS; it++) wo[it] = ks * PK + it * 4 * LPR + 4 * sl;
+
+    // this block's rows of expert e, kept in registers for every pair of the bucket
+    uint4 wv[NSTK][RPW][ITERS];
+    float sc[NSTK][RPW][ITERS], bo[NSTK][RPW][ITERS];
 #pragma unroll
-        for (int it = 0; it < ITERS; it++)
-            wv[r][it] = buf_load16_nt(rw, ((row0 + r) * P + it * 4 * LPR + 4 * sl) * 4);
+    for (int t = 0; t < NSTK; t++) {
+        const auto rw = make_rsrc(a.w[t] + e * (int64_t)N * P, N * P * 4);
 #pragma unroll
-    for (int r = 0; r < RPW; r++)
+        for (int r = 0; r < RPW; r++)
 #pragma unroll
-        for (int it = 0; it < ITERS; it++) {
-            const uint32_t off = ((row0 + r) * G + ((32u * (it * LPR + sl)) >> gs_log2)) * 2;
-            const uint16_t sh = buf_load2(rs, off), bh = buf_load2(rb, off);
-            const float s = SB_F16 ? f16_to_f32(sh) : bf16_to_f32(sh);
-            const float b = SB_F16 ? f16_to_f32(bh) : bf16_to_f32(bh);
-            sc[r][it] = s;
-            bo[r][it] = fmaf(-kCodeOffset, s, b);
-        }
+            for (int it = 0; it < ITERS; it++)
+                wv[t][r][it] = buf_load16_nt(rw, ((row0 + r) * P + wo[it]) * 4);
+    }
+#pragma unroll
+    for (int t = 0; t < NSTK; t++) {
+        const auto rs = make_rsrc(a.s[t] + e * (int64_t)N * G, N * G * 2);
+        const auto rb = make_rsrc(a.b[t] + e * (int64_t)N * G, N * G * 2);
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int it = 0; it < ITERS; it++) {
+                const uint32_t off = ((row0 + r) * G + ((8u * wo[it]) >> a.gs_log2)) * 2;
+                const uint16_t sh = buf_load2(rs, off), bh = buf_load2(rb, off);
+                const float s = SB_F16 ? f16_to_f32(sh) : bf16_to_f32(sh);
+                const float b = SB_F16 ? f16_to_f32(bh) : bf16_to_f32(bh);
+                sc[t][r][it] = s;
+                bo[t][r][it] = fmaf(-kCodeOffset, s, b);
+            }
+    }
 
     for (int pi = p_begin; pi < p_end; pi++) {
         const int64_t pair = pairs[pi];
-        const int64_t l = pair / k_slots, k = pair - l * k_slots;
-        const int64_t xrow = l * a_vectors + (a_vectors == 1 ? 0 : k);
-        const uint16_t* xr = X + xrow * K;
-        float part[RPW];
+        const int64_t l = pair / a.k_slots, k = pair - l * a.k_slots;
+        const int64_t xrow = l * a.a_vectors + (a.a_vectors == 1 ? 0 : k);
+        const uint16_t* xr = a.x + xrow * K;
+        float part[NSTK][RPW];
 #pragma unroll
-        for (int r = 0; r < RPW; r++) part[r] = 0.0f;
+        for (int t = 0; t < NSTK; t++)
+#pragma unroll
+            for (int r = 0; r < RPW; r++) part[t][r] = 0.0f;
 #pragma unroll
         for (int it = 0; it < ITERS; it++) {
-            const uint4* xv = reinterpret_cast<const uint4*>(xr + 32 * (it * LPR + sl));
-            const uint4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
-            const float xs = (sum8_bf16(x0) + sum8_bf16(x1)) + (sum8_bf16(x2) + sum8_bf16(x3));
+            const uint4* xv = reinterpret_cast<const uint4*>(xr + 8 * wo[it]);
+            uint32_t xp[16];
+            float xs = 0.0f;
+            {
+                const uint4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
+                xs = (pair_up(x0, &xp[0]) + pair_up(x1, &xp[4])) +
+                     (pair_up(x2, &xp[8]) + pair_up(x3, &xp[12]));
+            }
+#pragma unroll
+            for (int t = 0; t < NSTK; t++)
+#pragma unroll
+                for (int r = 0; r < RPW; r++) {
+                    float d = 0.0f;
+                    d = word_dot(wv[t][r][it].x, &xp[0], d);
+                    d = word_dot(wv[t][r][it].y, &xp[4], d);
+                    d = word_dot(wv[t][r][it].z, &xp[8], d);
+                    d = word_dot(wv[t][r][it].w, &xp[12], d);
+                    part[t][r] = fmaf(sc[t][r][it], d, part[t][r]);
+                    part[t][r] = fmaf(bo[t][r][it], xs, part[t][r]);
+                }
+        }
+#pragma unroll
+        for (int t = 0; t < NSTK; t++)
+#pragma unroll
+            for (int r = 0; r < RPW; r++) part[t][r] = slice_sum_last<LPR>(part[t][r]);
+        if constexpr (KSPLIT > 1) {
+            if (ks > 0 && sl == LPR - 1)
+#pragma unroll
+                for (int t = 0; t < NSTK; t++)
+#pragma unroll
+                    for (int r = 0; r < RPW; r++)
+                        red[((ks - 1) * NSTK + t) * ROWS_PER_BLOCK + slot + r] = part[t][r];
+            __syncthreads();
+            if (ks == 0 && sl == LPR - 1)
+#pragma unroll
+                for (int kp = 1; kp < KSPLIT; kp++)
+#pragma unroll
+                    for (int t = 0; t < NSTK; t++)
+#pragma unroll
+                        for (int r = 0; r < RPW; r++)
+                            part[t][r] += red[((kp - 1) * NSTK + t) * ROWS_PER_BLOCK + slot + r];
+            __syncthreads();  // red is rewritten by the next pair
+        }
+        if (ks == 0 && sl == LPR - 1) {
 #pragma unroll
             for (int r = 0; r < RPW; r++) {
-                float d = 0.0f;
-                d = word_dot(wv[r][it].x, x0, d);
-                d = word_dot(wv[r][it].y, x1, d);
-                d = word_dot(wv[r][it].z, x2, d);
-                d = word_dot(wv[r][it].w, x3, d);
-                part[r] = fmaf(sc[r][it], d, part[r]);
-                part[r] = fmaf(bo[r][it], xs, part[r]);
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < RPW; r++) {
-            const float v = slice_sum_last<LPR>(part[r]);
-            const uint32_t row = row0 + r;
-            if (sl == LPR - 1 && row < N) {
-                if (y_dt == JH_BF16)
-                    static_cast<uint16_t*>(Y)[pair * N + row] = f32_to_bf16_hw(v);
-                else
-                    static_cast<float*>(Y)[pair * N + row] = v;
+                const uint32_t row = row0 + r;
+                if (row >= N) continue;
+                if constexpr (EPI == EPI_COMBINE) {
+                    atomicAdd(static_cast<float*>(a.y) + l * N + row, a.scores[pair] * part[0][r]);
+                } else {
+                    const float v = EPI == EPI_SWIGLU ? silu(part[0][r]) * part[NSTK - 1][r] : part[0][r];
+                    if (a.y_dt == JH_BF16)
+                        static_cast<uint16_t*>(a.y)[pair * N + row] = f32_to_bf16_hw(v);
+                    else
+                        static_cast<float*>(a.y)[pair * N + row] = v;
+                }
             }
         }
     }
 }
 
-template <int LPR, int ITERS, int RPW, bool SB_F16, bool FUSED>
-Status run_fast_sb(const GatherArgs& a, int64_t max_u, int gs_log2, hipStream_t st) {
-    constexpr int64_t rows_per_block = 4 * (64 / LPR) * RPW;
-    const int64_t blocks = (a.m.rows + rows_per_block - 1) / rows_per_block;
-    hipLaunchKernelGGL((gather_qmv_kernel<LPR, ITERS, RPW, SB_F16, FUSED>),
-                       dim3((unsigned)blocks, (unsigned)max_u), dim3(256), 0, st, a.m.w,
-                       static_cast<const uint16_t*>(a.m.scales), static_cast<const uint16_t*>(a.m.biases),
-                       static_cast<const uint16_t*>(a.x), a.y, a.y_dtype, (uint32_t)a.m.rows, gs_log2,
-                       static_cast<const int*>(a.workspace), a.idx, (int)(a.n_lead * a.k_slots),
-                       a.n_experts, a.k_slots, a.a_vectors);
-    return Status::ok();
+// out[t, :] = 0, or NaN for a token with an expert index outside [0, E).
+__global__ __launch_bounds__(256) void moe_init_out_kernel(float* __restrict__ out, int64_t n_tok, int64_t H,
+                                                           const int32_t* __restrict__ idx, int64_t K,
+                                                           int64_t E) {
+    const int64_t n = n_tok * H;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = i / H;
+        bool bad = false;
+        for (int64_t k = 0; k < K; k++) {
+            const int32_t e = idx[t * K + k];
+            bad |= e < 0 || e >= E;
+        }
+        out[i] = bad ? __uint_as_float(0x7fc00000u) : 0.0f;
+    }
 }
 
-template <int LPR, int ITERS, int RPW>
-Status run_fast(const GatherArgs& a, int64_t max_u, int gs_log2, bool fused, hipStream_t st) {
-    if (fused) {
-        if (a.m.sb_dtype == JH_F16) return run_fast_sb<LPR, ITERS, RPW, true, true>(a, max_u, gs_log2, st);
-        return run_fast_sb<LPR, ITERS, RPW, false, true>(a, max_u, gs_log2, st);
-    }
-    if (a.m.sb_dtype == JH_F16) return run_fast_sb<LPR, ITERS, RPW, true, false>(a, max_u, gs_log2, st);
-    return run_fast_sb<LPR, ITERS, RPW, false, false>(a, max_u, gs_log2, st);
+__global__ __launch_bounds__(256) void moe_narrow_kernel(const float* __restrict__ acc, void* __restrict__ out,
+                                                         int dt, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        store_y(out, i, acc[i], dt);
 }
 
 int log2_exact(int v) {
     int l = 0;
     while ((1 << l) < v) l++;
     return ((1 << l) == v) ? l : -1;
+}
+
+template <int LPR, int ITERS, int RPW, int KSPLIT, int EPI>
+void run_tile(const MoeArgs& a, bool sb_f16, bool fused, int64_t max_u, hipStream_t st) {
+    constexpr int64_t rows_per_block = (4 / KSPLIT) * (64 / LPR) * RPW;
+    const dim3 grid((unsigned)((a.N + rows_per_block - 1) / rows_per_block), (unsigned)max_u);
+    if (fused) {
+        if (sb_f16)
+            hipLaunchKernelGGL((moe_qmv_kernel<LPR, ITERS, RPW, KSPLIT, true, EPI, true>), grid, dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((moe_qmv_kernel<LPR, ITERS, RPW, KSPLIT, false, EPI, true>), grid, dim3(256), 0, st, a);
+    } else {
+        if (sb_f16)
+            hipLaunchKernelGGL((moe_qmv_kernel<LPR, ITERS, RPW, KSPLIT, true, EPI, false>), grid, dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((moe_qmv_kernel<LPR, ITERS, RPW, KSPLIT, false, EPI, false>), grid, dim3(256), 0, st, a);
+    }
+}
+
+// Tile per row length P (32-bit words). SWIGLU holds two stacks' rows, so it
+// takes half the rows per wave of the single-stack epilogues.
+template <int EPI>
+bool run_fast(const MoeArgs& a, int64_t P, bool sb_f16, bool fused, int64_t max_u, hipStream_t st) {
+    constexpr int R4 = EPI == EPI_SWIGLU ? 2 : 4;
+    constexpr int R2 = EPI == EPI_SWIGLU ? 1 : 2;
+    switch (P) {
+        case 256 * 1: run_tile<64, 1, R4, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        case 256 * 2: run_tile<64, 2, R2, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        case 256 * 3: run_tile<64, 3, R2, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        case 256 * 4: run_tile<64, 4, 1, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        case 256 * 6: run_tile<64, 6, 1, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        case 128 * 1: run_tile<32, 1, R4, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        case 128 * 3: run_tile<32, 3, R2, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        case 64 * 1: run_tile<16, 1, R4, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        case 64 * 3: run_tile<16, 3, R2, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        case 32 * 1: run_tile<8, 1, R4, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        case 32 * 3: run_tile<8, 3, R2, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        default: return false;
+    }
 }
 
 bool fast_tile_exists(int64_t P) {
@@ -305,6 +428,27 @@ bool fast_tile_exists(int64_t P) {
     }
 }
 
+// Shapes the register-tile kernel takes: bf16 x, power-of-two groups of
+// 32..128, 16-bit scales, byte offsets inside one expert below 2^31.
+bool fast_ok(const QuantMatrix& m, int x_dtype) {
+    const int gl = log2_exact(m.group_size);
+    return x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0 &&
+           (m.sb_dtype == JH_BF16 || m.sb_dtype == JH_F16) &&
+           (m.rows + 64) * (m.in / 2) < ((int64_t)1 << 31) && fast_tile_exists(m.in / 8);
+}
+
+MoeArgs single_stack(const QuantMatrix& m) {
+    MoeArgs a{};
+    a.w[0] = a.w[1] = m.w;
+    a.s[0] = a.s[1] = static_cast<const uint16_t*>(m.scales);
+    a.b[0] = a.b[1] = static_cast<const uint16_t*>(m.biases);
+    a.N = (uint32_t)m.rows;
+    a.gs_log2 = log2_exact(m.group_size);
+    return a;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
 }  // namespace
 
 size_t gather_workspace_bytes(int64_t n_experts, int64_t n_pairs) {
@@ -312,11 +456,7 @@ size_t gather_workspace_bytes(int64_t n_experts, int64_t n_pairs) {
 }
 
 bool gather_uses_workspace(const GatherArgs& a) {
-    const int gl = log2_exact(a.m.group_size);
-    const bool fast = a.x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (a.m.in % a.m.group_size) == 0 &&
-                      (a.m.sb_dtype == JH_BF16 || a.m.sb_dtype == JH_F16) &&
-                      (a.m.rows + 64) * (a.m.in / 2) < ((int64_t)1 << 31) && fast_tile_exists(a.m.in / 8);
-    return !(fast && a.n_lead * a.k_slots <= kFusedMaxPairs);
+    return !(fast_ok(a.m, a.x_dtype) && a.n_lead * a.k_slots <= kFusedMaxPairs);
 }
 
 Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st) {
@@ -326,30 +466,22 @@ Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st) {
         return Status::fail(JH_ERR_UNSUPPORTED, "gather_quant_matmul: more than 4096 experts");
     const int64_t max_u = n_pairs < a.n_experts ? n_pairs : a.n_experts;
     if (max_u > 65535) return Status::fail(JH_ERR_UNSUPPORTED, "gather_quant_matmul: too many experts in one call");
-    const int gl = log2_exact(a.m.group_size);
     const bool fused = !gather_uses_workspace(a);
     if (!fused)
         hipLaunchKernelGGL(moe_bucket_kernel, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.n_experts,
                            static_cast<int*>(a.workspace), a.y, a.y_dtype, a.m.rows);
-    const int64_t P = a.m.in / 8;
-    const bool fast_ok = a.x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (a.m.in % a.m.group_size) == 0 &&
-                         (a.m.sb_dtype == JH_BF16 || a.m.sb_dtype == JH_F16) &&
-                         (a.m.rows + 64) * (a.m.in / 2) < ((int64_t)1 << 31);
-    if (fast_ok) {
-        switch (P) {
-            case 256 * 1: return run_fast<64, 1, 4>(a, max_u, gl, fused, st);
-            case 256 * 2: return run_fast<64, 2, 2>(a, max_u, gl, fused, st);
-            case 256 * 3: return run_fast<64, 3, 2>(a, max_u, gl, fused, st);
-            case 256 * 4: return run_fast<64, 4, 1>(a, max_u, gl, fused, st);
-            case 256 * 6: return run_fast<64, 6, 1>(a, max_u, gl, fused, st);
-            case 128 * 1: return run_fast<32, 1, 4>(a, max_u, gl, fused, st);
-            case 128 * 3: return run_fast<32, 3, 2>(a, max_u, gl, fused, st);
-            case 64 * 1: return run_fast<16, 1, 4>(a, max_u, gl, fused, st);
-            case 64 * 3: return run_fast<16, 3, 2>(a, max_u, gl, fused, st);
-            case 32 * 1: return run_fast<8, 1, 4>(a, max_u, gl, fused, st);
-            case 32 * 3: return run_fast<8, 3, 2>(a, max_u, gl, fused, st);
-            default: break;
-        }
+    if (fast_ok(a.m, a.x_dtype)) {
+        MoeArgs m = single_stack(a.m);
+        m.x = static_cast<const uint16_t*>(a.x);
+        m.y = a.y;
+        m.y_dt = a.y_dtype;
+        m.ws = static_cast<const int*>(a.workspace);
+        m.idx = a.idx;
+        m.n_pairs = (int)n_pairs;
+        m.E = a.n_experts;
+        m.k_slots = a.k_slots;
+        m.a_vectors = a.a_vectors;
+        if (run_fast<EPI_PLAIN>(m, a.m.in / 8, a.m.sb_dtype == JH_F16, fused, max_u, st)) return Status::ok();
     }
     int64_t blocks = (a.m.rows + 3) / 4;
     const int64_t cap = (int64_t)num_cus * 4;
@@ -358,6 +490,90 @@ Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st) {
                        a.m.w, a.m.scales, a.m.biases, a.m.sb_dtype, a.x, a.x_dtype, a.y, a.y_dtype,
                        a.m.rows, a.m.in, a.m.group_size, (int64_t)0,
                        static_cast<const int*>(a.workspace), a.n_experts, a.k_slots, a.a_vectors);
+    return Status::ok();
+}
+
+const char* moe_unsupported(const MoeMlpArgs& a) {
+    if (a.n_experts > kMaxExperts) return "more than 4096 experts";
+    if (a.gate.rows != a.up.rows || a.gate.in != a.up.in || a.down.in != a.gate.rows)
+        return "gate/up must be [E, I, H] and down [E, H, I]";
+    if (a.gate.sb_dtype != a.up.sb_dtype || a.gate.sb_dtype != a.down.sb_dtype)
+        return "the three stacks must share one scale dtype";
+    if (!fast_ok(a.gate, JH_BF16) || !fast_ok(a.down, JH_BF16))
+        return "shape outside the expert tiles (bf16 scales, group 32/64/128, H and I in "
+               "{256, 512, 768, 1024, 1536, 2048, 3072, 4096, 6144, 8192, 12288})";
+    const int64_t max_u = std::min<int64_t>(a.n_tok * a.k_slots, a.n_experts);
+    if (max_u > 65535) return "too many experts in one call";
+    return nullptr;
+}
+
+size_t moe_workspace_bytes(const MoeMlpArgs& a) {
+    const int64_t n_pairs = a.n_tok * a.k_slots;
+    size_t b = align256(sizeof(uint16_t) * (size_t)(n_pairs * a.gate.rows));  // h
+    if (a.out_dtype != JH_F32) b += align256(sizeof(float) * (size_t)(a.n_tok * a.down.rows));
+    if (n_pairs > kFusedMaxPairs) b += gather_workspace_bytes(a.n_experts, n_pairs);
+    return b;
+}
+
+Status launch_moe_mlp(const MoeMlpArgs& a, void* workspace, hipStream_t st) {
+    const int64_t n_pairs = a.n_tok * a.k_slots;
+    if (a.n_tok == 0) return Status::ok();
+    if (const char* why = moe_unsupported(a)) return Status::fail(JH_ERR_UNSUPPORTED, std::string("moe_swiglu: ") + why);
+    const int64_t H = a.down.rows, I = a.gate.rows;
+    const int64_t max_u = std::min<int64_t>(n_pairs, a.n_experts);
+    const bool fused = n_pairs <= kFusedMaxPairs;
+    const bool f16 = a.gate.sb_dtype == JH_F16;
+    char* wsp = static_cast<char*>(workspace);
+    uint16_t* h = reinterpret_cast<uint16_t*>(wsp);
+    wsp += align256(sizeof(uint16_t) * (size_t)(n_pairs * I));
+    float* acc = static_cast<float*>(a.out);
+    if (a.out_dtype != JH_F32) {
+        acc = reinterpret_cast<float*>(wsp);
+        wsp += align256(sizeof(float) * (size_t)(a.n_tok * H));
+    }
+    int* buckets = fused ? nullptr : reinterpret_cast<int*>(wsp);
+
+    const int64_t n_out = a.n_tok * H;
+    const unsigned init_blocks = (unsigned)std::min<int64_t>((n_out + 255) / 256, 4096);
+    hipLaunchKernelGGL(moe_init_out_kernel, dim3(init_blocks), dim3(256), 0, st, acc, a.n_tok, H, a.idx,
+                       a.k_slots, a.n_experts);
+    if (n_pairs > 0) {  // with no slots, out is the empty sum
+        if (!fused)
+            hipLaunchKernelGGL(moe_bucket_kernel, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.n_experts, buckets,
+                               static_cast<void*>(nullptr), (int)JH_BF16, (int64_t)0);
+
+        MoeArgs g = single_stack(a.gate);
+        g.w[1] = a.up.w;
+        g.s[1] = static_cast<const uint16_t*>(a.up.scales);
+        g.b[1] = static_cast<const uint16_t*>(a.up.biases);
+        g.x = static_cast<const uint16_t*>(a.x);
+        g.y = h;
+        g.y_dt = JH_BF16;
+        g.ws = buckets;
+        g.idx = a.idx;
+        g.n_pairs = (int)n_pairs;
+        g.E = a.n_experts;
+        g.k_slots = a.k_slots;
+        g.a_vectors = 1;
+        if (!run_fast<EPI_SWIGLU>(g, a.gate.in / 8, f16, fused, max_u, st))
+            return Status::fail(JH_ERR_UNSUPPORTED, "moe_swiglu: no tile for the gate/up shape");
+
+        MoeArgs d = single_stack(a.down);
+        d.x = h;
+        d.y = acc;
+        d.y_dt = JH_F32;
+        d.ws = buckets;
+        d.idx = a.idx;
+        d.n_pairs = (int)n_pairs;
+        d.E = a.n_experts;
+        d.k_slots = a.k_slots;
+        d.a_vectors = a.k_slots;
+        d.scores = a.scores;
+        if (!run_fast<EPI_COMBINE>(d, a.down.in / 8, f16, fused, max_u, st))
+            return Status::fail(JH_ERR_UNSUPPORTED, "moe_swiglu: no tile for the down shape");
+    }
+    if (a.out_dtype != JH_F32)
+        hipLaunchKernelGGL(moe_narrow_kernel, dim3(init_blocks), dim3(256), 0, st, acc, a.out, a.out_dtype, n_out);
     return Status::ok();
 }
 

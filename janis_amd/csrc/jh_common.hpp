@@ -156,4 +156,20 @@ size_t gather_workspace_bytes(int64_t n_experts, int64_t n_pairs);
 bool gather_uses_workspace(const GatherArgs& a);
 Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st);
 
+// One MoE expert MLP over stacked experts: out = sum_k score * down(SiLU(gate x) * up x).
+struct MoeMlpArgs {
+    QuantMatrix gate, up, down;  // one expert's shapes; pointers at expert 0
+    int64_t n_experts;
+    const void* x;               // bf16 [n_tok, H]
+    int64_t n_tok, k_slots;
+    const int32_t* idx;          // [n_tok, k_slots]
+    const float* scores;         // [n_tok, k_slots]
+    void* out;                   // [n_tok, H]
+    int out_dtype;
+};
+// Why the fused kernels cannot take this call, or nullptr.
+const char* moe_unsupported(const MoeMlpArgs& a);
+size_t moe_workspace_bytes(const MoeMlpArgs& a);
+Status launch_moe_mlp(const MoeMlpArgs& a, void* workspace, hipStream_t st);
+
 }  // namespace jh

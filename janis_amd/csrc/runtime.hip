@@ -335,4 +335,57 @@ int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n
     return finish(c, jh::launch_gather(a, c->num_cus, c->stream), "gather");
 }
 
+int jh_moe_swiglu(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n_tok, const uint32_t* w_gate,
+                  const void* s_gate, const void* b_gate, const uint32_t* w_up, const void* s_up,
+                  const void* b_up, const uint32_t* w_down, const void* s_down, const void* b_down,
+                  jh_dtype sb_dtype, int64_t n_experts, int64_t hidden, int64_t intermediate,
+                  const int32_t* rhs_indices, const float* scores, int64_t k_slots, int group_size,
+                  int bits, void* out, jh_dtype out_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_moe_swiglu";
+    if (int r = check_quant(c, op, w_gate, s_gate, b_gate, sb_dtype, intermediate, hidden, group_size, bits))
+        return r;
+    if (int r = check_quant(c, op, w_up, s_up, b_up, sb_dtype, intermediate, hidden, group_size, bits))
+        return r;
+    if (int r = check_quant(c, op, w_down, s_down, b_down, sb_dtype, hidden, intermediate, group_size, bits))
+        return r;
+    if (x_dtype != JH_BF16) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": x must be bf16");
+    if (int r = check_act_dtype(c, op, "out", out_dtype)) return r;
+    if (n_tok < 0 || k_slots < 0 || n_experts <= 0 || intermediate <= 0)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad n_tok / k_slots / n_experts / intermediate");
+    const int64_t n_pairs = n_tok * k_slots;
+    if (n_tok == 0) return JH_OK;
+    if (n_pairs > (int64_t)1 << 30) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": too many slots");
+    if (!x || !out || !aligned16(x) || !aligned16(out) || (n_pairs > 0 && (!rhs_indices || !scores)))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": null or unaligned x / out / indices / scores");
+    jh::MoeMlpArgs a;
+    a.gate = jh::QuantMatrix{w_gate, s_gate, b_gate, sb_dtype, intermediate, hidden, group_size};
+    a.up = jh::QuantMatrix{w_up, s_up, b_up, sb_dtype, intermediate, hidden, group_size};
+    a.down = jh::QuantMatrix{w_down, s_down, b_down, sb_dtype, hidden, intermediate, group_size};
+    a.n_experts = n_experts;
+    a.x = x;
+    a.n_tok = n_tok;
+    a.k_slots = k_slots;
+    a.idx = rhs_indices;
+    a.scores = scores;
+    a.out = out;
+    a.out_dtype = out_dtype;
+    if (const char* why = jh::moe_unsupported(a))
+        return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": " + why);
+    if (c->checks && n_pairs > 0) {
+        std::vector<int32_t> h((size_t)n_pairs);
+        JH_HIP(c, hipMemcpyAsync(h.data(), rhs_indices, h.size() * sizeof(int32_t),
+                                 hipMemcpyDeviceToHost, c->stream));
+        JH_HIP(c, hipStreamSynchronize(c->stream));
+        for (size_t i = 0; i < h.size(); i++)
+            if (h[i] < 0 || h[i] >= n_experts)
+                return fail(c, JH_ERR_INVALID,
+                            std::string(op) + ": expert index " + std::to_string(h[i]) +
+                                " at slot " + std::to_string(i) + " outside [0, " +
+                                std::to_string(n_experts) + ")");
+    }
+    if (int r = ensure_workspace(c, jh::moe_workspace_bytes(a), op)) return r;
+    return finish(c, jh::launch_moe_mlp(a, c->ws, c->stream), "moe_swiglu");
+}
+
 }  // extern "C"

@@ -230,6 +230,37 @@ class HipBackend:
             groupSize, bits, y.ptr, y.dtype))
         return y
 
+    def MoeSwiGLU(self, x: Tensor, gate: tuple, up: tuple, down: tuple, rhsIndices: Tensor,
+                  scores: Tensor, groupSize: int, bits: int, out: Tensor | None = None,
+                  out_dtype: int | None = None) -> Tensor:
+        """The expert MLP of moeApply (qwen/moe.go:501-511) as one operator:
+        sum_k scores[t, k] * down(SiLU(gate x_t) * up x_t) over the routed
+        experts. x [lead.., H] bf16; gate/up/down are (W, S, B) stacks
+        [E, I, H/8], [E, I, H/8], [E, H, I/8]; rhsIndices I32 and scores F32
+        [lead.., K]. Returns [lead.., H] (F32 unless out_dtype says BF16)."""
+        (wg, sg, bg), (wu, su, bu), (wd, sd, bd) = gate, up, down
+        for w in (wg, wu, wd):
+            if w.dtype != U32 or len(w.shape) != 3:
+                raise JanisHipError(_lib.JH_ERR_INVALID, "MoeSwiGLU: stacks must be U32 [E, out, P]")
+        if rhsIndices.dtype != I32 or scores.dtype != F32 or rhsIndices.shape != scores.shape:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "MoeSwiGLU: indices I32 and scores F32 of one shape")
+        E, I, Pg = wg.shape
+        H = Pg * (32 // bits)
+        if wu.shape != wg.shape or wd.shape != (E, H, I * bits // 32):
+            raise JanisHipError(_lib.JH_ERR_INVALID, "MoeSwiGLU: stack shapes do not match")
+        rs = rhsIndices.shape
+        K = rs[-1]
+        n_tok = int(np.prod(rs[:-1], dtype=np.int64)) if len(rs) > 1 else 1
+        if x.shape[-1] != H or x.numel != n_tok * H:
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"MoeSwiGLU: x {list(x.shape)} vs hidden={H}")
+        od = out_dtype if out_dtype is not None else (out.dtype if out is not None else F32)
+        y = out if out is not None else self.empty(od, *rs[:-1], H)
+        check(self._ctx, self._L.jh_moe_swiglu(
+            self._ctx, x.ptr, x.dtype, n_tok, wg.ptr, sg.ptr, bg.ptr, wu.ptr, su.ptr, bu.ptr,
+            wd.ptr, sd.ptr, bd.ptr, self._sb_dtype(sg, bg), E, H, I, rhsIndices.ptr, scores.ptr, K,
+            groupSize, bits, y.ptr, y.dtype))
+        return y
+
     def __del__(self):
         try:
             self.Close()

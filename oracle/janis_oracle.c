@@ -354,6 +354,48 @@ int or_qmv_avx2_parallel(const float *x, const uint32_t *w, const float *s, cons
     return (int)n;
 }
 
+/* qwen/moe.go:501-511 */
+int or_moe_apply(const float *x, int64_t n_tok, const uint32_t *wg, const float *sg,
+                 const float *bg, const uint32_t *wu, const float *su, const float *bu,
+                 const uint32_t *wd, const float *sd, const float *bd, int64_t E, int64_t H,
+                 int64_t I, const int32_t *idx, const float *scores, int64_t k_slots, float *out,
+                 int group_size, int simd) {
+    const int64_t np = n_tok * k_slots;
+    float *g = (float *)malloc((size_t)(np * I + 1) * sizeof(float));
+    float *u = (float *)malloc((size_t)(np * I + 1) * sizeof(float));
+    float *d = (float *)malloc((size_t)(np * H + 1) * sizeof(float));
+    if (!g || !u || !d) abort();
+    int rc = or_gather_quant_matmul(x, n_tok, 1, wg, sg, bg, E, idx, k_slots, g, I, H, group_size, 4, simd);
+    if (rc == 0)
+        rc = or_gather_quant_matmul(x, n_tok, 1, wu, su, bu, E, idx, k_slots, u, I, H, group_size, 4, simd);
+    if (rc == 0) {
+        for (int64_t i = 0; i < np * I; i++) {
+            const float v = g[i];
+            const float e = (float)exp((double)(-v));
+            const float silu = v / (1.0f + e);
+            g[i] = silu * u[i];
+        }
+        rc = or_gather_quant_matmul(g, n_tok, k_slots, wd, sd, bd, E, idx, k_slots, d, H, I, group_size, 4,
+                                    simd);
+    }
+    if (rc == 0) {
+        for (int64_t t = 0; t < n_tok; t++)
+            for (int64_t j = 0; j < H; j++) {
+                float acc = 0.0f;
+                for (int64_t k = 0; k < k_slots; k++) {
+                    const float p = d[(t * k_slots + k) * H + j] * scores[t * k_slots + k];
+                    acc = acc + p;
+                }
+                const float mean = acc / (float)k_slots;
+                out[t * H + j] = mean * (float)k_slots;
+            }
+    }
+    free(g);
+    free(u);
+    free(d);
+    return rc;
+}
+
 /* ---- MoE routing helpers ----------------------------------------------- */
 
 /* qwen/moe.go:420-444 */

@@ -106,6 +106,19 @@ int or_gather_quant_matmul(const float *x, int64_t n_lead, int64_t A, const uint
 int or_qmv_avx2_parallel(const float *x, const uint32_t *w, const float *s, const float *b,
                          float *y, int64_t N, int64_t K, int group_size, int workers);
 
+/* moeApply (qwen/moe.go:501-511) with resident stacks and global expert ids:
+ *   g = gather(x, gate), u = gather(x, up)          (A = 1: one vector per token)
+ *   h = SiLU(g) * u, SiLU(v) = v / (1 + fl32(exp(-v)))   (cpu/cpu.go:327-329, :304-306)
+ *   d = gather(h, down)                              (A = k_slots)
+ *   out[t, :] = fl32(fl32(sum_k d[t,k,:]*score[t,k]) / K) * K   (cpu/cpu_ops.go:113-142, cpu/cpu_misc.go:24-26)
+ * x [n_tok, H], stacks gate/up [E, I, H/8] and down [E, H, I/8] (4-bit), idx and
+ * scores [n_tok, K], out [n_tok, H]. Returns 0, or -1 on an index out of range. */
+int or_moe_apply(const float *x, int64_t n_tok, const uint32_t *wg, const float *sg,
+                 const float *bg, const uint32_t *wu, const float *su, const float *bu,
+                 const uint32_t *wd, const float *sd, const float *bd, int64_t E, int64_t H,
+                 int64_t I, const int32_t *idx, const float *scores, int64_t k_slots, float *out,
+                 int group_size, int simd);
+
 /* Router top-k (qwen/moe.go:420-444): selection sort on a copy of the index
  * order, strict '>' comparison, k passes; writes idx[k], val[k]. */
 void or_topk(const float *row, int n, int k, int32_t *idx, float *val);

@@ -57,6 +57,9 @@ def lib() -> ctypes.CDLL:
         L.or_gather_quant_matmul.restype = _int
         L.or_qmv_avx2_parallel.argtypes = [_f32p, _u32p, _f32p, _f32p, _f32p, _i64, _i64, _int, _int]
         L.or_qmv_avx2_parallel.restype = _int
+        L.or_moe_apply.argtypes = [_f32p, _i64, _u32p, _f32p, _f32p, _u32p, _f32p, _f32p, _u32p, _f32p, _f32p,
+                                   _i64, _i64, _i64, _i32p, _f32p, _i64, _f32p, _int, _int]
+        L.or_moe_apply.restype = _int
         L.or_topk.argtypes = [_f32p, _int, _int, _i32p, _f32p]
         L.or_topk.restype = None
         L.or_softmax_row.argtypes = [_f32p, _f32p, _int]
@@ -146,6 +149,24 @@ def gather_quant_matmul(x, w, s, b, idx, group_size: int, bits: int = 4, simd: b
     if rc != 0:
         raise IndexError("expert index out of range")
     return y
+
+
+def moe_apply(x, gate, up, down, idx, scores, group_size: int = 64, simd: bool = True) -> np.ndarray:
+    """qwen/moe.go:501-511 over resident stacks. gate/up/down are (w, s, b)
+    triples of float32 scales/biases; x [n_tok, H]; idx, scores [n_tok, K]."""
+    x = _f32(x)
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    scores = _f32(scores)
+    n_tok, k = idx.shape
+    (wg, sg, bg), (wu, su, bu), (wd, sd, bd) = gate, up, down
+    E, I, _ = wg.shape
+    H = x.shape[-1]
+    out = np.zeros((n_tok, H), dtype=np.float32)
+    rc = lib().or_moe_apply(x, n_tok, _u32(wg), _f32(sg), _f32(bg), _u32(wu), _f32(su), _f32(bu),
+                            _u32(wd), _f32(sd), _f32(bd), E, H, I, idx, scores, k, out, group_size, int(simd))
+    if rc != 0:
+        raise IndexError("expert index out of range")
+    return out
 
 
 def qmv_avx2_parallel(x, w, s, b, group_size: int, workers: int) -> tuple[np.ndarray, int]:

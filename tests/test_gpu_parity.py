@@ -227,6 +227,17 @@ def test_qmm_rows_are_independent(hip):
 
 # -- MoE gather ------------------------------------------------------------------
 
+_STACKS = {}
+
+
+def _qwen3_moe_stack(proj):
+    """Config-3 expert stacks (128 experts, hidden 2048, moe_intermediate 768),
+    generated once per session: gate/up [128, 768, 2048/8], down [128, 2048, 768/8]."""
+    if proj not in _STACKS:
+        n, k = (2048, 768) if proj == "down" else (768, 2048)
+        _STACKS[proj] = synth.quant_linear({"gate": 9768, "up": 9769, "down": 11048}[proj], n, k, lead=(128,))
+    return _STACKS[proj]
+
 @pytest.mark.parametrize("n_tok", [1, 16])
 @pytest.mark.parametrize("proj", ["gate", "down"])
 def test_gather_qwen3_30b_a3b(hip, oracle, n_tok, proj):
@@ -236,7 +247,7 @@ def test_gather_qwen3_30b_a3b(hip, oracle, n_tok, proj):
     E, K = 128, 8
     n, k = (768, 2048) if proj == "gate" else (2048, 768)
     A = 1 if proj == "gate" else K
-    q = synth.quant_linear(9000 + n, n, k, lead=(E,))
+    q = _qwen3_moe_stack(proj)
     idx, _ = synth.route(9100 + n_tok, n_tok, E, K)
     xb, x = synth.activations(9200 + n_tok, (n_tok, A, 1, k))
     w, s, b = upload_quant(hip, q)
@@ -303,6 +314,114 @@ def test_gather_out_of_range_index(hip):
             hip.GatherQuantMatmul(hip.FromBF16Bits(xb, 1, 1, 1, 512), w, s, b, idx, True, 64, 4)
     finally:
         hip.SetChecks(False)
+
+
+# -- MoE expert MLP (moeApply as one operator) ----------------------------------------
+
+def _moe_upload(hip, qs):
+    return [upload_quant(hip, q) for q in qs]
+
+
+def _moe_case(hip, oracle, qs, x_shape, idx, sc, out_dtype=F32):
+    xb, x = synth.activations(sum(x_shape) + int(idx.sum()), x_shape)
+    st = _moe_upload(hip, qs)
+    out = hip.MoeSwiGLU(hip.FromBF16Bits(xb, *x_shape), *st, hip.FromInt32(idx), hip.FromFloats(sc), 64, 4,
+                        out_dtype=out_dtype)
+    want = oracle.moe_apply(x, *[(q.w, q.s, q.b) for q in qs], idx, sc)
+    return hip.Floats(out), want
+
+
+@pytest.mark.parametrize("n_tok", [1, 16])
+def test_moe_swiglu_qwen3_30b_a3b(hip, oracle, n_tok):
+    """Config 3 end to end: top-8 of 128 experts from a seeded router, the
+    gate+up SwiGLU launch and the score-weighted down launch against the
+    oracle's moeApply (qwen/moe.go:501-511). h is bf16 on the device and fp32
+    in the oracle, inside the bf16 bar."""
+    qs = [_qwen3_moe_stack(p) for p in ("gate", "up", "down")]
+    idx, sc = synth.route(9300 + n_tok, n_tok, 128, 8)
+    step(f"jh_moe_swiglu qwen3-30b-a3b T={n_tok} U={len(np.unique(idx))}")
+    got, want = _moe_case(hip, oracle, qs, (n_tok, 2048), idx, sc)
+    assert got.shape == (n_tok, 2048)
+    ok, d, s = rel_ok(got, want, BF16_TOL)
+    assert ok, (d, s)
+
+
+@pytest.mark.parametrize("n_tok,E,H,I,out_dtype", [(4, 6, 512, 256, F32), (3, 5, 1024, 768, BF16),
+                                                    (2, 3, 256, 512, F32)])
+def test_moe_swiglu_small_with_collisions(hip, oracle, n_tok, E, H, I, out_dtype):
+    """Several slots per expert, repeated experts inside one token, bf16 output."""
+    K = 8
+    qs = [synth.quant_linear(400 + i + H, *(I, H) if i < 2 else (H, I), lead=(E,)) for i in range(3)]
+    idx = np.random.default_rng(E * H).integers(0, E, (n_tok, K)).astype(np.int32)
+    sc = np.random.default_rng(E + H).random((n_tok, K)).astype(np.float32)
+    step(f"jh_moe_swiglu T={n_tok} E={E} H={H} I={I} out={out_dtype}")
+    got, want = _moe_case(hip, oracle, qs, (n_tok, H), idx, sc, out_dtype)
+    ok, d, s = rel_ok(got, want, BF16_TOL)
+    assert ok, (d, s)
+
+
+def test_moe_swiglu_many_pairs_workspace_path(hip, oracle):
+    """More than 1024 (token, slot) pairs: the separate bucketing launch."""
+    n_tok, E, H, I, K = 160, 16, 512, 256, 8
+    qs = [synth.quant_linear(500 + i, *(I, H) if i < 2 else (H, I), lead=(E,)) for i in range(3)]
+    idx, sc = synth.route(510, n_tok, E, K)
+    step(f"jh_moe_swiglu pairs={n_tok * K}")
+    got, want = _moe_case(hip, oracle, qs, (n_tok, H), idx, sc)
+    ok, d, s = rel_ok(got, want, BF16_TOL)
+    assert ok, (d, s)
+
+
+def test_moe_swiglu_matches_gather_composition(hip):
+    """The fused operator against the reference's composition run through this
+    library's GatherQuantMatmul (fp32 h there, bf16 h here)."""
+    n_tok, E, H, I, K = 2, 8, 1024, 512, 4
+    qs = [synth.quant_linear(600 + i, *(I, H) if i < 2 else (H, I), lead=(E,)) for i in range(3)]
+    (wg, sg, bg), (wu, su, bu), (wd, sd, bd) = _moe_upload(hip, qs)
+    idx, sc = synth.route(610, n_tok, E, K)
+    xb, _ = synth.activations(611, (n_tok, H))
+    it = hip.FromInt32(idx)
+    x4 = hip.FromBF16Bits(xb, n_tok, 1, 1, H)
+    step("jh_gather_quant_matmul x3 composition vs jh_moe_swiglu")
+    g = hip.Floats(hip.GatherQuantMatmul(x4, wg, sg, bg, it, True, 64, 4, out_dtype=F32)).astype(np.float64)
+    u = hip.Floats(hip.GatherQuantMatmul(x4, wu, su, bu, it, True, 64, 4, out_dtype=F32)).astype(np.float64)
+    h = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+    d = hip.Floats(hip.GatherQuantMatmul(hip.FromFloats(h), wd, sd, bd, it, True, 64, 4, out_dtype=F32))
+    want = (d[:, :, 0, :].astype(np.float64) * sc[:, :, None]).sum(axis=1)
+    got = hip.Floats(hip.MoeSwiGLU(hip.FromBF16Bits(xb, n_tok, H), (wg, sg, bg), (wu, su, bu), (wd, sd, bd),
+                                   it, hip.FromFloats(sc), 64, 4))
+    ok, dd, s = rel_ok(got, want, BF16_TOL)
+    assert ok, (dd, s)
+
+
+def test_moe_swiglu_out_of_range_and_unsupported(hip):
+    E, H, I = 4, 512, 256
+    qs = [synth.quant_linear(700 + i, *(I, H) if i < 2 else (H, I), lead=(E,)) for i in range(3)]
+    st = _moe_upload(hip, qs)
+    xb, _ = synth.activations(701, (2, H))
+    x = hip.FromBF16Bits(xb, 2, H)
+    idx = hip.FromInt32(np.array([[0, 3], [1, 9]], np.int32))
+    sc = hip.FromFloats(np.full((2, 2), 0.5, np.float32))
+    step("jh_moe_swiglu bad index, checks off")
+    y = hip.Floats(hip.MoeSwiGLU(x, *st, idx, sc, 64, 4))
+    assert np.isfinite(y[0]).all() and np.isnan(y[1]).all()
+    hip.SetChecks(True)
+    try:
+        step("jh_moe_swiglu bad index, checks on")
+        with pytest.raises(JanisHipError):
+            hip.MoeSwiGLU(x, *st, idx, sc, 64, 4)
+    finally:
+        hip.SetChecks(False)
+    step("jh_moe_swiglu no slots -> zeros")
+    z = hip.Floats(hip.MoeSwiGLU(x, *st, hip.FromInt32(np.zeros((2, 0), np.int32)),
+                                 hip.FromFloats(np.zeros((2, 0), np.float32)), 64, 4))
+    assert z.shape == (2, H) and not z.any()
+    step("jh_moe_swiglu f32 x / untiled hidden -> unsupported")
+    with pytest.raises(JanisHipError):
+        hip.MoeSwiGLU(hip.FromFloats(np.zeros((2, H), np.float32)), *st, idx, sc, 64, 4)
+    q6 = [synth.quant_linear(710 + i, *(I, 640) if i < 2 else (640, I), lead=(E,)) for i in range(3)]
+    xb6, _ = synth.activations(711, (2, 640))
+    with pytest.raises(JanisHipError):
+        hip.MoeSwiGLU(hip.FromBF16Bits(xb6, 2, 640), *_moe_upload(hip, q6), idx, sc, 64, 4)
 
 
 # -- errors (the reference panics) ---------------------------------------------------

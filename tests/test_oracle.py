@@ -233,6 +233,81 @@ def test_gather_rejects_out_of_range_index(oracle):
                                    np.array([[0, 2]], np.int32), 64)
 
 
+# -- moeApply ------------------------------------------------------------------
+
+def _moe_stacks(seed, E, H, I):
+    gate = synth.quant_linear(seed, I, H, lead=(E,))
+    up = synth.quant_linear(seed + 1, I, H, lead=(E,))
+    down = synth.quant_linear(seed + 2, H, I, lead=(E,))
+    return [(q.w, q.s, q.b) for q in (gate, up, down)]
+
+
+def moe_f64(oracle, x, stacks, idx, scores):
+    """float64 brute force of qwen/moe.go:501-511 over exactly dequantized stacks:
+    out[t] = sum_k score[t,k] * Wd[e] (silu(Wg[e] x_t) * (Wu[e] x_t))."""
+    deq = [[oracle.dequantize(w[e], s[e], b[e], 64).astype(np.float64) for e in range(w.shape[0])]
+           for (w, s, b) in stacks]
+    x = np.asarray(x, np.float64)
+    out = np.zeros((x.shape[0], deq[2][0].shape[0]))
+    for t in range(x.shape[0]):
+        for k in range(idx.shape[1]):
+            e = idx[t, k]
+            g, u = deq[0][e] @ x[t], deq[1][e] @ x[t]
+            out[t] += scores[t, k] * (deq[2][e] @ (g / (1.0 + np.exp(-g)) * u))
+    return out
+
+
+@pytest.mark.parametrize("n_tok", [1, 3])
+def test_moe_apply_matches_float64(oracle, n_tok):
+    E, H, I, K = 6, 256, 128, 4
+    stacks = _moe_stacks(30, E, H, I)
+    _, x = synth.activations(31, (n_tok, H))
+    idx, sc = synth.route(32, n_tok, E, K)
+    out = oracle.moe_apply(x, *stacks, idx, sc)
+    ok, d, s = rel_ok(out, moe_f64(oracle, x, stacks, idx, sc), 1e-4)
+    assert ok, (d, s)
+
+
+def test_moe_apply_is_the_gather_composition(oracle):
+    """Bit-identical to composing the pinned gather the way moeApply does:
+    g, u with A = 1, h = SiLU(g)*u (cpu/cpu.go:327-329), d with A = K, then
+    fl32(fl32(sum_k d*score) / K) * K (cpu/cpu_ops.go:113-142)."""
+    E, H, I, K, n = 5, 256, 128, 3, 2
+    stacks = _moe_stacks(33, E, H, I)
+    _, x = synth.activations(34, (n, H))
+    idx, sc = synth.route(35, n, E, K)
+    (wg, sg, bg), (wu, su, bu), (wd, sd, bd) = stacks
+    g = oracle.gather_quant_matmul(x[:, None, None, :], wg, sg, bg, idx, 64)
+    u = oracle.gather_quant_matmul(x[:, None, None, :], wu, su, bu, idx, 64)
+    e = np.exp(-g.astype(np.float64)).astype(np.float32)
+    h = ((g / (np.float32(1) + e)).astype(np.float32) * u).astype(np.float32)
+    d = oracle.gather_quant_matmul(h, wd, sd, bd, idx, 64)[:, :, 0, :]
+    acc = np.zeros((n, H), np.float32)
+    for k in range(K):
+        acc = (acc + (d[:, k, :] * sc[:, k, None]).astype(np.float32)).astype(np.float32)
+    want = ((acc / np.float32(K)).astype(np.float32) * np.float32(K)).astype(np.float32)
+    assert np.array_equal(oracle.moe_apply(x, *stacks, idx, sc), want)
+
+
+def test_moe_f64_catches_swapped_scores(oracle):
+    """The float64 check fails on a planted mistake: each slot weighted by its
+    neighbour's score."""
+    E, H, I, K = 6, 256, 128, 4
+    stacks = _moe_stacks(36, E, H, I)
+    _, x = synth.activations(37, (1, H))
+    idx, sc = synth.route(38, 1, E, K)
+    out = oracle.moe_apply(x, *stacks, idx, sc[:, ::-1].copy())
+    ok, _, _ = rel_ok(out, moe_f64(oracle, x, stacks, idx, sc), 1e-3)
+    assert not ok
+
+
+def test_moe_apply_rejects_out_of_range_index(oracle):
+    stacks = _moe_stacks(39, 2, 256, 128)
+    with pytest.raises(IndexError):
+        oracle.moe_apply(np.zeros((1, 256), np.float32), *stacks, np.array([[0, 2]], np.int32),
+                         np.ones((1, 2), np.float32))
+
+
 # -- router helpers ------------------------------------------------------------
 
 def test_topk_selection_sort_ties(oracle):
