@@ -59,6 +59,28 @@ __device__ __forceinline__ float widen_sb(uint32_t bits) {
         return bf16_to_f32((uint16_t)bits);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// One packed word -> 8 bf16 weights fl32(q*s + b) rounded to nearest even, in
+// word order (q0 = lowest nibble): 3 masks, 8 v_cvt_f32_ubyteN, 8 FMAs and 4
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ bf16x8_t dequant_word(uint32_t word, float sc, float bi) {
+    uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
+    // An empty asm hides where lo and hi came from, so the byte extractions
+    // below stay single v_cvt_f32_ubyteN instead of being re-derived as
+    // per-nibble shifts and masks of `word`.
+    asm("" : "+v"(lo), "+v"(hi));
+    uint32_t o[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const f32x2_t f = {fmaf((float)((lo >> (8 * p)) & 0xFFu), sc, bi),
+                           fmaf((float)((hi >> (8 * p)) & 0xFFu), sc, bi)};
+        o[p] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+    }
+    return __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
 // One K step of one thread's staging work, held in registers between the
 // global loads and the LDS stores. X: the tile's 256 rows x 8 chunks of 16 bytes
 // are numbered c = 8 * row + chunk and thread t loads chunks t, t + 512, ...,
@@ -129,20 +151,10 @@ __device__ __forceinline__ void store_x(const Stage<XF32>& st, uint8_t* buf, int
 }
 
 // Word j (0 or 1) of the thread's W quarter, dequantized to 8 bf16 in LDS.
-// Even codes (0,2,4,6) sit one per byte of lo, odd codes (1,3,5,7) of hi;
-// v_cvt_f32_ubyte0..3 widen them without shifts.
 __device__ __forceinline__ void store_w(uint32_t word, float sc, float bi, uint8_t* buf, int tid, int j) {
     uint8_t* ws = buf + BM * ROW_BYTES;
-    const uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
-    uint32_t o[4];
-#pragma unroll
-    for (int bsel = 0; bsel < 4; bsel++) {
-        const float qe = (float)((lo >> (8 * bsel)) & 0xFFu);
-        const float qo = (float)((hi >> (8 * bsel)) & 0xFFu);
-        o[bsel] = (uint32_t)f32_to_bf16_hw(fmaf(qe, sc, bi)) | ((uint32_t)f32_to_bf16_hw(fmaf(qo, sc, bi)) << 16);
-    }
     const int row = tid >> 2, chunk = 2 * (tid & 3) + j;
-    *reinterpret_cast<uint4*>(ws + swz(row, chunk)) = make_uint4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<bf16x8_t*>(ws + swz(row, chunk)) = dequant_word(word, sc, bi);
 }
 
 template <bool XF32, int SBT>
@@ -279,20 +291,321 @@ int log2_exact(int v) {
     return ((1 << l) == v) ? l : -1;
 }
 
+// ---- W-in-registers tile ---------------------------------------------------------
+//
+// Lane l of v_mfma_f32_32x32x16_bf16 supplies B[k = 8*(l/32) .. +8][j = l % 32]:
+// eight consecutive k of one weight row, i.e. exactly one packed word. So W
+// never goes through LDS: each wave loads its columns' words straight into
+// registers and dequantizes them into B fragments just before the MFMAs that
+// use them; only X is staged in LDS, shared by every wave of the block.
+//
+// K is walked in super-steps of 256 (four 64-wide steps). Inside a super-step
+// the K order is permuted identically on both operands so that every lane's
+// weights are one contiguous 64-byte run of its row: lane half h holds words
+// 16h .. 16h+15 of the row's 128-byte super-step segment, and MFMA k16 step s of
+// step t uses word 16h + 4t + s, i.e. actual k = 128h + 32t + 8s .. +8. The X tile
+// of step t therefore holds, per row, the k runs [32t, 32t+32) and
+// [128+32t, 128+32t+32) as logical 16-byte chunks 0-3 and 4-7, and lane half h
+// reads chunk 4h + s. A lane's scales and biases for a super-step are
+// 128/group_size consecutive groups, fetched with one load each.
+//
+// Each wave owns a 128 x (32*WNF) block of Y (4 x WNF MFMA tiles), so every
+// dequantized weight feeds 128 rows of X.
+constexpr int RBM = 128;                    // rows of X per block (and per wave)
+constexpr int RXT = RBM * ROW_BYTES;        // 16 KiB X tile per K step
+
+// Scales/biases of one lane for one super-step of SUP: the lane's K half spans
+// SUP/2 elements, i.e. NG groups (at least one).
+template <int SBT, int GSL, int SUP>
+struct SbRegs {
+    static constexpr int NG = ((SUP / 2) >> GSL) > 0 ? ((SUP / 2) >> GSL) : 1;
+    static constexpr int BYTES = NG * (SBT == 2 ? 4 : 2);
+    static constexpr int WORDS = BYTES >= 4 ? BYTES / 4 : 1;
+    uint32_t s[WORDS], b[WORDS];
+};
+
+template <int SBT, int GSL, int SUP>
+__device__ __forceinline__ void load_sb_run(SbRegs<SBT, GSL, SUP>& r, __amdgpu_buffer_rsrc_t rs,
+                                            __amdgpu_buffer_rsrc_t rb, uint32_t off) {
+    using R = SbRegs<SBT, GSL, SUP>;
+    if constexpr (R::BYTES == 2) {
+        r.s[0] = buf_load2(rs, off);
+        r.b[0] = buf_load2(rb, off);
+    } else if constexpr (R::BYTES == 4) {
+        r.s[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+        r.b[0] = __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0);
+    } else if constexpr (R::BYTES == 8) {
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const u32x2_t a = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+        const u32x2_t c = __builtin_amdgcn_raw_buffer_load_b64(rb, off, 0, 0);
+        r.s[0] = a.x, r.s[1] = a.y, r.b[0] = c.x, r.b[1] = c.y;
+    } else {
+        const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+        const u32x4_t c = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0);
+        r.s[0] = a.x, r.s[1] = a.y, r.s[2] = a.z, r.s[3] = a.w;
+        r.b[0] = c.x, r.b[1] = c.y, r.b[2] = c.z, r.b[3] = c.w;
+    }
+}
+
+// Group element e of a lane's run as fp32.
+template <int SBT, int GSL>
+__device__ __forceinline__ float sb_elem(const uint32_t* words, int e) {
+    if constexpr (SBT == 2) return __uint_as_float(words[e]);
+    const uint32_t w = words[e >> 1];
+    const uint16_t h16 = (e & 1) ? (uint16_t)(w >> 16) : (uint16_t)w;
+    return SBT == 1 ? f16_to_f32(h16) : bf16_to_f32(h16);
+}
+
+template <int WNF, int SBT, int GSL, int SUP>
+struct WRegs {
+    uint4 w[WNF][SUP / 64];     // SUP/16 words of column j for this lane's K half
+    SbRegs<SBT, GSL, SUP> sb[WNF];
+};
+
+// Physical 16-byte chunk of logical chunk c in row r of an X tile.
+__device__ __forceinline__ uint32_t xswz(int r, int c) { return r * ROW_BYTES + ((c ^ ((r >> 1) & 7)) << 4); }
+
+template <bool SPLIT, bool XF32, int SBT, int GSL, int NW, int WNF, int SUP>
+__global__ __launch_bounds__(64 * NW, 2) void qmm_wreg_kernel(
+    const uint32_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ B,
+    const void* __restrict__ X, void* __restrict__ Y, int y_dt, uint32_t M, uint32_t N, uint32_t K,
+    uint32_t k_per_split, float* __restrict__ acc_out) {
+    constexpr int NTH = 64 * NW;
+    constexpr int RBN = 32 * WNF * NW;
+    constexpr int XCH = RBM * 8 / NTH;  // 16-byte X chunks per thread per step
+    constexpr int XL = XCH * (XF32 ? 2 : 1);
+    constexpr uint32_t SBB = SBT == 2 ? 4 : 2;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * RXT];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, c32 = lane & 31;
+    const uint32_t m0 = blockIdx.y * RBM, n0 = blockIdx.x * RBN + wave * 32 * WNF;
+    const uint32_t P = K >> 3, G = K >> GSL;
+    const auto rx = make_rsrc(X, M * K * (XF32 ? 4 : 2));
+    const auto rw = make_rsrc(W, N * P * 4);
+    const auto rs = make_rsrc(S, N * G * SBB);
+    const auto rb = make_rsrc(B, N * G * SBB);
+    const uint32_t kb = blockIdx.z * k_per_split;
+    const uint32_t ke = min(K, kb + k_per_split);
+    constexpr int SPS = SUP / 64;  // 64-wide steps per super-step
+    const int nsup = kb < ke ? (int)((ke - kb) / SUP) : 0;  // super-steps
+    const int nsteps = SPS * nsup;
+
+    floatx16 acc[4][WNF];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < WNF; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    // Super-steps past the last are clamped to it: their loads are repeats, so
+    // the pipeline needs no branches.
+    auto ksup = [&](int sup) { return kb + (uint32_t)min(sup, nsup - 1) * SUP; };
+    auto load_w = [&](WRegs<WNF, SBT, GSL, SUP>& wr, int sup) {
+        const uint32_t k0 = ksup(sup);
+        const uint32_t g0 = (k0 + (SUP / 2) * h) >> GSL;
+#pragma unroll
+        for (int j = 0; j < WNF; j++) {
+            const uint32_t n = n0 + 32 * j + c32;
+            const uint32_t off = (n * P + (k0 >> 3) + (SUP / 16) * h) * 4;
+#pragma unroll
+            for (int q = 0; q < SPS; q++) wr.w[j][q] = buf_load16_nt(rw, off + 16 * q);
+            load_sb_run<SBT, GSL, SUP>(wr.sb[j], rs, rb, (n * G + g0) * SBB);
+        }
+    };
+    struct XRegs {
+        uint4 v[XL];
+    };
+    // X of step `step` (super-step step/SPS, t = step%SPS): logical chunk c of
+    // row r holds k = (SUP/2)*(c/4) + 32t + 8*(c%4) .. +8 of the super-step.
+    auto load_x = [&](XRegs& xr, int step) {
+        const uint32_t k0 = ksup(step / SPS) + 32 * (step % SPS);
+#pragma unroll
+        for (int q = 0; q < XCH; q++) {
+            const uint32_t c = NTH * q + tid;
+            const uint32_t kc = k0 + (SUP / 2) * ((c >> 2) & 1) + 8 * (c & 3);
+            const uint32_t off = ((m0 + (c >> 3)) * K + kc) * (XF32 ? 4 : 2);
+            if constexpr (XF32) {
+                const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+                const u32x4_t b = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16, 0, 0);
+                xr.v[2 * q] = make_uint4(a.x, a.y, a.z, a.w);
+                xr.v[2 * q + 1] = make_uint4(b.x, b.y, b.z, b.w);
+            } else {
+                const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+                xr.v[q] = make_uint4(v.x, v.y, v.z, v.w);
+            }
+        }
+    };
+    auto store_xq = [&](const XRegs& xr, uint8_t* buf, int q) {
+        const int c = NTH * q + tid;
+        uint4 v;
+        if constexpr (XF32) {
+            const uint4 a = xr.v[2 * q], b = xr.v[2 * q + 1];
+            v = make_uint4(pack_bf16x2(__uint_as_float(a.x), __uint_as_float(a.y)),
+                           pack_bf16x2(__uint_as_float(a.z), __uint_as_float(a.w)),
+                           pack_bf16x2(__uint_as_float(b.x), __uint_as_float(b.y)),
+                           pack_bf16x2(__uint_as_float(b.z), __uint_as_float(b.w)));
+        } else {
+            v = xr.v[q];
+        }
+        *reinterpret_cast<uint4*>(buf + xswz(c >> 3, c & 7)) = v;
+    };
+
+    // Step t of a super-step: X from LDS `xs`, W words 4t..4t+3 of `wr`; the X
+    // chunks of the next step (in xr) are stored into `xn` between the MFMAs.
+    // The A fragments and B fragments of k16 step s+1 are produced while the
+    // MFMAs of step s run.
+    auto compute = [&](const uint8_t* xs, const WRegs<WNF, SBT, GSL, SUP>& wr, int t, const XRegs& xr,
+                       uint8_t* xn, bool live) {
+        float sc[WNF], bi[WNF];
+#pragma unroll
+        for (int j = 0; j < WNF; j++) {
+            const int e = (32 * t) >> GSL;  // group of this step inside the lane's run
+            sc[j] = sb_elem<SBT, GSL>(wr.sb[j].s, e);
+            bi[j] = sb_elem<SBT, GSL>(wr.sb[j].b, e);
+        }
+        bf16x8_t a[2][4], bq[2][WNF];
+        auto read_a = [&](int s, int buf) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                a[buf][i] = *reinterpret_cast<const bf16x8_t*>(xs + xswz(32 * i + c32, 4 * h + s));
+        };
+        auto deq = [&](int s, int buf) {
+#pragma unroll
+            for (int j = 0; j < WNF; j++) {
+                const uint4 q4 = wr.w[j][t];
+                const uint32_t word = s == 0 ? q4.x : s == 1 ? q4.y : s == 2 ? q4.z : q4.w;
+                bq[buf][j] = dequant_word(word, sc[j], bi[j]);
+            }
+        };
+        read_a(0, 0);
+        deq(0, 0);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            if (s < 3) {
+                read_a(s + 1, (s + 1) & 1);
+                deq(s + 1, (s + 1) & 1);
+            }
+            if (live) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < WNF; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s & 1][i], bq[s & 1][j], acc[i][j], 0, 0, 0);
+            }
+            if (s < XCH) store_xq(xr, xn, s);
+        }
+#pragma unroll
+        for (int q = 4; q < XCH; q++) store_xq(xr, xn, q);
+    };
+
+    // W: two super-step slots (the next super-step's runs load during the
+    // current one). X: two register sets, about one and a half steps ahead, and
+    // two LDS buffers (step t+1 is stored during step t).
+    WRegs<WNF, SBT, GSL, SUP> wa, wb;
+    XRegs xa, xb;
+    if (nsteps > 0) {
+        load_x(xa, 0);
+        load_w(wa, 0);
+        load_x(xb, 1);
+#pragma unroll
+        for (int q = 0; q < XCH; q++) store_xq(xa, lds, q);
+        load_x(xa, 2);
+    }
+    __syncthreads();
+    // top of step t: LDS[t % 2] holds X of step t; X of steps t+1 and t+2 are in
+    // the register sets (t+1) % 2 and t % 2.
+    auto step = [&](int t, WRegs<WNF, SBT, GSL, SUP>& wcur, XRegs& xnext, uint8_t* lcur, uint8_t* lnext) {
+        compute(lcur, wcur, t % SPS, xnext, lnext, t < nsteps);
+        load_x(xnext, t + 3);
+        __syncthreads();
+    };
+    // Unrolled over two super-steps (the W slots) with no early exit: an exit
+    // per step would keep one copy of the accumulators live per exit. Steps past
+    // the end skip their MFMAs. SPS is even, so step parity (LDS buffer and X
+    // register set) is static.
+    for (int t = 0; t < nsteps; t += 2 * SPS) {
+        load_w(wb, t / SPS + 1);
+#pragma unroll
+        for (int u = 0; u < SPS; u += 2) {
+            step(t + u, wa, xb, lds, lds + RXT);
+            step(t + u + 1, wa, xa, lds + RXT, lds);
+        }
+        load_w(wa, t / SPS + 2);
+#pragma unroll
+        for (int u = 0; u < SPS; u += 2) {
+            step(t + SPS + u, wb, xb, lds, lds + RXT);
+            step(t + SPS + u + 1, wb, xa, lds + RXT, lds);
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < WNF; j++) {
+            const uint32_t n = n0 + 32 * j + c32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m < M && n < N) {
+                    if constexpr (SPLIT)
+                        atomicAdd(acc_out + (size_t)m * N + n, acc[i][j][r]);
+                    else
+                        store_y(Y, (int64_t)m * N + n, acc[i][j][r], y_dt);
+                }
+            }
+        }
+}
+
 }  // namespace
 
 Status launch_generic(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y,
                       int y_dtype, int num_cus, hipStream_t st);
 
-constexpr int kBM = BM, kBN = BN;  // tile used by the launcher
+constexpr int kBM = BM, kBN = BN;  // the LDS tile
 
-int64_t qmm_split(const QuantMatrix& m, int64_t rows, int num_cus) {
+// How one prefill product is launched. K divisible by 256 takes the W-in-
+// registers tile: 8 waves (128 x 256 of Y per block, one block per CU) when that
+// already gives every CU a block, else 4 waves (128 x 128, two blocks per CU)
+// with K split until the grid covers the CUs' block slots (at most 8 ways).
+// Other K (multiples of 64) take the LDS tile. Measured on MI355X for the
+// Qwen3-8B MLP shapes at M = 128, 512 and 2048.
+struct QmmPlan {
+    bool wreg;
+    int nw;
+    int64_t split;
+    uint32_t k_per_split;
+    dim3 grid;
+};
+
+QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus) {
+    QmmPlan p{};
+    const int64_t mt = (rows + RBM - 1) / RBM;
+    if (m.in % 256 == 0) {
+        p.wreg = true;
+        const int64_t tiles8 = ((m.rows + 255) / 256) * mt;
+        p.nw = tiles8 >= num_cus ? 8 : 4;
+        const int64_t rbn = 32 * p.nw;
+        const int64_t tiles = ((m.rows + rbn - 1) / rbn) * mt;
+        const int64_t slots = (int64_t)num_cus * (p.nw == 8 ? 1 : 2);
+        const int64_t nsup = m.in / 256;
+        p.split = 1;
+        while (p.split < 8 && tiles * p.split * 2 <= slots && nsup / (p.split * 2) >= 2) p.split *= 2;
+        p.k_per_split = (uint32_t)(((nsup + p.split - 1) / p.split) * 256);
+        p.grid = dim3((unsigned)((m.rows + rbn - 1) / rbn), (unsigned)mt, (unsigned)p.split);
+        return p;
+    }
+    p.wreg = false;
+    p.nw = NT / 64;
     const int64_t tiles = ((m.rows + kBN - 1) / kBN) * ((rows + kBM - 1) / kBM);
     const int64_t ksteps = m.in / BK;
-    int64_t split = 1;
+    p.split = 1;
     // aim for two tiles per CU, keep at least 8 K steps per split
-    while (tiles * split < 2 * num_cus && ksteps / (split * 2) >= 8) split *= 2;
-    return split;
+    while (tiles * p.split < 2 * num_cus && ksteps / (p.split * 2) >= 8) p.split *= 2;
+    p.k_per_split = (uint32_t)(((ksteps + p.split - 1) / p.split) * BK);
+    p.grid = dim3((unsigned)((m.rows + kBN - 1) / kBN), (unsigned)((rows + kBM - 1) / kBM), (unsigned)p.split);
+    return p;
 }
 
 bool qmm_uses_mfma(const QuantMatrix& m, int64_t rows, int x_dtype) {
@@ -303,8 +616,29 @@ bool qmm_uses_mfma(const QuantMatrix& m, int64_t rows, int x_dtype) {
 }
 
 size_t qmm_workspace_bytes(const QuantMatrix& m, int64_t rows, int x_dtype, int y_dtype, int num_cus) {
-    if (!qmm_uses_mfma(m, rows, x_dtype) || qmm_split(m, rows, num_cus) == 1 || y_dtype == JH_F32) return 0;
+    if (!qmm_uses_mfma(m, rows, x_dtype) || qmm_plan(m, rows, num_cus).split == 1 || y_dtype == JH_F32) return 0;
     return sizeof(float) * (size_t)(rows * m.rows);
+}
+
+template <int NW, int WNF, int SUP, bool SPLIT, bool XF32>
+void launch_tile_wreg(const QuantMatrix& m, const void* x, int64_t rows, void* y, int y_dtype, int gl,
+                      uint32_t k_per_split, float* acc, dim3 grid, hipStream_t st) {
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(64 * NW), 0, st, m.w, m.scales, m.biases, x, y, y_dtype,
+                           (uint32_t)rows, (uint32_t)m.rows, (uint32_t)m.in, k_per_split, acc);
+    };
+    auto by_gs = [&](auto sbt) {
+        constexpr int SBT = decltype(sbt)::value;
+        if (gl == 5) go(qmm_wreg_kernel<SPLIT, XF32, SBT, 5, NW, WNF, SUP>);
+        else if (gl == 6) go(qmm_wreg_kernel<SPLIT, XF32, SBT, 6, NW, WNF, SUP>);
+        else go(qmm_wreg_kernel<SPLIT, XF32, SBT, 7, NW, WNF, SUP>);
+    };
+    if (m.sb_dtype == JH_F32)
+        by_gs(std::integral_constant<int, 2>{});
+    else if (m.sb_dtype == JH_F16)
+        by_gs(std::integral_constant<int, 1>{});
+    else
+        by_gs(std::integral_constant<int, 0>{});
 }
 
 template <bool SPLIT, bool XF32>
@@ -326,16 +660,25 @@ Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows
                   int y_dtype, int num_cus, hipStream_t st, void* workspace) {
     if (!qmm_uses_mfma(m, rows, x_dtype)) return launch_generic(m, x, x_dtype, rows, y, y_dtype, num_cus, st);
     const int gl = log2_exact(m.group_size);
-    const int64_t split = qmm_split(m, rows, num_cus);
-    const int64_t ksteps = m.in / BK;
-    const uint32_t k_per_split = (uint32_t)(((ksteps + split - 1) / split) * BK);
-    const dim3 grid((unsigned)((m.rows + kBN - 1) / kBN), (unsigned)((rows + kBM - 1) / kBM), (unsigned)split);
+    const QmmPlan p = qmm_plan(m, rows, num_cus);
     const bool xf32 = x_dtype == JH_F32;
-    if (split == 1) {
-        if (xf32)
-            launch_tile<false, true>(m, x, rows, y, y_dtype, gl, k_per_split, nullptr, grid, st);
-        else
-            launch_tile<false, false>(m, x, rows, y, y_dtype, gl, k_per_split, nullptr, grid, st);
+    auto tile = [&](auto split_c, float* acc) {
+        constexpr bool SPLIT = decltype(split_c)::value;
+        if (p.wreg) {
+            if (p.nw == 8) {
+                if (xf32) launch_tile_wreg<8, 1, 256, SPLIT, true>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+                else launch_tile_wreg<8, 1, 256, SPLIT, false>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+            } else {
+                if (xf32) launch_tile_wreg<4, 1, 256, SPLIT, true>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+                else launch_tile_wreg<4, 1, 256, SPLIT, false>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+            }
+        } else {
+            if (xf32) launch_tile<SPLIT, true>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+            else launch_tile<SPLIT, false>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+        }
+    };
+    if (p.split == 1) {
+        tile(std::false_type{}, nullptr);
         return Status::ok();
     }
     // split K: fp32 partial tiles meet by atomic adds (in y itself when y is fp32)
@@ -344,10 +687,7 @@ Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows
     const int64_t n = rows * m.rows;
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256),
                        0, st, acc, n);
-    if (xf32)
-        launch_tile<true, true>(m, x, rows, y, y_dtype, gl, k_per_split, acc, grid, st);
-    else
-        launch_tile<true, false>(m, x, rows, y, y_dtype, gl, k_per_split, acc, grid, st);
+    tile(std::true_type{}, acc);
     if (y_dtype != JH_F32)
         hipLaunchKernelGGL(f32_to_y_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)),
                            dim3(256), 0, st, acc, y, y_dtype, n);
