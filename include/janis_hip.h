@@ -114,9 +114,10 @@ JH_API int jh_d2h(jh_ctx *ctx, void *dst_host, const void *src_device, size_t by
  *   scales  [rows, in_features / group_size] of sb_dtype (JH_BF16, JH_F16 or JH_F32);
  *   biases  same shape and dtype as scales;
  * and element (r, j) is  scale * code + bias  with the group's scale and bias.
- * Supported here: bits == 4 (other widths return JH_ERR_UNSUPPORTED) and any
- * group_size that divides in_features; group sizes 32, 64 and 128 with bf16
- * activations take the fast kernels, the rest a slower generic kernel.
+ * Supported here: bits 2, 4 and 8 (32/bits codes per word; other widths return
+ * JH_ERR_UNSUPPORTED) and any group_size that divides in_features. 4-bit weights
+ * with group sizes 32, 64 and 128 and bf16 activations take the fast kernels;
+ * everything else a slower generic kernel.
  * w, x and y must be 16-byte aligned (jh_alloc gives 256). */
 
 /* Backend.Dequantize (engine/backend.go:261-263; cpu/cpu_misc.go:134-161):

@@ -35,7 +35,7 @@ namespace jh {
 __global__ __launch_bounds__(256) void qmv_generic_kernel(
     const uint32_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ B,
     int sb_dt, const void* __restrict__ X, int x_dt, void* __restrict__ Y, int y_dt, int64_t N,
-    int64_t K, int gs, int64_t M, const int* __restrict__ ws, int64_t n_experts,
+    int64_t K, int gs, int bits, int64_t M, const int* __restrict__ ws, int64_t n_experts,
     int64_t k_slots, int64_t a_vectors);
 
 namespace {
@@ -432,7 +432,7 @@ bool fast_tile_exists(int64_t P) {
 // 32..128, 16-bit scales, byte offsets inside one expert below 2^31.
 bool fast_ok(const QuantMatrix& m, int x_dtype) {
     const int gl = log2_exact(m.group_size);
-    return x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0 &&
+    return m.bits == 4 && x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0 &&
            (m.sb_dtype == JH_BF16 || m.sb_dtype == JH_F16) &&
            (m.rows + 64) * (m.in / 2) < ((int64_t)1 << 31) && fast_tile_exists(m.in / 8);
 }
@@ -488,7 +488,7 @@ Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st) {
     if (blocks > cap) blocks = cap;
     hipLaunchKernelGGL(qmv_generic_kernel, dim3((unsigned)blocks, (unsigned)max_u), dim3(256), 0, st,
                        a.m.w, a.m.scales, a.m.biases, a.m.sb_dtype, a.x, a.x_dtype, a.y, a.y_dtype,
-                       a.m.rows, a.m.in, a.m.group_size, (int64_t)0,
+                       a.m.rows, a.m.in, a.m.group_size, a.m.bits, (int64_t)0,
                        static_cast<const int*>(a.workspace), a.n_experts, a.k_slots, a.a_vectors);
     return Status::ok();
 }

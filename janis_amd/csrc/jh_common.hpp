@@ -117,6 +117,7 @@ struct QuantMatrix {
     int64_t rows;        // out_features
     int64_t in;          // in_features (K)
     int group_size;
+    int bits = 4;        // 2, 4 or 8: 32/bits codes per word
 };
 
 struct Status {

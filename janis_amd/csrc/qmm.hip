@@ -611,7 +611,7 @@ QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus) {
 bool qmm_uses_mfma(const QuantMatrix& m, int64_t rows, int x_dtype) {
     const int gl = log2_exact(m.group_size);
     const int64_t xb = x_dtype == JH_F32 ? 4 : 2;
-    return gl >= 5 && gl <= 7 && (m.in % BK) == 0 && (m.in % m.group_size) == 0 &&
+    return m.bits == 4 && gl >= 5 && gl <= 7 && (m.in % BK) == 0 && (m.in % m.group_size) == 0 &&
            (m.rows + 256) * (m.in / 2) < ((int64_t)1 << 31) && (rows + 512) * m.in * xb < ((int64_t)1 << 31);
 }
 

@@ -241,10 +241,12 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
 __global__ __launch_bounds__(256) void qmv_generic_kernel(
     const uint32_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ B,
     int sb_dt, const void* __restrict__ X, int x_dt, void* __restrict__ Y, int y_dt, int64_t N,
-    int64_t K, int gs, int64_t M, const int* __restrict__ ws, int64_t n_experts,
+    int64_t K, int gs, int bits, int64_t M, const int* __restrict__ ws, int64_t n_experts,
     int64_t k_slots, int64_t a_vectors) {
     const int lane = threadIdx.x & 63;
-    const int64_t P = K >> 3, G = K / gs;
+    const int vpw = 32 / bits;
+    const uint32_t mask = (1u << bits) - 1u;
+    const int64_t P = K / vpw, G = K / gs;
     int64_t e = 0, p_begin = 0, p_end = M;
     const int* pairs = nullptr;
     if (ws) {
@@ -273,13 +275,12 @@ __global__ __launch_bounds__(256) void qmv_generic_kernel(
             float part = 0.0f;
             for (int64_t p = lane; p < P; p += 64) {
                 const uint32_t word = We[row * P + p];
-#pragma unroll
-                for (int l = 0; l < 8; l++) {
-                    const int64_t j = 8 * p + l;
+                for (int l = 0; l < vpw; l++) {
+                    const int64_t j = vpw * p + l;
                     const int64_t g = j / gs;
                     const float s = load_sb(S, sb0 + row * G + g, sb_dt);
                     const float b = load_sb(B, sb0 + row * G + g, sb_dt);
-                    const float w = fmaf((float)((word >> (4 * l)) & 0xFu), s, b);
+                    const float w = fmaf((float)((word >> (bits * l)) & mask), s, b);
                     const float xv = (x_dt == JH_BF16)
                                          ? bf16_to_f32(static_cast<const uint16_t*>(X)[xrow * K + j])
                                          : static_cast<const float*>(X)[xrow * K + j];
@@ -343,7 +344,7 @@ Status launch_generic(const QuantMatrix& m, const void* x, int x_dtype, int64_t 
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(qmv_generic_kernel, dim3((unsigned)blocks, 1), dim3(256), 0, st, m.w,
                        m.scales, m.biases, m.sb_dtype, x, x_dtype, y, y_dtype, m.rows, m.in,
-                       m.group_size, rows, nullptr, (int64_t)1, (int64_t)1, (int64_t)1);
+                       m.group_size, m.bits, rows, nullptr, (int64_t)1, (int64_t)1, (int64_t)1);
     return Status::ok();
 }
 
@@ -351,7 +352,7 @@ Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int
                   int num_cus, hipStream_t st) {
     const int gl = log2_exact(m.group_size);
     const int64_t P = m.in / 8;
-    const bool fast_ok = x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0 &&
+    const bool fast_ok = m.bits == 4 && x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0 &&
                          (m.sb_dtype == JH_BF16 || m.sb_dtype == JH_F16) &&
                          (m.rows + 64) * (m.in / 2) < ((int64_t)1 << 31);
     if (fast_ok) {

@@ -76,17 +76,18 @@ int ensure_workspace(jh_ctx* c, size_t need, const char* op) {
 
 int check_quant(jh_ctx* c, const char* op, const uint32_t* w, const void* s, const void* b,
                 int sb_dtype, int64_t rows, int64_t in, int group_size, int bits) {
-    if (bits != 4)
+    if (bits != 2 && bits != 4 && bits != 8)
         return fail(c, JH_ERR_UNSUPPORTED,
-                    std::string(op) + ": only 4-bit weights are implemented (bits=" +
+                    std::string(op) + ": bits must be 2, 4 or 8 (32/bits codes per word; bits=" +
                         std::to_string(bits) + ")");
     if (sb_dtype != JH_BF16 && sb_dtype != JH_F16 && sb_dtype != JH_F32)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": scales/biases must be bf16, f16 or f32");
     if (rows < 0 || in <= 0)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape");
-    if (in % 8 != 0)
+    if (in % (32 / bits) != 0)
         return fail(c, JH_ERR_INVALID,
-                    std::string(op) + ": in_features must be a multiple of 8 for 4-bit words");
+                    std::string(op) + ": in_features must be a multiple of " + std::to_string(32 / bits) +
+                        " (codes per word)");
     if (group_size <= 0 || in % group_size != 0)
         return fail(c, JH_ERR_INVALID,
                     std::string(op) + ": group_size " + std::to_string(group_size) +
@@ -249,8 +250,8 @@ int jh_dequantize(jh_ctx* c, const uint32_t* w, const void* scales, const void* 
         return fail(c, JH_ERR_INVALID, "jh_dequantize: out_dtype must be f32 or bf16");
     if (rows == 0) return JH_OK;
     if (!out || !aligned16(out)) return fail(c, JH_ERR_INVALID, "jh_dequantize: out must be 16-byte aligned");
-    jh::QuantMatrix m{w, scales, biases, sb_dtype, rows, in_features, group_size};
-    return finish(c, jh::launch_dequantize(m, out, out_dtype, c->stream), "dequant4_kernel");
+    jh::QuantMatrix m{w, scales, biases, sb_dtype, rows, in_features, group_size, bits};
+    return finish(c, jh::launch_dequantize(m, out, out_dtype, c->stream), "dequant_kernel");
 }
 
 int jh_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, const uint32_t* w,
@@ -271,7 +272,7 @@ int jh_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, co
     if (rows == 0 || out_features == 0) return JH_OK;
     if (!x || !y || !aligned16(x) || !aligned16(y))
         return fail(c, JH_ERR_INVALID, "jh_quant_matmul: x and y must be non-null and 16-byte aligned");
-    jh::QuantMatrix m{w, scales, biases, sb_dtype, out_features, in_features, group_size};
+    jh::QuantMatrix m{w, scales, biases, sb_dtype, out_features, in_features, group_size, bits};
     if (rows == 1)
         return finish(c, jh::launch_qmv(m, x, x_dtype, y, y_dtype, c->num_cus, c->stream), "qmv");
     const size_t need = jh::qmm_workspace_bytes(m, rows, x_dtype, y_dtype, c->num_cus);
@@ -317,7 +318,7 @@ int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n
                                 std::to_string(n_experts) + ")");
     }
     jh::GatherArgs a;
-    a.m = jh::QuantMatrix{w, scales, biases, sb_dtype, out_features, in_features, group_size};
+    a.m = jh::QuantMatrix{w, scales, biases, sb_dtype, out_features, in_features, group_size, bits};
     a.n_experts = n_experts;
     a.x = x;
     a.x_dtype = x_dtype;
@@ -350,6 +351,7 @@ int jh_moe_swiglu(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n_tok, con
     if (int r = check_quant(c, op, w_down, s_down, b_down, sb_dtype, hidden, intermediate, group_size, bits))
         return r;
     if (x_dtype != JH_BF16) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": x must be bf16");
+    if (bits != 4) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": only 4-bit expert stacks are fused");
     if (int r = check_act_dtype(c, op, "out", out_dtype)) return r;
     if (n_tok < 0 || k_slots < 0 || n_experts <= 0 || intermediate <= 0)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": bad n_tok / k_slots / n_experts / intermediate");

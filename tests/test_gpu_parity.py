@@ -424,6 +424,78 @@ def test_moe_swiglu_out_of_range_and_unsupported(hip):
         hip.MoeSwiGLU(hip.FromBF16Bits(xb6, 2, 640), *_moe_upload(hip, q6), idx, sc, 64, 4)
 
 
+# -- other widths (2- and 8-bit: 32/bits codes per word) ----------------------------
+
+def _width_case(bits, N, K, gs, E=None, seed=0, sb_f32=False):
+    """Random packed words of `bits`-wide codes with bf16 (or f32) scales/biases."""
+    rng = np.random.default_rng(seed)
+    lead = () if E is None else (E,)
+    P = K * bits // 32
+    w = rng.integers(0, 2**32, lead + (N, P), dtype=np.uint64).astype(np.uint32)
+    s = (np.abs(rng.standard_normal(lead + (N, K // gs))) * 0.02).astype(np.float32)
+    b = (-(2 ** (bits - 1)) * s + rng.standard_normal(s.shape) * 1e-3).astype(np.float32)
+    if not sb_f32:
+        s = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(s))
+        b = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(b))
+    return w, s, b
+
+
+def _upload_width(hip, w, s, b, sb_f32=False):
+    if sb_f32:
+        return hip.FromRaw(U32, w, *w.shape), hip.FromFloats(s), hip.FromFloats(b)
+    return (hip.FromRaw(U32, w, *w.shape), hip.FromBF16Bits(synth.f32_to_bf16_bits(s)),
+            hip.FromBF16Bits(synth.f32_to_bf16_bits(b)))
+
+
+@pytest.mark.parametrize("bits,gs,sb_f32", [(8, 64, False), (8, 32, True), (2, 64, False), (2, 128, True)])
+def test_dequantize_other_widths_bit_exact(hip, oracle, bits, gs, sb_f32):
+    """cpu/cpu_misc.go:134-161 for any 32/bits codes per word, bit for bit."""
+    N, K = 48, 1024
+    w, s, b = _width_case(bits, N, K, gs, seed=bits * 100 + gs, sb_f32=sb_f32)
+    tw, ts, tb = _upload_width(hip, w, s, b, sb_f32)
+    step(f"jh_dequantize bits={bits} gs={gs} f32 scales={sb_f32}")
+    got = hip.Floats(hip.Dequantize(tw, ts, tb, gs, bits))
+    want = oracle.dequantize(w, s, b, gs, bits)
+    assert got.shape == (N, K)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    gotb = hip.Floats(hip.Dequantize(tw, ts, tb, gs, bits, out_dtype=BF16))
+    np.testing.assert_array_equal(gotb, synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(want)))
+
+
+@pytest.mark.parametrize("bits", [8, 2])
+@pytest.mark.parametrize("rows", [1, 5])
+def test_quant_matmul_other_widths(hip, oracle, bits, rows):
+    """Decode (rows = 1, cpu/cpu_misc.go:350-375) and prefill (rows > 1, the wbuf
+    path) at 2 and 8 bits, e.g. the 8-bit MoE router of mlx-community checkpoints
+    (qwen/config.go:57-60)."""
+    N, K, gs = 128, 2048, 64
+    w, s, b = _width_case(bits, N, K, gs, seed=7 * bits + rows)
+    tw, ts, tb = _upload_width(hip, w, s, b)
+    xb, x = synth.activations(40 + bits + rows, (rows, K))
+    step(f"jh_quant_matmul bits={bits} rows={rows}")
+    y = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, rows, K), tw, ts, tb, True, gs, bits, out_dtype=F32))
+    want = oracle.quant_matmul(x, w, s, b, gs, bits=bits)
+    ok, d, sc = rel_ok(y, want, F32_TOL)
+    assert ok, (d, sc)
+    yb = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, rows, K), tw, ts, tb, True, gs, bits))
+    ok, d, sc = rel_ok(yb, want, BF16_TOL)
+    assert ok, ("bf16 y", d, sc)
+
+
+def test_gather_8bit(hip, oracle):
+    E, N, K, gs, T, Kk = 5, 64, 512, 64, 3, 4
+    w, s, b = _width_case(8, N, K, gs, E=E, seed=99)
+    tw, ts, tb = _upload_width(hip, w, s, b)
+    idx = np.random.default_rng(98).integers(0, E, (T, Kk)).astype(np.int32)
+    xb, x = synth.activations(97, (T, 1, 1, K))
+    step("jh_gather_quant_matmul bits=8")
+    y = hip.Floats(hip.GatherQuantMatmul(hip.FromBF16Bits(xb, T, 1, 1, K), tw, ts, tb, hip.FromInt32(idx),
+                                         True, gs, 8, out_dtype=F32))
+    want = oracle.gather_quant_matmul(x, w, s, b, idx, gs, bits=8)
+    ok, d, sc = rel_ok(y, want, F32_TOL)
+    assert ok, (d, sc)
+
+
 # -- errors (the reference panics) ---------------------------------------------------
 
 def test_bad_arguments_raise(hip):
@@ -431,8 +503,8 @@ def test_bad_arguments_raise(hip):
     w, s, b = upload_quant(hip, q)
     xb, _ = synth.activations(1, (1, 256))
     x = hip.FromBF16Bits(xb, 1, 256)
-    with pytest.raises(JanisHipError):  # 8-bit not implemented
-        hip.QuantMatmul(x, w, s, b, True, 64, 8)
+    with pytest.raises(JanisHipError):  # 3-bit codes do not divide a word
+        hip.Dequantize(w, s, b, 64, 3)
     with pytest.raises(JanisHipError):  # transpose=false
         hip.QuantMatmul(x, w, s, b, False, 64, 4)
     with pytest.raises(JanisHipError):  # group does not divide K

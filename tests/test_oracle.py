@@ -207,6 +207,25 @@ def test_generic_width_path_8bit(oracle):
     assert np.array_equal(wd.astype(np.float32), (qs + b[:, g]).astype(np.float32))
 
 
+def test_generic_width_path_2bit(oracle):
+    rng = np.random.default_rng(4)
+    N, K, gs = 8, 512, 64
+    w = rng.integers(0, 2**32, (N, K // 16), dtype=np.uint64).astype(np.uint32)
+    s = (rng.random((N, K // gs), dtype=np.float32) * 0.01).astype(np.float32)
+    b = (-rng.random((N, K // gs), dtype=np.float32)).astype(np.float32)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    wd = oracle.dequantize(w, s, b, gs, 2).astype(np.float64)
+    codes = ((w[:, :, None] >> (2 * np.arange(16, dtype=np.uint32))) & 0x3).reshape(N, K)
+    g = np.arange(K) // gs
+    qs = (codes.astype(np.float32) * s[:, g]).astype(np.float32)
+    assert np.array_equal(wd.astype(np.float32), (qs + b[:, g]).astype(np.float32))
+    for rows in (1, 3):
+        xr = np.repeat(x, rows, 0)
+        y = oracle.quant_matmul(xr, w, s, b, gs, bits=2)
+        ok, d, sc = rel_ok(y, xr.astype(np.float64) @ wd.T, 1e-5)
+        assert ok, (rows, d, sc)
+
+
 # -- gather ------------------------------------------------------------------
 
 @pytest.mark.parametrize("n_lead,A", [(1, 1), (1, 8), (4, 1), (4, 8)])
