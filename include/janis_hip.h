@@ -157,6 +157,22 @@ JH_API int jh_gather_quant_matmul(jh_ctx *ctx, const void *x, jh_dtype x_dtype, 
                            int64_t k_slots, int transpose, int group_size, int bits, void *y,
                            jh_dtype y_dtype);
 
+/* The router of MoEBlock.Forward (qwen/moe.go:455-491) on the device, for a
+ * backend that offers it: per token, softmax over the n_experts logits
+ * (cpu/cpu.go:461-499), the k largest by the reference's selection sort
+ * (qwen/moe.go:420-444, ties as it breaks them), and with norm_topk != 0 the k
+ * scores divided by their sum (NormTopk, :472-481). The reference copies the
+ * probabilities to the host for this (the per-layer sync at :459); here the
+ * indices and scores stay on the device for jh_moe_swiglu or
+ * jh_gather_quant_matmul. Bit-identical to the CPU backend: the same fp32 order
+ * of operations and exp evaluated in double.
+ *   logits       [n_tok, n_experts] of logits_dtype (JH_F32 or JH_BF16), device
+ *   rhs_indices  int32 [n_tok, k] (global expert ids), device
+ *   scores       fp32 [n_tok, k], device
+ * n_experts up to 4096. */
+JH_API int jh_moe_route(jh_ctx *ctx, const void *logits, jh_dtype logits_dtype, int64_t n_tok,
+                 int64_t n_experts, int64_t k, int norm_topk, int32_t *rhs_indices, float *scores);
+
 /* The expert MLP of moeApply (qwen/moe.go:501-511) in one call, for a backend
  * that offers it (the engine's optional-capability pattern,
  * engine/backend.go:38-112). The reference composes it from three

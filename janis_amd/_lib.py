@@ -19,7 +19,7 @@ EXPORTS = [
     "jh_version", "jh_create", "jh_destroy", "jh_last_error", "jh_device_info",
     "jh_set_stream", "jh_get_stream", "jh_set_checks", "jh_sync", "jh_alloc", "jh_free",
     "jh_h2d", "jh_d2h", "jh_dequantize", "jh_quant_matmul", "jh_gather_quant_matmul",
-    "jh_moe_swiglu",
+    "jh_moe_route", "jh_moe_swiglu",
 ]
 
 _lib = None
@@ -78,6 +78,8 @@ def load() -> ctypes.CDLL:
     L.jh_gather_quant_matmul.argtypes = [c_ctx, p, i, i64, i64, p, p, p, i, i64, i64, i64, p,
                                          i64, i, i, i, p, i]
     L.jh_gather_quant_matmul.restype = i
+    L.jh_moe_route.argtypes = [c_ctx, p, i, i64, i64, i64, i, p, p]
+    L.jh_moe_route.restype = i
     L.jh_moe_swiglu.argtypes = [c_ctx, p, i, i64, p, p, p, p, p, p, p, p, p, i, i64, i64, i64,
                                 p, p, i64, i, i, p, i]
     L.jh_moe_swiglu.restype = i

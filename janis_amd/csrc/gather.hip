@@ -43,6 +43,7 @@ namespace {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 constexpr int kMaxExperts = 4096;
 constexpr int kFusedMaxPairs = 1024;
+constexpr int kMaxRouteExperts = 4096;
 enum { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_COMBINE = 2 };
 
 __device__ __forceinline__ void nan_row(void* Y, int y_dt, int64_t p, int64_t N, int tid, int nthreads) {
@@ -490,6 +491,91 @@ Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st) {
                        a.m.w, a.m.scales, a.m.biases, a.m.sb_dtype, a.x, a.x_dtype, a.y, a.y_dtype,
                        a.m.rows, a.m.in, a.m.group_size, a.m.bits, (int64_t)0,
                        static_cast<const int*>(a.workspace), a.n_experts, a.k_slots, a.a_vectors);
+    return Status::ok();
+}
+
+// ---- router: softmax over the experts, top-k, optional renormalisation ----------
+//
+// One wave per token, the arithmetic of the CPU backend step by step so that the
+// chosen experts and their scores are bit-identical to it: the row max; e_i =
+// fl32(exp(fl64(fl32(v_i - max)))) (cpu/cpu.go:461-499); the sum of the e_i in
+// index order by one lane; p_i = e_i / sum. Top-k is the reference's selection
+// sort (qwen/moe.go:420-444): pass i takes the first position j >= i (in the
+// current order array) holding the largest probability, then swaps order[i] and
+// order[j]. Each pass is a wave-wide argmax with ties going to the smaller j,
+// which is the strict '>' scan. Renormalisation divides by the in-order sum of
+// the k scores when it is positive (qwen/moe.go:472-481).
+__global__ __launch_bounds__(64) void moe_route_kernel(const void* __restrict__ logits, int l_dt, int E, int k,
+                                                       int norm, int32_t* __restrict__ idx_out,
+                                                       float* __restrict__ score_out) {
+    __shared__ float p[kMaxRouteExperts];
+    __shared__ int order[kMaxRouteExperts];
+    __shared__ float sum_s;
+    const int lane = threadIdx.x;
+    const int64_t t = blockIdx.x;
+    float mx = -__builtin_inff();
+    for (int i = lane; i < E; i += 64) {
+        const float v = l_dt == JH_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(logits)[t * E + i])
+                                        : static_cast<const float*>(logits)[t * E + i];
+        p[i] = v;
+        order[i] = i;
+        mx = fmaxf(mx, v);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    for (int i = lane; i < E; i += 64) p[i] = (float)exp((double)(p[i] - mx));
+    __syncthreads();
+    if (lane == 0) {
+        float s = 0.0f;
+        for (int i = 0; i < E; i++) s += p[i];
+        sum_s = s;
+    }
+    __syncthreads();
+    const float sum = sum_s;
+    for (int i = lane; i < E; i += 64) p[i] = p[i] / sum;
+    __syncthreads();
+    for (int it = 0; it < k; it++) {
+        float bv = -__builtin_inff();
+        int bj = E;
+        for (int j = it + lane; j < E; j += 64) {
+            const float v = p[order[j]];
+            if (v > bv) bv = v, bj = j;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oj = __shfl_xor(bj, o, 64);
+            if (ov > bv || (ov == bv && oj < bj)) bv = ov, bj = oj;
+        }
+        if (lane == 0 && bj < E) {
+            const int a = order[it];
+            order[it] = order[bj];
+            order[bj] = a;
+        }
+        __syncthreads();
+    }
+    if (lane == 0) {
+        float s = 0.0f;
+        for (int i = 0; i < k; i++) s += p[order[i]];
+        sum_s = s;
+    }
+    __syncthreads();
+    const float ks = sum_s;
+    for (int i = lane; i < k; i += 64) {
+        float v = p[order[i]];
+        if (norm && ks > 0.0f) v = v / ks;
+        idx_out[t * k + i] = order[i];
+        score_out[t * k + i] = v;
+    }
+}
+
+Status launch_moe_route(const void* logits, int l_dt, int64_t n_tok, int E, int k, bool norm, int32_t* idx,
+                        float* scores, hipStream_t st) {
+    if (n_tok == 0 || k == 0) return Status::ok();
+    if (E > kMaxRouteExperts) return Status::fail(JH_ERR_UNSUPPORTED, "moe_route: more than 4096 experts");
+    if (n_tok > 0x7fffffff) return Status::fail(JH_ERR_UNSUPPORTED, "moe_route: too many tokens");
+    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)n_tok), dim3(64), 0, st, logits, l_dt, E, k, norm ? 1 : 0,
+                       idx, scores);
     return Status::ok();
 }
 

@@ -168,6 +168,9 @@ struct MoeMlpArgs {
     void* out;                   // [n_tok, H]
     int out_dtype;
 };
+// Router: per token softmax over E logits, top-k, optional renormalisation.
+Status launch_moe_route(const void* logits, int l_dt, int64_t n_tok, int E, int k, bool norm, int32_t* idx,
+                        float* scores, hipStream_t st);
 // Why the fused kernels cannot take this call, or nullptr.
 const char* moe_unsupported(const MoeMlpArgs& a);
 size_t moe_workspace_bytes(const MoeMlpArgs& a);

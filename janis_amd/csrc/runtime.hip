@@ -336,6 +336,21 @@ int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n
     return finish(c, jh::launch_gather(a, c->num_cus, c->stream), "gather");
 }
 
+int jh_moe_route(jh_ctx* c, const void* logits, jh_dtype logits_dtype, int64_t n_tok, int64_t n_experts,
+                 int64_t k, int norm_topk, int32_t* rhs_indices, float* scores) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_moe_route";
+    if (int r = check_act_dtype(c, op, "logits", logits_dtype)) return r;
+    if (n_tok < 0 || n_experts <= 0 || k < 0 || k > n_experts)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": need n_tok >= 0 and 0 <= k <= n_experts");
+    if (n_tok == 0 || k == 0) return JH_OK;
+    if (!logits || !rhs_indices || !scores)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": null logits / indices / scores");
+    return finish(c, jh::launch_moe_route(logits, logits_dtype, n_tok, (int)n_experts, (int)k, norm_topk != 0,
+                                          rhs_indices, scores, c->stream),
+                  "moe_route");
+}
+
 int jh_moe_swiglu(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n_tok, const uint32_t* w_gate,
                   const void* s_gate, const void* b_gate, const uint32_t* w_up, const void* s_up,
                   const void* b_up, const uint32_t* w_down, const void* s_down, const void* b_down,

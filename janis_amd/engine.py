@@ -230,6 +230,19 @@ class HipBackend:
             groupSize, bits, y.ptr, y.dtype))
         return y
 
+    def MoeRoute(self, logits: Tensor, k: int, normTopk: bool = True) -> tuple:
+        """The router of MoEBlock.Forward (qwen/moe.go:455-491) on the device:
+        softmax over the last axis, top-k (selection-sort ties), optional
+        renormalisation. Returns (indices I32 [lead.., k], scores F32 [lead.., k])."""
+        E = logits.shape[-1]
+        n_tok = logits.numel // E if E else 0
+        lead = logits.shape[:-1]
+        idx = self.empty(I32, *lead, k)
+        sc = self.empty(F32, *lead, k)
+        check(self._ctx, self._L.jh_moe_route(self._ctx, logits.ptr, logits.dtype, n_tok, E, k,
+                                              int(bool(normTopk)), idx.ptr, sc.ptr))
+        return idx, sc
+
     def MoeSwiGLU(self, x: Tensor, gate: tuple, up: tuple, down: tuple, rhsIndices: Tensor,
                   scores: Tensor, groupSize: int, bits: int, out: Tensor | None = None,
                   out_dtype: int | None = None) -> Tensor:

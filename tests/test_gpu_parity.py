@@ -424,6 +424,76 @@ def test_moe_swiglu_out_of_range_and_unsupported(hip):
         hip.MoeSwiGLU(hip.FromBF16Bits(xb6, 2, 640), *_moe_upload(hip, q6), idx, sc, 64, 4)
 
 
+# -- MoE router on the device ------------------------------------------------------------
+
+def _route_oracle(oracle, logits, k, norm):
+    """MoEBlock.Forward's routing (qwen/moe.go:455-481) with the pinned oracle
+    softmax and selection-sort top-k; renorm by the in-order fp32 sum when > 0."""
+    n, E = logits.shape
+    idx = np.empty((n, k), np.int32)
+    sc = np.empty((n, k), np.float32)
+    for t in range(n):
+        i, v = oracle.topk(oracle.softmax_row(logits[t]), k)
+        if norm:
+            s = np.float32(0)
+            for u in v:
+                s = np.float32(s + u)
+            if s > 0:
+                v = (v / s).astype(np.float32)
+        idx[t], sc[t] = i, v
+    return idx, sc
+
+
+@pytest.mark.parametrize("n,E,k,norm,kind", [(16, 128, 8, True, "normal"), (16, 128, 8, False, "normal"),
+                                             (9, 128, 8, True, "ties"), (5, 60, 60, True, "ties"),
+                                             (7, 257, 1, True, "normal"), (4, 64, 4, True, "bf16")])
+def test_moe_route_bit_exact(hip, oracle, n, E, k, norm, kind):
+    """Indices and scores identical to the CPU path, ties included (the selection
+    sort's swaps decide them)."""
+    rng = np.random.default_rng(n * E + k)
+    if kind == "ties":
+        logits = rng.integers(0, 4, (n, E)).astype(np.float32)
+    else:
+        logits = rng.standard_normal((n, E)).astype(np.float32)
+    if kind == "bf16":
+        bits = synth.f32_to_bf16_bits(logits)
+        logits = synth.bf16_bits_to_f32(bits)
+        t = hip.FromBF16Bits(bits, n, E)
+    else:
+        t = hip.FromFloats(logits)
+    step(f"jh_moe_route n={n} E={E} k={k} norm={norm} {kind}")
+    it, st = hip.MoeRoute(t, k, norm)
+    got_i, got_s = hip.Ints(it), hip.Floats(st)
+    want_i, want_s = _route_oracle(oracle, logits, k, norm)
+    assert np.array_equal(got_i, want_i)
+    assert np.array_equal(got_s.view(np.uint32), want_s.view(np.uint32))
+
+
+def test_moe_block_on_device(hip, oracle):
+    """A whole MoE block without a host round trip: 8-bit router QuantMatmul,
+    jh_moe_route, jh_moe_swiglu, against the oracle's moeApply on the same
+    routing (computed from the device logits, so near-ties cannot diverge)."""
+    n_tok, E, H, I, K = 4, 16, 512, 256, 4
+    qs = [synth.quant_linear(800 + i, *(I, H) if i < 2 else (H, I), lead=(E,)) for i in range(3)]
+    st = [upload_quant(hip, q) for q in qs]
+    rw, rs, rb = _width_case(8, E, H, 64, seed=801)
+    router = _upload_width(hip, rw, rs, rb)
+    xb, x = synth.activations(802, (n_tok, H))
+    xt = hip.FromBF16Bits(xb, n_tok, H)
+    step("router QuantMatmul (8-bit) -> jh_moe_route -> jh_moe_swiglu")
+    logits = hip.QuantMatmul(xt, *router, True, 64, 8, out_dtype=F32)
+    it, sct = hip.MoeRoute(logits, K, True)
+    out = hip.Floats(hip.MoeSwiGLU(xt, *st, it, sct, 64, 4))
+    lg = hip.Floats(logits)
+    ok, d, sc = rel_ok(lg, oracle.quant_matmul(x, rw, rs, rb, 64, bits=8), F32_TOL)
+    assert ok, ("router", d, sc)
+    idx, scores = _route_oracle(oracle, lg, K, True)
+    assert np.array_equal(hip.Ints(it), idx)
+    want = oracle.moe_apply(x, *[(q.w, q.s, q.b) for q in qs], idx, scores)
+    ok, d, sc = rel_ok(out, want, BF16_TOL)
+    assert ok, (d, sc)
+
+
 # -- other widths (2- and 8-bit: 32/bits codes per word) ----------------------------
 
 def _width_case(bits, N, K, gs, E=None, seed=0, sb_f32=False):
