@@ -159,26 +159,19 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     const auto rb = make_rsrc(B, N * G * 2);
     __shared__ float red[(KSPLIT > 1) ? (KSPLIT - 1) * RGROUPS * ROWS_PER_WAVE : 1];
 
-    // this lane's part of x, as (x_p, x_{p+4}) bf16 pairs, and its sums
-    uint32_t xp[ITERS][16];
-    float xs[ITERS];
     uint32_t gi[ITERS], wo[ITERS];
 #pragma unroll
     for (int it = 0; it < ITERS; it++) {
         wo[it] = ks * PK + it * 4 * LPR + 4 * sl;   // word offset inside a row
-        const uint32_t e0 = 8u * wo[it];
-        const uint4* xv = reinterpret_cast<const uint4*>(X + e0);
-        float sum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) sum += pair_up(xv[j], &xp[it][4 * j]);
-        xs[it] = sum;
-        gi[it] = e0 >> gs_log2;
+        gi[it] = (8u * wo[it]) >> gs_log2;
     }
-
-    for (uint32_t bbase = blockIdx.x * ROWS_PER_BLOCK; bbase < N; bbase += gridDim.x * ROWS_PER_BLOCK) {
-        const uint32_t row0 = bbase + rg * ROWS_PER_WAVE + (uint32_t)slice * RPW;
-        uint4 wv[RPW][ITERS];
-        uint16_t sh[RPW][ITERS], bh[RPW][ITERS];
+    uint4 wv[RPW][ITERS];
+    uint16_t sh[RPW][ITERS], bh[RPW][ITERS];
+    // Loads complete in issue order. The raw x loads go first, then the first
+    // pass's weights (which do not depend on x), and only then is x regrouped:
+    // that waits for x alone while the weights are still in flight. Rows past N
+    // read as zero (buffer bounds).
+    auto load_pass = [&](uint32_t row0) {
 #pragma unroll
         for (int r = 0; r < RPW; r++)
 #pragma unroll
@@ -192,6 +185,31 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
                 sh[r][it] = buf_load2(rs, off);
                 bh[r][it] = buf_load2(rb, off);
             }
+    };
+    uint4 xraw[ITERS][4];
+#pragma unroll
+    for (int it = 0; it < ITERS; it++) {
+        const uint4* xv = reinterpret_cast<const uint4*>(X + 8u * wo[it]);
+#pragma unroll
+        for (int j = 0; j < 4; j++) xraw[it][j] = xv[j];
+    }
+    const uint32_t lane_row = rg * ROWS_PER_WAVE + (uint32_t)slice * RPW;
+    load_pass(blockIdx.x * ROWS_PER_BLOCK + lane_row);
+
+    // this lane's part of x, as (x_p, x_{p+4}) bf16 pairs, and its sums
+    uint32_t xp[ITERS][16];
+    float xs[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; it++) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) sum += pair_up(xraw[it][j], &xp[it][4 * j]);
+        xs[it] = sum;
+    }
+
+    for (uint32_t bbase = blockIdx.x * ROWS_PER_BLOCK; bbase < N; bbase += gridDim.x * ROWS_PER_BLOCK) {
+        const uint32_t row0 = bbase + lane_row;
+        if (bbase != blockIdx.x * ROWS_PER_BLOCK) load_pass(row0);
         float part[RPW];
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
