@@ -432,3 +432,114 @@ void or_softmax_row(const float *x, float *out, int n) {
     }
     for (int i = 0; i < n; i++) out[i] = out[i] / sum;
 }
+
+/* ---- decode-step operators ------------------------------------------------ */
+
+/* cpu/cpu_ops.go:144-162: per row, ss = sum x^2 in index order (fp32),
+ * inv = 1 / fl32(sqrt(fl64(ss/d + eps))), out = x * inv * w (left to right). */
+void or_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t d, float eps) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float *xr = x + r * d;
+        float ss = 0.0f;
+        for (int64_t i = 0; i < d; i++) {
+            const float v = xr[i];
+            ss = ss + v * v;
+        }
+        const float inv = 1.0f / (float)sqrt((double)(ss / (float)d + eps));
+        for (int64_t i = 0; i < d; i++) {
+            const float t = xr[i] * inv;
+            out[r * d + i] = t * w[i];
+        }
+    }
+}
+
+/* cpu/cpu_attn.go:13-62. x holds rows of D features; the row's position is
+ * offset + (r % L). inv[i] = fl32(base^(-2i/dims)) (RoPE) or 1/freqs[i]
+ * (RoPEFreqs, freqs != NULL). Non-traditional pairs (i, i+dims/2), traditional
+ * (2i, 2i+1); features past `dims` pass through. */
+void or_rope(const float *x, float *out, int64_t rows, int64_t L, int64_t D, int dims, int traditional,
+             float base, float scale, int64_t offset, const float *freqs) {
+    const int half = dims / 2;
+    float *inv = (float *)malloc((size_t)(half > 0 ? half : 1) * sizeof(float));
+    if (!inv) abort();
+    for (int i = 0; i < half; i++)
+        inv[i] = freqs ? 1.0f / freqs[i] : (float)pow((double)base, -(double)(2 * i) / (double)dims);
+    memcpy(out, x, (size_t)(rows * D) * sizeof(float));
+    for (int64_t r = 0; r < rows; r++) {
+        const float pos = (float)(offset + r % L);
+        const int64_t o = r * D;
+        for (int i = 0; i < half; i++) {
+            const float theta = pos * scale * inv[i];
+            const float c = (float)cos((double)theta);
+            const float s = (float)sin((double)theta);
+            const int64_t i0 = traditional ? o + 2 * i : o + i;
+            const int64_t i1 = traditional ? o + 2 * i + 1 : o + i + half;
+            const float a = x[i0], b2 = x[i1];
+            const float ac = a * c, bs = b2 * s, as_ = a * s, bc = b2 * c;
+            out[i0] = ac - bs;
+            out[i1] = as_ + bc;
+        }
+    }
+    free(inv);
+}
+
+/* cpu/cpu_attn.go:64-119: q [B, Hq, Lq, Dh], k/v [B, Hk, Lk, Dh] contiguous,
+ * out [B, Hq, Lq, Dh]. Query head h reads kv head h / (Hq/Hk). With causal, row
+ * i sees keys j <= (Lk - Lq) + i. Scores are fp32 dots in index order times
+ * scale; softmax with exp in double; out = sum_j (e_j / sum) * v_j in key order. */
+void or_sdpa(const float *q, const float *k, const float *v, float *out, int64_t B, int64_t Hq, int64_t Hk,
+             int64_t Lq, int64_t Lk, int64_t Dh, float scale, int causal) {
+    const int64_t group = Hq / Hk, delta = Lk - Lq;
+    float *sc = (float *)malloc((size_t)(Lk > 0 ? Lk : 1) * sizeof(float));
+    if (!sc) abort();
+    for (int64_t bi = 0; bi < B; bi++)
+        for (int64_t h = 0; h < Hq; h++) {
+            const int64_t hk = h / group;
+            for (int64_t i = 0; i < Lq; i++) {
+                const int64_t limit = causal ? delta + i + 1 : Lk;
+                const float *qr = q + ((bi * Hq + h) * Lq + i) * Dh;
+                float mx = -INFINITY;
+                for (int64_t j = 0; j < limit; j++) {
+                    const float *kr = k + ((bi * Hk + hk) * Lk + j) * Dh;
+                    float s = 0.0f;
+                    for (int64_t d = 0; d < Dh; d++) s = s + qr[d] * kr[d];
+                    s = s * scale;
+                    sc[j] = s;
+                    if (s > mx) mx = s;
+                }
+                float sum = 0.0f;
+                for (int64_t j = 0; j < limit; j++) {
+                    const float e = (float)exp((double)(sc[j] - mx));
+                    sc[j] = e;
+                    sum = sum + e;
+                }
+                float *orow = out + ((bi * Hq + h) * Lq + i) * Dh;
+                for (int64_t d = 0; d < Dh; d++) {
+                    float acc = 0.0f;
+                    for (int64_t j = 0; j < limit; j++) {
+                        const float *vr = v + ((bi * Hk + hk) * Lk + j) * Dh;
+                        acc = acc + (sc[j] / sum) * vr[d];
+                    }
+                    orow[d] = acc;
+                }
+            }
+        }
+    free(sc);
+}
+
+/* cpu/cpu.go:327-329 */
+void or_silu(const float *x, float *out, int64_t n) {
+    for (int64_t i = 0; i < n; i++) out[i] = x[i] / (1.0f + (float)exp((double)(-x[i])));
+}
+
+/* cpu/cpu_misc.go:91-121 over the last axis: first index of the maximum
+ * (strict '>'), 0 when no element beats -inf. */
+void or_argmax(const float *x, int64_t rows, int64_t n, int32_t *out) {
+    for (int64_t r = 0; r < rows; r++) {
+        float best = -INFINITY;
+        int32_t bi = 0;
+        for (int64_t i = 0; i < n; i++)
+            if (x[r * n + i] > best) best = x[r * n + i], bi = (int32_t)i;
+        out[r] = bi;
+    }
+}

@@ -127,6 +127,25 @@ void or_topk(const float *row, int n, int k, int32_t *idx, float *val);
  * rounded to float, fp32 running sum, divide. */
 void or_softmax_row(const float *x, float *out, int n);
 
+/* ---- decode-step operators (engine.Backend methods of the CPU backend) ---- */
+
+/* RMSNorm (cpu/cpu_ops.go:144-162) over rows of d. */
+void or_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t d, float eps);
+
+/* RoPE / RoPEFreqs (cpu/cpu_attn.go:13-62); freqs may be NULL. */
+void or_rope(const float *x, float *out, int64_t rows, int64_t L, int64_t D, int dims, int traditional,
+             float base, float scale, int64_t offset, const float *freqs);
+
+/* SDPA (cpu/cpu_attn.go:64-119), GQA and the offset causal mask. */
+void or_sdpa(const float *q, const float *k, const float *v, float *out, int64_t B, int64_t Hq, int64_t Hk,
+             int64_t Lq, int64_t Lk, int64_t Dh, float scale, int causal);
+
+/* SiLU (cpu/cpu.go:327-329). */
+void or_silu(const float *x, float *out, int64_t n);
+
+/* Argmax over the last axis (cpu/cpu_misc.go:91-121). */
+void or_argmax(const float *x, int64_t rows, int64_t n, int32_t *out);
+
 #ifdef __cplusplus
 }
 #endif

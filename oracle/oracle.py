@@ -64,6 +64,17 @@ def lib() -> ctypes.CDLL:
         L.or_topk.restype = None
         L.or_softmax_row.argtypes = [_f32p, _f32p, _int]
         L.or_softmax_row.restype = None
+        _f = ctypes.c_float
+        L.or_rms_norm.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _f]
+        L.or_rms_norm.restype = None
+        L.or_rope.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _int, _int, _f, _f, _i64, ctypes.c_void_p]
+        L.or_rope.restype = None
+        L.or_sdpa.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64, _i64, _f, _int]
+        L.or_sdpa.restype = None
+        L.or_silu.argtypes = [_f32p, _f32p, _i64]
+        L.or_silu.restype = None
+        L.or_argmax.argtypes = [_f32p, _i64, _i64, _i32p]
+        L.or_argmax.restype = None
         _lib = L
     return _lib
 
@@ -190,3 +201,51 @@ def softmax_row(x) -> np.ndarray:
     out = np.empty_like(x)
     lib().or_softmax_row(x, out, x.size)
     return out
+
+
+# -- decode-step operators ------------------------------------------------------------
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    """cpu/cpu_ops.go:144-162 over the last axis."""
+    x, w = _f32(x), _f32(w)
+    d = x.shape[-1]
+    out = np.empty_like(x)
+    lib().or_rms_norm(x, w, out, x.size // d, d, ctypes.c_float(eps))
+    return out
+
+
+def rope(x, dims: int, traditional: bool, base: float, scale: float, offset: int, freqs=None) -> np.ndarray:
+    """cpu/cpu_attn.go:13-62; x [..., L, D]."""
+    x = _f32(x)
+    D, L = x.shape[-1], x.shape[-2]
+    out = np.empty_like(x)
+    fr = None if freqs is None else _f32(freqs)
+    lib().or_rope(x, out, x.size // D, L, D, dims, int(traditional), ctypes.c_float(base), ctypes.c_float(scale),
+                  offset, None if fr is None else fr.ctypes.data_as(ctypes.c_void_p))
+    return out
+
+
+def sdpa(q, k, v, scale: float, causal: bool) -> np.ndarray:
+    """cpu/cpu_attn.go:64-119; q [B, Hq, Lq, Dh], k/v [B, Hk, Lk, Dh]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, Hq, Lq, Dh = q.shape
+    Hk, Lk = k.shape[1], k.shape[2]
+    out = np.empty_like(q)
+    lib().or_sdpa(q, k, v, out, B, Hq, Hk, Lq, Lk, Dh, ctypes.c_float(scale), int(causal))
+    return out
+
+
+def silu(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().or_silu(x, out, x.size)
+    return out
+
+
+def argmax(x) -> np.ndarray:
+    x = _f32(x)
+    n = x.shape[-1]
+    out = np.empty(x.shape[:-1], dtype=np.int32)
+    lib().or_argmax(x, x.size // n, n, out)
+    return out
+

@@ -346,3 +346,119 @@ def test_synth_router_matches_oracle(oracle):
         assert list(oi) == list(idx[t])
         np.testing.assert_allclose(sc[t], ov / ov.sum(), rtol=1e-5)
         assert list(oi) == list(np.argsort(-p.astype(np.float64), kind="stable")[:8])
+
+
+# -- decode-step operators ----------------------------------------------------------
+
+def test_rms_norm_float64_and_weight(oracle):
+    rng = np.random.default_rng(50)
+    x = rng.standard_normal((5, 4096)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(4096)).astype(np.float32)
+    out = oracle.rms_norm(x, w, 1e-6)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * w
+    ok, d, sc = rel_ok(out, want, 1e-6)
+    assert ok, (d, sc)
+    # a planted mistake (weight ignored) fails the same check
+    ok, _, _ = rel_ok(oracle.rms_norm(x, np.ones_like(w), 1e-6), want, 1e-6)
+    assert not ok
+
+
+def _rope64(x, dims, traditional, base, offset):
+    x = x.astype(np.float64)
+    out = x.copy()
+    L = x.shape[-2]
+    half = dims // 2
+    inv = base ** (-np.arange(half) * 2.0 / dims)
+    pos = offset + np.arange(L)[:, None]
+    th = pos * inv[None, :]
+    c, s = np.cos(th), np.sin(th)
+    i0 = 2 * np.arange(half) if traditional else np.arange(half)
+    i1 = i0 + 1 if traditional else i0 + half
+    a, b = x[..., i0], x[..., i1]
+    out[..., i0] = a * c - b * s
+    out[..., i1] = a * s + b * c
+    return out
+
+
+@pytest.mark.parametrize("traditional", [False, True])
+@pytest.mark.parametrize("dims", [128, 64])
+def test_rope_float64_and_invariants(oracle, traditional, dims):
+    rng = np.random.default_rng(51 + dims)
+    x = rng.standard_normal((2, 8, 7, 128)).astype(np.float32)
+    out = oracle.rope(x, dims, traditional, 1e6, 1.0, 301)
+    ok, d, sc = rel_ok(out, _rope64(x, dims, traditional, 1e6, 301), 2e-5)
+    assert ok, (d, sc)
+    assert np.array_equal(out[..., dims:], x[..., dims:])  # pass-through
+    # position 0 is the identity
+    assert np.array_equal(oracle.rope(x[:, :, :1], dims, traditional, 1e6, 1.0, 0), x[:, :, :1])
+    # each rotated pair keeps its length
+    half = dims // 2
+    i0 = 2 * np.arange(half) if traditional else np.arange(half)
+    i1 = i0 + 1 if traditional else i0 + half
+    n_in = np.hypot(x[..., i0].astype(np.float64), x[..., i1])
+    n_out = np.hypot(out[..., i0].astype(np.float64), out[..., i1])
+    np.testing.assert_allclose(n_out, n_in, rtol=1e-5)
+
+
+def test_rope_freqs_matches_base_form(oracle):
+    """RoPEFreqs with freqs = base^(2i/dims) equals RoPE with that base."""
+    x = np.random.default_rng(52).standard_normal((1, 4, 3, 64)).astype(np.float32)
+    freqs = (1e4 ** (np.arange(32) * 2.0 / 64)).astype(np.float32)
+    a = oracle.rope(x, 64, False, 1e4, 1.0, 17, freqs=freqs)
+    b = oracle.rope(x, 64, False, 1e4, 1.0, 17)
+    ok, d, sc = rel_ok(a, b, 1e-5)
+    assert ok, (d, sc)
+
+
+def _sdpa64(q, k, v, scale, causal):
+    B, Hq, Lq, Dh = q.shape
+    Hk, Lk = k.shape[1], k.shape[2]
+    g = Hq // Hk
+    kk = np.repeat(k.astype(np.float64), g, axis=1)
+    vv = np.repeat(v.astype(np.float64), g, axis=1)
+    s = np.einsum("bhid,bhjd->bhij", q.astype(np.float64), kk) * scale
+    if causal:
+        mask = np.arange(Lk)[None, :] > (Lk - Lq) + np.arange(Lq)[:, None]
+        s = np.where(mask, -np.inf, s)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    return np.einsum("bhij,bhjd->bhid", p, vv)
+
+
+@pytest.mark.parametrize("Hq,Hk,Lq,Lk,causal", [(8, 2, 1, 37, False), (8, 2, 1, 37, True), (4, 4, 6, 6, True),
+                                               (6, 3, 5, 13, True), (4, 1, 3, 9, False)])
+def test_sdpa_float64(oracle, Hq, Hk, Lq, Lk, causal):
+    rng = np.random.default_rng(Hq * 100 + Lk)
+    q = rng.standard_normal((2, Hq, Lq, 64)).astype(np.float32)
+    k = rng.standard_normal((2, Hk, Lk, 64)).astype(np.float32)
+    v = rng.standard_normal((2, Hk, Lk, 64)).astype(np.float32)
+    out = oracle.sdpa(q, k, v, 64 ** -0.5, causal)
+    ok, d, sc = rel_ok(out, _sdpa64(q, k, v, 64 ** -0.5, causal), 1e-5)
+    assert ok, (d, sc)
+
+
+def test_sdpa_invariants(oracle):
+    rng = np.random.default_rng(53)
+    q = rng.standard_normal((1, 4, 4, 32)).astype(np.float32)
+    k = np.repeat(rng.standard_normal((1, 2, 1, 32)).astype(np.float32), 10, axis=2)
+    v = rng.standard_normal((1, 2, 10, 32)).astype(np.float32)
+    # identical keys: every query gets the mean of the values (non-causal)
+    out = oracle.sdpa(q, k, v, 0.2, False)
+    np.testing.assert_allclose(out, np.repeat(v.mean(axis=2, keepdims=True), 2, axis=1).repeat(4, axis=2),
+                               rtol=1e-5, atol=1e-6)
+    # causal: keys after a row's limit do not change that row
+    k2 = rng.standard_normal((1, 2, 10, 32)).astype(np.float32)
+    a = oracle.sdpa(q, k2, v, 0.2, True)
+    k3, v3 = k2.copy(), v.copy()
+    k3[:, :, 9], v3[:, :, 9] = 100.0, -100.0  # only the last row may see key 9
+    b = oracle.sdpa(q, k3, v3, 0.2, True)
+    assert np.array_equal(a[:, :, :3], b[:, :, :3]) and not np.array_equal(a[:, :, 3], b[:, :, 3])
+
+
+def test_silu_and_argmax(oracle):
+    x = np.linspace(-30, 30, 1001).astype(np.float32)
+    ok, d, sc = rel_ok(oracle.silu(x), x.astype(np.float64) / (1 + np.exp(-x.astype(np.float64))), 1e-6)
+    assert ok, (d, sc)
+    t = np.array([[1, 5, 5, 2], [-np.inf, -np.inf, -np.inf, -np.inf], [np.nan, 1, 3, 3]], np.float32)
+    assert list(oracle.argmax(t)) == [1, 0, 2]
