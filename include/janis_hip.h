@@ -106,6 +106,14 @@ JH_API int jh_h2d(jh_ctx *ctx, void *dst_device, const void *src_host, size_t by
  * (engine/backend.go:276-283). */
 JH_API int jh_d2h(jh_ctx *ctx, void *dst_host, const void *src_device, size_t bytes);
 
+/* Element-wise operators of jh_elementwise. */
+typedef enum {
+    JH_OP_ADD = 0,      /* a + b            Backend.Add  (cpu/cpu.go:300-302) */
+    JH_OP_MUL = 1,      /* a * b            Backend.Mul  (cpu/cpu.go:304-306) */
+    JH_OP_SILU = 2,     /* a / (1 + e^-a)   Backend.SiLU (cpu/cpu.go:327-329); b unused */
+    JH_OP_SILU_MUL = 3  /* SiLU(a) * b      MLP.Forward's Mul(SiLU(gate), up) (qwen/mlp.go:33-35) */
+} jh_op;
+
 /* ---- MLX affine-quantized operators ---------------------------------------- *
  * Layout (MLX, cpu/cpu_misc.go:124-130): a quantized matrix of `rows` rows and
  * `in_features` columns is
@@ -156,6 +164,57 @@ JH_API int jh_gather_quant_matmul(jh_ctx *ctx, const void *x, jh_dtype x_dtype, 
                            int64_t out_features, int64_t in_features, const int32_t *rhs_indices,
                            int64_t k_slots, int transpose, int group_size, int bits, void *y,
                            jh_dtype y_dtype);
+
+/* ---- the other operators of a decode step ---------------------------------- *
+ * Activations are JH_BF16 or JH_F32 (norm weights also JH_F16); arithmetic is
+ * fp32 with exp/sqrt/cos/sin/pow in double as the CPU backend evaluates them.
+ * All pointers are device memory. */
+
+/* Backend.RMSNorm (engine/backend.go; cpu/cpu_ops.go:144-162) over rows of d:
+ * out = x / sqrt(mean(x^2) + eps) * w. */
+JH_API int jh_rms_norm(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t rows, int64_t d,
+                const void *w, jh_dtype w_dtype, float eps, void *out, jh_dtype out_dtype);
+
+/* Backend.RoPE / RoPEFreqs (cpu/cpu_attn.go:13-62): x holds rows of D features,
+ * the row's position is offset + (row % L); the first `dims` features rotate
+ * (traditional: pairs (2i, 2i+1), else (i, i+dims/2)) by pos*scale*inv_i with
+ * inv_i = base^(-2i/dims), or 1/freqs[i] when freqs (fp32 [dims/2]) is given. */
+JH_API int jh_rope(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t rows, int64_t L, int64_t D,
+            int dims, int traditional, float base, float scale, int64_t offset, const float *freqs,
+            void *out, jh_dtype out_dtype);
+
+/* Backend.SDPA (cpu/cpu_attn.go:64-119): q [B, Hq, Lq, Dh]; k, v laid out as
+ * [B, Hk, kv_capacity, Dh] with the first Lk rows valid (a KV cache, or
+ * kv_capacity == Lk for plain tensors); GQA (head h reads kv head h/(Hq/Hk));
+ * causal masks keys past (Lk - Lq) + i for query row i. out [B, Hq, Lq, Dh].
+ * Lq == 1 with bf16 k/v, Dh == 128 and Hq/Hk in {1,2,4,8} runs split over the
+ * keys (flash-decoding); other shapes a per-row kernel. */
+JH_API int jh_sdpa(jh_ctx *ctx, const void *q, jh_dtype q_dtype, const void *k, const void *v,
+            jh_dtype kv_dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t Lq, int64_t Lk,
+            int64_t kv_capacity, int64_t Dh, float scale, int causal, void *out, jh_dtype out_dtype);
+
+/* Backend.Add / Mul / SiLU and the SwiGLU product, over n elements of equal
+ * shape (b ignored for JH_OP_SILU). */
+JH_API int jh_elementwise(jh_ctx *ctx, jh_op op, const void *a, jh_dtype a_dtype, const void *b,
+                   jh_dtype b_dtype, int64_t n, void *out, jh_dtype out_dtype);
+
+/* Backend.Argmax over the last axis (cpu/cpu_misc.go:91-121): the first index
+ * of the maximum of each of `rows` rows of n; int32 out. */
+JH_API int jh_argmax(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t rows, int64_t n, int32_t *out);
+
+/* Backend.TakeAxis on axis 0 (cpu/cpu_misc.go:48-89) for any element type:
+ * out[i] = table row ids[i] (row_bytes each); ids is int32, device. An id
+ * outside [0, n_rows) gives a zero row (JH_ERR_INVALID with checks on). With
+ * Dequantize this is QuantEmbedding.Forward (qwen/embed.go:78-83). */
+JH_API int jh_take_rows(jh_ctx *ctx, const void *table, int64_t row_bytes, int64_t n_rows,
+                 const int32_t *ids, int64_t n_ids, void *out);
+
+/* KV-cache append (the KVAppender capability, engine/backend.go:56-61; the
+ * reference KVCache.Update, qwen/cache.go:90): writes k_new/v_new
+ * [BH, L, Dh] into rows pos .. pos+L-1 of the caches [BH, capacity, Dh]. */
+JH_API int jh_kv_append(jh_ctx *ctx, void *k_cache, void *v_cache, jh_dtype cache_dtype, int64_t BH,
+                 int64_t capacity, int64_t pos, const void *k_new, const void *v_new,
+                 jh_dtype new_dtype, int64_t L, int64_t Dh);
 
 /* The router of MoEBlock.Forward (qwen/moe.go:455-491) on the device, for a
  * backend that offers it: per token, softmax over the n_experts logits

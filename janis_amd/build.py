@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libjanis_hip.so")
-SOURCES = ["runtime.hip", "qmv.hip", "qmm.hip", "gather.hip", "dequant.hip"]
+SOURCES = ["runtime.hip", "qmv.hip", "qmm.hip", "gather.hip", "dequant.hip", "decode.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

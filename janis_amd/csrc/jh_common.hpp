@@ -168,6 +168,26 @@ struct MoeMlpArgs {
     void* out;                   // [n_tok, H]
     int out_dtype;
 };
+// ---- decode-step operators (decode.hip) ----
+Status launch_rms_norm(const void* x, int x_dt, const void* w, int w_dt, float eps, void* out, int out_dt,
+                       int64_t rows, int64_t d, hipStream_t st);
+Status launch_rope(const void* x, int x_dt, void* out, int out_dt, int64_t rows, int64_t L, int64_t D, int dims,
+                   bool traditional, float base, float scale, int64_t offset, const float* freqs, hipStream_t st);
+bool sdpa_decode_ok(int q_dt, int kv_dt, int64_t Hq, int64_t Hk, int64_t Lq, int64_t Dh);
+int64_t sdpa_splits(int64_t B, int64_t Hk, int64_t Lk, int num_cus);
+size_t sdpa_workspace_bytes(int q_dt, int kv_dt, int64_t B, int64_t Hq, int64_t Hk, int64_t Lq, int64_t Lk,
+                            int64_t Dh, int num_cus);
+Status launch_sdpa(const void* q, int q_dt, const void* k, const void* v, int kv_dt, void* out, int out_dt,
+                   int64_t B, int64_t Hq, int64_t Hk, int64_t Lq, int64_t Lk, int64_t kcap, int64_t Dh, float scale,
+                   bool causal, void* workspace, int num_cus, hipStream_t st);
+Status launch_elementwise(int op, const void* a, int a_dt, const void* b, int b_dt, void* out, int out_dt, int64_t n,
+                          hipStream_t st);
+Status launch_argmax(const void* x, int x_dt, int64_t rows, int64_t n, int32_t* out, hipStream_t st);
+Status launch_take_rows(const void* table, int64_t row_bytes, int64_t n_rows, const int32_t* ids, int64_t n_ids,
+                        void* out, hipStream_t st);
+Status launch_kv_append(void* kc, void* vc, int c_dt, const void* kn, const void* vn, int n_dt, int64_t BH,
+                        int64_t cap, int64_t pos, int64_t L, int64_t Dh, hipStream_t st);
+
 // Router: per token softmax over E logits, top-k, optional renormalisation.
 Status launch_moe_route(const void* logits, int l_dt, int64_t n_tok, int E, int k, bool norm, int32_t* idx,
                         float* scores, hipStream_t st);

@@ -336,6 +336,124 @@ int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n
     return finish(c, jh::launch_gather(a, c->num_cus, c->stream), "gather");
 }
 
+int jh_rms_norm(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, int64_t d, const void* w,
+                jh_dtype w_dtype, float eps, void* out, jh_dtype out_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_rms_norm";
+    if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "out", out_dtype)) return r;
+    if (w_dtype != JH_BF16 && w_dtype != JH_F16 && w_dtype != JH_F32)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": weight must be bf16, f16 or f32");
+    if (rows < 0 || d <= 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape");
+    if (rows == 0) return JH_OK;
+    if (!x || !w || !out) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    return finish(c, jh::launch_rms_norm(x, x_dtype, w, w_dtype, eps, out, out_dtype, rows, d, c->stream), op);
+}
+
+int jh_rope(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, int64_t L, int64_t D, int dims,
+            int traditional, float base, float scale, int64_t offset, const float* freqs, void* out,
+            jh_dtype out_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_rope";
+    if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "out", out_dtype)) return r;
+    if (rows < 0 || L <= 0 || D <= 0 || dims <= 0 || dims > D || (dims & 1) || offset < 0)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape (need 0 < dims <= D, dims even)");
+    if (rows == 0) return JH_OK;
+    if (!x || !out) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    return finish(c, jh::launch_rope(x, x_dtype, out, out_dtype, rows, L, D, dims, traditional != 0, base, scale,
+                                     offset, freqs, c->stream),
+                  op);
+}
+
+int jh_sdpa(jh_ctx* c, const void* q, jh_dtype q_dtype, const void* k, const void* v, jh_dtype kv_dtype, int64_t B,
+            int64_t Hq, int64_t Hk, int64_t Lq, int64_t Lk, int64_t kv_capacity, int64_t Dh, float scale, int causal,
+            void* out, jh_dtype out_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_sdpa";
+    if (int r = check_act_dtype(c, op, "q", q_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "k/v", kv_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "out", out_dtype)) return r;
+    if (B < 0 || Hq <= 0 || Hk <= 0 || Hq % Hk || Lq < 0 || Lk < 0 || kv_capacity < Lk || Dh <= 0)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape (Hq must be a multiple of Hk, capacity >= Lk)");
+    if (B * Hq * Lq == 0) return JH_OK;
+    if (B * Hq * Lq > 0x7fffffff || Lk > 0x7fffffff || kv_capacity > 0x7fffffff)
+        return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": too large");
+    if (!q || !out || (Lk > 0 && (!k || !v))) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    const bool fast = jh::sdpa_decode_ok(q_dtype, kv_dtype, Hq, Hk, Lq, Dh);
+    if (fast && (!aligned16(k) || !aligned16(v)))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": k and v must be 16-byte aligned");
+    const size_t need = jh::sdpa_workspace_bytes(q_dtype, kv_dtype, B, Hq, Hk, Lq, Lk, Dh, c->num_cus);
+    if (need)
+        if (int r = ensure_workspace(c, need, op)) return r;
+    return finish(c, jh::launch_sdpa(q, q_dtype, k, v, kv_dtype, out, out_dtype, B, Hq, Hk, Lq, Lk, kv_capacity, Dh,
+                                     scale, causal != 0, c->ws, c->num_cus, c->stream),
+                  op);
+}
+
+int jh_elementwise(jh_ctx* c, jh_op opk, const void* a, jh_dtype a_dtype, const void* b, jh_dtype b_dtype, int64_t n,
+                   void* out, jh_dtype out_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_elementwise";
+    if (opk != JH_OP_ADD && opk != JH_OP_MUL && opk != JH_OP_SILU && opk != JH_OP_SILU_MUL)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": unknown operator");
+    if (int r = check_act_dtype(c, op, "a", a_dtype)) return r;
+    if (opk != JH_OP_SILU)
+        if (int r = check_act_dtype(c, op, "b", b_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "out", out_dtype)) return r;
+    if (n < 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": n < 0");
+    if (n == 0) return JH_OK;
+    if (!a || !out || (opk != JH_OP_SILU && !b)) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    return finish(c, jh::launch_elementwise((int)opk, a, a_dtype, b, b_dtype, out, out_dtype, n, c->stream), op);
+}
+
+int jh_argmax(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, int64_t n, int32_t* out) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_argmax";
+    if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
+    if (rows < 0 || n <= 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape");
+    if (rows == 0) return JH_OK;
+    if (rows > 0x7fffffff) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": too many rows");
+    if (!x || !out) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    return finish(c, jh::launch_argmax(x, x_dtype, rows, n, out, c->stream), op);
+}
+
+int jh_take_rows(jh_ctx* c, const void* table, int64_t row_bytes, int64_t n_rows, const int32_t* ids, int64_t n_ids,
+                 void* out) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_take_rows";
+    if (row_bytes < 0 || n_rows < 0 || n_ids < 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape");
+    if (n_ids == 0 || row_bytes == 0) return JH_OK;
+    if (n_ids > 0x7fffffff) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": too many ids");
+    if (!table || !ids || !out) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    if (c->checks) {
+        std::vector<int32_t> h((size_t)n_ids);
+        JH_HIP(c, hipMemcpyAsync(h.data(), ids, h.size() * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+        JH_HIP(c, hipStreamSynchronize(c->stream));
+        for (size_t i = 0; i < h.size(); i++)
+            if (h[i] < 0 || h[i] >= n_rows)
+                return fail(c, JH_ERR_INVALID, std::string(op) + ": id " + std::to_string(h[i]) + " at " +
+                                                   std::to_string(i) + " outside [0, " + std::to_string(n_rows) + ")");
+    }
+    return finish(c, jh::launch_take_rows(table, row_bytes, n_rows, ids, n_ids, out, c->stream), op);
+}
+
+int jh_kv_append(jh_ctx* c, void* k_cache, void* v_cache, jh_dtype cache_dtype, int64_t BH, int64_t capacity,
+                 int64_t pos, const void* k_new, const void* v_new, jh_dtype new_dtype, int64_t L, int64_t Dh) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_kv_append";
+    if (int r = check_act_dtype(c, op, "cache", cache_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "new rows", new_dtype)) return r;
+    if (BH < 0 || capacity < 0 || pos < 0 || L < 0 || Dh <= 0 || pos + L > capacity)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": rows " + std::to_string(pos) + ".." +
+                                           std::to_string(pos + L) + " do not fit capacity " + std::to_string(capacity));
+    if (BH * L == 0) return JH_OK;
+    if (!k_cache || !v_cache || !k_new || !v_new) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    return finish(c, jh::launch_kv_append(k_cache, v_cache, cache_dtype, k_new, v_new, new_dtype, BH, capacity, pos, L,
+                                          Dh, c->stream),
+                  op);
+}
+
 int jh_moe_route(jh_ctx* c, const void* logits, jh_dtype logits_dtype, int64_t n_tok, int64_t n_experts,
                  int64_t k, int norm_topk, int32_t* rhs_indices, float* scores) {
     if (int r = enter(c)) return r;

@@ -230,6 +230,116 @@ class HipBackend:
             groupSize, bits, y.ptr, y.dtype))
         return y
 
+    # -- the other operators of a decode step ----------------------------------------
+    def Reshape(self, x: Tensor, *shape) -> Tensor:
+        """engine.Backend.Reshape: a view over the same memory (one -1 allowed)."""
+        shape = list(shape)
+        if shape.count(-1) == 1:
+            known = int(np.prod([d for d in shape if d != -1], dtype=np.int64))
+            shape[shape.index(-1)] = x.numel // known if known else 0
+        if int(np.prod(shape, dtype=np.int64)) != x.numel:
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"Reshape: {list(x.shape)} -> {shape}")
+        return Tensor(self, x.ptr, shape, x.dtype, owned=False, keep=x)
+
+    def Transpose(self, x: Tensor, *perm) -> Tensor:
+        """engine.Backend.Transpose where it moves only length-1 axes (a view);
+        other permutations are not implemented here."""
+        kept = [a for a in perm if x.shape[a] != 1]
+        if kept != sorted(kept):
+            raise JanisHipError(_lib.JH_ERR_UNSUPPORTED, "Transpose: only layout-preserving permutations")
+        return Tensor(self, x.ptr, [x.shape[a] for a in perm], x.dtype, owned=False, keep=x)
+
+    def RMSNorm(self, x: Tensor, weight: Tensor, eps: float, out_dtype: int | None = None) -> Tensor:
+        """cpu/cpu_ops.go:144-162 over the last axis."""
+        d = x.shape[-1]
+        out = self.empty(out_dtype if out_dtype is not None else x.dtype, *x.shape)
+        check(self._ctx, self._L.jh_rms_norm(self._ctx, x.ptr, x.dtype, x.numel // d, d, weight.ptr, weight.dtype,
+                                             float(eps), out.ptr, out.dtype))
+        return out
+
+    def _rope(self, x, dims, traditional, base, scale, offset, freqs, out_dtype):
+        D, L = x.shape[-1], x.shape[-2]
+        out = self.empty(out_dtype if out_dtype is not None else x.dtype, *x.shape)
+        check(self._ctx, self._L.jh_rope(self._ctx, x.ptr, x.dtype, x.numel // D, L, D, dims, int(bool(traditional)),
+                                         float(base), float(scale), int(offset), freqs.ptr if freqs else None,
+                                         out.ptr, out.dtype))
+        return out
+
+    def RoPE(self, x: Tensor, dims: int, traditional: bool, base: float, scale: float, offset: int,
+             out_dtype: int | None = None) -> Tensor:
+        """cpu/cpu_attn.go:13-20; x [..., L, D]."""
+        return self._rope(x, dims, traditional, base, scale, offset, None, out_dtype)
+
+    def RoPEFreqs(self, x: Tensor, dims: int, traditional: bool, scale: float, offset: int, freqs: Tensor,
+                  out_dtype: int | None = None) -> Tensor:
+        """cpu/cpu_attn.go:22-34 (freqs fp32 [dims/2])."""
+        if freqs.dtype != F32:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "RoPEFreqs: freqs must be F32")
+        return self._rope(x, dims, traditional, 1.0, scale, offset, freqs, out_dtype)
+
+    def SDPA(self, q: Tensor, k: Tensor, v: Tensor, scale: float, causal: bool, kv_len: int | None = None,
+             out_dtype: int | None = None) -> Tensor:
+        """cpu/cpu_attn.go:64-119: q [B, Hq, Lq, Dh]; k/v [B, Hk, cap, Dh] whose first
+        kv_len rows are valid (all of them when kv_len is None)."""
+        B, Hq, Lq, Dh = q.shape
+        Hk, cap = k.shape[1], k.shape[2]
+        if k.shape != v.shape or k.dtype != v.dtype or k.shape[0] != B or k.shape[3] != Dh:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "SDPA: k/v shapes do not match q")
+        Lk = cap if kv_len is None else kv_len
+        out = self.empty(out_dtype if out_dtype is not None else q.dtype, B, Hq, Lq, Dh)
+        check(self._ctx, self._L.jh_sdpa(self._ctx, q.ptr, q.dtype, k.ptr, v.ptr, k.dtype, B, Hq, Hk, Lq, Lk, cap,
+                                         Dh, float(scale), int(bool(causal)), out.ptr, out.dtype))
+        return out
+
+    def _elementwise(self, op, a, b, out_dtype):
+        if b is not None and b.numel != a.numel:
+            raise JanisHipError(_lib.JH_ERR_UNSUPPORTED, "elementwise: operands must have the same size")
+        out = self.empty(out_dtype if out_dtype is not None else a.dtype, *a.shape)
+        check(self._ctx, self._L.jh_elementwise(self._ctx, op, a.ptr, a.dtype, b.ptr if b is not None else None,
+                                                b.dtype if b is not None else a.dtype, a.numel, out.ptr, out.dtype))
+        return out
+
+    def Add(self, a: Tensor, b: Tensor, out_dtype: int | None = None) -> Tensor:
+        return self._elementwise(_lib.JH_OP_ADD, a, b, out_dtype)
+
+    def Mul(self, a: Tensor, b: Tensor, out_dtype: int | None = None) -> Tensor:
+        return self._elementwise(_lib.JH_OP_MUL, a, b, out_dtype)
+
+    def SiLU(self, x: Tensor, out_dtype: int | None = None) -> Tensor:
+        return self._elementwise(_lib.JH_OP_SILU, x, None, out_dtype)
+
+    def SiLUMul(self, gate: Tensor, up: Tensor, out_dtype: int | None = None) -> Tensor:
+        """Mul(SiLU(gate), up) in one pass (qwen/mlp.go:33-35)."""
+        return self._elementwise(_lib.JH_OP_SILU_MUL, gate, up, out_dtype)
+
+    def Argmax(self, x: Tensor, axis: int = -1) -> Tensor:
+        """cpu/cpu_misc.go:91-121, last axis only."""
+        if axis not in (-1, len(x.shape) - 1):
+            raise JanisHipError(_lib.JH_ERR_UNSUPPORTED, "Argmax: last axis only")
+        n = x.shape[-1]
+        out = self.empty(I32, *x.shape[:-1])
+        check(self._ctx, self._L.jh_argmax(self._ctx, x.ptr, x.dtype, x.numel // n, n, out.ptr))
+        return out
+
+    def TakeAxis(self, a: Tensor, indices: Tensor, axis: int = 0) -> Tensor:
+        """cpu/cpu_misc.go:48-89 on axis 0 (rows of any dtype, packed words included)."""
+        if axis != 0 or indices.dtype != I32:
+            raise JanisHipError(_lib.JH_ERR_UNSUPPORTED, "TakeAxis: axis 0 with I32 indices only")
+        rows = a.shape[0]
+        row_bytes = a.nbytes // rows if rows else 0
+        out = self.empty(a.dtype, *indices.shape, *a.shape[1:])
+        check(self._ctx, self._L.jh_take_rows(self._ctx, a.ptr, row_bytes, rows, indices.ptr, indices.numel, out.ptr))
+        return out
+
+    def AppendKV(self, k_cache: Tensor, v_cache: Tensor, pos: int, k_new: Tensor, v_new: Tensor) -> None:
+        """KV-cache append: caches [B, Hk, cap, Dh], new rows [B, Hk, L, Dh] at pos."""
+        B, Hk, cap, Dh = k_cache.shape
+        L = k_new.shape[-2]
+        if k_new.shape != v_new.shape or k_new.dtype != v_new.dtype or k_new.numel != B * Hk * L * Dh:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "AppendKV: new rows do not match the cache")
+        check(self._ctx, self._L.jh_kv_append(self._ctx, k_cache.ptr, v_cache.ptr, k_cache.dtype, B * Hk, cap,
+                                              int(pos), k_new.ptr, v_new.ptr, k_new.dtype, L, Dh))
+
     def MoeRoute(self, logits: Tensor, k: int, normTopk: bool = True) -> tuple:
         """The router of MoEBlock.Forward (qwen/moe.go:455-491) on the device:
         softmax over the last axis, top-k (selection-sort ties), optional
