@@ -211,6 +211,7 @@ def main() -> int:
 
     if not args.quick:
         extra.update(prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args))
+        extra.update(decode_step_figures(hip, torch, dev, capture, time_graph, args))
 
     # ---- CPU baseline --------------------------------------------------------------------
     cpu = None
@@ -321,6 +322,51 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
     del stacks
     torch.cuda.empty_cache()
     return res
+
+
+def decode_step_figures(hip, torch, dev, capture, time_graph, args):
+    """Config 4: the whole Qwen3-8B-architecture decode step (36 layers: RMSNorm,
+    q/k/v product, per-head q/k RMSNorm, RoPE, KV append, SDPA over the cache, o
+    product, residual, RMSNorm, gate/up product, SiLU*mul, down product,
+    residual; final norm, lm_head, argmax) on random-init 4-bit weights, bf16 KV
+    caches filled with N(0,1) to ctx tokens, one new token at position ctx, as
+    one graph of the engine-level operators (janis_amd/qwen3_decode.py, fused:
+    norms in the products they feed, residual adds in the products' epilogues)."""
+    from janis_amd.engine import I32
+    from janis_amd.qwen3_decode import Qwen3Config, decode_step, random_model
+
+    cfg = Qwen3Config()
+    t0 = time.time()
+    m, _ = random_model(hip, cfg, 8192 + 1, seed=4, torch=torch, dev=dev)
+    for L in m.layers:
+        L.k_cache._keep.normal_()
+        L.v_cache._keep.normal_()
+    torch.cuda.synchronize()
+    log(f"decode-step model ready in {time.time() - t0:.1f}s")
+    tok = torch.tensor([1234], dtype=torch.int32, device=dev)
+    tt = hip.Wrap(tok.data_ptr(), (1,), I32, keep=tok)
+    arena = hip.make_arena(64 << 20)
+    H, Hq, Hk, Dh, I = cfg.hidden, cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.inter
+    per_layer = (qbytes((Hq + 2 * Hk) * Dh, H) + qbytes(H, Hq * Dh) + qbytes(2 * I, H) + qbytes(H, I))
+    weights = cfg.layers * per_layer + qbytes(cfg.vocab, H) + (H // 2 + 4 * (H // GS))  # + one embedding row
+    # embedding (3 row gathers + dequantize), 7 per layer, lm_head + 2-stage argmax
+    launches = 4 + cfg.layers * 7 + 3
+    res = {}
+    for ctx in (512, 8192):
+        def fn(ctx=ctx):
+            with hip.use_arena(arena):
+                decode_step(hip, m, tt, ctx)
+        g = capture(fn)
+        ms = time_graph(g, max(5, args.steps // 4), 3)
+        kv = cfg.layers * 2 * Hk * (ctx + 1) * Dh * 2
+        res[f"ctx{ctx}"] = {"us_per_token": round(ms * 1e3, 1), "tok_s": round(1000.0 / ms, 1),
+                            "GB_s": round((weights + kv) / (ms * 1e-3) / 1e9, 1), "kv_bytes": kv,
+                            "launches_per_token": launches}
+        del g
+    log("decode step:", res)
+    del m, arena
+    torch.cuda.empty_cache()
+    return {"qwen3_8b_decode_step": res}
 
 
 def cpu_baseline(seconds: float, bytes_token: int):

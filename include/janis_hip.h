@@ -216,6 +216,21 @@ JH_API int jh_kv_append(jh_ctx *ctx, void *k_cache, void *v_cache, jh_dtype cach
                  int64_t capacity, int64_t pos, const void *k_new, const void *v_new,
                  jh_dtype new_dtype, int64_t L, int64_t Dh);
 
+/* The middle of Attention.ForwardCached for one token (qwen/attention.go:101-122)
+ * in one launch, for a backend that offers it: from the token's q/k/v product
+ * [(n_heads + 2 n_kv_heads) * head_dim] (q heads, then k, then v), each query
+ * head is RMS-normalised with q_norm_w and rotated (non-traditional RoPE,
+ * inv_i = rope_base^(-2i/head_dim), angle pos * rope_scale * inv_i) into q_out
+ * [n_heads, head_dim]; each key head normalised with k_norm_w, rotated and
+ * written to row pos of k_cache [n_kv_heads, capacity, head_dim]; each value
+ * head copied to row pos of v_cache. Same arithmetic as jh_rms_norm + jh_rope +
+ * jh_kv_append. head_dim must be 128. */
+JH_API int jh_qk_norm_rope_append(jh_ctx *ctx, const void *qkv, jh_dtype qkv_dtype, int64_t n_heads,
+                           int64_t n_kv_heads, int64_t head_dim, const void *q_norm_w,
+                           const void *k_norm_w, jh_dtype w_dtype, float eps, float rope_base,
+                           float rope_scale, int64_t pos, void *k_cache, void *v_cache,
+                           jh_dtype cache_dtype, int64_t capacity, void *q_out, jh_dtype q_out_dtype);
+
 /* The router of MoEBlock.Forward (qwen/moe.go:455-491) on the device, for a
  * backend that offers it: per token, softmax over the n_experts logits
  * (cpu/cpu.go:461-499), the k largest by the reference's selection sort
@@ -264,6 +279,42 @@ JH_API int jh_moe_swiglu(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t n
                   jh_dtype sb_dtype, int64_t n_experts, int64_t hidden, int64_t intermediate,
                   const int32_t *rhs_indices, const float *scores, int64_t k_slots,
                   int group_size, int bits, void *out, jh_dtype out_dtype);
+
+/* Prologues of jh_quant_matvec_fused. */
+typedef enum {
+    JH_PRO_NONE = 0,     /* x_in = x (JH_BF16 or JH_F32) */
+    JH_PRO_RMSNORM = 1,  /* x_in = RMSNorm(x, norm_w, eps): Block.ForwardCached's InputNorm /
+                            PostNorm feeding q/k/v and gate/up (qwen/block.go:59-60), and the
+                            final norm feeding the LM head (qwen/model.go:294-303) */
+    JH_PRO_SILU_MUL = 2  /* x holds [gate | up] (2 * in_features): x_in = SiLU(gate) * up,
+                            MLP.Forward's input to Down (qwen/mlp.go:33-35) */
+} jh_prologue;
+
+/* One decode product with the operators on either side of it, for a backend
+ * that offers it (the engine's optional-capability pattern,
+ * engine/backend.go:38-112). It replaces the reference's sequences
+ *   RMSNorm -> QuantMatmul            (prologue JH_PRO_RMSNORM)
+ *   Mul(SiLU(gate), up) -> QuantMatmul (prologue JH_PRO_SILU_MUL)
+ *   QuantMatmul -> Add(resid, .)       (resid != NULL: the residual adds of
+ *                                       qwen/block.go:59-60)
+ * for one row (rows == 1 of jh_quant_matmul, transpose = true):
+ *   x_in = bf16(prologue(x))            (as jh_rms_norm / jh_elementwise with a bf16 out)
+ *   y    = x_in . W^T                   (fp32 accumulation, as jh_quant_matmul)
+ *   y    = resid + y                    (fp32; y_dtype must be JH_F32; resid may be y)
+ * The prologue is computed inside the product's launch (each block
+ * normalises its own copy of x, so no normalised copy goes through HBM) and the
+ * add in its epilogue: one launch instead of two or three. Shapes outside the
+ * decode tiles (see the quantized operators above), f16 scales with a
+ * prologue or add, or other dtypes run the same arithmetic as separate
+ * launches through the context's workspace.
+ *   JH_PRO_RMSNORM   x fp32 (the residual stream) [in_features], norm_w bf16
+ *                    [in_features] for the one-launch path (any dtypes otherwise)
+ *   JH_PRO_SILU_MUL  x [2 * in_features] bf16 (the gate/up product) */
+JH_API int jh_quant_matvec_fused(jh_ctx *ctx, jh_prologue prologue, const void *x, jh_dtype x_dtype,
+                          const void *norm_w, jh_dtype norm_w_dtype, float eps, const uint32_t *w,
+                          const void *scales, const void *biases, jh_dtype sb_dtype,
+                          int64_t out_features, int64_t in_features, int group_size, int bits,
+                          const float *resid, void *y, jh_dtype y_dtype);
 
 #ifdef __cplusplus
 }

@@ -43,10 +43,68 @@ __device__ float block_sum256(float v, float* red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// ---- RMSNorm: one block per row --------------------------------------------------
-__global__ __launch_bounds__(256) void rms_norm_kernel(const void* __restrict__ x, int x_dt,
-                                                       const void* __restrict__ w, int w_dt, float eps,
-                                                       void* __restrict__ out, int out_dt, int64_t d) {
+// ---- RMSNorm -------------------------------------------------------------------
+// A row's elements are loaded into registers in one burst (no load waits on an
+// earlier one), squared and summed, then scaled from the registers: x is read
+// once. Rows of up to 1024 take one wave each (per-head norms), longer rows one
+// block of 256 threads.
+template <int PER>  // elements per lane (wave kernel) or per thread (block kernel)
+__device__ __forceinline__ void load_row(const void* x, int x_dt, int64_t base, int64_t d, int t, int stride,
+                                         float* v) {
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+        const int64_t i = t + (int64_t)e * stride;
+        v[e] = i < d ? ld_act(x, base + i, x_dt) : 0.0f;
+    }
+}
+
+template <int PER>
+__global__ __launch_bounds__(256) void rms_norm_wave_kernel(const void* __restrict__ x, int x_dt,
+                                                            const void* __restrict__ w, int w_dt, float eps,
+                                                            void* __restrict__ out, int out_dt, int64_t rows,
+                                                            int64_t d) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    float v[PER];
+    load_row<PER>(x, x_dt, r * d, d, lane, 64, v);
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PER; e++) ss = fmaf(v[e], v[e], ss);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float inv = 1.0f / (float)sqrt((double)(ss / (float)d + eps));
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+        const int64_t i = lane + (int64_t)e * 64;
+        if (i < d) st_act(out, r * d + i, (v[e] * inv) * ld_act(w, i, w_dt), out_dt);
+    }
+}
+
+template <int PER>
+__global__ __launch_bounds__(256) void rms_norm_block_kernel(const void* __restrict__ x, int x_dt,
+                                                             const void* __restrict__ w, int w_dt, float eps,
+                                                             void* __restrict__ out, int out_dt, int64_t d) {
+    __shared__ float red[4];
+    const int64_t r = blockIdx.x;
+    float v[PER];
+    load_row<PER>(x, x_dt, r * d, d, threadIdx.x, 256, v);
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PER; e++) ss = fmaf(v[e], v[e], ss);
+    ss = block_sum256(ss, red);
+    const float inv = 1.0f / (float)sqrt((double)(ss / (float)d + eps));
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+        const int64_t i = threadIdx.x + (int64_t)e * 256;
+        if (i < d) st_act(out, r * d + i, (v[e] * inv) * ld_act(w, i, w_dt), out_dt);
+    }
+}
+
+// Rows longer than 256 * 64 elements: two passes over x.
+__global__ __launch_bounds__(256) void rms_norm_long_kernel(const void* __restrict__ x, int x_dt,
+                                                            const void* __restrict__ w, int w_dt, float eps,
+                                                            void* __restrict__ out, int out_dt, int64_t d) {
     __shared__ float red[4];
     const int64_t r = blockIdx.x;
     float ss = 0.0f;
@@ -56,10 +114,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const void* __restrict__ 
     }
     ss = block_sum256(ss, red);
     const float inv = 1.0f / (float)sqrt((double)(ss / (float)d + eps));
-    for (int64_t i = threadIdx.x; i < d; i += 256) {
-        const float t = ld_act(x, r * d + i, x_dt) * inv;
-        st_act(out, r * d + i, t * ld_act(w, i, w_dt), out_dt);
-    }
+    for (int64_t i = threadIdx.x; i < d; i += 256)
+        st_act(out, r * d + i, (ld_act(x, r * d + i, x_dt) * inv) * ld_act(w, i, w_dt), out_dt);
 }
 
 // ---- RoPE: one thread per rotated pair --------------------------------------------
@@ -156,6 +212,20 @@ __global__ __launch_bounds__(256) void sdpa_rows_kernel(const void* __restrict__
 constexpr int kDecodeMaxGroup = 8;  // query heads per kv head
 constexpr int kDecodeDh = 128;
 
+// Sum over each row of 16 lanes, the total in every lane, with DPP (VALU only):
+// xor 1 and xor 2 inside quads, then the mirrors of 8 and of 16 lanes.
+__device__ __forceinline__ float row16_sum(float v) {
+    auto dpp = [](float x, auto ctrl) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                     decltype(ctrl)::value, 0xF, 0xF, false));
+    };
+    v += dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+    v += dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+    v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+    v += dpp(v, std::integral_constant<int, 0x140>{});  // row_mirror
+    return v;
+}
+
 template <int G>
 __global__ __launch_bounds__(256) void sdpa_decode_split_kernel(const void* __restrict__ q, int q_dt,
                                                                 const uint16_t* __restrict__ k,
@@ -187,9 +257,19 @@ __global__ __launch_bounds__(256) void sdpa_decode_split_kernel(const void* __re
     const int j_begin = split * keys_per_split;
     const int j_end = min(Lk, j_begin + keys_per_split);
     const int64_t kbase = (int64_t)bhk * kcap * Dh;
-    for (int j = j_begin + wave * 4 + kg; j < j_end; j += 16) {
-        const uint4 kr = *reinterpret_cast<const uint4*>(k + kbase + (int64_t)j * Dh + 8 * kl);
-        const uint4 vr = *reinterpret_cast<const uint4*>(v + kbase + (int64_t)j * Dh + 8 * kl);
+    // the next key's rows are loaded before this key is scored
+    int j = j_begin + wave * 4 + kg;
+    uint4 kn = make_uint4(0, 0, 0, 0), vn = kn;
+    if (j < j_end) {
+        kn = *reinterpret_cast<const uint4*>(k + kbase + (int64_t)j * Dh + 8 * kl);
+        vn = *reinterpret_cast<const uint4*>(v + kbase + (int64_t)j * Dh + 8 * kl);
+    }
+    for (; j < j_end; j += 16) {
+        const uint4 kr = kn, vr = vn;
+        if (j + 16 < j_end) {
+            kn = *reinterpret_cast<const uint4*>(k + kbase + (int64_t)(j + 16) * Dh + 8 * kl);
+            vn = *reinterpret_cast<const uint4*>(v + kbase + (int64_t)(j + 16) * Dh + 8 * kl);
+        }
         const float kf[8] = {__uint_as_float(kr.x << 16), __uint_as_float(kr.x & 0xFFFF0000u),
                              __uint_as_float(kr.y << 16), __uint_as_float(kr.y & 0xFFFF0000u),
                              __uint_as_float(kr.z << 16), __uint_as_float(kr.z & 0xFFFF0000u),
@@ -203,8 +283,7 @@ __global__ __launch_bounds__(256) void sdpa_decode_split_kernel(const void* __re
             float s = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; e++) s = fmaf(qv[g][e], kf[e], s);
-#pragma unroll
-            for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 16);
+            s = row16_sum(s);
             const float mn = fmaxf(m[g], s);
             const float corr = __expf(m[g] - mn);
             const float p = __expf(s - mn);
@@ -248,27 +327,93 @@ __global__ __launch_bounds__(256) void sdpa_decode_split_kernel(const void* __re
     }
 }
 
-// Merge the splits of one (b, query head): thread d owns feature d.
+// Merge the splits of one (b, query head): thread d owns feature d. The splits'
+// maxima and sums are staged in LDS first so no load waits on another.
+constexpr int kMaxSplits = 1024;
+
 __global__ __launch_bounds__(128) void sdpa_decode_merge_kernel(const float* __restrict__ part, int Hk, int G,
                                                                 int nsplit, void* __restrict__ out, int out_dt) {
     constexpr int Dh = kDecodeDh;
+    __shared__ float sm[kMaxSplits], sc[kMaxSplits];
+    __shared__ float red[2];
     const int bh = blockIdx.x;  // b*Hq + h
     const int Hq = Hk * G;
     const int b = bh / Hq, h = bh - b * Hq;
     const int hk = h / G, g = h - hk * G;
     const int d = threadIdx.x;
-    const float* base = part + ((int64_t)(b * Hk + hk) * nsplit) * G * (Dh + 2) + g * (Dh + 2);
+    const int64_t stride = (int64_t)G * (Dh + 2);
+    const float* base = part + ((int64_t)(b * Hk + hk) * nsplit) * stride + g * (Dh + 2);
     float M = -__builtin_inff();
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, base[(int64_t)s * G * (Dh + 2)]);
-    float L = 0.0f, A = 0.0f;
-    for (int s = 0; s < nsplit; s++) {
-        const float* ps = base + (int64_t)s * G * (Dh + 2);
-        if (ps[0] == -__builtin_inff()) continue;
-        const float c = __expf(ps[0] - M);
-        L = fmaf(ps[1], c, L);
-        A = fmaf(ps[2 + d], c, A);
+    for (int s = d; s < nsplit; s += 128) {
+        sm[s] = base[s * stride];
+        M = fmaxf(M, sm[s]);
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if ((d & 63) == 0) red[d >> 6] = M;
+    __syncthreads();
+    M = fmaxf(red[0], red[1]);
+    float L = 0.0f;
+    for (int s = d; s < nsplit; s += 128) {
+        const float c = sm[s] == -__builtin_inff() ? 0.0f : __expf(sm[s] - M);
+        sc[s] = c;
+        L = fmaf(base[s * stride + 1], c, L);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+    __syncthreads();
+    if ((d & 63) == 0) red[d >> 6] = L;
+    __syncthreads();
+    L = red[0] + red[1];
+    float A = 0.0f;
+#pragma unroll 8
+    for (int s = 0; s < nsplit; s++) A = fmaf(base[s * stride + 2 + d], sc[s], A);
     st_act(out, (int64_t)bh * Dh + d, A / L, out_dt);
+}
+
+// ---- Qwen3 attention prologue: per-head q/k RMSNorm, RoPE, KV append ------------
+// One wave per head of one token's q/k/v vector [(Hq + 2Hk) * 128]: query heads
+// are normalised with q_norm and rotated into q_out; key heads normalised with
+// k_norm, rotated and written to row `pos` of the key cache; value heads copied
+// to the value cache. head_dim 128, non-traditional RoPE: lane i holds features
+// i and i + 64, which is exactly one rotated pair, so the rotation is lane-local.
+// (qwen/attention.go:101-122: QNorm/KNorm.Forward, RoPE, KVCache.Update.)
+__global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
+    const void* __restrict__ qkv, int qkv_dt, int Hq, int Hk, const void* __restrict__ qn_w,
+    const void* __restrict__ kn_w, int w_dt, float eps, float base, float scale, int64_t pos,
+    void* __restrict__ kc, void* __restrict__ vc, int c_dt, int64_t cap, void* __restrict__ q_out, int q_dt) {
+    constexpr int Dh = 128, half = 64;
+    const int head = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int i = threadIdx.x & 63;
+    if (head >= Hq + 2 * Hk) return;
+    const int64_t o = (int64_t)head * Dh;
+    float a = ld_act(qkv, o + i, qkv_dt), b = ld_act(qkv, o + i + half, qkv_dt);
+    if (head >= Hq + Hk) {  // value head: to the cache as is
+        const int64_t dst = ((int64_t)(head - Hq - Hk) * cap + pos) * Dh;
+        st_act(vc, dst + i, a, c_dt);
+        st_act(vc, dst + i + half, b, c_dt);
+        return;
+    }
+    const bool is_q = head < Hq;
+    const void* w = is_q ? qn_w : kn_w;
+    float ss = fmaf(a, a, b * b);
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) ss += __shfl_xor(ss, s, 64);
+    const float inv = 1.0f / (float)sqrt((double)(ss / (float)Dh + eps));
+    a = (a * inv) * ld_act(w, i, w_dt);
+    b = (b * inv) * ld_act(w, i + half, w_dt);
+    const float fi = (float)pow((double)base, -(double)(2 * i) / (double)Dh);
+    const float theta = (float)pos * scale * fi;
+    const float c = (float)cos((double)theta), sn = (float)sin((double)theta);
+    const float ra = a * c - b * sn, rb = a * sn + b * c;
+    if (is_q) {
+        st_act(q_out, o + i, ra, q_dt);
+        st_act(q_out, o + i + half, rb, q_dt);
+    } else {
+        const int64_t dst = ((int64_t)(head - Hq) * cap + pos) * Dh;
+        st_act(kc, dst + i, ra, c_dt);
+        st_act(kc, dst + i + half, rb, c_dt);
+    }
 }
 
 // ---- elementwise -----------------------------------------------------------------
@@ -288,30 +433,60 @@ __global__ __launch_bounds__(256) void elementwise_kernel(int op, const void* __
     }
 }
 
-// ---- Argmax: one block of 1024 per row; first index of the maximum ----------------
-__global__ __launch_bounds__(1024) void argmax_kernel(const void* __restrict__ x, int x_dt, int64_t n,
-                                                      int32_t* __restrict__ out) {
-    __shared__ float bv[16];
-    __shared__ int64_t bi[16];
-    const int64_t r = blockIdx.x;
+// ---- Argmax: first index of the maximum; blocks take chunks, one block merges ----
+constexpr int kArgmaxChunks = 128;
+
+__device__ __forceinline__ void better(float& bv, int64_t& bi, float v, int64_t i) {
+    if (v > bv || (v == bv && i < bi)) bv = v, bi = i;
+}
+
+// Block (chunk c, row r): the best (value, index) of chunk c of row r, with the
+// loads of each thread issued together.
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const void* __restrict__ x, int x_dt, int64_t n,
+                                                             float* __restrict__ pv, int64_t* __restrict__ pi) {
+    __shared__ float sv[4];
+    __shared__ int64_t si[4];
+    const int64_t r = blockIdx.y;
+    const int64_t chunk = (n + kArgmaxChunks - 1) / kArgmaxChunks;
+    const int64_t lo = blockIdx.x * chunk, hi = min(n, lo + chunk);
     float best = -__builtin_inff();
     int64_t idx = n;  // "none": loses every tie
-    for (int64_t i = threadIdx.x; i < n; i += 1024) {
-        const float v = ld_act(x, r * n + i, x_dt);
-        if (v > best) best = v, idx = i;
+    constexpr int U = 8;
+    for (int64_t i0 = lo + threadIdx.x; i0 < hi; i0 += 256 * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t i = i0 + (int64_t)u * 256;
+            v[u] = i < hi ? ld_act(x, r * n + i, x_dt) : -__builtin_inff();
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (v[u] > best) best = v[u], idx = i0 + (int64_t)u * 256;  // ascending i per thread
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o, 64);
-        const int64_t oi = __shfl_xor(idx, o, 64);
-        if (ov > best || (ov == best && oi < idx)) best = ov, idx = oi;
-    }
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) bv[w] = best, bi[w] = idx;
+    for (int o = 32; o > 0; o >>= 1) better(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
+    if ((threadIdx.x & 63) == 0) sv[threadIdx.x >> 6] = best, si[threadIdx.x >> 6] = idx;
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int k = 1; k < 16; k++)
-            if (bv[k] > best || (bv[k] == best && bi[k] < idx)) best = bv[k], idx = bi[k];
+        for (int k = 1; k < 4; k++) better(best, idx, sv[k], si[k]);
+        pv[r * kArgmaxChunks + blockIdx.x] = best;
+        pi[r * kArgmaxChunks + blockIdx.x] = idx;
+    }
+}
+
+__global__ __launch_bounds__(128) void argmax_final_kernel(const float* __restrict__ pv, const int64_t* __restrict__ pi,
+                                                           int64_t n, int32_t* __restrict__ out) {
+    const int64_t r = blockIdx.x;
+    float best = pv[r * kArgmaxChunks + threadIdx.x];
+    int64_t idx = pi[r * kArgmaxChunks + threadIdx.x];
+    __shared__ float sv[2];
+    __shared__ int64_t si[2];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) better(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
+    if ((threadIdx.x & 63) == 0) sv[threadIdx.x >> 6] = best, si[threadIdx.x >> 6] = idx;
+    __syncthreads();
+    if (threadIdx.x == 0) {  // holds wave 0's result
+        better(best, idx, sv[1], si[1]);
         out[r] = idx < n ? (int32_t)idx : 0;
     }
 }
@@ -352,8 +527,17 @@ unsigned grid_for(int64_t n, int64_t per_block, int64_t cap) {
 Status launch_rms_norm(const void* x, int x_dt, const void* w, int w_dt, float eps, void* out, int out_dt,
                        int64_t rows, int64_t d, hipStream_t st) {
     if (rows == 0) return Status::ok();
-    if (rows > 0x7fffffff) return Status::fail(JH_ERR_UNSUPPORTED, "rms_norm: too many rows");
-    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, x_dt, w, w_dt, eps, out, out_dt, d);
+    if (rows > 0x7fffffff / 4) return Status::fail(JH_ERR_UNSUPPORTED, "rms_norm: too many rows");
+    const dim3 wg((unsigned)((rows + 3) / 4)), bg((unsigned)rows);
+    auto wave = [&](auto k) { hipLaunchKernelGGL(k, wg, dim3(256), 0, st, x, x_dt, w, w_dt, eps, out, out_dt, rows, d); };
+    auto block = [&](auto k) { hipLaunchKernelGGL(k, bg, dim3(256), 0, st, x, x_dt, w, w_dt, eps, out, out_dt, d); };
+    if (d <= 128) wave(rms_norm_wave_kernel<2>);
+    else if (d <= 256) wave(rms_norm_wave_kernel<4>);
+    else if (d <= 1024) wave(rms_norm_wave_kernel<16>);
+    else if (d <= 4096) block(rms_norm_block_kernel<16>);
+    else if (d <= 8192) block(rms_norm_block_kernel<32>);
+    else if (d <= 16384) block(rms_norm_block_kernel<64>);
+    else block(rms_norm_long_kernel);
     return Status::ok();
 }
 
@@ -373,11 +557,12 @@ bool sdpa_decode_ok(int q_dt, int kv_dt, int64_t Hq, int64_t Hk, int64_t Lq, int
 }
 
 int64_t sdpa_splits(int64_t B, int64_t Hk, int64_t Lk, int num_cus) {
-    // about two blocks per CU, at least 64 keys per block
+    // at least two blocks per CU and at most 64 keys per block, but no fewer
+    // than 16 keys per block (one per key slot)
     int64_t n = (2 * (int64_t)num_cus + B * Hk - 1) / (B * Hk);
-    const int64_t by_len = (Lk + 63) / 64;
-    if (n > by_len) n = by_len;
-    if (n > 65535) n = 65535;
+    n = std::max<int64_t>(n, (Lk + 63) / 64);
+    n = std::min<int64_t>(n, (Lk + 15) / 16);
+    n = std::min<int64_t>(n, kMaxSplits);
     return n < 1 ? 1 : n;
 }
 
@@ -417,6 +602,15 @@ Status launch_sdpa(const void* q, int q_dt, const void* k, const void* v, int kv
     return Status::ok();
 }
 
+Status launch_qk_norm_rope_append(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w,
+                                  int w_dt, float eps, float base, float scale, int64_t pos, void* kc, void* vc,
+                                  int c_dt, int64_t cap, void* q_out, int q_dt, hipStream_t st) {
+    const int heads = Hq + 2 * Hk;
+    hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3((unsigned)((heads + 3) / 4)), dim3(256), 0, st, qkv, qkv_dt, Hq,
+                       Hk, qn_w, kn_w, w_dt, eps, base, scale, pos, kc, vc, c_dt, cap, q_out, q_dt);
+    return Status::ok();
+}
+
 Status launch_elementwise(int op, const void* a, int a_dt, const void* b, int b_dt, void* out, int out_dt, int64_t n,
                           hipStream_t st) {
     if (n == 0) return Status::ok();
@@ -425,9 +619,15 @@ Status launch_elementwise(int op, const void* a, int a_dt, const void* b, int b_
     return Status::ok();
 }
 
-Status launch_argmax(const void* x, int x_dt, int64_t rows, int64_t n, int32_t* out, hipStream_t st) {
+size_t argmax_workspace_bytes(int64_t rows) { return (size_t)rows * kArgmaxChunks * (sizeof(float) + sizeof(int64_t)); }
+
+Status launch_argmax(const void* x, int x_dt, int64_t rows, int64_t n, int32_t* out, void* workspace, hipStream_t st) {
     if (rows == 0) return Status::ok();
-    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(1024), 0, st, x, x_dt, n, out);
+    if (rows > 65535) return Status::fail(JH_ERR_UNSUPPORTED, "argmax: more than 65535 rows");
+    int64_t* pi = static_cast<int64_t*>(workspace);
+    float* pv = reinterpret_cast<float*>(pi + rows * kArgmaxChunks);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxChunks, (unsigned)rows), dim3(256), 0, st, x, x_dt, n, pv, pi);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)rows), dim3(kArgmaxChunks), 0, st, pv, pi, n, out);
     return Status::ok();
 }
 

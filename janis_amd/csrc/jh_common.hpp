@@ -136,6 +136,13 @@ struct Status {
 Status launch_dequantize(const QuantMatrix& m, void* out, int out_dtype, hipStream_t st);
 Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int y_dtype,
                   int num_cus, hipStream_t st);
+// Decode product with a fused prologue (pro: 0 none, 1 RMSNorm of fp32 x with
+// weight nw, 2 SiLU(x[:K]) * x[K:]) and optionally y = resid + product (fp32).
+size_t qmv_fused_workspace_bytes(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, bool resid_add,
+                                 int y_dtype);
+Status launch_qmv_fused(const QuantMatrix& m, int pro, const void* x, int x_dtype, const void* nw, int nw_dtype,
+                        float eps, bool resid_add, const float* resid, void* y, int y_dtype, int num_cus,
+                        hipStream_t st, void* workspace);
 Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y,
                   int y_dtype, int num_cus, hipStream_t st, void* workspace);
 // fp32 accumulation buffer a split-K prefill needs (0 when none).
@@ -182,7 +189,11 @@ Status launch_sdpa(const void* q, int q_dt, const void* k, const void* v, int kv
                    bool causal, void* workspace, int num_cus, hipStream_t st);
 Status launch_elementwise(int op, const void* a, int a_dt, const void* b, int b_dt, void* out, int out_dt, int64_t n,
                           hipStream_t st);
-Status launch_argmax(const void* x, int x_dt, int64_t rows, int64_t n, int32_t* out, hipStream_t st);
+size_t argmax_workspace_bytes(int64_t rows);
+Status launch_argmax(const void* x, int x_dt, int64_t rows, int64_t n, int32_t* out, void* workspace, hipStream_t st);
+Status launch_qk_norm_rope_append(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w,
+                                  int w_dt, float eps, float base, float scale, int64_t pos, void* kc, void* vc,
+                                  int c_dt, int64_t cap, void* q_out, int q_dt, hipStream_t st);
 Status launch_take_rows(const void* table, int64_t row_bytes, int64_t n_rows, const int32_t* ids, int64_t n_ids,
                         void* out, hipStream_t st);
 Status launch_kv_append(void* kc, void* vc, int c_dt, const void* kn, const void* vn, int n_dt, int64_t BH,

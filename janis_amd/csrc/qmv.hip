@@ -137,11 +137,31 @@ __device__ __forceinline__ void store_rows(void* Y, int y_dt, uint32_t row0, uin
 // LDS barriers are reached by all waves). Weights and scales are read through
 // buffer resources: rows past N read as zero, so every load is unconditional
 // and issues back to back; only the stores are predicated.
-template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16>
+// Fusions around the product (decode only), chosen at compile time:
+//   PRO_NONE     x is bf16 [K]
+//   PRO_RMSNORM  x is the fp32 residual stream [K]; the product runs on
+//                bf16(x / sqrt(mean(x^2) + eps) * nw) (RMSNorm, cpu/cpu_ops.go:144-162).
+//                Every block sums x^2 over its waves' K parts (which together
+//                cover K) through LDS, so no separate norm launch is needed.
+//   PRO_SILU_MUL x is bf16 [2K] = [gate | up]; the product runs on
+//                bf16(SiLU(gate) * up) (MLP.Forward, qwen/mlp.go:33-35).
+//   EPI_STORE    y = dot
+//   EPI_RESID    y (fp32) = resid + dot; resid may alias y (the residual Add of
+//                qwen/block.go:59-60 done in place).
+enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2 };
+enum { EPI_STORE = 0, EPI_RESID = 1 };
+
+struct QmvFusion {
+    const uint16_t* nw = nullptr;  // bf16 norm weight [K] (PRO_RMSNORM)
+    float eps = 0.0f;
+    const float* resid = nullptr;  // fp32 [N] (EPI_RESID)
+};
+
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int PRO = PRO_NONE, int EPI = EPI_STORE>
 __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     const uint32_t* __restrict__ W, const uint16_t* __restrict__ S,
-    const uint16_t* __restrict__ B, const uint16_t* __restrict__ X, void* __restrict__ Y,
-    int y_dt, uint32_t N, int gs_log2) {
+    const uint16_t* __restrict__ B, const void* __restrict__ Xv, void* __restrict__ Y,
+    int y_dt, uint32_t N, int gs_log2, QmvFusion fu) {
     constexpr int SLICES = 64 / LPR;
     constexpr int RGROUPS = 4 / KSPLIT;                 // row groups per block
     constexpr uint32_t PK = 4 * LPR * ITERS;            // words per K part
@@ -158,6 +178,8 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     const auto rs = make_rsrc(S, N * G * 2);
     const auto rb = make_rsrc(B, N * G * 2);
     __shared__ float red[(KSPLIT > 1) ? (KSPLIT - 1) * RGROUPS * ROWS_PER_WAVE : 1];
+    __shared__ float ssq[4];
+    constexpr uint32_t K = 8 * P;
 
     uint32_t gi[ITERS], wo[ITERS];
 #pragma unroll
@@ -186,15 +208,97 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
                 bh[r][it] = buf_load2(rb, off);
             }
     };
-    uint4 xraw[ITERS][4];
+    // raw x: 32 elements per lane per ITER (bf16, fp32 for the norm, or gate + up)
+    constexpr int XW = PRO == PRO_RMSNORM ? 8 : 4;  // 16-byte chunks per 32 elements
+    uint4 xraw[ITERS][XW];
+    uint4 xaux[ITERS][4];  // norm weights (PRO_RMSNORM) or up (PRO_SILU_MUL)
 #pragma unroll
     for (int it = 0; it < ITERS; it++) {
-        const uint4* xv = reinterpret_cast<const uint4*>(X + 8u * wo[it]);
+        const uint32_t e0 = 8u * wo[it];
+        if constexpr (PRO == PRO_RMSNORM) {
+            const uint4* xv = reinterpret_cast<const uint4*>(static_cast<const float*>(Xv) + e0);
 #pragma unroll
-        for (int j = 0; j < 4; j++) xraw[it][j] = xv[j];
+            for (int j = 0; j < 8; j++) xraw[it][j] = xv[j];
+        } else {
+            const uint4* xv = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(Xv) + e0);
+#pragma unroll
+            for (int j = 0; j < 4; j++) xraw[it][j] = xv[j];
+        }
     }
     const uint32_t lane_row = rg * ROWS_PER_WAVE + (uint32_t)slice * RPW;
     load_pass(blockIdx.x * ROWS_PER_BLOCK + lane_row);
+    if constexpr (PRO == PRO_RMSNORM || PRO == PRO_SILU_MUL) {
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+            const uint4* av = PRO == PRO_RMSNORM ? reinterpret_cast<const uint4*>(fu.nw + 8u * wo[it])
+                                                 : reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(Xv) + K + 8u * wo[it]);
+#pragma unroll
+            for (int j = 0; j < 4; j++) xaux[it][j] = av[j];
+        }
+    }
+    // the product's input as bf16, 8 per uint4
+    uint4 xin[ITERS][4];
+    if constexpr (PRO == PRO_NONE) {
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) xin[it][j] = xraw[it][j];
+    } else if constexpr (PRO == PRO_SILU_MUL) {
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t g[4] = {xraw[it][j].x, xraw[it][j].y, xraw[it][j].z, xraw[it][j].w};
+                const uint32_t u[4] = {xaux[it][j].x, xaux[it][j].y, xaux[it][j].z, xaux[it][j].w};
+                uint32_t o[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float g0 = __uint_as_float(g[q] << 16), g1 = __uint_as_float(g[q] & 0xFFFF0000u);
+                    const float u0 = __uint_as_float(u[q] << 16), u1 = __uint_as_float(u[q] & 0xFFFF0000u);
+                    const float a0 = g0 / (1.0f + __expf(-g0)) * u0, a1 = g1 / (1.0f + __expf(-g1)) * u1;
+                    o[q] = (uint32_t)f32_to_bf16_hw(a0) | ((uint32_t)f32_to_bf16_hw(a1) << 16);
+                }
+                xin[it][j] = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+    } else {
+        // sum of squares of this wave's K part (each slice holds the whole part)
+        float ss = 0.0f;
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const uint4 v = xraw[it][j];
+                ss = fmaf(__uint_as_float(v.x), __uint_as_float(v.x), ss);
+                ss = fmaf(__uint_as_float(v.y), __uint_as_float(v.y), ss);
+                ss = fmaf(__uint_as_float(v.z), __uint_as_float(v.z), ss);
+                ss = fmaf(__uint_as_float(v.w), __uint_as_float(v.w), ss);
+            }
+        ss = slice_sum_last<LPR>(ss);
+        if (slice == 0 && sl == LPR - 1) ssq[wv_id] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KSPLIT; k++) tot += ssq[rg * KSPLIT + k];
+        const float inv = 1.0f / (float)sqrt((double)(tot / (float)K + fu.eps));
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint4 a = xraw[it][2 * j], b = xraw[it][2 * j + 1], w = xaux[it][j];
+                const float xs8[8] = {__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z),
+                                      __uint_as_float(a.w), __uint_as_float(b.x), __uint_as_float(b.y),
+                                      __uint_as_float(b.z), __uint_as_float(b.w)};
+                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+                uint32_t o[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float n0 = (xs8[2 * q] * inv) * __uint_as_float(ww[q] << 16);
+                    const float n1 = (xs8[2 * q + 1] * inv) * __uint_as_float(ww[q] & 0xFFFF0000u);
+                    o[q] = (uint32_t)f32_to_bf16_hw(n0) | ((uint32_t)f32_to_bf16_hw(n1) << 16);
+                }
+                xin[it][j] = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+    }
 
     // this lane's part of x, as (x_p, x_{p+4}) bf16 pairs, and its sums
     uint32_t xp[ITERS][16];
@@ -203,7 +307,7 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     for (int it = 0; it < ITERS; it++) {
         float sum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) sum += pair_up(xraw[it][j], &xp[it][4 * j]);
+        for (int j = 0; j < 4; j++) sum += pair_up(xin[it][j], &xp[it][4 * j]);
         xs[it] = sum;
     }
 
@@ -244,7 +348,15 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
                         part[r] += red[((k - 1) * RGROUPS * SLICES * RPW) + slot + r];
             __syncthreads();
         }
-        if (ks == 0 && sl == LPR - 1) store_rows<RPW>(Y, y_dt, row0, N, part);
+        if (ks == 0 && sl == LPR - 1) {
+            if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+                for (int r = 0; r < RPW; r++)
+                    if (row0 + r < N) static_cast<float*>(Y)[row0 + r] = fu.resid[row0 + r] + part[r];
+            } else {
+                store_rows<RPW>(Y, y_dt, row0, N, part);
+            }
+        }
     }
 }
 
@@ -314,11 +426,11 @@ __global__ __launch_bounds__(256) void qmv_generic_kernel(
 
 namespace {
 
-template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16>
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int PRO = PRO_NONE, int EPI = EPI_STORE>
 Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gs_log2,
-                   int num_cus, hipStream_t st) {
+                   int num_cus, hipStream_t st, const QmvFusion& fu = QmvFusion{}) {
     constexpr int64_t rows_per_block = (4 / KSPLIT) * (64 / LPR) * RPW;
-    auto kern = qmv_bf16x_kernel<LPR, ITERS, RPW, KSPLIT, SB_F16>;
+    auto kern = qmv_bf16x_kernel<LPR, ITERS, RPW, KSPLIT, SB_F16, PRO, EPI>;
     // persistent-style grid: at most what is resident at once, so multi-pass
     // shapes reuse the x registers instead of queueing more blocks
     static int resident = 0;
@@ -333,17 +445,9 @@ Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, in
     if (blocks > cap) blocks = cap;
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, st, m.w,
-                       static_cast<const uint16_t*>(m.scales), static_cast<const uint16_t*>(m.biases),
-                       static_cast<const uint16_t*>(x), y, y_dtype, (uint32_t)m.rows, gs_log2);
+                       static_cast<const uint16_t*>(m.scales), static_cast<const uint16_t*>(m.biases), x, y,
+                       y_dtype, (uint32_t)m.rows, gs_log2, fu);
     return Status::ok();
-}
-
-template <int LPR, int ITERS, int RPW, int KSPLIT = 1>
-Status run_fast(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gs_log2,
-                int num_cus, hipStream_t st) {
-    if (m.sb_dtype == JH_F16)
-        return run_fast_sb<LPR, ITERS, RPW, KSPLIT, true>(m, x, y, y_dtype, gs_log2, num_cus, st);
-    return run_fast_sb<LPR, ITERS, RPW, KSPLIT, false>(m, x, y, y_dtype, gs_log2, num_cus, st);
 }
 
 int log2_exact(int v) {
@@ -366,35 +470,135 @@ Status launch_generic(const QuantMatrix& m, const void* x, int x_dtype, int64_t 
     return Status::ok();
 }
 
-Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int y_dtype,
-                  int num_cus, hipStream_t st) {
-    const int gl = log2_exact(m.group_size);
-    const int64_t P = m.in / 8;
-    const bool fast_ok = m.bits == 4 && x_dtype == JH_BF16 && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0 &&
-                         (m.sb_dtype == JH_BF16 || m.sb_dtype == JH_F16) &&
-                         (m.rows + 64) * (m.in / 2) < ((int64_t)1 << 31);
-    if (fast_ok) {
-        // Tile per row length, from a sweep of the Qwen3-8B shapes on MI355X:
-        // splitting K over 2-4 waves per row beats one wave per row at every
-        // shape (more waves in flight, shorter per-wave dependency chains).
-        if (P == 512 && m.rows >= 65536) return run_fast<64, 1, 8, 2>(m, x, y, y_dtype, gl, num_cus, st);
-        switch (P) {
-            case 512 * 1: return run_fast<32, 1, 4, 4>(m, x, y, y_dtype, gl, num_cus, st);
-            case 512 * 2: return run_fast<32, 2, 2, 4>(m, x, y, y_dtype, gl, num_cus, st);
-            case 512 * 3: return run_fast<32, 3, 2, 4>(m, x, y, y_dtype, gl, num_cus, st);
-            case 512 * 4: return run_fast<32, 4, 2, 4>(m, x, y, y_dtype, gl, num_cus, st);
-            case 256 * 1: return run_fast<32, 1, 4, 2>(m, x, y, y_dtype, gl, num_cus, st);
-            case 256 * 3: return run_fast<32, 3, 2, 2>(m, x, y, y_dtype, gl, num_cus, st);
-            case 128 * 1: return run_fast<16, 1, 4, 2>(m, x, y, y_dtype, gl, num_cus, st);
-            case 128 * 3: return run_fast<16, 3, 2, 2>(m, x, y, y_dtype, gl, num_cus, st);
-            case 64 * 1: return run_fast<16, 1, 4, 1>(m, x, y, y_dtype, gl, num_cus, st);
-            case 64 * 3: return run_fast<16, 3, 2, 1>(m, x, y, y_dtype, gl, num_cus, st);
-            case 32 * 1: return run_fast<8, 1, 4, 1>(m, x, y, y_dtype, gl, num_cus, st);
-            case 32 * 3: return run_fast<8, 3, 2, 1>(m, x, y, y_dtype, gl, num_cus, st);
-            default: break;
+namespace {
+
+// One tile of the table. Fused prologues/epilogues are built for bf16 scales
+// only (the checkpoints' format); an f16-scale fused call returns false and is
+// composed from separate launches by the caller.
+template <int LPR, int ITERS, int RPW, int KSPLIT, int PRO, int EPI>
+bool tile(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gl, int num_cus, hipStream_t st,
+          const QmvFusion& fu) {
+    if (m.sb_dtype == JH_F16) {
+        if constexpr (PRO == PRO_NONE && EPI == EPI_STORE) {
+            run_fast_sb<LPR, ITERS, RPW, KSPLIT, true, PRO, EPI>(m, x, y, y_dtype, gl, num_cus, st, fu);
+            return true;
+        } else {
+            return false;
         }
     }
+    run_fast_sb<LPR, ITERS, RPW, KSPLIT, false, PRO, EPI>(m, x, y, y_dtype, gl, num_cus, st, fu);
+    return true;
+}
+
+// The register tiles take 4-bit weights, groups of 32/64/128 dividing K, 16-bit
+// scales, matrices under 2 GiB and the row lengths P = K/8 of the table below.
+bool qmv_fast_shape(const QuantMatrix& m) {
+    const int gl = log2_exact(m.group_size);
+    if (!(m.bits == 4 && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0 &&
+          (m.sb_dtype == JH_BF16 || m.sb_dtype == JH_F16) && (m.rows + 64) * (m.in / 2) < ((int64_t)1 << 31)))
+        return false;
+    switch (m.in / 8) {
+        case 512: case 1024: case 1536: case 2048: case 256: case 768:
+        case 128: case 384: case 64: case 192: case 32: case 96:
+            return (m.in % 8) == 0;
+        default:
+            return false;
+    }
+}
+
+// Tile per row length, from a sweep of the Qwen3-8B shapes on MI355X: splitting
+// K over 2-4 waves per row beats one wave per row at every shape (more waves in
+// flight, shorter per-wave dependency chains).
+template <int PRO, int EPI>
+bool launch_tiles(const QuantMatrix& m, const void* x, void* y, int y_dtype, int num_cus, hipStream_t st,
+                  const QmvFusion& fu) {
+    if (!qmv_fast_shape(m)) return false;
+    const int gl = log2_exact(m.group_size);
+#define JH_TILE(L, I, R, KS) return tile<L, I, R, KS, PRO, EPI>(m, x, y, y_dtype, gl, num_cus, st, fu)
+    if (m.in == 4096 && m.rows >= 65536) JH_TILE(64, 1, 8, 2);
+    switch (m.in / 8) {
+        case 512 * 1: JH_TILE(32, 1, 4, 4);
+        case 512 * 2: JH_TILE(32, 2, 2, 4);
+        case 512 * 3: JH_TILE(32, 3, 2, 4);
+        case 512 * 4: JH_TILE(32, 4, 2, 4);
+        case 256 * 1: JH_TILE(32, 1, 4, 2);
+        case 256 * 3: JH_TILE(32, 3, 2, 2);
+        case 128 * 1: JH_TILE(16, 1, 4, 2);
+        case 128 * 3: JH_TILE(16, 3, 2, 2);
+        case 64 * 1: JH_TILE(16, 1, 4, 1);
+        case 64 * 3: JH_TILE(16, 3, 2, 1);
+        case 32 * 1: JH_TILE(8, 1, 4, 1);
+        case 32 * 3: JH_TILE(8, 3, 2, 1);
+        default: return false;
+    }
+#undef JH_TILE
+}
+
+}  // namespace
+
+Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int y_dtype,
+                  int num_cus, hipStream_t st) {
+    if (x_dtype == JH_BF16 && launch_tiles<PRO_NONE, EPI_STORE>(m, x, y, y_dtype, num_cus, st, QmvFusion{}))
+        return Status::ok();
     return launch_generic(m, x, x_dtype, 1, y, y_dtype, num_cus, st);
+}
+
+// True when one register-tile launch takes the fused call (no workspace).
+bool qmv_fused_single(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, bool resid_add, int y_dtype) {
+    if (pro == PRO_RMSNORM ? (x_dtype != JH_F32 || nw_dtype != JH_BF16) : x_dtype != JH_BF16) return false;
+    if (resid_add && y_dtype != JH_F32) return false;
+    if (!qmv_fast_shape(m)) return false;
+    if (m.sb_dtype != JH_BF16 && (pro != PRO_NONE || resid_add)) return false;
+    return pro == PRO_NONE || (pro == PRO_RMSNORM && !resid_add) || (pro == PRO_SILU_MUL && resid_add);
+}
+
+size_t qmv_fused_workspace_bytes(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, bool resid_add,
+                                 int y_dtype) {
+    if (qmv_fused_single(m, pro, x_dtype, nw_dtype, resid_add, y_dtype)) return 0;
+    return ((size_t)m.in * 2 + 255) / 256 * 256 + (size_t)m.rows * 4;
+}
+
+Status launch_qmv_fused(const QuantMatrix& m, int pro, const void* x, int x_dtype, const void* nw, int nw_dtype,
+                        float eps, bool resid_add, const float* resid, void* y, int y_dtype, int num_cus,
+                        hipStream_t st, void* workspace) {
+    // one launch when a register tile takes the shape
+    if (qmv_fused_single(m, pro, x_dtype, nw_dtype, resid_add, y_dtype)) {
+        QmvFusion fu;
+        fu.nw = static_cast<const uint16_t*>(nw);
+        fu.eps = eps;
+        fu.resid = resid;
+        bool done = false;
+        if (pro == PRO_NONE && !resid_add)
+            done = launch_tiles<PRO_NONE, EPI_STORE>(m, x, y, y_dtype, num_cus, st, fu);
+        else if (pro == PRO_NONE)
+            done = launch_tiles<PRO_NONE, EPI_RESID>(m, x, y, y_dtype, num_cus, st, fu);
+        else if (pro == PRO_RMSNORM && !resid_add)
+            done = launch_tiles<PRO_RMSNORM, EPI_STORE>(m, x, y, y_dtype, num_cus, st, fu);
+        else if (pro == PRO_SILU_MUL && resid_add)
+            done = launch_tiles<PRO_SILU_MUL, EPI_RESID>(m, x, y, y_dtype, num_cus, st, fu);
+        if (done) return Status::ok();
+        return Status::fail(JH_ERR_UNSUPPORTED, "qmv_fused: no tile for a shape the planner accepted");
+    }
+    // otherwise the same arithmetic as separate launches through the workspace
+    uint16_t* xin = static_cast<uint16_t*>(workspace);
+    float* tmp = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((size_t)m.in * 2 + 255) / 256 * 256);
+    const void* xp = x;
+    int xdt = x_dtype;
+    if (pro == PRO_RMSNORM) {
+        Status s = launch_rms_norm(x, x_dtype, nw, nw_dtype, eps, xin, JH_BF16, 1, m.in, st);
+        if (s.code != JH_OK) return s;
+        xp = xin, xdt = JH_BF16;
+    } else if (pro == PRO_SILU_MUL) {
+        const size_t esz = x_dtype == JH_F32 ? 4 : 2;
+        Status s = launch_elementwise(JH_OP_SILU_MUL, x, x_dtype, static_cast<const char*>(x) + m.in * esz, x_dtype,
+                                      xin, JH_BF16, m.in, st);
+        if (s.code != JH_OK) return s;
+        xp = xin, xdt = JH_BF16;
+    }
+    if (!resid_add) return launch_qmv(m, xp, xdt, y, y_dtype, num_cus, st);
+    Status s = launch_qmv(m, xp, xdt, tmp, JH_F32, num_cus, st);
+    if (s.code != JH_OK) return s;
+    return launch_elementwise(JH_OP_ADD, resid, JH_F32, tmp, JH_F32, y, y_dtype, m.rows, st);
 }
 
 }  // namespace jh

@@ -281,6 +281,34 @@ int jh_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, co
     return finish(c, jh::launch_qmm(m, x, x_dtype, rows, y, y_dtype, c->num_cus, c->stream, c->ws), "qmm");
 }
 
+int jh_quant_matvec_fused(jh_ctx* c, jh_prologue pro, const void* x, jh_dtype x_dtype, const void* norm_w,
+                          jh_dtype norm_w_dtype, float eps, const uint32_t* w, const void* scales,
+                          const void* biases, jh_dtype sb_dtype, int64_t out_features, int64_t in_features,
+                          int group_size, int bits, const float* resid, void* y, jh_dtype y_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_quant_matvec_fused";
+    if (pro != JH_PRO_NONE && pro != JH_PRO_RMSNORM && pro != JH_PRO_SILU_MUL)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": unknown prologue");
+    if (int r = check_quant(c, op, w, scales, biases, sb_dtype, out_features, in_features, group_size, bits))
+        return r;
+    if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "y", y_dtype)) return r;
+    if (pro == JH_PRO_RMSNORM && norm_w_dtype != JH_BF16 && norm_w_dtype != JH_F16 && norm_w_dtype != JH_F32)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": norm weight must be bf16, f16 or f32");
+    if (resid && y_dtype != JH_F32)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": the residual add writes fp32 (y_dtype must be JH_F32)");
+    if (out_features == 0) return JH_OK;
+    if (!x || !y || !aligned16(x) || !aligned16(y) || (pro == JH_PRO_RMSNORM && (!norm_w || !aligned16(norm_w))))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": x, y (and norm_w) must be non-null and 16-byte aligned");
+    jh::QuantMatrix m{w, scales, biases, sb_dtype, out_features, in_features, group_size, bits};
+    const size_t need = jh::qmv_fused_workspace_bytes(m, (int)pro, x_dtype, norm_w_dtype, resid != nullptr, y_dtype);
+    if (need)
+        if (int r = ensure_workspace(c, need, op)) return r;
+    return finish(c, jh::launch_qmv_fused(m, (int)pro, x, x_dtype, norm_w, norm_w_dtype, eps, resid != nullptr,
+                                          resid, y, y_dtype, c->num_cus, c->stream, c->ws),
+                  op);
+}
+
 int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n_lead,
                            int64_t a_vectors, const uint32_t* w, const void* scales,
                            const void* biases, jh_dtype sb_dtype, int64_t n_experts,
@@ -415,7 +443,30 @@ int jh_argmax(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, int64_t 
     if (rows == 0) return JH_OK;
     if (rows > 0x7fffffff) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": too many rows");
     if (!x || !out) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
-    return finish(c, jh::launch_argmax(x, x_dtype, rows, n, out, c->stream), op);
+    if (int r = ensure_workspace(c, jh::argmax_workspace_bytes(rows), op)) return r;
+    return finish(c, jh::launch_argmax(x, x_dtype, rows, n, out, c->ws, c->stream), op);
+}
+
+int jh_qk_norm_rope_append(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t n_heads, int64_t n_kv_heads,
+                           int64_t head_dim, const void* q_norm_w, const void* k_norm_w, jh_dtype w_dtype, float eps,
+                           float rope_base, float rope_scale, int64_t pos, void* k_cache, void* v_cache,
+                           jh_dtype cache_dtype, int64_t capacity, void* q_out, jh_dtype q_out_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_qk_norm_rope_append";
+    if (int r = check_act_dtype(c, op, "qkv", qkv_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "cache", cache_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "q_out", q_out_dtype)) return r;
+    if (w_dtype != JH_BF16 && w_dtype != JH_F16 && w_dtype != JH_F32)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": norm weights must be bf16, f16 or f32");
+    if (head_dim != 128) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": head_dim must be 128");
+    if (n_heads <= 0 || n_kv_heads <= 0 || n_heads > 4096 || n_kv_heads > 4096 || pos < 0 || pos >= capacity)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad heads, or pos outside the cache capacity");
+    if (!qkv || !q_norm_w || !k_norm_w || !k_cache || !v_cache || !q_out)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    return finish(c, jh::launch_qk_norm_rope_append(qkv, qkv_dtype, (int)n_heads, (int)n_kv_heads, q_norm_w, k_norm_w,
+                                                    w_dtype, eps, rope_base, rope_scale, pos, k_cache, v_cache,
+                                                    cache_dtype, capacity, q_out, q_out_dtype, c->stream),
+                  op);
 }
 
 int jh_take_rows(jh_ctx* c, const void* table, int64_t row_bytes, int64_t n_rows, const int32_t* ids, int64_t n_ids,

@@ -15,6 +15,7 @@ when the handle is collected, like the Go finalizers of the ggml backend
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import numpy as np
@@ -71,6 +72,7 @@ class HipBackend:
             raise JanisHipError(rc, (L.jh_last_error(None) or b"").decode())
         self._L = L
         self._ctx = ctx
+        self._arena = None  # [base tensor, offset] while an arena is in use
 
     # -- lifecycle / info ------------------------------------------------------
     def Version(self) -> str:
@@ -98,8 +100,33 @@ class HipBackend:
         check(self._ctx, self._L.jh_set_checks(self._ctx, int(bool(on))))
 
     # -- creation ----------------------------------------------------------------
+    def make_arena(self, nbytes: int) -> Tensor:
+        """One device allocation that `use_arena` carves results from."""
+        return self.empty(U8, int(nbytes))
+
+    @contextlib.contextmanager
+    def use_arena(self, arena: Tensor):
+        """While active, every result tensor is carved from `arena` (256-byte
+        aligned, from its start) instead of allocated: no jh_alloc/jh_free inside,
+        so the operator sequence can be captured into a HIP graph, and two runs of
+        the same sequence get the same addresses. Results stay valid while the
+        arena lives and until the next use_arena on it."""
+        prev = self._arena
+        self._arena = [arena, 0]
+        try:
+            yield arena
+        finally:
+            self._arena = prev
+
     def empty(self, dtype: int, *shape) -> Tensor:
         n = int(np.prod(shape, dtype=np.int64)) if shape else 1
+        if self._arena is not None:
+            base, off = self._arena
+            need = max(1, n * DTYPE_SIZE[dtype])
+            if off + need > base.nbytes:
+                raise JanisHipError(_lib.JH_ERR_OOM, f"arena of {base.nbytes} bytes exhausted")
+            self._arena[1] = (off + need + 255) & ~255
+            return Tensor(self, base.ptr + off, shape, dtype, owned=False, keep=base)
         p = ctypes.c_void_p()
         check(self._ctx, self._L.jh_alloc(self._ctx, max(1, n * DTYPE_SIZE[dtype]), ctypes.byref(p)))
         return Tensor(self, p.value, shape, dtype)
@@ -339,6 +366,53 @@ class HipBackend:
             raise JanisHipError(_lib.JH_ERR_INVALID, "AppendKV: new rows do not match the cache")
         check(self._ctx, self._L.jh_kv_append(self._ctx, k_cache.ptr, v_cache.ptr, k_cache.dtype, B * Hk, cap,
                                               int(pos), k_new.ptr, v_new.ptr, k_new.dtype, L, Dh))
+
+    def QKNormRoPEAppend(self, qkv: Tensor, n_heads: int, n_kv_heads: int, q_norm: Tensor, k_norm: Tensor,
+                         eps: float, base: float, scale: float, pos: int, k_cache: Tensor, v_cache: Tensor,
+                         out_dtype: int | None = None) -> Tensor:
+        """qwen/attention.go:101-122 for one token: per-head q/k RMSNorm, RoPE and
+        the KV append in one launch. qkv [.., (Hq+2Hk)*128]; caches [1, Hk, cap, 128].
+        Returns q [1, Hq, 1, 128]."""
+        if q_norm.dtype != k_norm.dtype:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QKNormRoPEAppend: norm weights differ in dtype")
+        Dh = 128
+        cap = k_cache.shape[-2]
+        q = self.empty(out_dtype if out_dtype is not None else qkv.dtype, 1, n_heads, 1, Dh)
+        check(self._ctx, self._L.jh_qk_norm_rope_append(
+            self._ctx, qkv.ptr, qkv.dtype, n_heads, n_kv_heads, Dh, q_norm.ptr, k_norm.ptr, q_norm.dtype,
+            float(eps), float(base), float(scale), int(pos), k_cache.ptr, v_cache.ptr, k_cache.dtype, cap,
+            q.ptr, q.dtype))
+        return q
+
+    def QuantMatvecFused(self, x: Tensor, w: Tensor, scales: Tensor, biases: Tensor, groupSize: int, bits: int,
+                         prologue: int = _lib.JH_PRO_NONE, norm: Tensor | None = None, eps: float = 0.0,
+                         resid: Tensor | None = None, out: Tensor | None = None,
+                         out_dtype: int | None = None) -> Tensor:
+        """One-token QuantMatmul (transpose=true) with the operator before it
+        fused in (JH_PRO_RMSNORM: RMSNorm(x, norm, eps), the norm feeding q/k/v,
+        gate/up and the LM head; JH_PRO_SILU_MUL: x = [gate | up] ->
+        SiLU(gate)*up, qwen/mlp.go:33-35) and, with resid, the residual Add
+        after it (qwen/block.go:59-60) into an fp32 result (out may be resid)."""
+        if w.dtype != U32:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: weight tensor is not packed U32")
+        n, P = w.shape[-2], w.shape[-1]
+        k = P * (32 // bits)
+        want = 2 * k if prologue == _lib.JH_PRO_SILU_MUL else k
+        if x.numel != want:
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"QuantMatvecFused: x has {x.numel} elements, needs {want}")
+        if resid is not None and (resid.dtype != F32 or resid.numel != n):
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: resid must be F32 [out_features]")
+        if prologue == _lib.JH_PRO_RMSNORM and (norm is None or norm.numel != k):
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: RMSNorm needs a weight of in_features")
+        yd = F32 if resid is not None else (
+            out_dtype if out_dtype is not None else (out.dtype if out is not None else x.dtype))
+        y = out if out is not None else self.empty(yd, 1, n)
+        check(self._ctx, self._L.jh_quant_matvec_fused(
+            self._ctx, int(prologue), x.ptr, x.dtype, norm.ptr if norm is not None else None,
+            norm.dtype if norm is not None else BF16, float(eps), w.ptr, scales.ptr, biases.ptr,
+            self._sb_dtype(scales, biases), n, k, groupSize, bits, resid.ptr if resid is not None else None,
+            y.ptr, y.dtype))
+        return y
 
     def MoeRoute(self, logits: Tensor, k: int, normTopk: bool = True) -> tuple:
         """The router of MoEBlock.Forward (qwen/moe.go:455-491) on the device:

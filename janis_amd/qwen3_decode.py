@@ -1,0 +1,169 @@
+"""One Qwen3 decode step on the HIP backend, written against the engine mirror
+the way the reference's model code is written against engine.Backend:
+forwardCachedT (qwen/model.go:294-303) -> Block.ForwardCached
+(qwen/block.go:58-61) -> Attention.ForwardCached (qwen/attention.go:98-128) and
+MLP.Forward (qwen/mlp.go:32-36). It is the caller above the boundary, kept here
+only to drive the decode-step operators for tests and measurement.
+
+Two layout choices, both exact: q/k/v rows are stacked into one quantized matrix
+and gate/up into another at load time (QuantMatmul rows are independent, so one
+launch gives the same numbers as three or two), and the residual stream stays
+fp32 while the inputs of the quantized products are bf16.
+"""
+from __future__ import annotations
+
+import zlib
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _lib
+from .engine import BF16, F32, I32, HipBackend, Tensor
+
+
+@dataclass
+class Qwen3Config:
+    hidden: int = 4096
+    inter: int = 12288
+    n_heads: int = 32
+    n_kv: int = 8
+    head_dim: int = 128
+    vocab: int = 151936
+    layers: int = 36
+    eps: float = 1e-6
+    theta: float = 1e6
+    group_size: int = 64
+    bits: int = 4
+
+
+@dataclass
+class Qwen3Layer:
+    qkv: tuple          # (W, S, B) [(Hq+2Hk)*Dh, hidden/8]
+    o: tuple            # [hidden, Hq*Dh/8]
+    gate_up: tuple      # [2*inter, hidden/8]
+    down: tuple         # [hidden, inter/8]
+    in_norm: Tensor     # [hidden]
+    post_norm: Tensor   # [hidden]
+    q_norm: Tensor      # [head_dim]
+    k_norm: Tensor      # [head_dim]
+    k_cache: Tensor     # [1, Hk, capacity, Dh] bf16
+    v_cache: Tensor
+
+
+@dataclass
+class Qwen3Model:
+    cfg: Qwen3Config
+    embed: tuple        # QuantEmbedding (W, S, B) [vocab, hidden/8]
+    layers: list = field(default_factory=list)
+    norm: Tensor = None
+    lm_head: tuple = None  # None: tied to the embedding (QuantEmbedding.AsLinear)
+
+
+def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bool = True) -> tuple:
+    """Runs token (I32 [1], device) at position pos through every layer, appends
+    its keys/values to the caches, returns (logits F32 [1, vocab], next token I32 [1]).
+    fused=True takes the backend's fused operators: each norm inside the product
+    it feeds, SiLU*mul inside the down product, the residual adds in the o/down
+    products' epilogues, and the q/k norms, RoPE and KV append in one launch
+    (7 launches per layer). fused=False spells the step out as the reference's
+    separate operators (15 per layer)."""
+    c = m.cfg
+    gs, bits = c.group_size, c.bits
+    H, Hq, Hk, Dh, I = c.hidden, c.n_heads, c.n_kv, c.head_dim, c.inter
+    RMS, SWIGLU = _lib.JH_PRO_RMSNORM, _lib.JH_PRO_SILU_MUL
+    # QuantEmbedding.Forward (qwen/embed.go:78-83)
+    ew, es, eb = m.embed
+    h = b.Dequantize(b.TakeAxis(ew, token), b.TakeAxis(es, token), b.TakeAxis(eb, token), gs, bits)  # F32 [1, H]
+    for L in m.layers:
+        # Attention.ForwardCached
+        if fused:
+            qkv = b.QuantMatvecFused(h, *L.qkv, gs, bits, RMS, L.in_norm, c.eps, out_dtype=F32)
+            q = b.QKNormRoPEAppend(qkv, Hq, Hk, L.q_norm, L.k_norm, c.eps, c.theta, 1.0, pos, L.k_cache, L.v_cache)
+        else:
+            xn = b.RMSNorm(h, L.in_norm, c.eps, out_dtype=BF16)
+            qkv = b.QuantMatmul(xn, *L.qkv, True, gs, bits, out_dtype=F32)  # [1, (Hq+2Hk)*Dh]
+            q = _rows(b, qkv, 0, Hq * Dh, (1, Hq, 1, Dh))
+            k = _rows(b, qkv, Hq * Dh, Hk * Dh, (1, Hk, 1, Dh))
+            v = _rows(b, qkv, (Hq + Hk) * Dh, Hk * Dh, (1, Hk, 1, Dh))
+            q = b.RoPE(b.RMSNorm(q, L.q_norm, c.eps), Dh, False, c.theta, 1.0, pos)
+            k = b.RoPE(b.RMSNorm(k, L.k_norm, c.eps), Dh, False, c.theta, 1.0, pos)
+            b.AppendKV(L.k_cache, L.v_cache, pos, k, v)
+        att = b.Reshape(b.SDPA(q, L.k_cache, L.v_cache, Dh ** -0.5, False, kv_len=pos + 1, out_dtype=BF16), 1, Hq * Dh)
+        # the residual adds and MLP.Forward
+        if fused:
+            b.QuantMatvecFused(att, *L.o, gs, bits, resid=h, out=h)
+            gu = b.QuantMatvecFused(h, *L.gate_up, gs, bits, RMS, L.post_norm, c.eps, out_dtype=BF16)
+            b.QuantMatvecFused(gu, *L.down, gs, bits, SWIGLU, resid=h, out=h)
+        else:
+            h = b.Add(h, b.QuantMatmul(att, *L.o, True, gs, bits, out_dtype=F32))
+            xn = b.RMSNorm(h, L.post_norm, c.eps, out_dtype=BF16)
+            gu = b.QuantMatmul(xn, *L.gate_up, True, gs, bits, out_dtype=BF16)  # [1, 2I]
+            act = b.SiLUMul(_rows(b, gu, 0, I, (1, I)), _rows(b, gu, I, I, (1, I)))
+            h = b.Add(h, b.QuantMatmul(act, *L.down, True, gs, bits, out_dtype=F32))
+    head = m.lm_head if m.lm_head is not None else m.embed
+    if fused:
+        logits = b.QuantMatvecFused(h, *head, gs, bits, RMS, m.norm, c.eps, out_dtype=F32)
+    else:
+        logits = b.QuantMatmul(b.RMSNorm(h, m.norm, c.eps, out_dtype=BF16), *head, True, gs, bits, out_dtype=F32)
+    return logits, b.Argmax(logits)
+
+
+def _rows(b: HipBackend, t: Tensor, start: int, n: int, shape) -> Tensor:
+    """A view of n contiguous elements from `start` (Slice on the last axis of a
+    one-row tensor)."""
+    esz = 2 if t.dtype == BF16 else 4
+    return Tensor(b, t.ptr + start * esz, shape, t.dtype, owned=False, keep=t)
+
+
+def random_model(b: HipBackend, cfg: Qwen3Config, capacity: int, seed: int = 0, torch=None, dev=None):
+    """Random-init weights of the architecture (codes uniform 0..15, scales
+    |N(0,1)|*0.02, biases -8*scale + N(0, 1e-3), norm weights 1 + N(0, 0.05))
+    and zeroed bf16 caches of `capacity` rows. With torch given, everything is
+    generated on the device (the 8B model in seconds); otherwise with numpy from
+    janis_amd.synth and uploaded (small models). Returns (model, host copies or
+    None)."""
+    from . import synth
+    from .engine import U32
+    gs = cfg.group_size
+    H, Hq, Hk, Dh, I = cfg.hidden, cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.inter
+    host = {} if torch is None else None
+
+    def qlin(name, n, k):
+        if torch is not None:
+            shape = (n, k // 8)
+            w = torch.randint(-2**31, 2**31 - 1, shape, dtype=torch.int32, device=dev)
+            s = (torch.randn((n, k // gs), device=dev).abs() * 0.02).to(torch.bfloat16)
+            bb = (-8.0 * s.float() + torch.randn((n, k // gs), device=dev) * 1e-3).to(torch.bfloat16)
+            return (b.Wrap(w.data_ptr(), shape, U32, keep=w), b.Wrap(s.data_ptr(), s.shape, BF16, keep=s),
+                    b.Wrap(bb.data_ptr(), bb.shape, BF16, keep=bb))
+        q = synth.quant_linear(synth.stream_seed(seed, zlib.crc32(name.encode())), n, k, gs)
+        host[name] = q
+        return (b.FromRaw(U32, q.w, *q.w.shape), b.FromBF16Bits(q.s_bits, *q.s_bits.shape),
+                b.FromBF16Bits(q.b_bits, *q.b_bits.shape))
+
+    def normw(name, n):
+        if torch is not None:
+            t = (1.0 + 0.05 * torch.randn(n, device=dev)).to(torch.bfloat16)
+            return b.Wrap(t.data_ptr(), (n,), BF16, keep=t)
+        rng = np.random.default_rng(synth.stream_seed(seed, zlib.crc32(name.encode())))
+        bits = synth.f32_to_bf16_bits((1.0 + 0.05 * rng.standard_normal(n)).astype(np.float32))
+        host[name] = synth.bf16_bits_to_f32(bits)
+        return b.FromBF16Bits(bits, n)
+
+    def cache():
+        if torch is not None:
+            t = torch.zeros((1, Hk, capacity, Dh), dtype=torch.bfloat16, device=dev)
+            return b.Wrap(t.data_ptr(), tuple(t.shape), BF16, keep=t)
+        return b.FromBF16Bits(np.zeros((1, Hk, capacity, Dh), np.uint16), 1, Hk, capacity, Dh)
+
+    m = Qwen3Model(cfg, qlin("embed", cfg.vocab, H))
+    for l in range(cfg.layers):
+        m.layers.append(Qwen3Layer(
+            qkv=qlin(f"l{l}.qkv", (Hq + 2 * Hk) * Dh, H), o=qlin(f"l{l}.o", H, Hq * Dh),
+            gate_up=qlin(f"l{l}.gate_up", 2 * I, H), down=qlin(f"l{l}.down", H, I),
+            in_norm=normw(f"l{l}.in_norm", H), post_norm=normw(f"l{l}.post_norm", H),
+            q_norm=normw(f"l{l}.q_norm", Dh), k_norm=normw(f"l{l}.k_norm", Dh),
+            k_cache=cache(), v_cache=cache()))
+    m.norm = normw("norm", H)
+    m.lm_head = qlin("lm_head", cfg.vocab, H)
+    return m, host

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from janis_amd import synth
-from janis_amd.engine import BF16, F32, I32, U32, JanisHipError
+from janis_amd.engine import BF16, F16, F32, I32, U32, JanisHipError
 from tests.conftest import rel_ok, step, upload_quant
 
 pytestmark = pytest.mark.gpu
@@ -185,3 +185,109 @@ def test_append_kv(hip):
     assert np.array_equal(gv[:, :, :10], v0) and np.array_equal(gv[:, :, 10:11], _bf16(v1))
     with pytest.raises(JanisHipError):
         hip.AppendKV(kc, vc, 64, _put(hip, k1, F32), _put(hip, v1, F32))
+
+
+def test_qk_norm_rope_append_matches_separate_ops(hip, oracle):
+    """jh_qk_norm_rope_append against the oracle's RMSNorm + RoPE and the cache rows."""
+    rng = np.random.default_rng(15)
+    Hq, Hk, Dh, cap, pos = 32, 8, 128, 40, 33
+    qkv = rng.standard_normal((1, (Hq + 2 * Hk) * Dh)).astype(np.float32)
+    qn, kn = _bf16(1 + 0.1 * rng.standard_normal(Dh)), _bf16(1 + 0.1 * rng.standard_normal(Dh))
+    kc, vc = hip.empty(BF16, 1, Hk, cap, Dh), hip.empty(BF16, 1, Hk, cap, Dh)
+    step("jh_qk_norm_rope_append")
+    q = hip.Floats(hip.QKNormRoPEAppend(hip.FromFloats(qkv), Hq, Hk, _put(hip, qn, BF16), _put(hip, kn, BF16), 1e-6,
+                                        1e6, 1.0, pos, kc, vc, out_dtype=F32))
+    qh = qkv[0, :Hq * Dh].reshape(1, Hq, 1, Dh)
+    kh = qkv[0, Hq * Dh:(Hq + Hk) * Dh].reshape(1, Hk, 1, Dh)
+    vh = qkv[0, (Hq + Hk) * Dh:].reshape(1, Hk, 1, Dh)
+    want_q = oracle.rope(oracle.rms_norm(qh, qn, 1e-6), Dh, False, 1e6, 1.0, pos)
+    want_k = oracle.rope(oracle.rms_norm(kh, kn, 1e-6), Dh, False, 1e6, 1.0, pos)
+    ok, dd, sc = rel_ok(q, want_q, 1e-5)
+    assert ok, (dd, sc)
+    gk, gv = hip.Floats(kc), hip.Floats(vc)
+    ok, dd, sc = rel_ok(gk[:, :, pos:pos + 1], want_k, 1e-2)
+    assert ok, (dd, sc)
+    assert np.array_equal(gv[:, :, pos:pos + 1], _bf16(vh))
+
+
+def _fused_case(rng, N, K, gs=64, seed=0):
+    q = synth.quant_linear(seed or N + K, N, K, gs)
+    h = (3.0 * rng.standard_normal((1, K))).astype(np.float32)
+    nw = _bf16(1 + 0.1 * rng.standard_normal(K))
+    return q, h, nw
+
+
+@pytest.mark.parametrize("N,K", [(6144, 4096), (70000, 4096), (4096, 12288), (300, 960)])
+def test_quant_matvec_fused_rmsnorm(hip, oracle, N, K):
+    """RMSNorm -> QuantMatmul in one call (the norm feeding q/k/v, gate/up and
+    the LM head): against the oracle's RMSNorm, bf16 rounding, QuantMatmul, and
+    against the backend's own two-launch composition. (300, 960) is outside the
+    register tiles and takes the composed path."""
+    from janis_amd import _lib
+    rng = np.random.default_rng(N + K)
+    q, h, nw = _fused_case(rng, N, K)
+    w, s, b = upload_quant(hip, q)
+    hd, nwd = hip.FromFloats(h), _put(hip, nw, BF16)
+    step(f"jh_quant_matvec_fused RMSNorm N={N} K={K}")
+    got = hip.Floats(hip.QuantMatvecFused(hd, w, s, b, 64, 4, _lib.JH_PRO_RMSNORM, nwd, 1e-6, out_dtype=F32))
+    xn = _bf16(oracle.rms_norm(h, nw, 1e-6))
+    want = oracle.quant_matmul(xn, q.w, q.s, q.b, 64)
+    ok, dd, sc = rel_ok(got, want, 1e-2)
+    assert ok, (dd, sc)
+    comp = hip.Floats(hip.QuantMatmul(hip.RMSNorm(hd, nwd, 1e-6, out_dtype=BF16), w, s, b, True, 64, 4,
+                                      out_dtype=F32))
+    ok, dd, sc = rel_ok(got, comp, 1e-3)
+    assert ok, (dd, sc)
+    gb = hip.Floats(hip.QuantMatvecFused(hd, w, s, b, 64, 4, _lib.JH_PRO_RMSNORM, nwd, 1e-6, out_dtype=BF16))
+    ok, dd, sc = rel_ok(gb, want, 1e-2)
+    assert ok, (dd, sc)
+
+
+@pytest.mark.parametrize("N,K", [(4096, 12288), (1024, 3072), (200, 960)])
+def test_quant_matvec_fused_swiglu_resid(hip, oracle, N, K):
+    """Mul(SiLU(gate), up) -> QuantMatmul -> Add(resid, .) in one call (the
+    down product of MLP.Forward and the block's second residual add), written
+    in place into the fp32 residual stream."""
+    from janis_amd import _lib
+    rng = np.random.default_rng(N * 3 + K)
+    q = synth.quant_linear(N + 7 * K, N, K, 64)
+    w, s, b = upload_quant(hip, q)
+    gu = _bf16(2.0 * rng.standard_normal((1, 2 * K)))
+    resid = (10.0 * rng.standard_normal((1, N))).astype(np.float32)
+    hd = hip.FromFloats(resid)
+    step(f"jh_quant_matvec_fused SiLU*mul + resid N={N} K={K}")
+    out = hip.QuantMatvecFused(_put(hip, gu, BF16), w, s, b, 64, 4, _lib.JH_PRO_SILU_MUL, resid=hd, out=hd)
+    assert out is hd
+    got = hip.Floats(hd)
+    act = _bf16(oracle.silu(gu[:, :K]) * gu[:, K:])
+    prod = oracle.quant_matmul(act, q.w, q.s, q.b, 64)
+    ok, dd, sc = rel_ok(got - resid, prod, 1e-2)
+    assert ok, (dd, sc)
+    ok, dd, sc = rel_ok(got, resid + prod, 1e-3)
+    assert ok, (dd, sc)
+
+
+@pytest.mark.parametrize("N,K,sb", [(4096, 4096, BF16), (4096, 4096, "f16")])
+def test_quant_matvec_fused_resid_only(hip, oracle, N, K, sb):
+    """QuantMatmul -> Add(resid, .) (the o product and the block's first
+    residual add); with f16 scales it is composed from two launches."""
+    from janis_amd import _lib
+    rng = np.random.default_rng(N + K + 1)
+    q = synth.quant_linear(N + K + 3, N, K, 64)
+    w, s, b = upload_quant(hip, q)
+    if sb == "f16":
+        s = hip.FromRaw(F16, q.s.astype(np.float16), *q.s.shape)
+        b = hip.FromRaw(F16, q.b.astype(np.float16), *q.b.shape)
+    x = _bf16(rng.standard_normal((1, K)))
+    resid = rng.standard_normal((1, N)).astype(np.float32)
+    hd = hip.FromFloats(resid)
+    step(f"jh_quant_matvec_fused resid N={N} K={K} scales={sb}")
+    hip.QuantMatvecFused(_put(hip, x, BF16), w, s, b, 64, 4, resid=hd, out=hd)
+    got = hip.Floats(hd)
+    sc_ = q.s.astype(np.float16).astype(np.float32) if sb == "f16" else q.s
+    bi_ = q.b.astype(np.float16).astype(np.float32) if sb == "f16" else q.b
+    want = resid + oracle.quant_matmul(x, q.w, sc_, bi_, 64)
+    ok, dd, sc = rel_ok(got, want, 1e-3)
+    assert ok, (dd, sc)
+    with pytest.raises(JanisHipError):
+        hip.QuantMatvecFused(_put(hip, x, BF16), w, s, b, 64, 4, resid=hip.FromFloats(resid[:, :10]))

@@ -1,0 +1,72 @@
+"""A small random Qwen3 decoded token by token on the GPU (config-4's step at a
+size the oracle finishes in seconds) against the same step composed from the
+oracle's operators, following qwen/model.go:294-303, qwen/block.go:58-61,
+qwen/attention.go:98-128 and qwen/mlp.go:32-36.
+
+The GPU feeds bf16 inputs to the quantized products and keeps a bf16 KV cache;
+the oracle is fp32 throughout, so logits are held to 3e-2 of max|logit| and the
+greedy token to equality whenever the oracle's top-2 margin exceeds that bar.
+Both sides are fed the same tokens (the GPU's choice) so a near-tie cannot make
+the trajectories diverge.
+"""
+import numpy as np
+import pytest
+
+from janis_amd.engine import F32
+from janis_amd.qwen3_decode import Qwen3Config, decode_step, random_model
+from tests.conftest import rel_ok, step
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_step(o, cfg, host, token, pos, kc, vc):
+    gs, eps = cfg.group_size, cfg.eps
+    H, Hq, Hk, Dh, I = cfg.hidden, cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.inter
+    e = host["embed"]
+    h = o.dequantize(e.w[[token]], e.s[[token]], e.b[[token]], gs)  # [1, H]
+    for l in range(cfg.layers):
+        q_ = lambda n: host[f"l{l}.{n}"]
+        xn = o.rms_norm(h, q_("in_norm"), eps)
+        w = q_("qkv")
+        qkv = o.quant_matmul(xn, w.w, w.s, w.b, gs)[0]
+        q = o.rms_norm(qkv[:Hq * Dh].reshape(1, Hq, 1, Dh), q_("q_norm"), eps)
+        k = o.rms_norm(qkv[Hq * Dh:(Hq + Hk) * Dh].reshape(1, Hk, 1, Dh), q_("k_norm"), eps)
+        v = qkv[(Hq + Hk) * Dh:].reshape(1, Hk, 1, Dh)
+        q = o.rope(q, Dh, False, cfg.theta, 1.0, pos)
+        k = o.rope(k, Dh, False, cfg.theta, 1.0, pos)
+        kc[l][:, :, pos:pos + 1], vc[l][:, :, pos:pos + 1] = k, v
+        att = o.sdpa(q, kc[l][:, :, :pos + 1], vc[l][:, :, :pos + 1], Dh ** -0.5, False).reshape(1, Hq * Dh)
+        w = q_("o")
+        h = (h + o.quant_matmul(att, w.w, w.s, w.b, gs)).astype(np.float32)
+        xn = o.rms_norm(h, q_("post_norm"), eps)
+        w = q_("gate_up")
+        gu = o.quant_matmul(xn, w.w, w.s, w.b, gs)[0]
+        act = (o.silu(gu[:I]) * gu[I:]).astype(np.float32)[None]
+        w = q_("down")
+        h = (h + o.quant_matmul(act, w.w, w.s, w.b, gs)).astype(np.float32)
+    hn = o.rms_norm(h, host["norm"], eps)
+    w = host["lm_head"]
+    return o.quant_matmul(hn, w.w, w.s, w.b, gs)[0]
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_qwen3_small_decode_matches_oracle(hip, oracle, fused):
+    cfg = Qwen3Config(hidden=512, inter=1024, n_heads=4, n_kv=2, head_dim=128, vocab=1000, layers=2)
+    cap, steps = 32, 6
+    m, host = random_model(hip, cfg, cap, seed=5)
+    kc = [np.zeros((1, cfg.n_kv, cap, cfg.head_dim), np.float32) for _ in range(cfg.layers)]
+    vc = [np.zeros((1, cfg.n_kv, cap, cfg.head_dim), np.float32) for _ in range(cfg.layers)]
+    token = 17
+    for pos in range(steps):
+        step(f"qwen3 small decode fused={fused} pos={pos} token={token}")
+        logits, nxt = decode_step(hip, m, hip.FromInt32(np.array([token], np.int32)), pos, fused=fused)
+        got = hip.Floats(logits)[0]
+        want = _oracle_step(oracle, cfg, host, token, pos, kc, vc)
+        ok, d, sc = rel_ok(got, want, 3e-2)
+        assert ok, (pos, d, sc)
+        g = int(hip.Ints(nxt)[0])
+        assert g == int(np.argmax(got))
+        top2 = np.sort(want)[-2:]
+        if top2[1] - top2[0] > 3e-2 * sc:
+            assert g == int(np.argmax(want)), (pos, g, int(np.argmax(want)))
+        token = g
