@@ -231,6 +231,38 @@ JH_API int jh_qk_norm_rope_append(jh_ctx *ctx, const void *qkv, jh_dtype qkv_dty
                            float rope_scale, int64_t pos, void *k_cache, void *v_cache,
                            jh_dtype cache_dtype, int64_t capacity, void *q_out, jh_dtype q_out_dtype);
 
+/* Attention.ForwardCached for one new token (qwen/attention.go:98-128) after
+ * the q/k/v product, in one launch, for a backend that offers it: the work of
+ * jh_qk_norm_rope_append (per-head q/k RMSNorm when q_norm_w/k_norm_w are given,
+ * non-traditional RoPE at pos, the new key and value rows written to row pos of
+ * the caches) followed by jh_sdpa over keys 0..pos (Lq = 1, one query row per
+ * head), with the same arithmetic. The new key and value enter the softmax as
+ * the bf16 values written to the cache. One launch when the cache is short;
+ * longer ones split the keys over blocks, which write partial softmaxes to the
+ * context's workspace for a second, merging launch.
+ *   qkv       [(n_heads + 2 n_kv_heads) * 128]: q heads, then k heads, then v heads
+ *   rope_cs   NULL, or jh_rope_table(128, rope_base, rope_scale, pos) (the same
+ *             factors, computed once for all layers)
+ *   caches    bf16 [n_kv_heads, capacity, 128]; pos < capacity
+ *   out       [n_heads * 128] (the input of the o product)
+ * head_dim must be 128, n_heads / n_kv_heads 1, 2, 4 or 8. */
+JH_API int jh_attention_decode(jh_ctx *ctx, const void *qkv, jh_dtype qkv_dtype, int64_t n_heads,
+                        int64_t n_kv_heads, int64_t head_dim, const void *q_norm_w,
+                        const void *k_norm_w, jh_dtype w_dtype, float eps, float rope_base,
+                        float rope_scale, const float *rope_cs, int64_t pos, void *k_cache,
+                        void *v_cache, jh_dtype cache_dtype, int64_t capacity, float scale, void *out,
+                        jh_dtype out_dtype);
+
+/* The RoPE factors at one position, for callers that rotate many heads there
+ * (the RoPE angles of cpu/cpu_attn.go:13-34): out[i] = cos(theta_i) and
+ * out[dims/2 + i] = sin(theta_i), theta_i = pos * scale * inv_i, inv_i =
+ * base^(-2i/dims) or 1/freqs[i] (freqs fp32 [dims/2], may be NULL); pow, cos
+ * and sin in double, rounded to fp32, as jh_rope evaluates them. out is fp32
+ * [dims], device. Computed once per decode step, it serves every layer's
+ * jh_attention_decode (rope_cs), which otherwise evaluates them in each block. */
+JH_API int jh_rope_table(jh_ctx *ctx, int dims, float base, float scale, int64_t pos, const float *freqs,
+                  float *out);
+
 /* The router of MoEBlock.Forward (qwen/moe.go:455-491) on the device, for a
  * backend that offers it: per token, softmax over the n_experts logits
  * (cpu/cpu.go:461-499), the k largest by the reference's selection sort
@@ -280,9 +312,9 @@ JH_API int jh_moe_swiglu(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t n
                   const int32_t *rhs_indices, const float *scores, int64_t k_slots,
                   int group_size, int bits, void *out, jh_dtype out_dtype);
 
-/* Prologues of jh_quant_matvec_fused. */
+/* Prologues and epilogues of jh_quant_matvec_fused. */
 typedef enum {
-    JH_PRO_NONE = 0,     /* x_in = x (JH_BF16 or JH_F32) */
+    JH_PRO_NONE = 0,     /* x_in = x */
     JH_PRO_RMSNORM = 1,  /* x_in = RMSNorm(x, norm_w, eps): Block.ForwardCached's InputNorm /
                             PostNorm feeding q/k/v and gate/up (qwen/block.go:59-60), and the
                             final norm feeding the LM head (qwen/model.go:294-303) */
@@ -290,31 +322,47 @@ typedef enum {
                             MLP.Forward's input to Down (qwen/mlp.go:33-35) */
 } jh_prologue;
 
+typedef enum {
+    JH_EPI_STORE = 0,    /* y = x_in . W^T */
+    JH_EPI_RESID = 1,    /* y = resid + x_in . W^T in fp32 (y_dtype JH_F32; resid may be y):
+                            the residual adds of Block.ForwardCached (qwen/block.go:59-60) */
+    JH_EPI_SWIGLU = 2    /* W holds 2 * out_features rows, the Gate rows then the Up rows
+                            (scales/biases likewise): y[j] = SiLU(g_j) * u_j with
+                            g = x_in . Gate^T, u = x_in . Up^T in fp32 (MLP.Forward's
+                            Mul(SiLU(Gate.Forward(x)), Up.Forward(x)), qwen/mlp.go:33-35) */
+} jh_epilogue;
+
 /* One decode product with the operators on either side of it, for a backend
  * that offers it (the engine's optional-capability pattern,
  * engine/backend.go:38-112). It replaces the reference's sequences
- *   RMSNorm -> QuantMatmul            (prologue JH_PRO_RMSNORM)
- *   Mul(SiLU(gate), up) -> QuantMatmul (prologue JH_PRO_SILU_MUL)
- *   QuantMatmul -> Add(resid, .)       (resid != NULL: the residual adds of
- *                                       qwen/block.go:59-60)
+ *   RMSNorm -> QuantMatmul                 (prologue JH_PRO_RMSNORM)
+ *   Mul(SiLU(gate), up) -> QuantMatmul      (prologue JH_PRO_SILU_MUL)
+ *   QuantMatmul -> Add(resid, .)            (epilogue JH_EPI_RESID)
+ *   QuantMatmul(Gate), QuantMatmul(Up) -> Mul(SiLU(.), .)  (epilogue JH_EPI_SWIGLU)
  * for one row (rows == 1 of jh_quant_matmul, transpose = true):
- *   x_in = bf16(prologue(x))            (as jh_rms_norm / jh_elementwise with a bf16 out)
- *   y    = x_in . W^T                   (fp32 accumulation, as jh_quant_matmul)
- *   y    = resid + y                    (fp32; y_dtype must be JH_F32; resid may be y)
- * The prologue is computed inside the product's launch (each block
- * normalises its own copy of x, so no normalised copy goes through HBM) and the
- * add in its epilogue: one launch instead of two or three. Shapes outside the
- * decode tiles (see the quantized operators above), f16 scales with a
- * prologue or add, or other dtypes run the same arithmetic as separate
- * launches through the context's workspace.
- *   JH_PRO_RMSNORM   x fp32 (the residual stream) [in_features], norm_w bf16
- *                    [in_features] for the one-launch path (any dtypes otherwise)
- *   JH_PRO_SILU_MUL  x [2 * in_features] bf16 (the gate/up product) */
+ *   x_in = bf16(prologue(x))  (as jh_rms_norm / jh_elementwise with a bf16 out)
+ *   the product with fp32 accumulation (as jh_quant_matmul), then the epilogue.
+ * On the one-launch path RMSNorm is applied as (bf16(x * norm_w) . W^T) /
+ * sqrt(mean(x^2) + eps): the same value up to where the bf16 rounding of the
+ * product's input falls (the product is linear in it), with no reduction
+ * ahead of the weight stream.
+ * One launch where the decode tiles take the shape (4-bit weights, group size
+ * 32/64/128, bf16 scales, K = in_features in {256, 512, 768, 1024, 1536, 2048,
+ * 3072, 4096, 6144, 8192, 12288, 16384}) and
+ *   JH_PRO_NONE with JH_EPI_STORE or JH_EPI_RESID, x bf16, or
+ *   JH_PRO_RMSNORM with JH_EPI_STORE or JH_EPI_SWIGLU, x fp32, norm_w bf16:
+ * each block normalises its own copy of x in registers (no normalised copy
+ * goes through HBM) and the add or SwiGLU happens in the product's epilogue.
+ * Everything else runs the same arithmetic as separate launches through the
+ * context's workspace.
+ *   x       [in_features] ([2 * in_features] for JH_PRO_SILU_MUL), device
+ *   resid   fp32 [out_features] for JH_EPI_RESID, else ignored
+ *   y       [out_features] of y_dtype */
 JH_API int jh_quant_matvec_fused(jh_ctx *ctx, jh_prologue prologue, const void *x, jh_dtype x_dtype,
                           const void *norm_w, jh_dtype norm_w_dtype, float eps, const uint32_t *w,
                           const void *scales, const void *biases, jh_dtype sb_dtype,
                           int64_t out_features, int64_t in_features, int group_size, int bits,
-                          const float *resid, void *y, jh_dtype y_dtype);
+                          jh_epilogue epilogue, const float *resid, void *y, jh_dtype y_dtype);
 
 #ifdef __cplusplus
 }

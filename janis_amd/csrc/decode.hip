@@ -34,8 +34,7 @@ __device__ __forceinline__ void st_act(void* p, int64_t i, float v, int dt) {
 
 // Sum over a block of 256 threads; every thread gets the total.
 __device__ float block_sum256(float v, float* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = wave_sum(v);
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
     __syncthreads();
     if (l == 0) red[w] = v;
@@ -71,8 +70,7 @@ __global__ __launch_bounds__(256) void rms_norm_wave_kernel(const void* __restri
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < PER; e++) ss = fmaf(v[e], v[e], ss);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    ss = wave_sum(ss);
     const float inv = 1.0f / (float)sqrt((double)(ss / (float)d + eps));
 #pragma unroll
     for (int e = 0; e < PER; e++) {
@@ -147,6 +145,21 @@ __global__ __launch_bounds__(256) void rope_kernel(const void* __restrict__ x, i
     }
 }
 
+// cos and sin of the RoPE angles at one position: out[i] = cos(theta_i),
+// out[dims/2 + i] = sin(theta_i), theta_i = pos * scale * inv_i with the same
+// inv_i and double evaluation as rope_kernel. Kernels that rotate many heads at
+// one position read these instead of each evaluating pow/cos/sin in double.
+__global__ __launch_bounds__(64) void rope_table_kernel(int dims, float base, float scale, int64_t pos,
+                                                         const float* __restrict__ freqs, float* __restrict__ out) {
+    const int half = dims / 2;
+    for (int i = threadIdx.x; i < half; i += 64) {
+        const float inv = freqs ? 1.0f / freqs[i] : (float)pow((double)base, -(double)(2 * i) / (double)dims);
+        const float theta = (float)pos * scale * inv;
+        out[i] = (float)cos((double)theta);
+        out[half + i] = (float)sin((double)theta);
+    }
+}
+
 // ---- SDPA, general: one block per (b, h, query row) --------------------------------
 // q [B, Hq, Lq, Dh]; k/v [B, Hk, kcap, Dh] with the first Lk rows valid.
 __global__ __launch_bounds__(256) void sdpa_rows_kernel(const void* __restrict__ q, int q_dt,
@@ -173,8 +186,7 @@ __global__ __launch_bounds__(256) void sdpa_rows_kernel(const void* __restrict__
         for (int d = 0; d < Dh; d++) s = fmaf(qs[d], ld_act(k, kbase + (int64_t)j * Dh + d, kv_dt), s);
         mx = fmaxf(mx, s * scale);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = wave_max(mx);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
@@ -209,22 +221,8 @@ __global__ __launch_bounds__(256) void sdpa_rows_kernel(const void* __restrict__
 // loads of bf16 keys), partial dots reduced across the 16 lanes with xor
 // shuffles so every lane of the group holds the score. Each lane keeps, for every
 // query head of the group, a running max, sum and 8 output features.
-constexpr int kDecodeMaxGroup = 8;  // query heads per kv head
 constexpr int kDecodeDh = 128;
 
-// Sum over each row of 16 lanes, the total in every lane, with DPP (VALU only):
-// xor 1 and xor 2 inside quads, then the mirrors of 8 and of 16 lanes.
-__device__ __forceinline__ float row16_sum(float v) {
-    auto dpp = [](float x, auto ctrl) {
-        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
-                                                                     decltype(ctrl)::value, 0xF, 0xF, false));
-    };
-    v += dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
-    v += dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
-    v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
-    v += dpp(v, std::integral_constant<int, 0x140>{});  // row_mirror
-    return v;
-}
 
 template <int G>
 __global__ __launch_bounds__(256) void sdpa_decode_split_kernel(const void* __restrict__ q, int q_dt,
@@ -327,15 +325,14 @@ __global__ __launch_bounds__(256) void sdpa_decode_split_kernel(const void* __re
     }
 }
 
-// Merge the splits of one (b, query head): thread d owns feature d. The splits'
-// maxima and sums are staged in LDS first so no load waits on another.
+// Merge the splits of one (b, query head): thread d owns feature d. The splits
+// are read 16 at a time, each chunk's loads issued together (one memory round
+// trip per chunk), and folded in with an online rescale.
 constexpr int kMaxSplits = 1024;
 
 __global__ __launch_bounds__(128) void sdpa_decode_merge_kernel(const float* __restrict__ part, int Hk, int G,
                                                                 int nsplit, void* __restrict__ out, int out_dt) {
-    constexpr int Dh = kDecodeDh;
-    __shared__ float sm[kMaxSplits], sc[kMaxSplits];
-    __shared__ float red[2];
+    constexpr int Dh = kDecodeDh, C = 16;
     const int bh = blockIdx.x;  // b*Hq + h
     const int Hq = Hk * G;
     const int b = bh / Hq, h = bh - b * Hq;
@@ -343,32 +340,63 @@ __global__ __launch_bounds__(128) void sdpa_decode_merge_kernel(const float* __r
     const int d = threadIdx.x;
     const int64_t stride = (int64_t)G * (Dh + 2);
     const float* base = part + ((int64_t)(b * Hk + hk) * nsplit) * stride + g * (Dh + 2);
-    float M = -__builtin_inff();
-    for (int s = d; s < nsplit; s += 128) {
-        sm[s] = base[s * stride];
-        M = fmaxf(M, sm[s]);
-    }
+    float M = -__builtin_inff(), L = 0.0f, A = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += C) {
+        float mv[C], lv[C], av[C];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    if ((d & 63) == 0) red[d >> 6] = M;
-    __syncthreads();
-    M = fmaxf(red[0], red[1]);
-    float L = 0.0f;
-    for (int s = d; s < nsplit; s += 128) {
-        const float c = sm[s] == -__builtin_inff() ? 0.0f : __expf(sm[s] - M);
-        sc[s] = c;
-        L = fmaf(base[s * stride + 1], c, L);
-    }
+        for (int u = 0; u < C; u++) {
+            const bool in = s0 + u < nsplit;
+            const float* ps = base + (int64_t)(in ? s0 + u : nsplit - 1) * stride;  // in bounds either way
+            mv[u] = in ? ps[0] : -__builtin_inff();
+            lv[u] = in ? ps[1] : 0.0f;
+            av[u] = in ? ps[2 + d] : 0.0f;
+        }
+        float mn = M;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
-    __syncthreads();
-    if ((d & 63) == 0) red[d >> 6] = L;
-    __syncthreads();
-    L = red[0] + red[1];
-    float A = 0.0f;
-#pragma unroll 8
-    for (int s = 0; s < nsplit; s++) A = fmaf(base[s * stride + 2 + d], sc[s], A);
+        for (int u = 0; u < C; u++) mn = fmaxf(mn, mv[u]);
+        if (mn == -__builtin_inff()) continue;  // no keys so far
+        const float corr = __expf(M - mn);
+        L *= corr;
+        A *= corr;
+#pragma unroll
+        for (int u = 0; u < C; u++) {
+            const float c = __expf(mv[u] - mn);
+            L = fmaf(lv[u], c, L);
+            A = fmaf(av[u], c, A);
+        }
+        M = mn;
+    }
     st_act(out, (int64_t)bh * Dh + d, A / L, out_dt);
+}
+
+// Per-head RMSNorm of one 128-feature head held as lane i: (a, b) = features
+// (i, i + 64) of a wave; w == nullptr skips the norm (heads without QNorm/KNorm).
+__device__ __forceinline__ void head_rms_norm(float& a, float& b, const void* w, int w_dt, float eps, int i) {
+    if (!w) return;
+    const float ss = wave_sum(fmaf(a, a, b * b));
+    const float inv = 1.0f / (float)sqrt((double)(ss / 128.0f + eps));
+    a = (a * inv) * ld_act(w, i, w_dt);
+    b = (b * inv) * ld_act(w, i + 64, w_dt);
+}
+
+// Non-traditional RoPE of the pair (i, i + 64) of a 128-feature head at `pos`:
+// angle pos * scale * base^(-2i/128), cos/sin/pow in double.
+// With `cs` (rope_table_kernel's output for this position) the factors are read.
+__device__ __forceinline__ void head_rope(float& a, float& b, float base, float scale, int64_t pos, int i,
+                                          const float* cs = nullptr) {
+    float c, sn;
+    if (cs) {
+        c = cs[i];
+        sn = cs[64 + i];
+    } else {
+        const float fi = (float)pow((double)base, -(double)(2 * i) / 128.0);
+        const float theta = (float)pos * scale * fi;
+        c = (float)cos((double)theta);
+        sn = (float)sin((double)theta);
+    }
+    const float ra = a * c - b * sn, rb = a * sn + b * c;
+    a = ra;
+    b = rb;
 }
 
 // ---- Qwen3 attention prologue: per-head q/k RMSNorm, RoPE, KV append ------------
@@ -395,17 +423,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
         return;
     }
     const bool is_q = head < Hq;
-    const void* w = is_q ? qn_w : kn_w;
-    float ss = fmaf(a, a, b * b);
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) ss += __shfl_xor(ss, s, 64);
-    const float inv = 1.0f / (float)sqrt((double)(ss / (float)Dh + eps));
-    a = (a * inv) * ld_act(w, i, w_dt);
-    b = (b * inv) * ld_act(w, i + half, w_dt);
-    const float fi = (float)pow((double)base, -(double)(2 * i) / (double)Dh);
-    const float theta = (float)pos * scale * fi;
-    const float c = (float)cos((double)theta), sn = (float)sin((double)theta);
-    const float ra = a * c - b * sn, rb = a * sn + b * c;
+    head_rms_norm(a, b, is_q ? qn_w : kn_w, w_dt, eps, i);
+    head_rope(a, b, base, scale, pos, i);
+    const float ra = a, rb = b;
     if (is_q) {
         st_act(q_out, o + i, ra, q_dt);
         st_act(q_out, o + i + half, rb, q_dt);
@@ -413,6 +433,245 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
         const int64_t dst = ((int64_t)(head - Hq) * cap + pos) * Dh;
         st_act(kc, dst + i, ra, c_dt);
         st_act(kc, dst + i + half, rb, c_dt);
+    }
+}
+
+// ---- one-token attention in one launch ---------------------------------------------
+// Attention.ForwardCached for one new token (qwen/attention.go:98-128) after the
+// q/k/v product: per-head q/k RMSNorm and RoPE, the KV-cache append, and SDPA
+// over keys 0..pos. Block (split, hk) takes keys [split*kps, min(pos+1,
+// (split+1)*kps)) for the G = Hq/Hk query heads of kv head hk:
+//   1. its K/V rows are requested first (they do not depend on q), then every
+//      block normalises and rotates its G query heads into LDS (a few hundred
+//      flops, cheaper than a launch); the block whose range holds `pos`
+//      normalises and rotates the new key, writes the new key and value rows to
+//      the caches, and scores them from LDS (bf16-rounded, as the cache holds
+//      them), never reading row pos back;
+//   2. 16 key slots per block (4 per wave, a 16-lane row per key, 8 features per
+//      lane) run an online softmax over the slot's keys, 4 keys per load batch;
+//   3. the slots merge in registers (cross-row permlane swaps) and then across
+//      the 4 waves in LDS;
+//   4. with one split the block writes the output; otherwise (max, sum,
+//      weighted values) go to the workspace in sdpa_decode_split_kernel's
+//      layout and sdpa_decode_merge_kernel merges them. (A last-block merge in
+//      the same launch needs an agent-scope release per block, an L2 writeback
+//      on this multi-L2 part, which cost ten times the merge launch.)
+struct AttnArgs {
+    const void* qkv;    // [(Hq + 2 Hk) * 128]: q heads, k heads, v heads
+    int qkv_dt;
+    const void* qn_w;   // [128] or nullptr
+    const void* kn_w;
+    int w_dt;
+    float eps, base, rscale, scale;
+    const float* rope_cs;  // [128]: cos, sin at pos (rope_table_kernel), or nullptr
+    int64_t pos;
+    uint16_t* kc;       // bf16 [Hk, cap, 128]
+    uint16_t* vc;
+    int64_t cap;
+    int Hk, nsplit, kps;
+    float* part;        // [Hk, nsplit, G, 130]
+    void* out;          // [Hq * 128]
+    int out_dt;
+};
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+    constexpr int Dh = 128, U = 4;
+    const int split = blockIdx.x, hk = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int kg = lane >> 4, kl = lane & 15;
+    const int Hq = a.Hk * G;
+    const int64_t Lk = a.pos + 1;
+    const int64_t j_begin = (int64_t)split * a.kps;
+    const int64_t j_end = min(Lk, j_begin + a.kps);
+    const bool owner = a.pos < j_end;  // the last split holds the new key
+    const int64_t jc_end = min(j_end, a.pos);  // cache rows scored by this block
+    const uint16_t* kb = a.kc + (int64_t)hk * a.cap * Dh + 8 * kl;
+    const uint16_t* vb = a.vc + (int64_t)hk * a.cap * Dh + 8 * kl;
+    const int slot = wave * 4 + kg;
+
+    // 1. the first batch of K/V rows, then the query heads (and the new key)
+    uint4 kr[U], vr[U];
+    auto load_batch = [&](int64_t j0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t j = j0 + 16 * u;
+            if (j < jc_end) {
+                kr[u] = *reinterpret_cast<const uint4*>(kb + j * Dh);
+                vr[u] = *reinterpret_cast<const uint4*>(vb + j * Dh);
+            } else {
+                kr[u] = make_uint4(0, 0, 0, 0);
+                vr[u] = make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    int64_t j0 = j_begin + slot;
+    load_batch(j0);
+
+    __shared__ float q_s[G][Dh];
+    __shared__ float kn_s[Dh], vn_s[Dh];
+    for (int g = wave; g < G; g += 4) {
+        const int64_t o = (int64_t)(hk * G + g) * Dh;
+        float x0 = ld_act(a.qkv, o + lane, a.qkv_dt), x1 = ld_act(a.qkv, o + lane + 64, a.qkv_dt);
+        head_rms_norm(x0, x1, a.qn_w, a.w_dt, a.eps, lane);
+        head_rope(x0, x1, a.base, a.rscale, a.pos, lane, a.rope_cs);
+        q_s[g][lane] = x0 * a.scale;
+        q_s[g][lane + 64] = x1 * a.scale;
+    }
+    if (owner && wave == 3) {
+        const int64_t ok = (int64_t)(Hq + hk) * Dh, ov = (int64_t)(Hq + a.Hk + hk) * Dh;
+        float k0 = ld_act(a.qkv, ok + lane, a.qkv_dt), k1 = ld_act(a.qkv, ok + lane + 64, a.qkv_dt);
+        const float v0 = ld_act(a.qkv, ov + lane, a.qkv_dt), v1 = ld_act(a.qkv, ov + lane + 64, a.qkv_dt);
+        head_rms_norm(k0, k1, a.kn_w, a.w_dt, a.eps, lane);
+        head_rope(k0, k1, a.base, a.rscale, a.pos, lane, a.rope_cs);
+        const uint16_t bk0 = f32_to_bf16(k0), bk1 = f32_to_bf16(k1);
+        const uint16_t bv0 = f32_to_bf16(v0), bv1 = f32_to_bf16(v1);
+        const int64_t row = ((int64_t)hk * a.cap + a.pos) * Dh;
+        a.kc[row + lane] = bk0;
+        a.kc[row + lane + 64] = bk1;
+        a.vc[row + lane] = bv0;
+        a.vc[row + lane + 64] = bv1;
+        kn_s[lane] = bf16_to_f32(bk0);
+        kn_s[lane + 64] = bf16_to_f32(bk1);
+        vn_s[lane] = bf16_to_f32(bv0);
+        vn_s[lane + 64] = bf16_to_f32(bv1);
+    }
+    __syncthreads();
+
+    // 2. online softmax over this slot's keys
+    float qv[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) qv[g][e] = q_s[g][8 * kl + e];
+    float m[G], l[G], acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -__builtin_inff();
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
+    }
+    auto unpack = [](uint4 r, float (&f)[8]) {
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            f[2 * q] = __uint_as_float(w[q] << 16);
+            f[2 * q + 1] = __uint_as_float(w[q] & 0xFFFF0000u);
+        }
+    };
+    for (; j0 < jc_end; j0 += 16 * U) {
+        float kf[U][8], vf[U][8];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            unpack(kr[u], kf[u]);
+            unpack(vr[u], vf[u]);
+        }
+        if (j0 + 16 * U < jc_end) load_batch(j0 + 16 * U);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float s[U];
+            float mn = m[g];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) d = fmaf(qv[g][e], kf[u][e], d);
+                d = row16_sum(d);
+                s[u] = (j0 + 16 * u < jc_end) ? d : -__builtin_inff();
+                mn = fmaxf(mn, s[u]);
+            }
+            // key u = 0 is always in range, so mn is finite here
+            const float corr = __expf(m[g] - mn);
+            l[g] *= corr;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[g][e] *= corr;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const float p = __expf(s[u] - mn);
+                l[g] += p;
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[g][e] = fmaf(p, vf[u][e], acc[g][e]);
+            }
+            m[g] = mn;
+        }
+    }
+    if (owner && slot == 0) {  // the new key, from LDS
+        float kf[8], vf[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) kf[e] = kn_s[8 * kl + e], vf[e] = vn_s[8 * kl + e];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) d = fmaf(qv[g][e], kf[e], d);
+            d = row16_sum(d);
+            const float mn = fmaxf(m[g], d);
+            const float corr = __expf(m[g] - mn), p = __expf(d - mn);
+            l[g] = fmaf(l[g], corr, p);
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[g][e] = fmaf(acc[g][e], corr, p * vf[e]);
+            m[g] = mn;
+        }
+    }
+
+    // 3. merge the wave's 4 slots (rows of 16 lanes, permlane swaps), then the 4 waves
+    __shared__ float wm[4][G], wl[4][G], wacc[4][G][Dh];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float M = rows4_max(m[g]);
+        const float c = m[g] == -__builtin_inff() ? 0.0f : __expf(m[g] - M);
+        const float L = rows4_sum(l[g] * c);
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[g][e] = rows4_sum(acc[g][e] * c);
+        if (kg == 0) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) wacc[wave][g][8 * kl + e] = acc[g][e];
+            if (kl == 0) wm[wave][g] = M, wl[wave][g] = L;
+        }
+    }
+    __syncthreads();
+    constexpr int PER = (G * Dh + 255) / 256;  // outputs per thread
+    float rM[PER], rL[PER], rA[PER];
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int t = threadIdx.x + 256 * r;
+        rM[r] = -__builtin_inff(), rL[r] = 0.0f, rA[r] = 0.0f;
+        if (t < G * Dh) {
+            const int g = t / Dh, d = t - g * Dh;
+            float M = wm[0][g];
+#pragma unroll
+            for (int w = 1; w < 4; w++) M = fmaxf(M, wm[w][g]);
+            float L = 0.0f, A = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float c = wm[w][g] == -__builtin_inff() ? 0.0f : __expf(wm[w][g] - M);
+                L = fmaf(wl[w][g], c, L);
+                A = fmaf(wacc[w][g][d], c, A);
+            }
+            rM[r] = M, rL[r] = L, rA[r] = A;
+        }
+    }
+    if (a.nsplit == 1) {
+#pragma unroll
+        for (int r = 0; r < PER; r++) {
+            const int t = threadIdx.x + 256 * r;
+            if (t < G * Dh) st_act(a.out, (int64_t)hk * G * Dh + t, rA[r] / rL[r], a.out_dt);
+        }
+        return;
+    }
+
+    // 4. partials out
+    constexpr int PS = Dh + 2;
+    float* mine = a.part + ((int64_t)hk * a.nsplit + split) * G * PS;
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int t = threadIdx.x + 256 * r;
+        if (t < G * Dh) {
+            const int g = t / Dh, d = t - g * Dh;
+            mine[g * PS + 2 + d] = rA[r];
+            if (d == 0) mine[g * PS] = rM[r], mine[g * PS + 1] = rL[r];
+        }
     }
 }
 
@@ -608,6 +867,49 @@ Status launch_qk_norm_rope_append(const void* qkv, int qkv_dt, int Hq, int Hk, c
     const int heads = Hq + 2 * Hk;
     hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3((unsigned)((heads + 3) / 4)), dim3(256), 0, st, qkv, qkv_dt, Hq,
                        Hk, qn_w, kn_w, w_dt, eps, base, scale, pos, kc, vc, c_dt, cap, q_out, q_dt);
+    return Status::ok();
+}
+
+// Keys per block: at least one full load batch per slot (64 keys: a block's
+// fixed prologue costs more than streaming 32 KB), and about 2 blocks per CU over
+// the kv heads for long caches, in multiples of 16 (one key per slot).
+int64_t attn_keys_per_split(int64_t Hk, int64_t Lk, int num_cus) {
+    const int64_t target = std::max<int64_t>(1, 2 * (int64_t)num_cus / Hk);
+    return std::max<int64_t>(64, 16 * ((Lk + 16 * target - 1) / (16 * target)));
+}
+
+size_t attn_decode_workspace_bytes(int64_t Hq, int64_t Hk, int64_t pos, int num_cus) {
+    const int64_t Lk = pos + 1, kps = attn_keys_per_split(Hk, Lk, num_cus);
+    const int64_t nsplit = (Lk + kps - 1) / kps;
+    return nsplit > 1 ? (size_t)(Hk * nsplit * (Hq / Hk) * (kDecodeDh + 2)) * sizeof(float) : 0;
+}
+
+Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt,
+                          float eps, float base, float rscale, const float* rope_cs, int64_t pos, void* kc,
+                          void* vc, int64_t cap, float scale, void* out, int out_dt, void* workspace, int num_cus,
+                          hipStream_t st) {
+    const int G = Hq / Hk;
+    const int64_t Lk = pos + 1, kps = attn_keys_per_split(Hk, Lk, num_cus);
+    const int64_t nsplit = (Lk + kps - 1) / kps;
+    if (nsplit > kMaxSplits || kps > 0x7fffffff) return Status::fail(JH_ERR_UNSUPPORTED, "attention: cache too long");
+    AttnArgs a{qkv, qkv_dt, qn_w, kn_w, w_dt, eps, base, rscale, scale, rope_cs, pos,
+               static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), cap, Hk, (int)nsplit, (int)kps,
+               static_cast<float*>(workspace), out, out_dt};
+    const dim3 grid((unsigned)nsplit, (unsigned)Hk);
+    if (G == 1) hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(256), 0, st, a);
+    else if (G == 2) hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(256), 0, st, a);
+    else if (G == 4) hipLaunchKernelGGL(attn_decode_kernel<4>, grid, dim3(256), 0, st, a);
+    else if (G == 8) hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(256), 0, st, a);
+    else return Status::fail(JH_ERR_UNSUPPORTED, "attention: n_heads / n_kv_heads must be 1, 2, 4 or 8");
+    if (nsplit > 1)
+        hipLaunchKernelGGL(sdpa_decode_merge_kernel, dim3((unsigned)Hq), dim3(kDecodeDh), 0, st,
+                           static_cast<const float*>(workspace), Hk, G, (int)nsplit, out, out_dt);
+    return Status::ok();
+}
+
+Status launch_rope_table(int dims, float base, float scale, int64_t pos, const float* freqs, float* out,
+                         hipStream_t st) {
+    hipLaunchKernelGGL(rope_table_kernel, dim3(1), dim3(64), 0, st, dims, base, scale, pos, freqs, out);
     return Status::ok();
 }
 

@@ -93,6 +93,44 @@ __device__ __forceinline__ float slice_sum_last(float v) {
     return v;
 }
 
+// ---- wave reductions without LDS -------------------------------------------------
+// DPP inside each row of 16 lanes (xor 1 and xor 2 inside quads, then the
+// mirrors of 8 and of 16 lanes), then gfx950's v_permlane16_swap /
+// v_permlane32_swap across rows: called with both operands v, the two results
+// hold, in every lane, v of this lane and v of the lane 16 (32) away in the
+// partner row (half), so their sum or max reduces over that pair. All VALU.
+template <bool MAX>
+__device__ __forceinline__ float row16_reduce(float v) {
+    auto dpp = [](float x, auto ctrl) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                     decltype(ctrl)::value, 0xF, 0xF, false));
+    };
+    auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+    v = op(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+    v = op(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+    v = op(v, dpp(v, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+    v = op(v, dpp(v, std::integral_constant<int, 0x140>{}));  // row_mirror
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) { return row16_reduce<false>(v); }
+
+template <bool MAX>
+__device__ __forceinline__ float pair16(float v) {  // rows (0,1) and (2,3)
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return MAX ? fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])) : __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+template <bool MAX>
+__device__ __forceinline__ float pair32(float v) {  // halves (0-31, 32-63)
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return MAX ? fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])) : __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Over the 4 rows, per lane position in the row (result in every lane).
+__device__ __forceinline__ float rows4_sum(float v) { return pair32<false>(pair16<false>(v)); }
+__device__ __forceinline__ float rows4_max(float v) { return pair32<true>(pair16<true>(v)); }
+// Over all 64 lanes (result in every lane).
+__device__ __forceinline__ float wave_sum(float v) { return rows4_sum(row16_reduce<false>(v)); }
+__device__ __forceinline__ float wave_max(float v) { return rows4_max(row16_reduce<true>(v)); }
+
 // Load element i of a scale/bias array of the given dtype as fp32 (exact).
 __device__ __forceinline__ float load_sb(const void* p, int64_t i, int dt) {
     if (dt == JH_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
@@ -137,12 +175,12 @@ Status launch_dequantize(const QuantMatrix& m, void* out, int out_dtype, hipStre
 Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int y_dtype,
                   int num_cus, hipStream_t st);
 // Decode product with a fused prologue (pro: 0 none, 1 RMSNorm of fp32 x with
-// weight nw, 2 SiLU(x[:K]) * x[K:]) and optionally y = resid + product (fp32).
-size_t qmv_fused_workspace_bytes(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, bool resid_add,
-                                 int y_dtype);
+// weight nw, 2 SiLU(x[:K]) * x[K:]) and epilogue (epi: 0 store, 1 y = resid +
+// product in fp32, 2 SwiGLU over W = [gate rows; up rows], y has m.rows / 2).
+size_t qmv_fused_workspace_bytes(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, int epi, int y_dtype);
 Status launch_qmv_fused(const QuantMatrix& m, int pro, const void* x, int x_dtype, const void* nw, int nw_dtype,
-                        float eps, bool resid_add, const float* resid, void* y, int y_dtype, int num_cus,
-                        hipStream_t st, void* workspace);
+                        float eps, int epi, const float* resid, void* y, int y_dtype, int num_cus, hipStream_t st,
+                        void* workspace);
 Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y,
                   int y_dtype, int num_cus, hipStream_t st, void* workspace);
 // fp32 accumulation buffer a split-K prefill needs (0 when none).
@@ -194,6 +232,15 @@ Status launch_argmax(const void* x, int x_dt, int64_t rows, int64_t n, int32_t* 
 Status launch_qk_norm_rope_append(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w,
                                   int w_dt, float eps, float base, float scale, int64_t pos, void* kc, void* vc,
                                   int c_dt, int64_t cap, void* q_out, int q_dt, hipStream_t st);
+// One-token attention (q/k norm, RoPE, KV append, SDPA over keys 0..pos): one
+// launch, plus a merge launch when the keys are split over blocks.
+size_t attn_decode_workspace_bytes(int64_t Hq, int64_t Hk, int64_t pos, int num_cus);
+Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt,
+                          float eps, float base, float rscale, const float* rope_cs, int64_t pos, void* kc,
+                          void* vc, int64_t cap, float scale, void* out, int out_dt, void* workspace, int num_cus,
+                          hipStream_t st);
+Status launch_rope_table(int dims, float base, float scale, int64_t pos, const float* freqs, float* out,
+                         hipStream_t st);
 Status launch_take_rows(const void* table, int64_t row_bytes, int64_t n_rows, const int32_t* ids, int64_t n_ids,
                         void* out, hipStream_t st);
 Status launch_kv_append(void* kc, void* vc, int c_dt, const void* kn, const void* vn, int n_dt, int64_t BH,

@@ -139,17 +139,22 @@ __device__ __forceinline__ void store_rows(void* Y, int y_dt, uint32_t row0, uin
 // and issues back to back; only the stores are predicated.
 // Fusions around the product (decode only), chosen at compile time:
 //   PRO_NONE     x is bf16 [K]
-//   PRO_RMSNORM  x is the fp32 residual stream [K]; the product runs on
-//                bf16(x / sqrt(mean(x^2) + eps) * nw) (RMSNorm, cpu/cpu_ops.go:144-162).
-//                Every block sums x^2 over its waves' K parts (which together
-//                cover K) through LDS, so no separate norm launch is needed.
-//   PRO_SILU_MUL x is bf16 [2K] = [gate | up]; the product runs on
-//                bf16(SiLU(gate) * up) (MLP.Forward, qwen/mlp.go:33-35).
+//   PRO_RMSNORM  x is the fp32 residual stream [K]; y = RMSNorm(x, nw) . W^T
+//                (cpu/cpu_ops.go:144-162) as (bf16(x * nw) . W^T) / sqrt(mean(x^2)
+//                + eps): the product is linear in its input, so the 1/rms factor
+//                is applied to the fp32 dot products and nothing waits for the
+//                sum of squares before them. Each wave sums x^2 over its K part;
+//                the parts meet in LDS at the first pass's K-split exchange.
 //   EPI_STORE    y = dot
 //   EPI_RESID    y (fp32) = resid + dot; resid may alias y (the residual Add of
 //                qwen/block.go:59-60 done in place).
-enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2 };
-enum { EPI_STORE = 0, EPI_RESID = 1 };
+//   EPI_SWIGLU   W holds 2N rows, the gate rows then the up rows; y[j] =
+//                SiLU(dot_j) * dot_{N+j} (MLP.Forward's Mul(SiLU(gate), up),
+//                qwen/mlp.go:33-35). A slice computes RPW/2 gate rows and the
+//                matching up rows, so both dots meet in one lane.
+enum { PRO_NONE = 0, PRO_RMSNORM = 1 };
+constexpr int kProSiluMul = 2;  // x = [gate | up]: composed from separate launches
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 
 struct QmvFusion {
     const uint16_t* nw = nullptr;  // bf16 norm weight [K] (PRO_RMSNORM)
@@ -160,24 +165,27 @@ struct QmvFusion {
 template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int PRO = PRO_NONE, int EPI = EPI_STORE>
 __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     const uint32_t* __restrict__ W, const uint16_t* __restrict__ S,
-    const uint16_t* __restrict__ B, const void* __restrict__ Xv, void* __restrict__ Y,
+    const uint16_t* __restrict__ B, const void* __restrict__ Xv, void* Y,
     int y_dt, uint32_t N, int gs_log2, QmvFusion fu) {
     constexpr int SLICES = 64 / LPR;
     constexpr int RGROUPS = 4 / KSPLIT;                 // row groups per block
     constexpr uint32_t PK = 4 * LPR * ITERS;            // words per K part
     constexpr uint32_t P = PK * KSPLIT;
-    constexpr int ROWS_PER_WAVE = SLICES * RPW;
+    constexpr int RO = EPI == EPI_SWIGLU ? RPW / 2 : RPW;  // output rows per slice and pass
+    constexpr int ROWS_PER_WAVE = SLICES * RO;
     constexpr int ROWS_PER_BLOCK = RGROUPS * ROWS_PER_WAVE;
+    static_assert(EPI != EPI_SWIGLU || RPW % 2 == 0, "SwiGLU pairs gate and up rows");
+    const uint32_t NW = EPI == EPI_SWIGLU ? 2 * N : N;     // rows of W
     const int lane = threadIdx.x & 63;
     const int wv_id = threadIdx.x >> 6;
     const int ks = wv_id % KSPLIT, rg = wv_id / KSPLIT;
     const int sl = lane % LPR;
     const int slice = lane / LPR;
     const uint32_t G = (P * 8) >> gs_log2;
-    const auto rw = make_rsrc(W, N * P * 4);
-    const auto rs = make_rsrc(S, N * G * 2);
-    const auto rb = make_rsrc(B, N * G * 2);
-    __shared__ float red[(KSPLIT > 1) ? (KSPLIT - 1) * RGROUPS * ROWS_PER_WAVE : 1];
+    const auto rw = make_rsrc(W, NW * P * 4);
+    const auto rs = make_rsrc(S, NW * G * 2);
+    const auto rb = make_rsrc(B, NW * G * 2);
+    __shared__ float red[(KSPLIT > 1) ? (KSPLIT - 1) * RGROUPS * SLICES * RPW : 1];
     __shared__ float ssq[4];
     constexpr uint32_t K = 8 * P;
 
@@ -189,29 +197,38 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     }
     uint4 wv[RPW][ITERS];
     uint16_t sh[RPW][ITERS], bh[RPW][ITERS];
+    float rv[EPI == EPI_RESID ? RPW : 1];  // the residual rows, fetched with the pass's weights
+    const auto rr = make_rsrc(fu.resid, EPI == EPI_RESID ? N * 4 : 0);
     // Loads complete in issue order. The raw x loads go first, then the first
     // pass's weights (which do not depend on x), and only then is x regrouped:
-    // that waits for x alone while the weights are still in flight. Rows past N
-    // read as zero (buffer bounds).
+    // that waits for x alone while the weights are still in flight. Rows past the
+    // matrix read as zero (buffer bounds).
+    auto wrow = [&](uint32_t row0, int r) -> uint32_t {
+        return EPI == EPI_SWIGLU ? row0 + (r % RO) + (r / RO) * N : row0 + r;
+    };
     auto load_pass = [&](uint32_t row0) {
 #pragma unroll
         for (int r = 0; r < RPW; r++)
 #pragma unroll
             for (int it = 0; it < ITERS; it++)
-                wv[r][it] = buf_load16_nt(rw, ((row0 + r) * P + wo[it]) * 4);
+                wv[r][it] = buf_load16_nt(rw, (wrow(row0, r) * P + wo[it]) * 4);
 #pragma unroll
         for (int r = 0; r < RPW; r++)
 #pragma unroll
             for (int it = 0; it < ITERS; it++) {
-                const uint32_t off = ((row0 + r) * G + gi[it]) * 2;
+                const uint32_t off = (wrow(row0, r) * G + gi[it]) * 2;
                 sh[r][it] = buf_load2(rs, off);
                 bh[r][it] = buf_load2(rb, off);
             }
+        if constexpr (EPI == EPI_RESID)
+#pragma unroll
+            for (int r = 0; r < RPW; r++)
+                rv[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr, (row0 + r) * 4, 0, 0));
     };
-    // raw x: 32 elements per lane per ITER (bf16, fp32 for the norm, or gate + up)
+    // raw x: 32 elements per lane per ITER (bf16, or fp32 for the norm)
     constexpr int XW = PRO == PRO_RMSNORM ? 8 : 4;  // 16-byte chunks per 32 elements
     uint4 xraw[ITERS][XW];
-    uint4 xaux[ITERS][4];  // norm weights (PRO_RMSNORM) or up (PRO_SILU_MUL)
+    uint4 xaux[ITERS][4];  // norm weights (PRO_RMSNORM)
 #pragma unroll
     for (int it = 0; it < ITERS; it++) {
         const uint32_t e0 = 8u * wo[it];
@@ -225,61 +242,30 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
             for (int j = 0; j < 4; j++) xraw[it][j] = xv[j];
         }
     }
-    const uint32_t lane_row = rg * ROWS_PER_WAVE + (uint32_t)slice * RPW;
-    load_pass(blockIdx.x * ROWS_PER_BLOCK + lane_row);
-    if constexpr (PRO == PRO_RMSNORM || PRO == PRO_SILU_MUL) {
+    // the norm weights go with x, ahead of the weights, so the normalisation
+    // waits for x and them alone
+    if constexpr (PRO == PRO_RMSNORM) {
 #pragma unroll
         for (int it = 0; it < ITERS; it++) {
-            const uint4* av = PRO == PRO_RMSNORM ? reinterpret_cast<const uint4*>(fu.nw + 8u * wo[it])
-                                                 : reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(Xv) + K + 8u * wo[it]);
+            const uint4* av = reinterpret_cast<const uint4*>(fu.nw + 8u * wo[it]);
 #pragma unroll
             for (int j = 0; j < 4; j++) xaux[it][j] = av[j];
         }
     }
+    const uint32_t lane_row = rg * ROWS_PER_WAVE + (uint32_t)slice * RO;
+    load_pass(blockIdx.x * ROWS_PER_BLOCK + lane_row);
     // the product's input as bf16, 8 per uint4
     uint4 xin[ITERS][4];
+    float ss_part = 0.0f;  // PRO_RMSNORM: sum of x^2 over this wave's K part
     if constexpr (PRO == PRO_NONE) {
 #pragma unroll
         for (int it = 0; it < ITERS; it++)
 #pragma unroll
             for (int j = 0; j < 4; j++) xin[it][j] = xraw[it][j];
-    } else if constexpr (PRO == PRO_SILU_MUL) {
-#pragma unroll
-        for (int it = 0; it < ITERS; it++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t g[4] = {xraw[it][j].x, xraw[it][j].y, xraw[it][j].z, xraw[it][j].w};
-                const uint32_t u[4] = {xaux[it][j].x, xaux[it][j].y, xaux[it][j].z, xaux[it][j].w};
-                uint32_t o[4];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const float g0 = __uint_as_float(g[q] << 16), g1 = __uint_as_float(g[q] & 0xFFFF0000u);
-                    const float u0 = __uint_as_float(u[q] << 16), u1 = __uint_as_float(u[q] & 0xFFFF0000u);
-                    const float a0 = g0 / (1.0f + __expf(-g0)) * u0, a1 = g1 / (1.0f + __expf(-g1)) * u1;
-                    o[q] = (uint32_t)f32_to_bf16_hw(a0) | ((uint32_t)f32_to_bf16_hw(a1) << 16);
-                }
-                xin[it][j] = make_uint4(o[0], o[1], o[2], o[3]);
-            }
     } else {
-        // sum of squares of this wave's K part (each slice holds the whole part)
+        // x * nw to bf16, and the sum of squares of this wave's K part (each
+        // slice holds the whole part)
         float ss = 0.0f;
-#pragma unroll
-        for (int it = 0; it < ITERS; it++)
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const uint4 v = xraw[it][j];
-                ss = fmaf(__uint_as_float(v.x), __uint_as_float(v.x), ss);
-                ss = fmaf(__uint_as_float(v.y), __uint_as_float(v.y), ss);
-                ss = fmaf(__uint_as_float(v.z), __uint_as_float(v.z), ss);
-                ss = fmaf(__uint_as_float(v.w), __uint_as_float(v.w), ss);
-            }
-        ss = slice_sum_last<LPR>(ss);
-        if (slice == 0 && sl == LPR - 1) ssq[wv_id] = ss;
-        __syncthreads();
-        float tot = 0.0f;
-#pragma unroll
-        for (int k = 0; k < KSPLIT; k++) tot += ssq[rg * KSPLIT + k];
-        const float inv = 1.0f / (float)sqrt((double)(tot / (float)K + fu.eps));
 #pragma unroll
         for (int it = 0; it < ITERS; it++)
 #pragma unroll
@@ -292,12 +278,17 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
                 uint32_t o[4];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const float n0 = (xs8[2 * q] * inv) * __uint_as_float(ww[q] << 16);
-                    const float n1 = (xs8[2 * q + 1] * inv) * __uint_as_float(ww[q] & 0xFFFF0000u);
+                    ss = fmaf(xs8[2 * q], xs8[2 * q], ss);
+                    ss = fmaf(xs8[2 * q + 1], xs8[2 * q + 1], ss);
+                    const float n0 = xs8[2 * q] * __uint_as_float(ww[q] << 16);
+                    const float n1 = xs8[2 * q + 1] * __uint_as_float(ww[q] & 0xFFFF0000u);
                     o[q] = (uint32_t)f32_to_bf16_hw(n0) | ((uint32_t)f32_to_bf16_hw(n1) << 16);
                 }
                 xin[it][j] = make_uint4(o[0], o[1], o[2], o[3]);
             }
+        ss_part = slice_sum_last<LPR>(ss);  // valid in the slice's last lane
+        if constexpr (KSPLIT > 1)
+            if (slice == 0 && sl == LPR - 1) ssq[wv_id] = ss_part;
     }
 
     // this lane's part of x, as (x_p, x_{p+4}) bf16 pairs, and its sums
@@ -348,11 +339,28 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
                         part[r] += red[((k - 1) * RGROUPS * SLICES * RPW) + slot + r];
             __syncthreads();
         }
+        if constexpr (PRO == PRO_RMSNORM) {
+            // the K parts' sums of squares are in LDS since the exchange above
+            float tot = ss_part;
+            if constexpr (KSPLIT > 1) {
+                tot = 0.0f;
+#pragma unroll
+                for (int k = 0; k < KSPLIT; k++) tot += ssq[rg * KSPLIT + k];
+            }
+            const float inv = 1.0f / (float)sqrt((double)(tot / (float)K + fu.eps));
+#pragma unroll
+            for (int r = 0; r < RPW; r++) part[r] *= inv;
+        }
         if (ks == 0 && sl == LPR - 1) {
             if constexpr (EPI == EPI_RESID) {
 #pragma unroll
                 for (int r = 0; r < RPW; r++)
-                    if (row0 + r < N) static_cast<float*>(Y)[row0 + r] = fu.resid[row0 + r] + part[r];
+                    if (row0 + r < N) static_cast<float*>(Y)[row0 + r] = rv[r] + part[r];
+            } else if constexpr (EPI == EPI_SWIGLU) {
+                float act[RO];
+#pragma unroll
+                for (int r = 0; r < RO; r++) act[r] = part[r] / (1.0f + (float)exp((double)(-part[r]))) * part[RO + r];
+                store_rows<RO>(Y, y_dt, row0, N, act);
             } else {
                 store_rows<RPW>(Y, y_dt, row0, N, part);
             }
@@ -429,7 +437,8 @@ namespace {
 template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int PRO = PRO_NONE, int EPI = EPI_STORE>
 Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gs_log2,
                    int num_cus, hipStream_t st, const QmvFusion& fu = QmvFusion{}) {
-    constexpr int64_t rows_per_block = (4 / KSPLIT) * (64 / LPR) * RPW;
+    constexpr int64_t rows_per_block = (4 / KSPLIT) * (64 / LPR) * (EPI == EPI_SWIGLU ? RPW / 2 : RPW);
+    const int64_t n_out = EPI == EPI_SWIGLU ? m.rows / 2 : m.rows;
     auto kern = qmv_bf16x_kernel<LPR, ITERS, RPW, KSPLIT, SB_F16, PRO, EPI>;
     // persistent-style grid: at most what is resident at once, so multi-pass
     // shapes reuse the x registers instead of queueing more blocks
@@ -440,13 +449,13 @@ Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, in
             per_cu = 2;
         resident = per_cu;
     }
-    int64_t blocks = (m.rows + rows_per_block - 1) / rows_per_block;
+    int64_t blocks = (n_out + rows_per_block - 1) / rows_per_block;
     const int64_t cap = (int64_t)num_cus * resident;
     if (blocks > cap) blocks = cap;
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, st, m.w,
                        static_cast<const uint16_t*>(m.scales), static_cast<const uint16_t*>(m.biases), x, y,
-                       y_dtype, (uint32_t)m.rows, gs_log2, fu);
+                       y_dtype, (uint32_t)n_out, gs_log2, fu);
     return Status::ok();
 }
 
@@ -544,42 +553,44 @@ Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int
 }
 
 // True when one register-tile launch takes the fused call (no workspace).
-bool qmv_fused_single(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, bool resid_add, int y_dtype) {
-    if (pro == PRO_RMSNORM ? (x_dtype != JH_F32 || nw_dtype != JH_BF16) : x_dtype != JH_BF16) return false;
-    if (resid_add && y_dtype != JH_F32) return false;
+bool qmv_fused_single(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, int epi, int y_dtype) {
+    if (pro == PRO_RMSNORM ? (x_dtype != JH_F32 || nw_dtype != JH_BF16) : (pro != PRO_NONE || x_dtype != JH_BF16))
+        return false;
+    if (epi == EPI_RESID && y_dtype != JH_F32) return false;
     if (!qmv_fast_shape(m)) return false;
-    if (m.sb_dtype != JH_BF16 && (pro != PRO_NONE || resid_add)) return false;
-    return pro == PRO_NONE || (pro == PRO_RMSNORM && !resid_add) || (pro == PRO_SILU_MUL && resid_add);
+    if (m.sb_dtype != JH_BF16 && (pro != PRO_NONE || epi != EPI_STORE)) return false;
+    if (pro == PRO_NONE) return epi == EPI_STORE || epi == EPI_RESID;
+    return epi == EPI_STORE || epi == EPI_SWIGLU;
 }
 
-size_t qmv_fused_workspace_bytes(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, bool resid_add,
-                                 int y_dtype) {
-    if (qmv_fused_single(m, pro, x_dtype, nw_dtype, resid_add, y_dtype)) return 0;
+size_t qmv_fused_workspace_bytes(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, int epi, int y_dtype) {
+    if (qmv_fused_single(m, pro, x_dtype, nw_dtype, epi, y_dtype)) return 0;
     return ((size_t)m.in * 2 + 255) / 256 * 256 + (size_t)m.rows * 4;
 }
 
 Status launch_qmv_fused(const QuantMatrix& m, int pro, const void* x, int x_dtype, const void* nw, int nw_dtype,
-                        float eps, bool resid_add, const float* resid, void* y, int y_dtype, int num_cus,
-                        hipStream_t st, void* workspace) {
+                        float eps, int epi, const float* resid, void* y, int y_dtype, int num_cus, hipStream_t st,
+                        void* workspace) {
     // one launch when a register tile takes the shape
-    if (qmv_fused_single(m, pro, x_dtype, nw_dtype, resid_add, y_dtype)) {
+    if (qmv_fused_single(m, pro, x_dtype, nw_dtype, epi, y_dtype)) {
         QmvFusion fu;
         fu.nw = static_cast<const uint16_t*>(nw);
         fu.eps = eps;
         fu.resid = resid;
         bool done = false;
-        if (pro == PRO_NONE && !resid_add)
+        if (pro == PRO_NONE && epi == EPI_STORE)
             done = launch_tiles<PRO_NONE, EPI_STORE>(m, x, y, y_dtype, num_cus, st, fu);
         else if (pro == PRO_NONE)
             done = launch_tiles<PRO_NONE, EPI_RESID>(m, x, y, y_dtype, num_cus, st, fu);
-        else if (pro == PRO_RMSNORM && !resid_add)
+        else if (epi == EPI_STORE)
             done = launch_tiles<PRO_RMSNORM, EPI_STORE>(m, x, y, y_dtype, num_cus, st, fu);
-        else if (pro == PRO_SILU_MUL && resid_add)
-            done = launch_tiles<PRO_SILU_MUL, EPI_RESID>(m, x, y, y_dtype, num_cus, st, fu);
+        else
+            done = launch_tiles<PRO_RMSNORM, EPI_SWIGLU>(m, x, y, y_dtype, num_cus, st, fu);
         if (done) return Status::ok();
         return Status::fail(JH_ERR_UNSUPPORTED, "qmv_fused: no tile for a shape the planner accepted");
     }
     // otherwise the same arithmetic as separate launches through the workspace
+    if (!workspace) return Status::fail(JH_ERR_INVALID, "qmv_fused: this combination needs a workspace");
     uint16_t* xin = static_cast<uint16_t*>(workspace);
     float* tmp = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((size_t)m.in * 2 + 255) / 256 * 256);
     const void* xp = x;
@@ -588,17 +599,19 @@ Status launch_qmv_fused(const QuantMatrix& m, int pro, const void* x, int x_dtyp
         Status s = launch_rms_norm(x, x_dtype, nw, nw_dtype, eps, xin, JH_BF16, 1, m.in, st);
         if (s.code != JH_OK) return s;
         xp = xin, xdt = JH_BF16;
-    } else if (pro == PRO_SILU_MUL) {
+    } else if (pro == kProSiluMul) {
         const size_t esz = x_dtype == JH_F32 ? 4 : 2;
         Status s = launch_elementwise(JH_OP_SILU_MUL, x, x_dtype, static_cast<const char*>(x) + m.in * esz, x_dtype,
                                       xin, JH_BF16, m.in, st);
         if (s.code != JH_OK) return s;
         xp = xin, xdt = JH_BF16;
     }
-    if (!resid_add) return launch_qmv(m, xp, xdt, y, y_dtype, num_cus, st);
+    if (epi == EPI_STORE) return launch_qmv(m, xp, xdt, y, y_dtype, num_cus, st);
     Status s = launch_qmv(m, xp, xdt, tmp, JH_F32, num_cus, st);
     if (s.code != JH_OK) return s;
-    return launch_elementwise(JH_OP_ADD, resid, JH_F32, tmp, JH_F32, y, y_dtype, m.rows, st);
+    if (epi == EPI_RESID) return launch_elementwise(JH_OP_ADD, resid, JH_F32, tmp, JH_F32, y, y_dtype, m.rows, st);
+    const int64_t n = m.rows / 2;
+    return launch_elementwise(JH_OP_SILU_MUL, tmp, JH_F32, tmp + n, JH_F32, y, y_dtype, n, st);
 }
 
 }  // namespace jh

@@ -284,28 +284,33 @@ int jh_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, co
 int jh_quant_matvec_fused(jh_ctx* c, jh_prologue pro, const void* x, jh_dtype x_dtype, const void* norm_w,
                           jh_dtype norm_w_dtype, float eps, const uint32_t* w, const void* scales,
                           const void* biases, jh_dtype sb_dtype, int64_t out_features, int64_t in_features,
-                          int group_size, int bits, const float* resid, void* y, jh_dtype y_dtype) {
+                          int group_size, int bits, jh_epilogue epi, const float* resid, void* y,
+                          jh_dtype y_dtype) {
     if (int r = enter(c)) return r;
     const char* op = "jh_quant_matvec_fused";
     if (pro != JH_PRO_NONE && pro != JH_PRO_RMSNORM && pro != JH_PRO_SILU_MUL)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": unknown prologue");
-    if (int r = check_quant(c, op, w, scales, biases, sb_dtype, out_features, in_features, group_size, bits))
-        return r;
+    if (epi != JH_EPI_STORE && epi != JH_EPI_RESID && epi != JH_EPI_SWIGLU)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": unknown epilogue");
+    if (out_features < 0 || (epi == JH_EPI_SWIGLU && out_features > ((int64_t)1 << 40)))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad out_features");
+    const int64_t w_rows = epi == JH_EPI_SWIGLU ? 2 * out_features : out_features;
+    if (int r = check_quant(c, op, w, scales, biases, sb_dtype, w_rows, in_features, group_size, bits)) return r;
     if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
     if (int r = check_act_dtype(c, op, "y", y_dtype)) return r;
     if (pro == JH_PRO_RMSNORM && norm_w_dtype != JH_BF16 && norm_w_dtype != JH_F16 && norm_w_dtype != JH_F32)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": norm weight must be bf16, f16 or f32");
-    if (resid && y_dtype != JH_F32)
-        return fail(c, JH_ERR_INVALID, std::string(op) + ": the residual add writes fp32 (y_dtype must be JH_F32)");
+    if (epi == JH_EPI_RESID && (y_dtype != JH_F32 || !resid))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": the residual add needs resid and writes fp32 (y_dtype JH_F32)");
     if (out_features == 0) return JH_OK;
     if (!x || !y || !aligned16(x) || !aligned16(y) || (pro == JH_PRO_RMSNORM && (!norm_w || !aligned16(norm_w))))
         return fail(c, JH_ERR_INVALID, std::string(op) + ": x, y (and norm_w) must be non-null and 16-byte aligned");
-    jh::QuantMatrix m{w, scales, biases, sb_dtype, out_features, in_features, group_size, bits};
-    const size_t need = jh::qmv_fused_workspace_bytes(m, (int)pro, x_dtype, norm_w_dtype, resid != nullptr, y_dtype);
+    jh::QuantMatrix m{w, scales, biases, sb_dtype, w_rows, in_features, group_size, bits};
+    const size_t need = jh::qmv_fused_workspace_bytes(m, (int)pro, x_dtype, norm_w_dtype, (int)epi, y_dtype);
     if (need)
         if (int r = ensure_workspace(c, need, op)) return r;
-    return finish(c, jh::launch_qmv_fused(m, (int)pro, x, x_dtype, norm_w, norm_w_dtype, eps, resid != nullptr,
-                                          resid, y, y_dtype, c->num_cus, c->stream, c->ws),
+    return finish(c, jh::launch_qmv_fused(m, (int)pro, x, x_dtype, norm_w, norm_w_dtype, eps, (int)epi, resid, y,
+                                          y_dtype, c->num_cus, c->stream, c->ws),
                   op);
 }
 
@@ -466,6 +471,48 @@ int jh_qk_norm_rope_append(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64
     return finish(c, jh::launch_qk_norm_rope_append(qkv, qkv_dtype, (int)n_heads, (int)n_kv_heads, q_norm_w, k_norm_w,
                                                     w_dtype, eps, rope_base, rope_scale, pos, k_cache, v_cache,
                                                     cache_dtype, capacity, q_out, q_out_dtype, c->stream),
+                  op);
+}
+
+int jh_rope_table(jh_ctx* c, int dims, float base, float scale, int64_t pos, const float* freqs, float* out) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_rope_table";
+    if (dims <= 0 || (dims & 1) || dims > 65536 || pos < 0)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad dims or position");
+    if (!out) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    return finish(c, jh::launch_rope_table(dims, base, scale, pos, freqs, out, c->stream), op);
+}
+
+int jh_attention_decode(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t n_heads, int64_t n_kv_heads,
+                        int64_t head_dim, const void* q_norm_w, const void* k_norm_w, jh_dtype w_dtype, float eps,
+                        float rope_base, float rope_scale, const float* rope_cs, int64_t pos, void* k_cache,
+                        void* v_cache,
+                        jh_dtype cache_dtype, int64_t capacity, float scale, void* out, jh_dtype out_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_attention_decode";
+    if (int r = check_act_dtype(c, op, "qkv", qkv_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "out", out_dtype)) return r;
+    if (head_dim != 128) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": head_dim must be 128");
+    if (cache_dtype != JH_BF16) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": the caches must be bf16");
+    if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads || n_heads > 65536)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad head counts");
+    const int64_t G = n_heads / n_kv_heads;
+    if (G != 1 && G != 2 && G != 4 && G != 8)
+        return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": n_heads / n_kv_heads must be 1, 2, 4 or 8");
+    if ((q_norm_w || k_norm_w) && w_dtype != JH_BF16 && w_dtype != JH_F16 && w_dtype != JH_F32)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": norm weights must be bf16, f16 or f32");
+    if (pos < 0 || pos >= capacity || capacity > 0x7fffffff)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": pos " + std::to_string(pos) + " outside the cache capacity " +
+                                           std::to_string(capacity));
+    if (!qkv || !out || !k_cache || !v_cache || !aligned16(k_cache) || !aligned16(v_cache))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer, or caches not 16-byte aligned");
+    const size_t need = jh::attn_decode_workspace_bytes(n_heads, n_kv_heads, pos, c->num_cus);
+    if (need)
+        if (int r = ensure_workspace(c, need, op)) return r;
+    return finish(c, jh::launch_attn_decode(qkv, qkv_dtype, (int)n_heads, (int)n_kv_heads, q_norm_w, k_norm_w, w_dtype,
+                                            eps, rope_base, rope_scale, rope_cs, pos, k_cache, v_cache, capacity, scale,
+                                            out,
+                                            out_dtype, c->ws, c->num_cus, c->stream),
                   op);
 }
 

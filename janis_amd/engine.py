@@ -386,33 +386,72 @@ class HipBackend:
 
     def QuantMatvecFused(self, x: Tensor, w: Tensor, scales: Tensor, biases: Tensor, groupSize: int, bits: int,
                          prologue: int = _lib.JH_PRO_NONE, norm: Tensor | None = None, eps: float = 0.0,
-                         resid: Tensor | None = None, out: Tensor | None = None,
+                         epilogue: int | None = None, resid: Tensor | None = None, out: Tensor | None = None,
                          out_dtype: int | None = None) -> Tensor:
         """One-token QuantMatmul (transpose=true) with the operator before it
         fused in (JH_PRO_RMSNORM: RMSNorm(x, norm, eps), the norm feeding q/k/v,
-        gate/up and the LM head; JH_PRO_SILU_MUL: x = [gate | up] ->
-        SiLU(gate)*up, qwen/mlp.go:33-35) and, with resid, the residual Add
-        after it (qwen/block.go:59-60) into an fp32 result (out may be resid)."""
+        gate/up and the LM head; JH_PRO_SILU_MUL: x = [gate | up] -> SiLU(gate)*up)
+        and the one after it (JH_EPI_RESID, the default when resid is given: the
+        residual Add of qwen/block.go:59-60 into an fp32 result, out may be resid;
+        JH_EPI_SWIGLU: w stacks the Gate rows then the Up rows and the result is
+        SiLU(gate)*up, qwen/mlp.go:33-35)."""
         if w.dtype != U32:
             raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: weight tensor is not packed U32")
-        n, P = w.shape[-2], w.shape[-1]
+        if epilogue is None:
+            epilogue = _lib.JH_EPI_RESID if resid is not None else _lib.JH_EPI_STORE
+        rows, P = w.shape[-2], w.shape[-1]
+        if epilogue == _lib.JH_EPI_SWIGLU and rows % 2:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: SwiGLU needs gate and up rows")
+        n = rows // 2 if epilogue == _lib.JH_EPI_SWIGLU else rows
         k = P * (32 // bits)
         want = 2 * k if prologue == _lib.JH_PRO_SILU_MUL else k
         if x.numel != want:
             raise JanisHipError(_lib.JH_ERR_INVALID, f"QuantMatvecFused: x has {x.numel} elements, needs {want}")
-        if resid is not None and (resid.dtype != F32 or resid.numel != n):
+        if epilogue == _lib.JH_EPI_RESID and (resid is None or resid.dtype != F32 or resid.numel != n):
             raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: resid must be F32 [out_features]")
         if prologue == _lib.JH_PRO_RMSNORM and (norm is None or norm.numel != k):
             raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: RMSNorm needs a weight of in_features")
-        yd = F32 if resid is not None else (
+        yd = F32 if epilogue == _lib.JH_EPI_RESID else (
             out_dtype if out_dtype is not None else (out.dtype if out is not None else x.dtype))
         y = out if out is not None else self.empty(yd, 1, n)
         check(self._ctx, self._L.jh_quant_matvec_fused(
             self._ctx, int(prologue), x.ptr, x.dtype, norm.ptr if norm is not None else None,
             norm.dtype if norm is not None else BF16, float(eps), w.ptr, scales.ptr, biases.ptr,
-            self._sb_dtype(scales, biases), n, k, groupSize, bits, resid.ptr if resid is not None else None,
-            y.ptr, y.dtype))
+            self._sb_dtype(scales, biases), n, k, groupSize, bits, int(epilogue),
+            resid.ptr if resid is not None else None, y.ptr, y.dtype))
         return y
+
+    def RoPETable(self, dims: int, base: float, scale: float, pos: int, freqs: Tensor | None = None) -> Tensor:
+        """cos and sin of the RoPE angles at pos (cpu/cpu_attn.go:13-34): F32
+        [dims] = [cos(theta_0..), sin(theta_0..)]."""
+        out = self.empty(F32, dims)
+        check(self._ctx, self._L.jh_rope_table(self._ctx, int(dims), float(base), float(scale), int(pos),
+                                               freqs.ptr if freqs is not None else None, out.ptr))
+        return out
+
+    def AttentionDecode(self, qkv: Tensor, n_heads: int, n_kv_heads: int, q_norm: Tensor | None,
+                        k_norm: Tensor | None, eps: float, base: float, rope_scale: float, pos: int,
+                        k_cache: Tensor, v_cache: Tensor, scale: float, out_dtype: int | None = None,
+                        rope_cs: Tensor | None = None) -> Tensor:
+        """Attention.ForwardCached for one token after the q/k/v product
+        (qwen/attention.go:98-128) in one launch: q/k RMSNorm (when the weights
+        are given), RoPE at pos, the KV append at row pos, and SDPA over keys
+        0..pos. qkv [.., (Hq+2Hk)*128]; caches bf16 [1, Hk, cap, 128]; rope_cs
+        optionally RoPETable(128, base, rope_scale, pos). Returns [1, Hq*128]."""
+        if q_norm is not None and k_norm is not None and q_norm.dtype != k_norm.dtype:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "AttentionDecode: norm weights differ in dtype")
+        if k_cache.dtype != v_cache.dtype or k_cache.shape != v_cache.shape:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "AttentionDecode: caches differ")
+        Dh = 128
+        cap = k_cache.shape[-2]
+        out = self.empty(out_dtype if out_dtype is not None else qkv.dtype, 1, n_heads * Dh)
+        wd = q_norm.dtype if q_norm is not None else (k_norm.dtype if k_norm is not None else BF16)
+        check(self._ctx, self._L.jh_attention_decode(
+            self._ctx, qkv.ptr, qkv.dtype, n_heads, n_kv_heads, Dh, q_norm.ptr if q_norm is not None else None,
+            k_norm.ptr if k_norm is not None else None, wd, float(eps), float(base), float(rope_scale),
+            rope_cs.ptr if rope_cs is not None else None, int(pos),
+            k_cache.ptr, v_cache.ptr, k_cache.dtype, cap, float(scale), out.ptr, out.dtype))
+        return out
 
     def MoeRoute(self, logits: Tensor, k: int, normTopk: bool = True) -> tuple:
         """The router of MoEBlock.Forward (qwen/moe.go:455-491) on the device:

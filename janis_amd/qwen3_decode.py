@@ -40,7 +40,7 @@ class Qwen3Config:
 class Qwen3Layer:
     qkv: tuple          # (W, S, B) [(Hq+2Hk)*Dh, hidden/8]
     o: tuple            # [hidden, Hq*Dh/8]
-    gate_up: tuple      # [2*inter, hidden/8]
+    gate_up: tuple      # [2*inter, hidden/8]: the gate rows, then the up rows
     down: tuple         # [hidden, inter/8]
     in_norm: Tensor     # [hidden]
     post_norm: Tensor   # [hidden]
@@ -63,22 +63,24 @@ def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bo
     """Runs token (I32 [1], device) at position pos through every layer, appends
     its keys/values to the caches, returns (logits F32 [1, vocab], next token I32 [1]).
     fused=True takes the backend's fused operators: each norm inside the product
-    it feeds, SiLU*mul inside the down product, the residual adds in the o/down
-    products' epilogues, and the q/k norms, RoPE and KV append in one launch
-    (7 launches per layer). fused=False spells the step out as the reference's
+    it feeds, SiLU*mul in the gate/up product's epilogue, the residual adds in
+    the o/down products' epilogues, and the q/k norms, RoPE, KV append and SDPA
+    in one launch plus a merge (6 launches per layer). fused=False spells the step out as the reference's
     separate operators (15 per layer)."""
     c = m.cfg
     gs, bits = c.group_size, c.bits
     H, Hq, Hk, Dh, I = c.hidden, c.n_heads, c.n_kv, c.head_dim, c.inter
-    RMS, SWIGLU = _lib.JH_PRO_RMSNORM, _lib.JH_PRO_SILU_MUL
+    RMS, SWIGLU = _lib.JH_PRO_RMSNORM, _lib.JH_EPI_SWIGLU
     # QuantEmbedding.Forward (qwen/embed.go:78-83)
     ew, es, eb = m.embed
     h = b.Dequantize(b.TakeAxis(ew, token), b.TakeAxis(es, token), b.TakeAxis(eb, token), gs, bits)  # F32 [1, H]
+    cs = b.RoPETable(Dh, c.theta, 1.0, pos) if fused else None  # shared by every layer
     for L in m.layers:
         # Attention.ForwardCached
         if fused:
             qkv = b.QuantMatvecFused(h, *L.qkv, gs, bits, RMS, L.in_norm, c.eps, out_dtype=F32)
-            q = b.QKNormRoPEAppend(qkv, Hq, Hk, L.q_norm, L.k_norm, c.eps, c.theta, 1.0, pos, L.k_cache, L.v_cache)
+            att = b.AttentionDecode(qkv, Hq, Hk, L.q_norm, L.k_norm, c.eps, c.theta, 1.0, pos, L.k_cache,
+                                    L.v_cache, Dh ** -0.5, out_dtype=BF16, rope_cs=cs)
         else:
             xn = b.RMSNorm(h, L.in_norm, c.eps, out_dtype=BF16)
             qkv = b.QuantMatmul(xn, *L.qkv, True, gs, bits, out_dtype=F32)  # [1, (Hq+2Hk)*Dh]
@@ -88,12 +90,14 @@ def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bo
             q = b.RoPE(b.RMSNorm(q, L.q_norm, c.eps), Dh, False, c.theta, 1.0, pos)
             k = b.RoPE(b.RMSNorm(k, L.k_norm, c.eps), Dh, False, c.theta, 1.0, pos)
             b.AppendKV(L.k_cache, L.v_cache, pos, k, v)
-        att = b.Reshape(b.SDPA(q, L.k_cache, L.v_cache, Dh ** -0.5, False, kv_len=pos + 1, out_dtype=BF16), 1, Hq * Dh)
+            att = b.Reshape(b.SDPA(q, L.k_cache, L.v_cache, Dh ** -0.5, False, kv_len=pos + 1, out_dtype=BF16),
+                            1, Hq * Dh)
         # the residual adds and MLP.Forward
         if fused:
             b.QuantMatvecFused(att, *L.o, gs, bits, resid=h, out=h)
-            gu = b.QuantMatvecFused(h, *L.gate_up, gs, bits, RMS, L.post_norm, c.eps, out_dtype=BF16)
-            b.QuantMatvecFused(gu, *L.down, gs, bits, SWIGLU, resid=h, out=h)
+            act = b.QuantMatvecFused(h, *L.gate_up, gs, bits, RMS, L.post_norm, c.eps, epilogue=SWIGLU,
+                                     out_dtype=BF16)
+            b.QuantMatvecFused(act, *L.down, gs, bits, resid=h, out=h)
         else:
             h = b.Add(h, b.QuantMatmul(att, *L.o, True, gs, bits, out_dtype=F32))
             xn = b.RMSNorm(h, L.post_norm, c.eps, out_dtype=BF16)
