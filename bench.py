@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # WRITE_SIZE over `bench.py --pmc-workload`, each scaled by what the counter reads
 # for a 256 MiB copy in the same run (FETCH_SIZE x2.0, WRITE_SIZE x1.0). Re-measure
 # after changing the kernel; the summary sits in profiles/.
-DOMINANT_TRAFFIC_BYTES = 26904323
+DOMINANT_TRAFFIC_BYTES = 26920686
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 HIDDEN, INTER, VOCAB, LAYERS, GS = 4096, 12288, 151936, 36, 64
 
@@ -58,6 +58,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="skip the extra per-config figures")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--decode-step", type=int, default=0, metavar="CTX",
+                    help="profiling workload: only the config-4 decode step at context CTX (graph "
+                         "replays, warmup + steps); prints one line to stderr")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="eager launches for rocprofv3 --pmc: a 256 MiB copy (counter calibration), "
                          "then one pass of the dominant kernel's launches; prints nothing else")
@@ -145,6 +148,12 @@ def main() -> int:
         e1.record(st)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps  # ms per replay
+
+    if args.decode_step:
+        res = decode_step_figures(hip, torch, dev, capture, time_graph, args, contexts=(args.decode_step,))
+        log("decode step only:", res)
+        hip.Close()
+        return 0
 
     if args.pmc_workload:
         # calibration: a plain copy of known size (reads and writes 256 MiB)
@@ -324,7 +333,7 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
     return res
 
 
-def decode_step_figures(hip, torch, dev, capture, time_graph, args):
+def decode_step_figures(hip, torch, dev, capture, time_graph, args, contexts=(512, 8192)):
     """Config 4: the whole Qwen3-8B-architecture decode step (36 layers: RMSNorm,
     q/k/v product, per-head q/k RMSNorm, RoPE, KV append, SDPA over the cache, o
     product, residual, RMSNorm, gate/up product, SiLU*mul, down product,
@@ -337,7 +346,7 @@ def decode_step_figures(hip, torch, dev, capture, time_graph, args):
 
     cfg = Qwen3Config()
     t0 = time.time()
-    m, _ = random_model(hip, cfg, 8192 + 1, seed=4, torch=torch, dev=dev)
+    m, _ = random_model(hip, cfg, max(contexts) + 1, seed=4, torch=torch, dev=dev)
     for L in m.layers:
         L.k_cache._keep.normal_()
         L.v_cache._keep.normal_()
@@ -352,7 +361,7 @@ def decode_step_figures(hip, torch, dev, capture, time_graph, args):
     # embedding (3 row gathers + dequantize), RoPE table, 6 per layer, lm_head + 2-stage argmax
     launches = 5 + cfg.layers * 6 + 3
     res = {}
-    for ctx in (512, 8192):
+    for ctx in contexts:
         def fn(ctx=ctx):
             with hip.use_arena(arena):
                 decode_step(hip, m, tt, ctx)
