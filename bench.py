@@ -358,8 +358,8 @@ def decode_step_figures(hip, torch, dev, capture, time_graph, args, contexts=(51
     H, Hq, Hk, Dh, I = cfg.hidden, cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.inter
     per_layer = (qbytes((Hq + 2 * Hk) * Dh, H) + qbytes(H, Hq * Dh) + qbytes(2 * I, H) + qbytes(H, I))
     weights = cfg.layers * per_layer + qbytes(cfg.vocab, H) + (H // 2 + 4 * (H // GS))  # + one embedding row
-    # embedding (3 row gathers + dequantize), RoPE table, 6 per layer, lm_head + 2-stage argmax
-    launches = 5 + cfg.layers * 6 + 3
+    # embedding (3 row gathers + dequantize), RoPE table, first norm, 6 per layer, lm_head + 2-stage argmax
+    launches = 6 + cfg.layers * 6 + 3
     res = {}
     for ctx in contexts:
         def fn(ctx=ctx):

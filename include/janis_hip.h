@@ -318,19 +318,31 @@ typedef enum {
     JH_PRO_RMSNORM = 1,  /* x_in = RMSNorm(x, norm_w, eps): Block.ForwardCached's InputNorm /
                             PostNorm feeding q/k/v and gate/up (qwen/block.go:59-60), and the
                             final norm feeding the LM head (qwen/model.go:294-303) */
-    JH_PRO_SILU_MUL = 2  /* x holds [gate | up] (2 * in_features): x_in = SiLU(gate) * up,
+    JH_PRO_SILU_MUL = 2, /* x holds [gate | up] (2 * in_features): x_in = SiLU(gate) * up,
                             MLP.Forward's input to Down (qwen/mlp.go:33-35) */
+    JH_PRO_NORMED = 3    /* the same RMSNorm, prepared by the producer of x: x is the bf16
+                            norm_out and norm_stats the statistics that a JH_EPI_RESID_NORM
+                            call (or jh_norm_prepare) wrote; the product is scaled by
+                            1 / sqrt(sum(norm_stats) / in_features + eps) */
 } jh_prologue;
 
 typedef enum {
     JH_EPI_STORE = 0,    /* y = x_in . W^T */
     JH_EPI_RESID = 1,    /* y = resid + x_in . W^T in fp32 (y_dtype JH_F32; resid may be y):
                             the residual adds of Block.ForwardCached (qwen/block.go:59-60) */
-    JH_EPI_SWIGLU = 2    /* W holds 2 * out_features rows, the Gate rows then the Up rows
+    JH_EPI_SWIGLU = 2,   /* W holds 2 * out_features rows, the Gate rows then the Up rows
                             (scales/biases likewise): y[j] = SiLU(g_j) * u_j with
                             g = x_in . Gate^T, u = x_in . Up^T in fp32 (MLP.Forward's
                             Mul(SiLU(Gate.Forward(x)), Up.Forward(x)), qwen/mlp.go:33-35) */
+    JH_EPI_RESID_NORM = 3 /* JH_EPI_RESID, and the input of the NEXT RMSNorm'd product:
+                            norm_out = bf16(y * norm_w) with norm_w that norm's weight
+                            [out_features], and norm_stats (JH_NORM_STATS fp32) the sum of
+                            y^2 split in partials; pass both to that product with
+                            JH_PRO_NORMED */
 } jh_epilogue;
+
+/* fp32 slots of the statistics buffer of JH_EPI_RESID_NORM / JH_PRO_NORMED. */
+#define JH_NORM_STATS 1024
 
 /* One decode product with the operators on either side of it, for a backend
  * that offers it (the engine's optional-capability pattern,
@@ -356,13 +368,29 @@ typedef enum {
  * Everything else runs the same arithmetic as separate launches through the
  * context's workspace.
  *   x       [in_features] ([2 * in_features] for JH_PRO_SILU_MUL), device
- *   resid   fp32 [out_features] for JH_EPI_RESID, else ignored
- *   y       [out_features] of y_dtype */
+ *   resid   fp32 [out_features] for JH_EPI_RESID / JH_EPI_RESID_NORM, else ignored
+ *   y       [out_features] of y_dtype
+ *   norm_stats, norm_out   for JH_PRO_NORMED (stats in) and JH_EPI_RESID_NORM
+ *           (stats and bf16 [out_features] out); a call cannot use both
+ * The split RMSNorm (JH_EPI_RESID_NORM then JH_PRO_NORMED) moves the x * w part
+ * of the norm into the epilogue of the product that makes x, so the product
+ * that consumes it reads bf16 x like a plain one: y = (bf16(x * w) . W^T) /
+ * sqrt(mean(x^2) + eps), with mean(x^2) summed from per-block partials in a
+ * fixed order. It needs the one-launch tiles (and bf16 norm weights); other
+ * shapes run as jh_norm_prepare-style and separate launches. */
 JH_API int jh_quant_matvec_fused(jh_ctx *ctx, jh_prologue prologue, const void *x, jh_dtype x_dtype,
                           const void *norm_w, jh_dtype norm_w_dtype, float eps, const uint32_t *w,
                           const void *scales, const void *biases, jh_dtype sb_dtype,
                           int64_t out_features, int64_t in_features, int group_size, int bits,
-                          jh_epilogue epilogue, const float *resid, void *y, jh_dtype y_dtype);
+                          jh_epilogue epilogue, const float *resid, void *y, jh_dtype y_dtype,
+                          float *norm_stats, void *norm_out);
+
+/* The producer half of a split RMSNorm for a row the caller already holds (the
+ * embedding row that enters the first block): norm_out = bf16(x * norm_w) [d]
+ * and norm_stats (JH_NORM_STATS fp32) = the sum of x^2 in partials (the rest 0), for a
+ * jh_quant_matvec_fused call with JH_PRO_NORMED. */
+JH_API int jh_norm_prepare(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t d, const void *norm_w,
+                    jh_dtype norm_w_dtype, void *norm_out, float *norm_stats);
 
 #ifdef __cplusplus
 }

@@ -15,8 +15,9 @@ LIB_PATH = os.path.join(HERE, "libjanis_hip.so")
 F32, F16, BF16, I32, U32, U8 = range(6)
 JH_OK, JH_ERR_INVALID, JH_ERR_UNSUPPORTED, JH_ERR_HIP, JH_ERR_OOM = range(5)
 JH_OP_ADD, JH_OP_MUL, JH_OP_SILU, JH_OP_SILU_MUL = range(4)  # jh_op
-JH_PRO_NONE, JH_PRO_RMSNORM, JH_PRO_SILU_MUL = range(3)  # jh_prologue
-JH_EPI_STORE, JH_EPI_RESID, JH_EPI_SWIGLU = range(3)  # jh_epilogue
+JH_PRO_NONE, JH_PRO_RMSNORM, JH_PRO_SILU_MUL, JH_PRO_NORMED = range(4)  # jh_prologue
+JH_EPI_STORE, JH_EPI_RESID, JH_EPI_SWIGLU, JH_EPI_RESID_NORM = range(4)  # jh_epilogue
+JH_NORM_STATS = 1024
 
 EXPORTS = [
     "jh_version", "jh_create", "jh_destroy", "jh_last_error", "jh_device_info",
@@ -24,7 +25,7 @@ EXPORTS = [
     "jh_h2d", "jh_d2h", "jh_dequantize", "jh_quant_matmul", "jh_gather_quant_matmul",
     "jh_moe_route", "jh_moe_swiglu", "jh_rms_norm", "jh_rope", "jh_sdpa", "jh_elementwise", "jh_argmax",
     "jh_take_rows", "jh_kv_append", "jh_qk_norm_rope_append", "jh_quant_matvec_fused",
-    "jh_attention_decode", "jh_rope_table",
+    "jh_attention_decode", "jh_rope_table", "jh_norm_prepare",
 ]
 
 _lib = None
@@ -95,9 +96,11 @@ def load() -> ctypes.CDLL:
     L.jh_attention_decode.argtypes = [c_ctx, p, i, i64, i64, i64, p, p, i, f32, f32, f32, p, i64, p, p, i, i64,
                                       f32, p, i]
     L.jh_rope_table.argtypes = [c_ctx, i, f32, f32, i64, p, p]
-    L.jh_quant_matvec_fused.argtypes = [c_ctx, i, p, i, p, i, f32, p, p, p, i, i64, i64, i, i, i, p, p, i]
+    L.jh_quant_matvec_fused.argtypes = [c_ctx, i, p, i, p, i, f32, p, p, p, i, i64, i64, i, i, i, p, p, i, p, p]
+    L.jh_norm_prepare.argtypes = [c_ctx, p, i, i64, p, i, p, p]
     for name in ("jh_rms_norm", "jh_rope", "jh_sdpa", "jh_elementwise", "jh_argmax", "jh_take_rows", "jh_kv_append",
-                 "jh_qk_norm_rope_append", "jh_quant_matvec_fused", "jh_attention_decode", "jh_rope_table"):
+                 "jh_qk_norm_rope_append", "jh_quant_matvec_fused", "jh_attention_decode", "jh_rope_table",
+                 "jh_norm_prepare"):
         getattr(L, name).restype = i
     L.jh_moe_route.argtypes = [c_ctx, p, i, i64, i64, i64, i, p, p]
     L.jh_moe_route.restype = i

@@ -160,6 +160,50 @@ __global__ __launch_bounds__(64) void rope_table_kernel(int dims, float base, fl
     }
 }
 
+// ---- the two halves of a split RMSNorm ---------------------------------------------
+// Producer half for one row of d: out = bf16(x * w); block b sums x^2 over its
+// 2048 elements into stats[b] (its 8 loads per thread issue together), block 0
+// zeroes the slots past the grid. Consumer half (the fallback of a product that
+// cannot apply the statistics in its epilogue): out = bf16(u / sqrt(sum(stats) /
+// d + eps)).
+constexpr int kPrepPer = 8;  // elements per thread of norm_prepare_kernel
+
+__global__ __launch_bounds__(256) void norm_prepare_kernel(const void* __restrict__ x, int x_dt, int64_t d,
+                                                           const void* __restrict__ w, int w_dt,
+                                                           uint16_t* __restrict__ out, float* __restrict__ stats) {
+    __shared__ float red[4];
+    const int64_t base = (int64_t)blockIdx.x * 256 * kPrepPer + threadIdx.x;
+    float xv[kPrepPer], wv[kPrepPer];
+#pragma unroll
+    for (int e = 0; e < kPrepPer; e++) {
+        const int64_t i = base + 256 * e;
+        xv[e] = i < d ? ld_act(x, i, x_dt) : 0.0f;
+        wv[e] = i < d ? ld_act(w, i, w_dt) : 0.0f;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kPrepPer; e++) {
+        const int64_t i = base + 256 * e;
+        ss = fmaf(xv[e], xv[e], ss);
+        if (i < d) out[i] = f32_to_bf16(xv[e] * wv[e]);
+    }
+    ss = block_sum256(ss, red);
+    if (threadIdx.x == 0) stats[blockIdx.x] = ss;
+    if (blockIdx.x == 0)
+        for (int i = gridDim.x + threadIdx.x; i < kNormSlots; i += 256) stats[i] = 0.0f;
+}
+
+__global__ __launch_bounds__(256) void norm_apply_kernel(const uint16_t* __restrict__ u, int64_t d,
+                                                         const float* __restrict__ stats, float eps,
+                                                         uint16_t* __restrict__ out) {
+    __shared__ float red[4];
+    float t = 0.0f;
+    for (int i = threadIdx.x; i < kNormSlots; i += 256) t += stats[i];
+    t = block_sum256(t, red);
+    const float inv = 1.0f / (float)sqrt((double)(t / (float)d + eps));
+    for (int64_t i = threadIdx.x; i < d; i += 256) out[i] = f32_to_bf16(bf16_to_f32(u[i]) * inv);
+}
+
 // ---- SDPA, general: one block per (b, h, query row) --------------------------------
 // q [B, Hq, Lq, Dh]; k/v [B, Hk, kcap, Dh] with the first Lk rows valid.
 __global__ __launch_bounds__(256) void sdpa_rows_kernel(const void* __restrict__ q, int q_dt,
@@ -904,6 +948,19 @@ Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const voi
     if (nsplit > 1)
         hipLaunchKernelGGL(sdpa_decode_merge_kernel, dim3((unsigned)Hq), dim3(kDecodeDh), 0, st,
                            static_cast<const float*>(workspace), Hk, G, (int)nsplit, out, out_dt);
+    return Status::ok();
+}
+
+Status launch_norm_prepare(const void* x, int x_dt, int64_t d, const void* w, int w_dt, uint16_t* out, float* stats,
+                           hipStream_t st) {
+    const int64_t blocks = (d + 256 * kPrepPer - 1) / (256 * kPrepPer);
+    if (blocks > kNormSlots) return Status::fail(JH_ERR_UNSUPPORTED, "norm_prepare: row too long");
+    hipLaunchKernelGGL(norm_prepare_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, x_dt, d, w, w_dt, out, stats);
+    return Status::ok();
+}
+
+Status launch_norm_apply(const uint16_t* u, int64_t d, const float* stats, float eps, uint16_t* out, hipStream_t st) {
+    hipLaunchKernelGGL(norm_apply_kernel, dim3(1), dim3(256), 0, st, u, d, stats, eps, out);
     return Status::ok();
 }
 

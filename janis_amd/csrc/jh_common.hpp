@@ -147,6 +147,10 @@ __device__ __forceinline__ void store_y(void* y, int64_t i, float v, int dt) {
 
 // ---- launch descriptors ------------------------------------------------------
 
+// Slots of the sum-of-squares statistics a residual-add product hands to the
+// next RMSNorm'd product (one partial per block, the rest zero).
+constexpr int kNormSlots = JH_NORM_STATS;
+
 struct QuantMatrix {
     const uint32_t* w;   // [rows, P]
     const void* scales;  // [rows, G]
@@ -177,10 +181,19 @@ Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int
 // Decode product with a fused prologue (pro: 0 none, 1 RMSNorm of fp32 x with
 // weight nw, 2 SiLU(x[:K]) * x[K:]) and epilogue (epi: 0 store, 1 y = resid +
 // product in fp32, 2 SwiGLU over W = [gate rows; up rows], y has m.rows / 2).
+struct NormSplit {
+    float* stats = nullptr;    // kNormSlots fp32: read by prologue 3, written by epilogue 3
+    uint16_t* out = nullptr;   // bf16 [rows]: epilogue 3's bf16(y * nw)
+};
 size_t qmv_fused_workspace_bytes(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, int epi, int y_dtype);
 Status launch_qmv_fused(const QuantMatrix& m, int pro, const void* x, int x_dtype, const void* nw, int nw_dtype,
-                        float eps, int epi, const float* resid, void* y, int y_dtype, int num_cus, hipStream_t st,
-                        void* workspace);
+                        float eps, int epi, const float* resid, void* y, int y_dtype, const NormSplit& ns,
+                        int num_cus, hipStream_t st, void* workspace);
+// out = bf16(x * w), stats = the sum of x^2 in per-block partials (one row of d).
+Status launch_norm_prepare(const void* x, int x_dt, int64_t d, const void* w, int w_dt, uint16_t* out, float* stats,
+                           hipStream_t st);
+// out = bf16(u / sqrt(sum(stats) / d + eps)).
+Status launch_norm_apply(const uint16_t* u, int64_t d, const float* stats, float eps, uint16_t* out, hipStream_t st);
 Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y,
                   int y_dtype, int num_cus, hipStream_t st, void* workspace);
 // fp32 accumulation buffer a split-K prefill needs (0 when none).

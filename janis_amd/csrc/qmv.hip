@@ -152,14 +152,24 @@ __device__ __forceinline__ void store_rows(void* Y, int y_dt, uint32_t row0, uin
 //                SiLU(dot_j) * dot_{N+j} (MLP.Forward's Mul(SiLU(gate), up),
 //                qwen/mlp.go:33-35). A slice computes RPW/2 gate rows and the
 //                matching up rows, so both dots meet in one lane.
-enum { PRO_NONE = 0, PRO_RMSNORM = 1 };
+//   PRO_NORMED   x is bf16(h * nw) from an EPI_RESID_NORM product, with the
+//                sum of h^2 in kNormSlots partials: each wave sums its share of
+//                the partials (loaded ahead of the weights), and the epilogue
+//                scales as PRO_RMSNORM does, so x costs what a plain one does.
+//   EPI_RESID_NORM  EPI_RESID, plus the next norm's input: nout[row] =
+//                bf16(y * nw[row]) and, per block, the sum of y^2 over its rows
+//                in stats[blockIdx.x] (grid <= kNormSlots; block 0 zeroes the
+//                unused slots). Fixed order: deterministic.
+enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_NORMED = 3 };
 constexpr int kProSiluMul = 2;  // x = [gate | up]: composed from separate launches
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_RESID_NORM = 3 };
 
 struct QmvFusion {
-    const uint16_t* nw = nullptr;  // bf16 norm weight [K] (PRO_RMSNORM)
+    const uint16_t* nw = nullptr;  // bf16 norm weight: [K] (PRO_RMSNORM) or [N] (EPI_RESID_NORM)
     float eps = 0.0f;
-    const float* resid = nullptr;  // fp32 [N] (EPI_RESID)
+    const float* resid = nullptr;  // fp32 [N] (EPI_RESID, EPI_RESID_NORM)
+    float* stats = nullptr;        // kNormSlots (PRO_NORMED: in; EPI_RESID_NORM: out)
+    uint16_t* nout = nullptr;      // bf16 [N] (EPI_RESID_NORM)
 };
 
 template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int PRO = PRO_NONE, int EPI = EPI_STORE>
@@ -197,8 +207,11 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     }
     uint4 wv[RPW][ITERS];
     uint16_t sh[RPW][ITERS], bh[RPW][ITERS];
-    float rv[EPI == EPI_RESID ? RPW : 1];  // the residual rows, fetched with the pass's weights
-    const auto rr = make_rsrc(fu.resid, EPI == EPI_RESID ? N * 4 : 0);
+    constexpr bool RESID = EPI == EPI_RESID || EPI == EPI_RESID_NORM;
+    float rv[RESID ? RPW : 1];  // the residual rows, fetched with the pass's weights
+    uint16_t nv[EPI == EPI_RESID_NORM ? RPW : 1];  // the next norm's weights for those rows
+    const auto rr = make_rsrc(fu.resid, RESID ? N * 4 : 0);
+    const auto rn = make_rsrc(fu.nw, EPI == EPI_RESID_NORM ? N * 2 : 0);
     // Loads complete in issue order. The raw x loads go first, then the first
     // pass's weights (which do not depend on x), and only then is x regrouped:
     // that waits for x alone while the weights are still in flight. Rows past the
@@ -220,10 +233,13 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
                 sh[r][it] = buf_load2(rs, off);
                 bh[r][it] = buf_load2(rb, off);
             }
-        if constexpr (EPI == EPI_RESID)
+        if constexpr (RESID)
 #pragma unroll
             for (int r = 0; r < RPW; r++)
                 rv[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr, (row0 + r) * 4, 0, 0));
+        if constexpr (EPI == EPI_RESID_NORM)
+#pragma unroll
+            for (int r = 0; r < RPW; r++) nv[r] = buf_load2(rn, (row0 + r) * 2);
     };
     // raw x: 32 elements per lane per ITER (bf16, or fp32 for the norm)
     constexpr int XW = PRO == PRO_RMSNORM ? 8 : 4;  // 16-byte chunks per 32 elements
@@ -252,12 +268,30 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
             for (int j = 0; j < 4; j++) xaux[it][j] = av[j];
         }
     }
+    // PRO_NORMED: this wave's share of the statistics partials, ahead of the weights
+    constexpr int SPL = PRO == PRO_NORMED ? kNormSlots / KSPLIT / 256 : 1;  // float4 per lane
+    static_assert(PRO != PRO_NORMED || SPL >= 1, "statistics split");
+    float4 st4[SPL];
+    if constexpr (PRO == PRO_NORMED) {
+        const float4* sp = reinterpret_cast<const float4*>(fu.stats) + ks * (kNormSlots / KSPLIT / 4);
+#pragma unroll
+        for (int j = 0; j < SPL; j++) st4[j] = sp[j * 64 + lane];
+    }
     const uint32_t lane_row = rg * ROWS_PER_WAVE + (uint32_t)slice * RO;
     load_pass(blockIdx.x * ROWS_PER_BLOCK + lane_row);
     // the product's input as bf16, 8 per uint4
     uint4 xin[ITERS][4];
-    float ss_part = 0.0f;  // PRO_RMSNORM: sum of x^2 over this wave's K part
-    if constexpr (PRO == PRO_NONE) {
+    float ss_part = 0.0f;  // PRO_RMSNORM / PRO_NORMED: sum of x^2 over this wave's share
+    float sq = 0.0f;       // EPI_RESID_NORM: sum of y^2 over the rows this lane stores
+    if constexpr (PRO == PRO_NORMED) {
+        float t = 0.0f;
+#pragma unroll
+        for (int j = 0; j < SPL; j++) t += (st4[j].x + st4[j].y) + (st4[j].z + st4[j].w);
+        ss_part = wave_sum(t);  // every lane holds the wave's share
+        if constexpr (KSPLIT > 1)
+            if (lane == 0) ssq[wv_id] = ss_part;
+    }
+    if constexpr (PRO == PRO_NONE || PRO == PRO_NORMED) {
 #pragma unroll
         for (int it = 0; it < ITERS; it++)
 #pragma unroll
@@ -339,7 +373,7 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
                         part[r] += red[((k - 1) * RGROUPS * SLICES * RPW) + slot + r];
             __syncthreads();
         }
-        if constexpr (PRO == PRO_RMSNORM) {
+        if constexpr (PRO == PRO_RMSNORM || PRO == PRO_NORMED) {
             // the K parts' sums of squares are in LDS since the exchange above
             float tot = ss_part;
             if constexpr (KSPLIT > 1) {
@@ -356,6 +390,15 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
 #pragma unroll
                 for (int r = 0; r < RPW; r++)
                     if (row0 + r < N) static_cast<float*>(Y)[row0 + r] = rv[r] + part[r];
+            } else if constexpr (EPI == EPI_RESID_NORM) {
+#pragma unroll
+                for (int r = 0; r < RPW; r++)
+                    if (row0 + r < N) {
+                        const float h = rv[r] + part[r];
+                        static_cast<float*>(Y)[row0 + r] = h;
+                        fu.nout[row0 + r] = f32_to_bf16_hw(h * bf16_to_f32(nv[r]));
+                        sq = fmaf(h, h, sq);
+                    }
             } else if constexpr (EPI == EPI_SWIGLU) {
                 float act[RO];
 #pragma unroll
@@ -365,6 +408,16 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
                 store_rows<RPW>(Y, y_dt, row0, N, part);
             }
         }
+    }
+    if constexpr (EPI == EPI_RESID_NORM) {
+        // this block's partial of the sum of y^2 (lanes that stored no row hold 0)
+        __shared__ float bsum[4];
+        const float w = wave_sum(sq);
+        if (lane == 0) bsum[wv_id] = w;
+        __syncthreads();
+        if (threadIdx.x == 0) fu.stats[blockIdx.x] = (bsum[0] + bsum[1]) + (bsum[2] + bsum[3]);
+        if (blockIdx.x == 0)
+            for (int i = gridDim.x + threadIdx.x; i < kNormSlots; i += 256) fu.stats[i] = 0.0f;
     }
 }
 
@@ -452,6 +505,7 @@ Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, in
     int64_t blocks = (n_out + rows_per_block - 1) / rows_per_block;
     const int64_t cap = (int64_t)num_cus * resident;
     if (blocks > cap) blocks = cap;
+    if (EPI == EPI_RESID_NORM && blocks > kNormSlots) blocks = kNormSlots;  // one partial per block
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, st, m.w,
                        static_cast<const uint16_t*>(m.scales), static_cast<const uint16_t*>(m.biases), x, y,
@@ -554,12 +608,14 @@ Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int
 
 // True when one register-tile launch takes the fused call (no workspace).
 bool qmv_fused_single(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, int epi, int y_dtype) {
-    if (pro == PRO_RMSNORM ? (x_dtype != JH_F32 || nw_dtype != JH_BF16) : (pro != PRO_NONE || x_dtype != JH_BF16))
+    if (pro == PRO_RMSNORM ? (x_dtype != JH_F32 || nw_dtype != JH_BF16)
+                           : ((pro != PRO_NONE && pro != PRO_NORMED) || x_dtype != JH_BF16))
         return false;
-    if (epi == EPI_RESID && y_dtype != JH_F32) return false;
+    if ((epi == EPI_RESID || epi == EPI_RESID_NORM) && y_dtype != JH_F32) return false;
+    if (epi == EPI_RESID_NORM && nw_dtype != JH_BF16) return false;
     if (!qmv_fast_shape(m)) return false;
     if (m.sb_dtype != JH_BF16 && (pro != PRO_NONE || epi != EPI_STORE)) return false;
-    if (pro == PRO_NONE) return epi == EPI_STORE || epi == EPI_RESID;
+    if (pro == PRO_NONE) return epi == EPI_STORE || epi == EPI_RESID || epi == EPI_RESID_NORM;
     return epi == EPI_STORE || epi == EPI_SWIGLU;
 }
 
@@ -569,23 +625,31 @@ size_t qmv_fused_workspace_bytes(const QuantMatrix& m, int pro, int x_dtype, int
 }
 
 Status launch_qmv_fused(const QuantMatrix& m, int pro, const void* x, int x_dtype, const void* nw, int nw_dtype,
-                        float eps, int epi, const float* resid, void* y, int y_dtype, int num_cus, hipStream_t st,
-                        void* workspace) {
+                        float eps, int epi, const float* resid, void* y, int y_dtype, const NormSplit& ns,
+                        int num_cus, hipStream_t st, void* workspace) {
     // one launch when a register tile takes the shape
     if (qmv_fused_single(m, pro, x_dtype, nw_dtype, epi, y_dtype)) {
         QmvFusion fu;
         fu.nw = static_cast<const uint16_t*>(nw);
         fu.eps = eps;
         fu.resid = resid;
+        fu.stats = ns.stats;
+        fu.nout = ns.out;
         bool done = false;
         if (pro == PRO_NONE && epi == EPI_STORE)
             done = launch_tiles<PRO_NONE, EPI_STORE>(m, x, y, y_dtype, num_cus, st, fu);
-        else if (pro == PRO_NONE)
+        else if (pro == PRO_NONE && epi == EPI_RESID)
             done = launch_tiles<PRO_NONE, EPI_RESID>(m, x, y, y_dtype, num_cus, st, fu);
-        else if (epi == EPI_STORE)
+        else if (pro == PRO_NONE)
+            done = launch_tiles<PRO_NONE, EPI_RESID_NORM>(m, x, y, y_dtype, num_cus, st, fu);
+        else if (pro == PRO_RMSNORM && epi == EPI_STORE)
             done = launch_tiles<PRO_RMSNORM, EPI_STORE>(m, x, y, y_dtype, num_cus, st, fu);
-        else
+        else if (pro == PRO_RMSNORM)
             done = launch_tiles<PRO_RMSNORM, EPI_SWIGLU>(m, x, y, y_dtype, num_cus, st, fu);
+        else if (epi == EPI_STORE)
+            done = launch_tiles<PRO_NORMED, EPI_STORE>(m, x, y, y_dtype, num_cus, st, fu);
+        else
+            done = launch_tiles<PRO_NORMED, EPI_SWIGLU>(m, x, y, y_dtype, num_cus, st, fu);
         if (done) return Status::ok();
         return Status::fail(JH_ERR_UNSUPPORTED, "qmv_fused: no tile for a shape the planner accepted");
     }
@@ -599,6 +663,11 @@ Status launch_qmv_fused(const QuantMatrix& m, int pro, const void* x, int x_dtyp
         Status s = launch_rms_norm(x, x_dtype, nw, nw_dtype, eps, xin, JH_BF16, 1, m.in, st);
         if (s.code != JH_OK) return s;
         xp = xin, xdt = JH_BF16;
+    } else if (pro == PRO_NORMED) {
+        if (x_dtype != JH_BF16) return Status::fail(JH_ERR_INVALID, "qmv_fused: a prepared norm input is bf16");
+        Status s = launch_norm_apply(static_cast<const uint16_t*>(x), m.in, ns.stats, eps, xin, st);
+        if (s.code != JH_OK) return s;
+        xp = xin, xdt = JH_BF16;
     } else if (pro == kProSiluMul) {
         const size_t esz = x_dtype == JH_F32 ? 4 : 2;
         Status s = launch_elementwise(JH_OP_SILU_MUL, x, x_dtype, static_cast<const char*>(x) + m.in * esz, x_dtype,
@@ -610,6 +679,11 @@ Status launch_qmv_fused(const QuantMatrix& m, int pro, const void* x, int x_dtyp
     Status s = launch_qmv(m, xp, xdt, tmp, JH_F32, num_cus, st);
     if (s.code != JH_OK) return s;
     if (epi == EPI_RESID) return launch_elementwise(JH_OP_ADD, resid, JH_F32, tmp, JH_F32, y, y_dtype, m.rows, st);
+    if (epi == EPI_RESID_NORM) {
+        s = launch_elementwise(JH_OP_ADD, resid, JH_F32, tmp, JH_F32, y, JH_F32, m.rows, st);
+        if (s.code != JH_OK) return s;
+        return launch_norm_prepare(y, JH_F32, m.rows, nw, nw_dtype, ns.out, ns.stats, st);
+    }
     const int64_t n = m.rows / 2;
     return launch_elementwise(JH_OP_SILU_MUL, tmp, JH_F32, tmp + n, JH_F32, y, y_dtype, n, st);
 }

@@ -285,22 +285,32 @@ int jh_quant_matvec_fused(jh_ctx* c, jh_prologue pro, const void* x, jh_dtype x_
                           jh_dtype norm_w_dtype, float eps, const uint32_t* w, const void* scales,
                           const void* biases, jh_dtype sb_dtype, int64_t out_features, int64_t in_features,
                           int group_size, int bits, jh_epilogue epi, const float* resid, void* y,
-                          jh_dtype y_dtype) {
+                          jh_dtype y_dtype, float* norm_stats, void* norm_out) {
     if (int r = enter(c)) return r;
     const char* op = "jh_quant_matvec_fused";
-    if (pro != JH_PRO_NONE && pro != JH_PRO_RMSNORM && pro != JH_PRO_SILU_MUL)
+    if (pro != JH_PRO_NONE && pro != JH_PRO_RMSNORM && pro != JH_PRO_SILU_MUL && pro != JH_PRO_NORMED)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": unknown prologue");
-    if (epi != JH_EPI_STORE && epi != JH_EPI_RESID && epi != JH_EPI_SWIGLU)
+    if (epi != JH_EPI_STORE && epi != JH_EPI_RESID && epi != JH_EPI_SWIGLU && epi != JH_EPI_RESID_NORM)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": unknown epilogue");
+    if (epi == JH_EPI_RESID_NORM && (pro == JH_PRO_NORMED || pro == JH_PRO_RMSNORM))
+        return fail(c, JH_ERR_UNSUPPORTED,
+                    std::string(op) + ": a split-norm epilogue cannot follow a norm prologue (one norm_w, one stats)");
+    if ((pro == JH_PRO_NORMED || epi == JH_EPI_RESID_NORM) && (!norm_stats || !aligned16(norm_stats)))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": the split norm needs 16-byte aligned norm_stats");
+    if (epi == JH_EPI_RESID_NORM && (!norm_out || !norm_w))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": JH_EPI_RESID_NORM needs norm_w and norm_out");
+    if (pro == JH_PRO_NORMED && x_dtype != JH_BF16)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": JH_PRO_NORMED takes the bf16 norm_out");
     if (out_features < 0 || (epi == JH_EPI_SWIGLU && out_features > ((int64_t)1 << 40)))
         return fail(c, JH_ERR_INVALID, std::string(op) + ": bad out_features");
     const int64_t w_rows = epi == JH_EPI_SWIGLU ? 2 * out_features : out_features;
     if (int r = check_quant(c, op, w, scales, biases, sb_dtype, w_rows, in_features, group_size, bits)) return r;
     if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
     if (int r = check_act_dtype(c, op, "y", y_dtype)) return r;
-    if (pro == JH_PRO_RMSNORM && norm_w_dtype != JH_BF16 && norm_w_dtype != JH_F16 && norm_w_dtype != JH_F32)
+    if ((pro == JH_PRO_RMSNORM || epi == JH_EPI_RESID_NORM) && norm_w_dtype != JH_BF16 && norm_w_dtype != JH_F16 &&
+        norm_w_dtype != JH_F32)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": norm weight must be bf16, f16 or f32");
-    if (epi == JH_EPI_RESID && (y_dtype != JH_F32 || !resid))
+    if ((epi == JH_EPI_RESID || epi == JH_EPI_RESID_NORM) && (y_dtype != JH_F32 || !resid))
         return fail(c, JH_ERR_INVALID, std::string(op) + ": the residual add needs resid and writes fp32 (y_dtype JH_F32)");
     if (out_features == 0) return JH_OK;
     if (!x || !y || !aligned16(x) || !aligned16(y) || (pro == JH_PRO_RMSNORM && (!norm_w || !aligned16(norm_w))))
@@ -309,8 +319,25 @@ int jh_quant_matvec_fused(jh_ctx* c, jh_prologue pro, const void* x, jh_dtype x_
     const size_t need = jh::qmv_fused_workspace_bytes(m, (int)pro, x_dtype, norm_w_dtype, (int)epi, y_dtype);
     if (need)
         if (int r = ensure_workspace(c, need, op)) return r;
+    jh::NormSplit ns;
+    ns.stats = norm_stats;
+    ns.out = static_cast<uint16_t*>(norm_out);
     return finish(c, jh::launch_qmv_fused(m, (int)pro, x, x_dtype, norm_w, norm_w_dtype, eps, (int)epi, resid, y,
-                                          y_dtype, c->num_cus, c->stream, c->ws),
+                                          y_dtype, ns, c->num_cus, c->stream, c->ws),
+                  op);
+}
+
+int jh_norm_prepare(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t d, const void* norm_w, jh_dtype norm_w_dtype,
+                    void* norm_out, float* norm_stats) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_norm_prepare";
+    if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
+    if (norm_w_dtype != JH_BF16 && norm_w_dtype != JH_F16 && norm_w_dtype != JH_F32)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": norm weight must be bf16, f16 or f32");
+    if (d <= 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": d <= 0");
+    if (!x || !norm_w || !norm_out || !norm_stats) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    return finish(c, jh::launch_norm_prepare(x, x_dtype, d, norm_w, norm_w_dtype, static_cast<uint16_t*>(norm_out),
+                                             norm_stats, c->stream),
                   op);
 }
 

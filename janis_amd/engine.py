@@ -387,14 +387,18 @@ class HipBackend:
     def QuantMatvecFused(self, x: Tensor, w: Tensor, scales: Tensor, biases: Tensor, groupSize: int, bits: int,
                          prologue: int = _lib.JH_PRO_NONE, norm: Tensor | None = None, eps: float = 0.0,
                          epilogue: int | None = None, resid: Tensor | None = None, out: Tensor | None = None,
-                         out_dtype: int | None = None) -> Tensor:
+                         out_dtype: int | None = None, stats: Tensor | None = None,
+                         norm_out: Tensor | None = None) -> Tensor:
         """One-token QuantMatmul (transpose=true) with the operator before it
         fused in (JH_PRO_RMSNORM: RMSNorm(x, norm, eps), the norm feeding q/k/v,
         gate/up and the LM head; JH_PRO_SILU_MUL: x = [gate | up] -> SiLU(gate)*up)
         and the one after it (JH_EPI_RESID, the default when resid is given: the
         residual Add of qwen/block.go:59-60 into an fp32 result, out may be resid;
         JH_EPI_SWIGLU: w stacks the Gate rows then the Up rows and the result is
-        SiLU(gate)*up, qwen/mlp.go:33-35)."""
+        SiLU(gate)*up, qwen/mlp.go:33-35). The split norm: JH_EPI_RESID_NORM
+        also writes norm_out = bf16(y * norm) (norm = the NEXT norm's weight)
+        and its statistics into `stats`; the product that consumes them takes
+        JH_PRO_NORMED with x = that norm_out and the same `stats`."""
         if w.dtype != U32:
             raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: weight tensor is not packed U32")
         if epilogue is None:
@@ -407,19 +411,41 @@ class HipBackend:
         want = 2 * k if prologue == _lib.JH_PRO_SILU_MUL else k
         if x.numel != want:
             raise JanisHipError(_lib.JH_ERR_INVALID, f"QuantMatvecFused: x has {x.numel} elements, needs {want}")
-        if epilogue == _lib.JH_EPI_RESID and (resid is None or resid.dtype != F32 or resid.numel != n):
+        residual = epilogue in (_lib.JH_EPI_RESID, _lib.JH_EPI_RESID_NORM)
+        if residual and (resid is None or resid.dtype != F32 or resid.numel != n):
             raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: resid must be F32 [out_features]")
         if prologue == _lib.JH_PRO_RMSNORM and (norm is None or norm.numel != k):
             raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: RMSNorm needs a weight of in_features")
-        yd = F32 if epilogue == _lib.JH_EPI_RESID else (
+        if epilogue == _lib.JH_EPI_RESID_NORM and (norm is None or norm.numel != n or norm_out is None
+                                                   or norm_out.dtype != BF16 or norm_out.numel != n):
+            raise JanisHipError(_lib.JH_ERR_INVALID,
+                                "QuantMatvecFused: the split norm needs norm [out] and a BF16 norm_out [out]")
+        if (prologue == _lib.JH_PRO_NORMED or epilogue == _lib.JH_EPI_RESID_NORM) and (
+                stats is None or stats.dtype != F32 or stats.numel != _lib.JH_NORM_STATS):
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: stats must be F32 [JH_NORM_STATS]")
+        yd = F32 if residual else (
             out_dtype if out_dtype is not None else (out.dtype if out is not None else x.dtype))
         y = out if out is not None else self.empty(yd, 1, n)
         check(self._ctx, self._L.jh_quant_matvec_fused(
             self._ctx, int(prologue), x.ptr, x.dtype, norm.ptr if norm is not None else None,
             norm.dtype if norm is not None else BF16, float(eps), w.ptr, scales.ptr, biases.ptr,
             self._sb_dtype(scales, biases), n, k, groupSize, bits, int(epilogue),
-            resid.ptr if resid is not None else None, y.ptr, y.dtype))
+            resid.ptr if resid is not None else None, y.ptr, y.dtype,
+            stats.ptr if stats is not None else None, norm_out.ptr if norm_out is not None else None))
         return y
+
+    def NormPrepare(self, x: Tensor, norm: Tensor, norm_out: Tensor | None = None,
+                    stats: Tensor | None = None) -> tuple:
+        """The producer half of a split RMSNorm for a row already at hand (the
+        embedding row): (bf16(x * norm) [1, d], F32 statistics [JH_NORM_STATS]),
+        for a QuantMatvecFused with JH_PRO_NORMED."""
+        d = x.shape[-1]
+        if x.numel != d or norm.numel != d:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "NormPrepare: one row and a weight of its length")
+        u = norm_out if norm_out is not None else self.empty(BF16, 1, d)
+        st = stats if stats is not None else self.empty(F32, _lib.JH_NORM_STATS)
+        check(self._ctx, self._L.jh_norm_prepare(self._ctx, x.ptr, x.dtype, d, norm.ptr, norm.dtype, u.ptr, st.ptr))
+        return u, st
 
     def RoPETable(self, dims: int, base: float, scale: float, pos: int, freqs: Tensor | None = None) -> Tensor:
         """cos and sin of the RoPE angles at pos (cpu/cpu_attn.go:13-34): F32

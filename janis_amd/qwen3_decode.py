@@ -62,53 +62,57 @@ class Qwen3Model:
 def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bool = True) -> tuple:
     """Runs token (I32 [1], device) at position pos through every layer, appends
     its keys/values to the caches, returns (logits F32 [1, vocab], next token I32 [1]).
-    fused=True takes the backend's fused operators: each norm inside the product
-    it feeds, SiLU*mul in the gate/up product's epilogue, the residual adds in
-    the o/down products' epilogues, and the q/k norms, RoPE, KV append and SDPA
-    in one launch plus a merge (6 launches per layer). fused=False spells the step out as the reference's
-    separate operators (15 per layer)."""
+    fused=True takes the backend's fused operators: each RMSNorm split between
+    the product that makes the residual stream (its epilogue writes bf16(h*w)
+    and the sum of h^2) and the product that reads it (which applies the
+    1/rms factor to its output), SiLU*mul in the gate/up product's epilogue,
+    the residual adds in the o/down products' epilogues, and the q/k norms,
+    RoPE, KV append and SDPA in one launch plus a merge (6 launches per layer).
+    fused=False spells the step out as the reference's separate operators (15
+    per layer)."""
     c = m.cfg
     gs, bits = c.group_size, c.bits
     H, Hq, Hk, Dh, I = c.hidden, c.n_heads, c.n_kv, c.head_dim, c.inter
-    RMS, SWIGLU = _lib.JH_PRO_RMSNORM, _lib.JH_EPI_SWIGLU
+    NORMED, SWIGLU, RESID_NORM = _lib.JH_PRO_NORMED, _lib.JH_EPI_SWIGLU, _lib.JH_EPI_RESID_NORM
     # QuantEmbedding.Forward (qwen/embed.go:78-83)
     ew, es, eb = m.embed
     h = b.Dequantize(b.TakeAxis(ew, token), b.TakeAxis(es, token), b.TakeAxis(eb, token), gs, bits)  # F32 [1, H]
-    cs = b.RoPETable(Dh, c.theta, 1.0, pos) if fused else None  # shared by every layer
-    for L in m.layers:
-        # Attention.ForwardCached
-        if fused:
-            qkv = b.QuantMatvecFused(h, *L.qkv, gs, bits, RMS, L.in_norm, c.eps, out_dtype=F32)
-            att = b.AttentionDecode(qkv, Hq, Hk, L.q_norm, L.k_norm, c.eps, c.theta, 1.0, pos, L.k_cache,
-                                    L.v_cache, Dh ** -0.5, out_dtype=BF16, rope_cs=cs)
-        else:
-            xn = b.RMSNorm(h, L.in_norm, c.eps, out_dtype=BF16)
-            qkv = b.QuantMatmul(xn, *L.qkv, True, gs, bits, out_dtype=F32)  # [1, (Hq+2Hk)*Dh]
-            q = _rows(b, qkv, 0, Hq * Dh, (1, Hq, 1, Dh))
-            k = _rows(b, qkv, Hq * Dh, Hk * Dh, (1, Hk, 1, Dh))
-            v = _rows(b, qkv, (Hq + Hk) * Dh, Hk * Dh, (1, Hk, 1, Dh))
-            q = b.RoPE(b.RMSNorm(q, L.q_norm, c.eps), Dh, False, c.theta, 1.0, pos)
-            k = b.RoPE(b.RMSNorm(k, L.k_norm, c.eps), Dh, False, c.theta, 1.0, pos)
-            b.AppendKV(L.k_cache, L.v_cache, pos, k, v)
-            att = b.Reshape(b.SDPA(q, L.k_cache, L.v_cache, Dh ** -0.5, False, kv_len=pos + 1, out_dtype=BF16),
-                            1, Hq * Dh)
-        # the residual adds and MLP.Forward
-        if fused:
-            b.QuantMatvecFused(att, *L.o, gs, bits, resid=h, out=h)
-            act = b.QuantMatvecFused(h, *L.gate_up, gs, bits, RMS, L.post_norm, c.eps, epilogue=SWIGLU,
-                                     out_dtype=BF16)
-            b.QuantMatvecFused(act, *L.down, gs, bits, resid=h, out=h)
-        else:
-            h = b.Add(h, b.QuantMatmul(att, *L.o, True, gs, bits, out_dtype=F32))
-            xn = b.RMSNorm(h, L.post_norm, c.eps, out_dtype=BF16)
-            gu = b.QuantMatmul(xn, *L.gate_up, True, gs, bits, out_dtype=BF16)  # [1, 2I]
-            act = b.SiLUMul(_rows(b, gu, 0, I, (1, I)), _rows(b, gu, I, I, (1, I)))
-            h = b.Add(h, b.QuantMatmul(act, *L.down, True, gs, bits, out_dtype=F32))
     head = m.lm_head if m.lm_head is not None else m.embed
     if fused:
-        logits = b.QuantMatvecFused(h, *head, gs, bits, RMS, m.norm, c.eps, out_dtype=F32)
-    else:
-        logits = b.QuantMatmul(b.RMSNorm(h, m.norm, c.eps, out_dtype=BF16), *head, True, gs, bits, out_dtype=F32)
+        cs = b.RoPETable(Dh, c.theta, 1.0, pos)  # shared by every layer
+        u, st = b.NormPrepare(h, m.layers[0].in_norm)  # the first block's InputNorm, producer half
+        for li, L in enumerate(m.layers):
+            nxt = m.layers[li + 1].in_norm if li + 1 < len(m.layers) else m.norm
+            qkv = b.QuantMatvecFused(u, *L.qkv, gs, bits, NORMED, eps=c.eps, stats=st, out_dtype=F32)
+            att = b.AttentionDecode(qkv, Hq, Hk, L.q_norm, L.k_norm, c.eps, c.theta, 1.0, pos, L.k_cache,
+                                    L.v_cache, Dh ** -0.5, out_dtype=BF16, rope_cs=cs)
+            b.QuantMatvecFused(att, *L.o, gs, bits, norm=L.post_norm, epilogue=RESID_NORM, resid=h, out=h,
+                               stats=st, norm_out=u)
+            act = b.QuantMatvecFused(u, *L.gate_up, gs, bits, NORMED, eps=c.eps, stats=st, epilogue=SWIGLU,
+                                     out_dtype=BF16)
+            b.QuantMatvecFused(act, *L.down, gs, bits, norm=nxt, epilogue=RESID_NORM, resid=h, out=h, stats=st,
+                               norm_out=u)
+        logits = b.QuantMatvecFused(u, *head, gs, bits, NORMED, eps=c.eps, stats=st, out_dtype=F32)
+        return logits, b.Argmax(logits)
+    for L in m.layers:
+        # Attention.ForwardCached
+        xn = b.RMSNorm(h, L.in_norm, c.eps, out_dtype=BF16)
+        qkv = b.QuantMatmul(xn, *L.qkv, True, gs, bits, out_dtype=F32)  # [1, (Hq+2Hk)*Dh]
+        q = _rows(b, qkv, 0, Hq * Dh, (1, Hq, 1, Dh))
+        k = _rows(b, qkv, Hq * Dh, Hk * Dh, (1, Hk, 1, Dh))
+        v = _rows(b, qkv, (Hq + Hk) * Dh, Hk * Dh, (1, Hk, 1, Dh))
+        q = b.RoPE(b.RMSNorm(q, L.q_norm, c.eps), Dh, False, c.theta, 1.0, pos)
+        k = b.RoPE(b.RMSNorm(k, L.k_norm, c.eps), Dh, False, c.theta, 1.0, pos)
+        b.AppendKV(L.k_cache, L.v_cache, pos, k, v)
+        att = b.Reshape(b.SDPA(q, L.k_cache, L.v_cache, Dh ** -0.5, False, kv_len=pos + 1, out_dtype=BF16),
+                        1, Hq * Dh)
+        # the residual adds and MLP.Forward
+        h = b.Add(h, b.QuantMatmul(att, *L.o, True, gs, bits, out_dtype=F32))
+        xn = b.RMSNorm(h, L.post_norm, c.eps, out_dtype=BF16)
+        gu = b.QuantMatmul(xn, *L.gate_up, True, gs, bits, out_dtype=BF16)  # [1, 2I]
+        act = b.SiLUMul(_rows(b, gu, 0, I, (1, I)), _rows(b, gu, I, I, (1, I)))
+        h = b.Add(h, b.QuantMatmul(act, *L.down, True, gs, bits, out_dtype=F32))
+    logits = b.QuantMatmul(b.RMSNorm(h, m.norm, c.eps, out_dtype=BF16), *head, True, gs, bits, out_dtype=F32)
     return logits, b.Argmax(logits)
 
 

@@ -414,3 +414,66 @@ def test_rope_table(hip, oracle, dims, pos, freqs):
     step(f"jh_rope_table dims={dims} pos={pos}")
     got = hip.Floats(hip.RoPETable(dims, 1e6, 1.0, pos, hip.FromFloats(fr) if freqs else None))
     assert np.array_equal(got, r)
+
+
+@pytest.mark.parametrize("N1,K1,N2", [(4096, 4096, 6144), (4096, 12288, 24576), (4096, 4096, 70000),
+                                      (960, 512, 300), (512, 1024, 512)])
+def test_split_rmsnorm_producer_consumer(hip, oracle, N1, K1, N2):
+    """JH_EPI_RESID_NORM then JH_PRO_NORMED: h = resid + x.W1^T (fp32, in place),
+    u = bf16(h * w) written by the producer with per-block sums of h^2, and the
+    consumer's (u.W2^T) / rms(h) equals RMSNorm(h, w) -> QuantMatmul(W2) within the
+    bf16 rounding of the product's input. With N2 = 24576 the consumer also
+    takes the SwiGLU epilogue. (960, 512, 300) is outside the register tiles
+    (composed launches)."""
+    from janis_amd import _lib
+    rng = np.random.default_rng(N1 + K1 + N2)
+    q1 = synth.quant_linear(N1 + 5, N1, K1, 64)
+    q2 = synth.quant_linear(N2 + 9, N2, N1, 64)
+    w1, s1, b1 = upload_quant(hip, q1)
+    w2, s2, b2 = upload_quant(hip, q2)
+    x = _bf16(rng.standard_normal((1, K1)))
+    resid = (3.0 * rng.standard_normal((1, N1))).astype(np.float32)
+    nw = _bf16(1 + 0.1 * rng.standard_normal(N1))
+    h_d, u_d = hip.FromFloats(resid), hip.empty(BF16, 1, N1)
+    st = hip.empty(F32, _lib.JH_NORM_STATS)
+    step(f"split RMSNorm producer N={N1} K={K1}")
+    hip.QuantMatvecFused(_put(hip, x, BF16), w1, s1, b1, 64, 4, norm=_put(hip, nw, BF16),
+                         epilogue=_lib.JH_EPI_RESID_NORM, resid=h_d, out=h_d, stats=st, norm_out=u_d)
+    h = hip.Floats(h_d)
+    want_h = resid + oracle.quant_matmul(x, q1.w, q1.s, q1.b, 64)
+    ok, dd, sc = rel_ok(h, want_h, 1e-3)
+    assert ok, (dd, sc)
+    assert np.array_equal(hip.Floats(u_d), _bf16(h * nw))  # exactly bf16(h * w) of the stored h
+    stats = hip.Floats(st)
+    assert abs(float(stats.astype(np.float64).sum()) - float((h.astype(np.float64) ** 2).sum())) <= \
+        1e-5 * float((h.astype(np.float64) ** 2).sum())
+    swiglu = N2 == 24576
+    step(f"split RMSNorm consumer N={N2} swiglu={swiglu}")
+    got = hip.Floats(hip.QuantMatvecFused(u_d, w2, s2, b2, 64, 4, _lib.JH_PRO_NORMED, eps=1e-6, stats=st,
+                                          epilogue=_lib.JH_EPI_SWIGLU if swiglu else _lib.JH_EPI_STORE,
+                                          out_dtype=F32))
+    y = oracle.quant_matmul(_bf16(oracle.rms_norm(h, nw, 1e-6)), q2.w, q2.s, q2.b, 64)[0]
+    if swiglu:
+        y = oracle.silu(y[:N2 // 2]) * y[N2 // 2:]
+    ok, dd, sc = rel_ok(got[0], y, 1e-2)
+    assert ok, (dd, sc)
+
+
+def test_norm_prepare(hip, oracle):
+    from janis_amd import _lib
+    rng = np.random.default_rng(77)
+    x = (2.0 * rng.standard_normal((1, 4096))).astype(np.float32)
+    nw = _bf16(1 + 0.1 * rng.standard_normal(4096))
+    step("jh_norm_prepare")
+    u, st = hip.NormPrepare(hip.FromFloats(x), _put(hip, nw, BF16))
+    assert np.array_equal(hip.Floats(u), _bf16(x * nw))
+    s = hip.Floats(st)
+    assert s.shape == (_lib.JH_NORM_STATS,) and not s[2:].any()  # 4096 elements: two block partials
+    ref = float((x.astype(np.float64) ** 2).sum())
+    assert abs(float(s.astype(np.float64).sum()) - ref) <= 1e-5 * ref
+    with pytest.raises(JanisHipError):  # one norm weight and one statistics buffer per call
+        q = synth.quant_linear(3, 256, 4096, 64)
+        w, s_, b_ = upload_quant(hip, q)
+        hip.QuantMatvecFused(hip.FromFloats(x), w, s_, b_, 64, 4, _lib.JH_PRO_RMSNORM, _put(hip, nw, BF16), 1e-6,
+                             epilogue=_lib.JH_EPI_RESID_NORM, resid=hip.FromFloats(np.zeros((1, 256), np.float32)),
+                             stats=st, norm_out=hip.empty(BF16, 1, 256))
