@@ -369,28 +369,35 @@ __global__ __launch_bounds__(256) void sdpa_decode_split_kernel(const void* __re
     }
 }
 
-// Merge the splits of one (b, query head): thread d owns feature d. The splits
-// are read 16 at a time, each chunk's loads issued together (one memory round
-// trip per chunk), and folded in with an online rescale.
+// Merge the splits of one (b, query head): blockDim / 128 groups (1 to 4, one
+// per 16 splits) of 128 threads each take a share of the splits (thread d of a
+// group owns feature d), reading them 16 at a time with each chunk's loads
+// issued together and folding them in with an online rescale; the groups meet
+// in LDS. Up to 64 splits cost one memory round trip.
 constexpr int kMaxSplits = 1024;
+constexpr int kMergeGroups = 4;
+int merge_groups(int64_t nsplit) { return (int)std::min<int64_t>(kMergeGroups, (nsplit + 15) / 16); }
 
-__global__ __launch_bounds__(128) void sdpa_decode_merge_kernel(const float* __restrict__ part, int Hk, int G,
-                                                                int nsplit, void* __restrict__ out, int out_dt) {
+__global__ __launch_bounds__(128 * kMergeGroups) void sdpa_decode_merge_kernel(const float* __restrict__ part, int Hk,
+                                                                               int G, int nsplit,
+                                                                               void* __restrict__ out, int out_dt) {
     constexpr int Dh = kDecodeDh, C = 16;
     const int bh = blockIdx.x;  // b*Hq + h
     const int Hq = Hk * G;
     const int b = bh / Hq, h = bh - b * Hq;
     const int hk = h / G, g = h - hk * G;
-    const int d = threadIdx.x;
+    const int d = threadIdx.x & (Dh - 1), grp = threadIdx.x / Dh, ng = blockDim.x / Dh;
     const int64_t stride = (int64_t)G * (Dh + 2);
     const float* base = part + ((int64_t)(b * Hk + hk) * nsplit) * stride + g * (Dh + 2);
+    const int per = (nsplit + ng - 1) / ng;
+    const int s_begin = grp * per, s_end = min(nsplit, s_begin + per);
     float M = -__builtin_inff(), L = 0.0f, A = 0.0f;
-    for (int s0 = 0; s0 < nsplit; s0 += C) {
+    for (int s0 = s_begin; s0 < s_end; s0 += C) {
         float mv[C], lv[C], av[C];
 #pragma unroll
         for (int u = 0; u < C; u++) {
-            const bool in = s0 + u < nsplit;
-            const float* ps = base + (int64_t)(in ? s0 + u : nsplit - 1) * stride;  // in bounds either way
+            const bool in = s0 + u < s_end;
+            const float* ps = base + (int64_t)(in ? s0 + u : s_end - 1) * stride;  // in bounds either way
             mv[u] = in ? ps[0] : -__builtin_inff();
             lv[u] = in ? ps[1] : 0.0f;
             av[u] = in ? ps[2 + d] : 0.0f;
@@ -410,7 +417,24 @@ __global__ __launch_bounds__(128) void sdpa_decode_merge_kernel(const float* __r
         }
         M = mn;
     }
-    st_act(out, (int64_t)bh * Dh + d, A / L, out_dt);
+    if (ng == 1) {
+        st_act(out, (int64_t)bh * Dh + d, A / L, out_dt);
+        return;
+    }
+    __shared__ float gm[kMergeGroups], gl[kMergeGroups], ga[kMergeGroups][Dh];
+    if (d == 0) gm[grp] = M, gl[grp] = L;
+    ga[grp][d] = A;
+    __syncthreads();
+    if (grp != 0) return;
+    float Mt = gm[0];
+    for (int q = 1; q < ng; q++) Mt = fmaxf(Mt, gm[q]);
+    float Lt = 0.0f, At = 0.0f;
+    for (int q = 0; q < ng; q++) {
+        const float c = gm[q] == -__builtin_inff() ? 0.0f : __expf(gm[q] - Mt);
+        Lt = fmaf(gl[q], c, Lt);
+        At = fmaf(ga[q][d], c, At);
+    }
+    st_act(out, (int64_t)bh * Dh + d, At / Lt, out_dt);
 }
 
 // Per-head RMSNorm of one 128-feature head held as lane i: (a, b) = features
@@ -483,16 +507,18 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
 // ---- one-token attention in one launch ---------------------------------------------
 // Attention.ForwardCached for one new token (qwen/attention.go:98-128) after the
 // q/k/v product: per-head q/k RMSNorm and RoPE, the KV-cache append, and SDPA
-// over keys 0..pos. Block (split, hk) takes keys [split*kps, min(pos+1,
-// (split+1)*kps)) for the G = Hq/Hk query heads of kv head hk:
+// over keys 0..pos. The pos cache rows are split evenly over blocks (split, hk),
+// kps rows each, for the G = Hq/Hk query heads of kv head hk; the new key at pos
+// has a block of its own (split 0) when the grid has room, else it joins the
+// last split:
 //   1. its K/V rows are requested first (they do not depend on q), then every
 //      block normalises and rotates its G query heads into LDS (a few hundred
-//      flops, cheaper than a launch); the block whose range holds `pos`
-//      normalises and rotates the new key, writes the new key and value rows to
-//      the caches, and scores them from LDS (bf16-rounded, as the cache holds
-//      them), never reading row pos back;
+//      flops, cheaper than a launch); the new key's block normalises and
+//      rotates it, writes the new key and value rows to the caches, and scores
+//      them from LDS (bf16-rounded, as the cache holds them), never reading row
+//      pos back;
 //   2. 16 key slots per block (4 per wave, a 16-lane row per key, 8 features per
-//      lane) run an online softmax over the slot's keys, 4 keys per load batch;
+//      lane) run an online softmax over the slot's keys, U keys per load batch;
 //   3. the slots merge in registers (cross-row permlane swaps) and then across
 //      the 4 waves in LDS;
 //   4. with one split the block writes the output; otherwise (max, sum,
@@ -513,44 +539,41 @@ struct AttnArgs {
     uint16_t* vc;
     int64_t cap;
     int Hk, nsplit, kps;
+    int owner_alone;    // 1: split 0 takes only the new key; 0: the last split also takes it
     float* part;        // [Hk, nsplit, G, 130]
     void* out;          // [Hq * 128]
     int out_dt;
 };
 
-template <int G>
+template <int G, int U>  // U: keys per slot per load batch
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
-    constexpr int Dh = 128, U = 4;
+    constexpr int Dh = 128;
     const int split = blockIdx.x, hk = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int kg = lane >> 4, kl = lane & 15;
     const int Hq = a.Hk * G;
-    const int64_t Lk = a.pos + 1;
-    const int64_t j_begin = (int64_t)split * a.kps;
-    const int64_t j_end = min(Lk, j_begin + a.kps);
-    const bool owner = a.pos < j_end;  // the last split holds the new key
-    const int64_t jc_end = min(j_end, a.pos);  // cache rows scored by this block
+    // the cache rows 0..pos-1 split evenly; the new key has a block of its own
+    // (split 0, dispatched first) or joins the last split
+    const bool owner = a.owner_alone ? split == 0 : split == a.nsplit - 1;
+    const int64_t cs = a.owner_alone ? (int64_t)split - 1 : split;  // -1: the new key's own block
+    const int64_t j_begin = cs < 0 ? 0 : cs * a.kps;
+    const int64_t jc_end = cs < 0 ? 0 : min(a.pos, j_begin + a.kps);  // cache rows scored by this block
     const uint16_t* kb = a.kc + (int64_t)hk * a.cap * Dh + 8 * kl;
     const uint16_t* vb = a.vc + (int64_t)hk * a.cap * Dh + 8 * kl;
     const int slot = wave * 4 + kg;
 
     // 1. the first batch of K/V rows, then the query heads (and the new key)
-    uint4 kr[U], vr[U];
-    auto load_batch = [&](int64_t j0) {
+    uint4 kr[U], vr[U];  // raw bf16 rows, unpacked one key at a time
+    auto load_rows = [&](uint4 (&r)[U], const uint16_t* src, int64_t j0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int64_t j = j0 + 16 * u;
-            if (j < jc_end) {
-                kr[u] = *reinterpret_cast<const uint4*>(kb + j * Dh);
-                vr[u] = *reinterpret_cast<const uint4*>(vb + j * Dh);
-            } else {
-                kr[u] = make_uint4(0, 0, 0, 0);
-                vr[u] = make_uint4(0, 0, 0, 0);
-            }
+            r[u] = j < jc_end ? *reinterpret_cast<const uint4*>(src + j * Dh) : make_uint4(0, 0, 0, 0);
         }
     };
     int64_t j0 = j_begin + slot;
-    load_batch(j0);
+    load_rows(kr, kb, j0);
+    load_rows(vr, vb, j0);
 
     __shared__ float q_s[G][Dh];
     __shared__ float kn_s[Dh], vn_s[Dh];
@@ -604,27 +627,32 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
             f[2 * q + 1] = __uint_as_float(w[q] & 0xFFFF0000u);
         }
     };
+    // Scores for the batch (keys unpacked one at a time), then the next batch's
+    // keys are requested while the softmax and the value sums run, and its
+    // values once those are done.
     for (; j0 < jc_end; j0 += 16 * U) {
-        float kf[U][8], vf[U][8];
+        const bool more = j0 + 16 * U < jc_end;
+        float s[G][U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            unpack(kr[u], kf[u]);
-            unpack(vr[u], vf[u]);
-        }
-        if (j0 + 16 * U < jc_end) load_batch(j0 + 16 * U);
+            float kf[8];
+            unpack(kr[u], kf);
+            const bool in = j0 + 16 * u < jc_end;
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            float s[U];
-            float mn = m[g];
-#pragma unroll
-            for (int u = 0; u < U; u++) {
+            for (int g = 0; g < G; g++) {
                 float d = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 8; e++) d = fmaf(qv[g][e], kf[u][e], d);
+                for (int e = 0; e < 8; e++) d = fmaf(qv[g][e], kf[e], d);
                 d = row16_sum(d);
-                s[u] = (j0 + 16 * u < jc_end) ? d : -__builtin_inff();
-                mn = fmaxf(mn, s[u]);
+                s[g][u] = in ? d : -__builtin_inff();
             }
+        }
+        if (more) load_rows(kr, kb, j0 + 16 * U);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float mn = m[g];
+#pragma unroll
+            for (int u = 0; u < U; u++) mn = fmaxf(mn, s[g][u]);
             // key u = 0 is always in range, so mn is finite here
             const float corr = __expf(m[g] - mn);
             l[g] *= corr;
@@ -632,13 +660,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
             for (int e = 0; e < 8; e++) acc[g][e] *= corr;
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const float p = __expf(s[u] - mn);
-                l[g] += p;
-#pragma unroll
-                for (int e = 0; e < 8; e++) acc[g][e] = fmaf(p, vf[u][e], acc[g][e]);
+                s[g][u] = __expf(s[g][u] - mn);
+                l[g] += s[g][u];
             }
             m[g] = mn;
         }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            float vf[8];
+            unpack(vr[u], vf);
+#pragma unroll
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[g][e] = fmaf(s[g][u], vf[e], acc[g][e]);
+        }
+        if (more) load_rows(vr, vb, j0 + 16 * U);
     }
     if (owner && slot == 0) {  // the new key, from LDS
         float kf[8], vf[8];
@@ -895,7 +931,8 @@ Status launch_sdpa(const void* q, int q_dt, const void* k, const void* v, int kv
         else if (G == 2) go(sdpa_decode_split_kernel<2>);
         else if (G == 4) go(sdpa_decode_split_kernel<4>);
         else go(sdpa_decode_split_kernel<8>);
-        hipLaunchKernelGGL(sdpa_decode_merge_kernel, dim3((unsigned)(B * Hq)), dim3(kDecodeDh), 0, st, part, (int)Hk, G,
+        hipLaunchKernelGGL(sdpa_decode_merge_kernel, dim3((unsigned)(B * Hq)), dim3(kDecodeDh * merge_groups(nsplit)), 0, st,
+                           part, (int)Hk, G,
                            (int)nsplit, out, out_dt);
         return Status::ok();
     }
@@ -914,18 +951,37 @@ Status launch_qk_norm_rope_append(const void* qkv, int qkv_dt, int Hq, int Hk, c
     return Status::ok();
 }
 
-// Keys per block: at least one full load batch per slot (64 keys: a block's
-// fixed prologue costs more than streaming 32 KB), and about 2 blocks per CU over
-// the kv heads for long caches, in multiples of 16 (one key per slot).
-int64_t attn_keys_per_split(int64_t Hk, int64_t Lk, int num_cus) {
+// The split of the `pos` cache rows over blocks: one load batch per slot where
+// possible (all of a block's K/V rows requested at once: a second batch waits a
+// whole memory latency), 4 keys per slot while that keeps the grid within about
+// 2 blocks per CU over the kv heads, else 8 (two such blocks fit a CU), and
+// several batches per block beyond that. The new key joins the last split, so
+// the grid stays within the target (the two-blocks-per-CU occupancy of the
+// 8-key kernel).
+struct AttnSplit {
+    int u;          // keys per slot per batch
+    int64_t kps;    // cache rows per split
+    int64_t nsplit;
+    bool owner_alone;
+};
+
+AttnSplit attn_split(int64_t Hk, int64_t pos, int num_cus) {
     const int64_t target = std::max<int64_t>(1, 2 * (int64_t)num_cus / Hk);
-    return std::max<int64_t>(64, 16 * ((Lk + 16 * target - 1) / (16 * target)));
+    AttnSplit sp;
+    sp.u = pos <= 64 * target ? 4 : 8;
+    const int64_t batch = 16 * sp.u;
+    sp.kps = batch * std::max<int64_t>(1, (pos + batch * target - 1) / (batch * target));
+    const int64_t cache_splits = (pos + sp.kps - 1) / sp.kps;
+    // the new key's own block keeps its q/k/v work off the longest block's path,
+    // when the grid has room for it
+    sp.owner_alone = cache_splits + 1 <= target || cache_splits == 0;
+    sp.nsplit = sp.owner_alone ? cache_splits + 1 : cache_splits;
+    return sp;
 }
 
 size_t attn_decode_workspace_bytes(int64_t Hq, int64_t Hk, int64_t pos, int num_cus) {
-    const int64_t Lk = pos + 1, kps = attn_keys_per_split(Hk, Lk, num_cus);
-    const int64_t nsplit = (Lk + kps - 1) / kps;
-    return nsplit > 1 ? (size_t)(Hk * nsplit * (Hq / Hk) * (kDecodeDh + 2)) * sizeof(float) : 0;
+    const AttnSplit sp = attn_split(Hk, pos, num_cus);
+    return sp.nsplit > 1 ? (size_t)(Hk * sp.nsplit * (Hq / Hk) * (kDecodeDh + 2)) * sizeof(float) : 0;
 }
 
 Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt,
@@ -933,20 +989,27 @@ Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const voi
                           void* vc, int64_t cap, float scale, void* out, int out_dt, void* workspace, int num_cus,
                           hipStream_t st) {
     const int G = Hq / Hk;
-    const int64_t Lk = pos + 1, kps = attn_keys_per_split(Hk, Lk, num_cus);
-    const int64_t nsplit = (Lk + kps - 1) / kps;
+    const AttnSplit sp = attn_split(Hk, pos, num_cus);
+    const int64_t kps = sp.kps, nsplit = sp.nsplit;
     if (nsplit > kMaxSplits || kps > 0x7fffffff) return Status::fail(JH_ERR_UNSUPPORTED, "attention: cache too long");
     AttnArgs a{qkv, qkv_dt, qn_w, kn_w, w_dt, eps, base, rscale, scale, rope_cs, pos,
                static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), cap, Hk, (int)nsplit, (int)kps,
-               static_cast<float*>(workspace), out, out_dt};
+               sp.owner_alone ? 1 : 0, static_cast<float*>(workspace), out, out_dt};
     const dim3 grid((unsigned)nsplit, (unsigned)Hk);
-    if (G == 1) hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(256), 0, st, a);
-    else if (G == 2) hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(256), 0, st, a);
-    else if (G == 4) hipLaunchKernelGGL(attn_decode_kernel<4>, grid, dim3(256), 0, st, a);
-    else if (G == 8) hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(256), 0, st, a);
+    const bool u8 = sp.u == 8;
+    auto go = [&](auto k4, auto k8) {
+        if (u8)
+            hipLaunchKernelGGL(k8, grid, dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL(k4, grid, dim3(256), 0, st, a);
+    };
+    if (G == 1) go(attn_decode_kernel<1, 4>, attn_decode_kernel<1, 8>);
+    else if (G == 2) go(attn_decode_kernel<2, 4>, attn_decode_kernel<2, 8>);
+    else if (G == 4) go(attn_decode_kernel<4, 4>, attn_decode_kernel<4, 8>);
+    else if (G == 8) go(attn_decode_kernel<8, 4>, attn_decode_kernel<8, 8>);
     else return Status::fail(JH_ERR_UNSUPPORTED, "attention: n_heads / n_kv_heads must be 1, 2, 4 or 8");
     if (nsplit > 1)
-        hipLaunchKernelGGL(sdpa_decode_merge_kernel, dim3((unsigned)Hq), dim3(kDecodeDh), 0, st,
+        hipLaunchKernelGGL(sdpa_decode_merge_kernel, dim3((unsigned)Hq), dim3(kDecodeDh * merge_groups(nsplit)), 0, st,
                            static_cast<const float*>(workspace), Hk, G, (int)nsplit, out, out_dt);
     return Status::ok();
 }
