@@ -202,6 +202,16 @@ JH_API int jh_elementwise(jh_ctx *ctx, jh_op op, const void *a, jh_dtype a_dtype
  * of the maximum of each of `rows` rows of n; int32 out. */
 JH_API int jh_argmax(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t rows, int64_t n, int32_t *out);
 
+/* The data movement behind Slice, Transpose, Concat, Cast and making a view
+ * contiguous (engine/backend.go: Slice, Transpose, Concat, Cast; CPU semantics
+ * cpu/cpu.go, cpu/cpu_misc.go): for every index of shape[ndim] (ndim <= 8),
+ * dst[index . dst_strides] = src[index . src_strides] (strides in elements, any
+ * sign, zero for broadcast; dst_strides NULL: dst contiguous), converted
+ * between JH_F32 / JH_F16 / JH_BF16 (round to nearest even); JH_I32 / JH_U32 /
+ * JH_U8 copy only to their own type. */
+JH_API int jh_copy_strided(jh_ctx *ctx, const void *src, jh_dtype src_dtype, int ndim, const int64_t *shape,
+                    const int64_t *src_strides, void *dst, jh_dtype dst_dtype, const int64_t *dst_strides);
+
 /* Backend.TakeAxis on axis 0 (cpu/cpu_misc.go:48-89) for any element type:
  * out[i] = table row ids[i] (row_bytes each); ids is int32, device. An id
  * outside [0, n_rows) gives a zero row (JH_ERR_INVALID with checks on). With

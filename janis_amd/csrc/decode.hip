@@ -831,6 +831,44 @@ __global__ __launch_bounds__(128) void argmax_final_kernel(const float* __restri
 }
 
 // ---- row gather and KV append ------------------------------------------------------
+// ---- strided copy with conversion (Slice / Transpose / Concat / Cast / contiguous) --
+// dst = src over `shape`, each side addressed through its own element strides,
+// converted between F32/F16/BF16; I32/U32/U8 copy only to their own type.
+struct NdDesc {
+    int nd;
+    int64_t shape[kMaxCopyDims];
+    int64_t stride[kMaxCopyDims];   // src
+    int64_t dstride[kMaxCopyDims];  // dst
+};
+
+__device__ __forceinline__ int elem_bytes(int dt) { return dt == JH_F32 || dt == JH_I32 || dt == JH_U32 ? 4 : dt == JH_U8 ? 1 : 2; }
+
+__global__ __launch_bounds__(256) void copy_strided_kernel(const void* __restrict__ src, int sdt,
+                                                           void* __restrict__ dst, int ddt, int64_t n, NdDesc d) {
+    const bool raw = sdt == ddt;
+    const int eb = elem_bytes(sdt);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t rem = i, off = 0, doff = 0;
+        for (int a = d.nd - 1; a >= 0; a--) {
+            const int64_t c = rem % d.shape[a];
+            rem /= d.shape[a];
+            off += c * d.stride[a];
+            doff += c * d.dstride[a];
+        }
+        if (raw) {
+            if (eb == 4) static_cast<uint32_t*>(dst)[doff] = static_cast<const uint32_t*>(src)[off];
+            else if (eb == 2) static_cast<uint16_t*>(dst)[doff] = static_cast<const uint16_t*>(src)[off];
+            else static_cast<uint8_t*>(dst)[doff] = static_cast<const uint8_t*>(src)[off];
+            continue;
+        }
+        const float v = ld_act(src, off, sdt);
+        if (ddt == JH_F16)
+            static_cast<uint16_t*>(dst)[doff] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+        else
+            st_act(dst, doff, v, ddt);
+    }
+}
+
 __global__ __launch_bounds__(256) void take_rows_kernel(const uint8_t* __restrict__ table, int64_t row_bytes,
                                                         int64_t n_rows, const int32_t* __restrict__ ids,
                                                         uint8_t* __restrict__ out) {
@@ -1050,6 +1088,22 @@ Status launch_argmax(const void* x, int x_dt, int64_t rows, int64_t n, int32_t* 
     float* pv = reinterpret_cast<float*>(pi + rows * kArgmaxChunks);
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxChunks, (unsigned)rows), dim3(256), 0, st, x, x_dt, n, pv, pi);
     hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)rows), dim3(kArgmaxChunks), 0, st, pv, pi, n, out);
+    return Status::ok();
+}
+
+Status launch_copy_strided(const void* src, int sdt, int nd, const int64_t* shape, const int64_t* strides, void* dst,
+                           int ddt, const int64_t* dst_strides, hipStream_t st) {
+    NdDesc d{};
+    d.nd = nd;
+    int64_t n = 1;
+    for (int a = nd - 1; a >= 0; a--) {
+        d.shape[a] = shape[a];
+        d.stride[a] = strides[a];
+        d.dstride[a] = dst_strides ? dst_strides[a] : n;  // contiguous by default
+        n *= shape[a];
+    }
+    if (n == 0) return Status::ok();
+    hipLaunchKernelGGL(copy_strided_kernel, dim3(grid_for(n, 256, 16384)), dim3(256), 0, st, src, sdt, dst, ddt, n, d);
     return Status::ok();
 }
 

@@ -254,6 +254,11 @@ Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const voi
                           hipStream_t st);
 Status launch_rope_table(int dims, float base, float scale, int64_t pos, const float* freqs, float* out,
                          hipStream_t st);
+constexpr int kMaxCopyDims = 8;
+// dst = src over shape, both through element strides (dst_strides nullptr:
+// contiguous), converting between F32/F16/BF16 (other types: same-type copies).
+Status launch_copy_strided(const void* src, int sdt, int nd, const int64_t* shape, const int64_t* strides, void* dst,
+                           int ddt, const int64_t* dst_strides, hipStream_t st);
 Status launch_take_rows(const void* table, int64_t row_bytes, int64_t n_rows, const int32_t* ids, int64_t n_ids,
                         void* out, hipStream_t st);
 Status launch_kv_append(void* kc, void* vc, int c_dt, const void* kn, const void* vn, int n_dt, int64_t BH,

@@ -543,6 +543,29 @@ int jh_attention_decode(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t 
                   op);
 }
 
+int jh_copy_strided(jh_ctx* c, const void* src, jh_dtype src_dtype, int ndim, const int64_t* shape,
+                    const int64_t* src_strides, void* dst, jh_dtype dst_dtype, const int64_t* dst_strides) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_copy_strided";
+    auto is_float = [](int dt) { return dt == JH_F32 || dt == JH_F16 || dt == JH_BF16; };
+    if (src_dtype < JH_F32 || src_dtype > JH_U8 || dst_dtype < JH_F32 || dst_dtype > JH_U8)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": unknown dtype");
+    if (src_dtype != dst_dtype && !(is_float(src_dtype) && is_float(dst_dtype)))
+        return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": integer types copy only to themselves");
+    if (ndim < 0 || ndim > jh::kMaxCopyDims || (ndim > 0 && (!shape || !src_strides)))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": ndim must be 0.." + std::to_string(jh::kMaxCopyDims));
+    int64_t n = 1;
+    for (int a = 0; a < ndim; a++) {
+        if (shape[a] < 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": negative extent");
+        n *= shape[a];
+    }
+    if (n == 0) return JH_OK;
+    if (!src || !dst) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    return finish(c, jh::launch_copy_strided(src, src_dtype, ndim, shape, src_strides, dst, dst_dtype, dst_strides,
+                                             c->stream),
+                  op);
+}
+
 int jh_take_rows(jh_ctx* c, const void* table, int64_t row_bytes, int64_t n_rows, const int32_t* ids, int64_t n_ids,
                  void* out) {
     if (int r = enter(c)) return r;

@@ -27,16 +27,36 @@ DTYPE_SIZE = {F32: 4, F16: 2, BF16: 2, I32: 4, U32: 4, U8: 1}
 DTYPE_NAME = {F32: "F32", F16: "F16", BF16: "BF16", I32: "I32", U32: "U32", U8: "U8"}
 
 
-class Tensor:
-    """Device tensor: shape, dtype, device pointer. engine.Tensor (engine/backend.go:24-26)."""
+def _dense_strides(shape) -> tuple:
+    st, acc = [], 1
+    for d in reversed(shape):
+        st.append(acc)
+        acc *= int(d)
+    return tuple(reversed(st))
 
-    def __init__(self, backend: "HipBackend", ptr: int, shape, dtype: int, owned: bool = True, keep=None):
+
+class Tensor:
+    """Device tensor: shape, dtype, device pointer, element strides (views from
+    Slice/Transpose/ExpandDims are strided, as MLX's are). engine.Tensor
+    (engine/backend.go:24-26)."""
+
+    def __init__(self, backend: "HipBackend", ptr: int, shape, dtype: int, owned: bool = True, keep=None,
+                 strides=None):
         self._b = backend
         self.ptr = int(ptr) if ptr else 0
         self.shape = tuple(int(d) for d in shape)
         self.dtype = dtype
         self._owned = owned
         self._keep = keep  # an object whose lifetime covers the memory (non-owned views)
+        self.strides = tuple(int(x) for x in strides) if strides is not None else _dense_strides(self.shape)
+        if backend is not None and owned and backend._sweeper is not None:
+            backend._sweeper.track(self)
+
+    @property
+    def contiguous(self) -> bool:
+        """Row-major dense (strides of length-1 axes do not matter)."""
+        dense = _dense_strides(self.shape)
+        return all(n == 1 or a == b for n, a, b in zip(self.shape, self.strides, dense))
 
     def Shape(self) -> list:
         return list(self.shape)
@@ -49,7 +69,8 @@ class Tensor:
     def nbytes(self) -> int:
         return self.numel * DTYPE_SIZE[self.dtype]
 
-    def __del__(self):
+    def free(self) -> None:
+        """Releases an owned allocation now (Freer.Free / Sweeper.Sweep)."""
         try:
             if self._owned and self.ptr and self._b._ctx:
                 _lib.load().jh_free(self._b._ctx, ctypes.c_void_p(self.ptr))
@@ -57,8 +78,53 @@ class Tensor:
             pass
         self.ptr = 0
 
+    def __del__(self):
+        self.free()
+
     def __repr__(self):
         return f"Tensor({DTYPE_NAME[self.dtype]}, {list(self.shape)})"
+
+
+class _Sweeper:
+    """engine.Sweeper bookkeeping (engine/backend.go:43-51): owned tensors made
+    while it is active are tracked; Sweep frees the unpinned ones still alive."""
+
+    def __init__(self):
+        import weakref
+        self._live = weakref.WeakValueDictionary()  # id -> Tensor
+        self._pinned = set()
+
+    def track(self, t: "Tensor") -> None:
+        self._live[id(t)] = t
+
+    def pin_all(self) -> None:
+        self._pinned.update(self._live.keys())
+
+    def pin(self, ts) -> None:
+        for t in ts:
+            if t is not None:
+                self._pinned.add(id(t))
+                keep = getattr(t, "_keep", None)  # a view pins the memory it views
+                if isinstance(keep, Tensor):
+                    self.pin([keep])
+
+    def unpin(self, ts) -> None:
+        for t in ts:
+            if t is not None:
+                self._pinned.discard(id(t))
+                keep = getattr(t, "_keep", None)
+                if isinstance(keep, Tensor):
+                    self.unpin([keep])
+
+    def sweep(self) -> int:
+        freed = 0
+        for key, t in list(self._live.items()):
+            if key not in self._pinned:
+                t.free()
+                del self._live[key]
+                freed += 1
+        self._pinned &= set(self._live.keys())
+        return freed
 
 
 class HipBackend:
@@ -73,6 +139,8 @@ class HipBackend:
         self._L = L
         self._ctx = ctx
         self._arena = None  # [base tensor, offset] while an arena is in use
+        self._sweeper = None  # set by PinAll (engine.Sweeper)
+        self._kv_reserve = 0  # CacheReserver.ReserveCache
 
     # -- lifecycle / info ------------------------------------------------------
     def Version(self) -> str:
@@ -95,6 +163,38 @@ class HipBackend:
     def SetStream(self, stream_handle: int | None) -> None:
         """Enqueue on a caller's hipStream_t (e.g. torch.cuda.current_stream().cuda_stream)."""
         check(self._ctx, self._L.jh_set_stream(self._ctx, ctypes.c_void_p(stream_handle or 0)))
+
+    # -- engine.Sweeper / engine.Freer ---------------------------------------------------
+    def PinAll(self) -> None:
+        """Pins everything made so far (after weight load) and starts tracking:
+        tensors made from now on are freed by Sweep unless pinned."""
+        if self._sweeper is None:
+            self._sweeper = _Sweeper()
+        self._sweeper.pin_all()
+
+    def Pin(self, *ts) -> None:
+        if self._sweeper is not None:
+            self._sweeper.pin(ts)
+
+    def Unpin(self, *ts) -> None:
+        if self._sweeper is not None:
+            self._sweeper.unpin(ts)
+
+    def Sweep(self) -> int:
+        """Frees every tracked, unpinned tensor (after the queued work that may
+        read it). Returns how many were freed."""
+        if self._sweeper is None:
+            return 0
+        self.Sync()
+        return self._sweeper.sweep()
+
+    def Free(self, *ts) -> None:
+        """engine.Freer: releases the given tensors now (pinned ones are kept)."""
+        self.Sync()
+        for t in ts:
+            if t is None or (self._sweeper is not None and id(t) in self._sweeper._pinned):
+                continue
+            t.free()
 
     def SetChecks(self, on: bool) -> None:
         check(self._ctx, self._L.jh_set_checks(self._ctx, int(bool(on))))
@@ -161,6 +261,7 @@ class HipBackend:
 
     # -- read back -------------------------------------------------------------------
     def Bytes(self, t: Tensor) -> bytes:
+        t = self._c(t)
         out = np.empty(t.nbytes, dtype=np.uint8)
         check(self._ctx, self._L.jh_d2h(self._ctx, out.ctypes.data_as(ctypes.c_void_p),
                                         ctypes.c_void_p(t.ptr), t.nbytes))
@@ -171,6 +272,7 @@ class HipBackend:
 
     def Floats(self, t: Tensor) -> np.ndarray:
         """engine/backend.go:276-277: evaluates and copies out as float32."""
+        t = self._c(t)
         raw = np.frombuffer(self.Bytes(t), dtype=np.uint8)
         if t.dtype == F32:
             a = raw.view(np.float32)
@@ -185,6 +287,7 @@ class HipBackend:
         return a.reshape(t.shape).copy()
 
     def Ints(self, t: Tensor) -> np.ndarray:
+        t = self._c(t)
         raw = np.frombuffer(self.Bytes(t), dtype=np.uint8)
         if t.dtype not in (I32, U32):
             raise JanisHipError(_lib.JH_ERR_INVALID, "Ints: tensor is not I32/U32")
@@ -202,6 +305,7 @@ class HipBackend:
         """engine/backend.go:261-263: w [..., P] U32 -> [..., P*32/bits] (cpu/cpu_misc.go:134-161)."""
         if w.dtype != U32:
             raise JanisHipError(_lib.JH_ERR_INVALID, "Dequantize: weight tensor is not packed U32")
+        w, scales, biases = self._c(w), self._c(scales), self._c(biases)
         P = w.shape[-1]
         k = P * (32 // bits)
         rows = w.numel // P
@@ -218,6 +322,7 @@ class HipBackend:
         unless out_dtype says otherwise; `out` may supply the result buffer."""
         if w.dtype != U32:
             raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatmul: weight tensor is not packed U32")
+        x, w, scales, biases = self._c(x), self._c(w), self._c(scales), self._c(biases)
         n, P = w.shape[-2], w.shape[-1]
         k = P * (32 // bits)
         if x.shape[-1] != k:
@@ -239,6 +344,7 @@ class HipBackend:
             raise JanisHipError(_lib.JH_ERR_INVALID, "GatherQuantMatmul: w must be U32 [E, out, P]")
         if rhsIndices.dtype != I32:
             raise JanisHipError(_lib.JH_ERR_INVALID, "GatherQuantMatmul: indices must be I32")
+        x, w, scales, biases, rhsIndices = (self._c(t) for t in (x, w, scales, biases, rhsIndices))
         E, n, P = w.shape
         k = P * (32 // bits)
         rs = rhsIndices.shape
@@ -258,26 +364,102 @@ class HipBackend:
         return y
 
     # -- the other operators of a decode step ----------------------------------------
+    # -- layout: views and copies (engine/backend.go: Reshape, Transpose, Slice, ...) --
+    def _copy(self, x: Tensor, dst: Tensor, dst_strides=None) -> None:
+        self._live(x), self._live(dst)
+        nd = len(x.shape)
+        sh = (ctypes.c_int64 * max(1, nd))(*x.shape)
+        st = (ctypes.c_int64 * max(1, nd))(*x.strides)
+        ds = (ctypes.c_int64 * max(1, nd))(*dst_strides) if dst_strides is not None else None
+        check(self._ctx, self._L.jh_copy_strided(self._ctx, x.ptr, x.dtype, nd, sh, st, dst.ptr, dst.dtype, ds))
+
+    @staticmethod
+    def _live(x: Tensor) -> Tensor:
+        """x, after checking that neither it nor the memory it views was freed
+        (Sweep / Free): a freed tensor's address must never reach a kernel."""
+        t = x
+        while isinstance(t, Tensor):
+            if t.ptr == 0 and (t._owned or t is x) and t.numel:
+                raise JanisHipError(_lib.JH_ERR_INVALID, "tensor used after it was freed (Sweep / Free)")
+            t = t._keep
+        return x
+
+    def _c(self, x: Tensor) -> Tensor:
+        """x itself when dense, else a dense copy (what an op that reads memory
+        linearly needs)."""
+        self._live(x)
+        if x.contiguous:
+            return x
+        out = self.empty(x.dtype, *x.shape)
+        self._copy(x, out)
+        return out
+
+    def _view(self, x: Tensor, shape, strides, offset: int = 0) -> Tensor:
+        return Tensor(self, x.ptr + offset * DTYPE_SIZE[x.dtype], shape, x.dtype, owned=False, keep=x,
+                      strides=strides)
+
     def Reshape(self, x: Tensor, *shape) -> Tensor:
-        """engine.Backend.Reshape: a view over the same memory (one -1 allowed)."""
+        """engine.Backend.Reshape: a view of the same memory when x is dense (one
+        -1 allowed), else of a dense copy."""
         shape = list(shape)
         if shape.count(-1) == 1:
             known = int(np.prod([d for d in shape if d != -1], dtype=np.int64))
             shape[shape.index(-1)] = x.numel // known if known else 0
         if int(np.prod(shape, dtype=np.int64)) != x.numel:
             raise JanisHipError(_lib.JH_ERR_INVALID, f"Reshape: {list(x.shape)} -> {shape}")
+        x = self._c(x)
         return Tensor(self, x.ptr, shape, x.dtype, owned=False, keep=x)
 
     def Transpose(self, x: Tensor, *perm) -> Tensor:
-        """engine.Backend.Transpose where it moves only length-1 axes (a view);
-        other permutations are not implemented here."""
-        kept = [a for a in perm if x.shape[a] != 1]
-        if kept != sorted(kept):
-            raise JanisHipError(_lib.JH_ERR_UNSUPPORTED, "Transpose: only layout-preserving permutations")
-        return Tensor(self, x.ptr, [x.shape[a] for a in perm], x.dtype, owned=False, keep=x)
+        """engine.Backend.Transpose: x's axes permuted, as a strided view."""
+        if sorted(perm) != list(range(len(x.shape))):
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"Transpose: {perm} is not a permutation of {len(x.shape)} axes")
+        return self._view(x, [x.shape[a] for a in perm], [x.strides[a] for a in perm])
+
+    def Slice(self, x: Tensor, axis: int, start: int, end: int) -> Tensor:
+        """engine.Backend.Slice: [start:end] along axis, a view (full extent elsewhere)."""
+        axis = axis % len(x.shape)
+        if not 0 <= start <= end <= x.shape[axis]:
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"Slice: [{start}:{end}] of axis {axis} sized {x.shape[axis]}")
+        shape = list(x.shape)
+        shape[axis] = end - start
+        return self._view(x, shape, x.strides, offset=start * x.strides[axis])
+
+    def ExpandDims(self, x: Tensor, axis: int) -> Tensor:
+        """engine.Backend.ExpandDims: a length-1 axis inserted, a view."""
+        axis = axis % (len(x.shape) + 1)
+        shape = list(x.shape)
+        strides = list(x.strides)
+        shape.insert(axis, 1)
+        strides.insert(axis, strides[axis] * x.shape[axis] if axis < len(x.shape) else 1)
+        return self._view(x, shape, strides)
+
+    def Concat(self, a: Tensor, b: Tensor, axis: int) -> Tensor:
+        """engine.Backend.Concat along axis (two strided copies into a new tensor)."""
+        axis = axis % len(a.shape)
+        if a.dtype != b.dtype or len(a.shape) != len(b.shape) or any(
+                i != axis and x != y for i, (x, y) in enumerate(zip(a.shape, b.shape))):
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"Concat: {list(a.shape)} and {list(b.shape)} on axis {axis}")
+        shape = list(a.shape)
+        shape[axis] = a.shape[axis] + b.shape[axis]
+        out = self.empty(a.dtype, *shape)
+        self._copy(a, out, out.strides)
+        tail = self._view(out, b.shape, out.strides, offset=a.shape[axis] * out.strides[axis])
+        self._copy(b, tail, tail.strides)
+        return out
+
+    def Cast(self, x: Tensor, dt: int) -> Tensor:
+        """engine.Backend.Cast between F32/F16/BF16 (round to nearest even)."""
+        out = self.empty(dt, *x.shape)
+        self._copy(x, out)
+        return out
+
+    def Contiguous(self, x: Tensor) -> Tensor:
+        return self._c(x)
 
     def RMSNorm(self, x: Tensor, weight: Tensor, eps: float, out_dtype: int | None = None) -> Tensor:
         """cpu/cpu_ops.go:144-162 over the last axis."""
+        x, weight = self._c(x), self._c(weight)
         d = x.shape[-1]
         out = self.empty(out_dtype if out_dtype is not None else x.dtype, *x.shape)
         check(self._ctx, self._L.jh_rms_norm(self._ctx, x.ptr, x.dtype, x.numel // d, d, weight.ptr, weight.dtype,
@@ -285,6 +467,8 @@ class HipBackend:
         return out
 
     def _rope(self, x, dims, traditional, base, scale, offset, freqs, out_dtype):
+        x = self._c(x)
+        freqs = self._c(freqs) if freqs is not None else None
         D, L = x.shape[-1], x.shape[-2]
         out = self.empty(out_dtype if out_dtype is not None else x.dtype, *x.shape)
         check(self._ctx, self._L.jh_rope(self._ctx, x.ptr, x.dtype, x.numel // D, L, D, dims, int(bool(traditional)),
@@ -306,19 +490,39 @@ class HipBackend:
 
     def SDPA(self, q: Tensor, k: Tensor, v: Tensor, scale: float, causal: bool, kv_len: int | None = None,
              out_dtype: int | None = None) -> Tensor:
-        """cpu/cpu_attn.go:64-119: q [B, Hq, Lq, Dh]; k/v [B, Hk, cap, Dh] whose first
-        kv_len rows are valid (all of them when kv_len is None)."""
+        """cpu/cpu_attn.go:64-119: q [B, Hq, Lq, Dh]; k/v [B, Hk, Lk, Dh], which may be
+        views of the first Lk rows of caches [B, Hk, cap, Dh] (AppendKV's views:
+        read in place), or whole caches of which the first kv_len rows count."""
+        q = self._c(q)
         B, Hq, Lq, Dh = q.shape
-        Hk, cap = k.shape[1], k.shape[2]
         if k.shape != v.shape or k.dtype != v.dtype or k.shape[0] != B or k.shape[3] != Dh:
             raise JanisHipError(_lib.JH_ERR_INVALID, "SDPA: k/v shapes do not match q")
-        Lk = cap if kv_len is None else kv_len
+        Hk = k.shape[1]
+        k, cap = self._kv_rows(k)
+        v, vcap = self._kv_rows(v)
+        if vcap != cap:  # one row stride for both
+            k, v = self._c(k), self._c(v)
+            cap = k.shape[2]
+        Lk = k.shape[2] if kv_len is None else kv_len
         out = self.empty(out_dtype if out_dtype is not None else q.dtype, B, Hq, Lq, Dh)
         check(self._ctx, self._L.jh_sdpa(self._ctx, q.ptr, q.dtype, k.ptr, v.ptr, k.dtype, B, Hq, Hk, Lq, Lk, cap,
                                          Dh, float(scale), int(bool(causal)), out.ptr, out.dtype))
         return out
 
+    def _kv_rows(self, t: Tensor) -> tuple:
+        """(t, row capacity) when t's rows sit in a [B, H, cap, D] buffer with
+        dense rows (a cache view), else (dense copy, its row count)."""
+        B, H, L, D = t.shape
+        st = t.strides
+        if st[3] == 1 and st[2] == D and st[1] % D == 0 and st[1] // D >= L and (B == 1 or st[0] == H * st[1]):
+            return t, st[1] // D
+        t = self._c(t)
+        return t, L
+
+
     def _elementwise(self, op, a, b, out_dtype):
+        a = self._c(a)
+        b = self._c(b) if b is not None else None
         if b is not None and b.numel != a.numel:
             raise JanisHipError(_lib.JH_ERR_UNSUPPORTED, "elementwise: operands must have the same size")
         out = self.empty(out_dtype if out_dtype is not None else a.dtype, *a.shape)
@@ -343,6 +547,7 @@ class HipBackend:
         """cpu/cpu_misc.go:91-121, last axis only."""
         if axis not in (-1, len(x.shape) - 1):
             raise JanisHipError(_lib.JH_ERR_UNSUPPORTED, "Argmax: last axis only")
+        x = self._c(x)
         n = x.shape[-1]
         out = self.empty(I32, *x.shape[:-1])
         check(self._ctx, self._L.jh_argmax(self._ctx, x.ptr, x.dtype, x.numel // n, n, out.ptr))
@@ -352,14 +557,45 @@ class HipBackend:
         """cpu/cpu_misc.go:48-89 on axis 0 (rows of any dtype, packed words included)."""
         if axis != 0 or indices.dtype != I32:
             raise JanisHipError(_lib.JH_ERR_UNSUPPORTED, "TakeAxis: axis 0 with I32 indices only")
+        a, indices = self._c(a), self._c(indices)
         rows = a.shape[0]
         row_bytes = a.nbytes // rows if rows else 0
         out = self.empty(a.dtype, *indices.shape, *a.shape[1:])
         check(self._ctx, self._L.jh_take_rows(self._ctx, a.ptr, row_bytes, rows, indices.ptr, indices.numel, out.ptr))
         return out
 
-    def AppendKV(self, k_cache: Tensor, v_cache: Tensor, pos: int, k_new: Tensor, v_new: Tensor) -> None:
-        """KV-cache append: caches [B, Hk, cap, Dh], new rows [B, Hk, L, Dh] at pos."""
+    KV_STEP = 256  # cache capacity granularity (tokens)
+    KV_AHEAD = 2048  # at most this many tokens of room beyond what a request needs now
+
+    def ReserveCache(self, tokens: int) -> None:
+        """engine.CacheReserver: size the caches made from now on for `tokens`."""
+        self._kv_reserve = int(tokens)
+
+    def AppendKV(self, buf: Tensor | None, view: Tensor | None, n: int, x: Tensor) -> tuple:
+        """engine.KVAppender (engine/backend.go:56-61): writes x [B, H, L, D] into buf
+        at token n (axis 2) in place, growing buf when it has no room (buf None: a
+        new one; view's first n tokens are copied in first), and returns (buf, the
+        view of its first n+L tokens). A new buffer holds max(need, min(reserve,
+        need + KV_AHEAD)) tokens rounded up to KV_STEP, as the MLX backend sizes
+        them (mlxc/mlxc.go:283-306); rows past the view are never read."""
+        B, H, L, D = x.shape
+        need = n + L
+        if buf is None or buf.shape[2] < need or buf.shape[:2] != (B, H) or buf.shape[3] != D:
+            cap = max(need, min(self._kv_reserve, need + self.KV_AHEAD))
+            cap = (cap + self.KV_STEP - 1) // self.KV_STEP * self.KV_STEP
+            grown = self.empty(x.dtype if buf is None else buf.dtype, B, H, cap, D)
+            if n > 0 and view is not None:
+                src = self.Slice(view, 2, 0, n)
+                self._copy(src, self._view(grown, src.shape, grown.strides), grown.strides)
+            buf = grown
+        dst = self._view(buf, x.shape, buf.strides, offset=n * buf.strides[2])
+        self._copy(x, dst, buf.strides)
+        return buf, self.Slice(buf, 2, 0, need)
+
+    def AppendKVRows(self, k_cache: Tensor, v_cache: Tensor, pos: int, k_new: Tensor, v_new: Tensor) -> None:
+        """Both caches at once with one launch: caches [B, Hk, cap, Dh], new rows
+        [B, Hk, L, Dh] at pos (jh_kv_append)."""
+        k_new, v_new = self._c(k_new), self._c(v_new)
         B, Hk, cap, Dh = k_cache.shape
         L = k_new.shape[-2]
         if k_new.shape != v_new.shape or k_new.dtype != v_new.dtype or k_new.numel != B * Hk * L * Dh:
@@ -375,6 +611,7 @@ class HipBackend:
         Returns q [1, Hq, 1, 128]."""
         if q_norm.dtype != k_norm.dtype:
             raise JanisHipError(_lib.JH_ERR_INVALID, "QKNormRoPEAppend: norm weights differ in dtype")
+        qkv, q_norm, k_norm = self._c(qkv), self._c(q_norm), self._c(k_norm)
         Dh = 128
         cap = k_cache.shape[-2]
         q = self.empty(out_dtype if out_dtype is not None else qkv.dtype, 1, n_heads, 1, Dh)
@@ -401,6 +638,9 @@ class HipBackend:
         JH_PRO_NORMED with x = that norm_out and the same `stats`."""
         if w.dtype != U32:
             raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: weight tensor is not packed U32")
+        x, w, scales, biases = self._c(x), self._c(w), self._c(scales), self._c(biases)
+        norm = self._c(norm) if norm is not None else None
+        resid = self._c(resid) if resid is not None else None
         if epilogue is None:
             epilogue = _lib.JH_EPI_RESID if resid is not None else _lib.JH_EPI_STORE
         rows, P = w.shape[-2], w.shape[-1]
@@ -439,6 +679,7 @@ class HipBackend:
         """The producer half of a split RMSNorm for a row already at hand (the
         embedding row): (bf16(x * norm) [1, d], F32 statistics [JH_NORM_STATS]),
         for a QuantMatvecFused with JH_PRO_NORMED."""
+        x, norm = self._c(x), self._c(norm)
         d = x.shape[-1]
         if x.numel != d or norm.numel != d:
             raise JanisHipError(_lib.JH_ERR_INVALID, "NormPrepare: one row and a weight of its length")
@@ -468,6 +709,11 @@ class HipBackend:
             raise JanisHipError(_lib.JH_ERR_INVALID, "AttentionDecode: norm weights differ in dtype")
         if k_cache.dtype != v_cache.dtype or k_cache.shape != v_cache.shape:
             raise JanisHipError(_lib.JH_ERR_INVALID, "AttentionDecode: caches differ")
+        if not (k_cache.contiguous and v_cache.contiguous):
+            raise JanisHipError(_lib.JH_ERR_INVALID, "AttentionDecode: the caches must be whole buffers")
+        qkv = self._c(qkv)
+        q_norm = self._c(q_norm) if q_norm is not None else None
+        k_norm = self._c(k_norm) if k_norm is not None else None
         Dh = 128
         cap = k_cache.shape[-2]
         out = self.empty(out_dtype if out_dtype is not None else qkv.dtype, 1, n_heads * Dh)
@@ -483,6 +729,7 @@ class HipBackend:
         """The router of MoEBlock.Forward (qwen/moe.go:455-491) on the device:
         softmax over the last axis, top-k (selection-sort ties), optional
         renormalisation. Returns (indices I32 [lead.., k], scores F32 [lead.., k])."""
+        logits = self._c(logits)
         E = logits.shape[-1]
         n_tok = logits.numel // E if E else 0
         lead = logits.shape[:-1]
@@ -500,7 +747,8 @@ class HipBackend:
         experts. x [lead.., H] bf16; gate/up/down are (W, S, B) stacks
         [E, I, H/8], [E, I, H/8], [E, H, I/8]; rhsIndices I32 and scores F32
         [lead.., K]. Returns [lead.., H] (F32 unless out_dtype says BF16)."""
-        (wg, sg, bg), (wu, su, bu), (wd, sd, bd) = gate, up, down
+        (wg, sg, bg), (wu, su, bu), (wd, sd, bd) = ((self._c(t) for t in m) for m in (gate, up, down))
+        x, rhsIndices, scores = self._c(x), self._c(rhsIndices), self._c(scores)
         for w in (wg, wu, wd):
             if w.dtype != U32 or len(w.shape) != 3:
                 raise JanisHipError(_lib.JH_ERR_INVALID, "MoeSwiGLU: stacks must be U32 [E, out, P]")

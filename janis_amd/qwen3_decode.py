@@ -68,8 +68,10 @@ def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bo
     1/rms factor to its output), SiLU*mul in the gate/up product's epilogue,
     the residual adds in the o/down products' epilogues, and the q/k norms,
     RoPE, KV append and SDPA in one launch plus a merge (6 launches per layer).
-    fused=False spells the step out as the reference's separate operators (15
-    per layer)."""
+    fused=False makes the reference's calls one for one (qwen/block.go,
+    qwen/attention.go, qwen/mlp.go, qwen/cache.go): separate q/k/v and gate/up
+    products on row views of the stacked matrices, Reshape/Transpose views, the
+    KVAppender, SDPA over the cache views."""
     c = m.cfg
     gs, bits = c.group_size, c.bits
     H, Hq, Hk, Dh, I = c.hidden, c.n_heads, c.n_kv, c.head_dim, c.inter
@@ -94,33 +96,44 @@ def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bo
                                norm_out=u)
         logits = b.QuantMatvecFused(u, *head, gs, bits, NORMED, eps=c.eps, stats=st, out_dtype=F32)
         return logits, b.Argmax(logits)
+    # the reference's operator sequence, call for call
+    B, T = 1, 1
     for L in m.layers:
-        # Attention.ForwardCached
-        xn = b.RMSNorm(h, L.in_norm, c.eps, out_dtype=BF16)
-        qkv = b.QuantMatmul(xn, *L.qkv, True, gs, bits, out_dtype=F32)  # [1, (Hq+2Hk)*Dh]
-        q = _rows(b, qkv, 0, Hq * Dh, (1, Hq, 1, Dh))
-        k = _rows(b, qkv, Hq * Dh, Hk * Dh, (1, Hk, 1, Dh))
-        v = _rows(b, qkv, (Hq + Hk) * Dh, Hk * Dh, (1, Hk, 1, Dh))
-        q = b.RoPE(b.RMSNorm(q, L.q_norm, c.eps), Dh, False, c.theta, 1.0, pos)
-        k = b.RoPE(b.RMSNorm(k, L.k_norm, c.eps), Dh, False, c.theta, 1.0, pos)
-        b.AppendKV(L.k_cache, L.v_cache, pos, k, v)
-        att = b.Reshape(b.SDPA(q, L.k_cache, L.v_cache, Dh ** -0.5, False, kv_len=pos + 1, out_dtype=BF16),
-                        1, Hq * Dh)
-        # the residual adds and MLP.Forward
-        h = b.Add(h, b.QuantMatmul(att, *L.o, True, gs, bits, out_dtype=F32))
+        # Block.ForwardCached (qwen/block.go:58-61): h = x + Attn(InputNorm(x))
+        x = b.Reshape(h, B, T, H)
+        xn = b.RMSNorm(x, L.in_norm, c.eps, out_dtype=BF16)
+        # Attention.ForwardCached (qwen/attention.go:98-128)
+        wq, wk, wv = (_linear_rows(b, L.qkv, r0, n) for r0, n in ((0, Hq * Dh), (Hq * Dh, Hk * Dh),
+                                                                    ((Hq + Hk) * Dh, Hk * Dh)))
+        q = b.Reshape(b.QuantMatmul(xn, *wq, True, gs, bits, out_dtype=F32), B, T, Hq, Dh)
+        k = b.Reshape(b.QuantMatmul(xn, *wk, True, gs, bits, out_dtype=F32), B, T, Hk, Dh)
+        q, k = b.RMSNorm(q, L.q_norm, c.eps), b.RMSNorm(k, L.k_norm, c.eps)
+        q, k = b.Transpose(q, 0, 2, 1, 3), b.Transpose(k, 0, 2, 1, 3)
+        v = b.Transpose(b.Reshape(b.QuantMatmul(xn, *wv, True, gs, bits, out_dtype=F32), B, T, Hk, Dh), 0, 2, 1, 3)
+        q = b.RoPE(q, Dh, False, c.theta, 1.0, pos)
+        k = b.RoPE(k, Dh, False, c.theta, 1.0, pos)
+        # KVCache.Update through engine.KVAppender (qwen/cache.go:90-98); the
+        # model's caches are the spare-room buffers, their first pos rows the views
+        _, kview = b.AppendKV(L.k_cache, b.Slice(L.k_cache, 2, 0, pos), pos, k)
+        _, vview = b.AppendKV(L.v_cache, b.Slice(L.v_cache, 2, 0, pos), pos, v)
+        att = b.SDPA(q, kview, vview, Dh ** -0.5, T > 1, out_dtype=BF16)
+        att = b.Reshape(b.Transpose(att, 0, 2, 1, 3), B, T, Hq * Dh)
+        h = b.Add(x, b.QuantMatmul(att, *_linear_rows(b, L.o, 0, H), True, gs, bits, out_dtype=F32))
+        # MLP.Forward (qwen/mlp.go:32-36) on PostNorm(h), and the second residual add
         xn = b.RMSNorm(h, L.post_norm, c.eps, out_dtype=BF16)
-        gu = b.QuantMatmul(xn, *L.gate_up, True, gs, bits, out_dtype=BF16)  # [1, 2I]
-        act = b.SiLUMul(_rows(b, gu, 0, I, (1, I)), _rows(b, gu, I, I, (1, I)))
-        h = b.Add(h, b.QuantMatmul(act, *L.down, True, gs, bits, out_dtype=F32))
-    logits = b.QuantMatmul(b.RMSNorm(h, m.norm, c.eps, out_dtype=BF16), *head, True, gs, bits, out_dtype=F32)
+        gate = b.SiLU(b.QuantMatmul(xn, *_linear_rows(b, L.gate_up, 0, I), True, gs, bits, out_dtype=BF16))
+        up = b.QuantMatmul(xn, *_linear_rows(b, L.gate_up, I, I), True, gs, bits, out_dtype=BF16)
+        h = b.Add(h, b.QuantMatmul(b.Mul(gate, up), *_linear_rows(b, L.down, 0, H), True, gs, bits, out_dtype=F32))
+    # forwardCachedT's last position, final norm, head (qwen/model.go:294-303)
+    hn = b.RMSNorm(b.Slice(h, 1, T - 1, T), m.norm, c.eps, out_dtype=BF16)
+    logits = b.Reshape(b.QuantMatmul(hn, *head, True, gs, bits, out_dtype=F32), 1, -1)
     return logits, b.Argmax(logits)
 
 
-def _rows(b: HipBackend, t: Tensor, start: int, n: int, shape) -> Tensor:
-    """A view of n contiguous elements from `start` (Slice on the last axis of a
-    one-row tensor)."""
-    esz = 2 if t.dtype == BF16 else 4
-    return Tensor(b, t.ptr + start * esz, shape, t.dtype, owned=False, keep=t)
+def _linear_rows(b: HipBackend, lin: tuple, r0: int, n: int) -> tuple:
+    """Rows r0..r0+n of a stacked quantized matrix (W, S, B): one of the
+    reference's separate QuantLinears (q/k/v or gate/up) as Slice views."""
+    return tuple(b.Slice(t, 0, r0, r0 + n) for t in lin)
 
 
 def random_model(b: HipBackend, cfg: Qwen3Config, capacity: int, seed: int = 0, torch=None, dev=None):

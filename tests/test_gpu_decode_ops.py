@@ -178,13 +178,13 @@ def test_append_kv(hip):
     k1 = rng.standard_normal((B, Hk, 1, Dh)).astype(np.float32)
     v1 = rng.standard_normal((B, Hk, 1, Dh)).astype(np.float32)
     step("jh_kv_append")
-    hip.AppendKV(kc, vc, 0, _put(hip, k0, BF16), _put(hip, v0, BF16))
-    hip.AppendKV(kc, vc, 10, _put(hip, k1, F32), _put(hip, v1, F32))  # fp32 rows into the bf16 cache
+    hip.AppendKVRows(kc, vc, 0, _put(hip, k0, BF16), _put(hip, v0, BF16))
+    hip.AppendKVRows(kc, vc, 10, _put(hip, k1, F32), _put(hip, v1, F32))  # fp32 rows into the bf16 cache
     gk, gv = hip.Floats(kc), hip.Floats(vc)
     assert np.array_equal(gk[:, :, :10], k0) and np.array_equal(gk[:, :, 10:11], _bf16(k1))
     assert np.array_equal(gv[:, :, :10], v0) and np.array_equal(gv[:, :, 10:11], _bf16(v1))
     with pytest.raises(JanisHipError):
-        hip.AppendKV(kc, vc, 64, _put(hip, k1, F32), _put(hip, v1, F32))
+        hip.AppendKVRows(kc, vc, 64, _put(hip, k1, F32), _put(hip, v1, F32))
 
 
 def test_qk_norm_rope_append_matches_separate_ops(hip, oracle):
