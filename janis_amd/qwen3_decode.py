@@ -34,6 +34,7 @@ class Qwen3Config:
     theta: float = 1e6
     group_size: int = 64
     bits: int = 4
+    tie: bool = False   # lm_head tied to the embedding (QuantEmbedding.AsLinear)
 
 
 @dataclass
