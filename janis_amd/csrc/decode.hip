@@ -25,6 +25,23 @@ __device__ __forceinline__ float ld_act(const void* p, int64_t i, int dt) {
     return static_cast<const float*>(p)[i];
 }
 
+// Element i of an activation as two steps, so that a kernel can issue the load
+// early and convert after later loads are in flight: ld_word reads the aligned
+// 32-bit word holding the element (the element itself for f32), with no branch
+// on the dtype; word_to_f32 extracts and converts it.
+__device__ __forceinline__ uint32_t ld_word(const void* p, int64_t i, int dt) {
+    // pointer arithmetic (not an integer round trip) keeps the load global
+    const char* e = static_cast<const char*>(p) + (dt == JH_F32 ? i * 4 : i * 2);
+    return *reinterpret_cast<const uint32_t*>(e - (reinterpret_cast<uintptr_t>(e) & 3));
+}
+
+__device__ __forceinline__ float word_to_f32(uint32_t w, const void* p, int64_t i, int dt) {
+    if (dt == JH_F32) return __uint_as_float(w);
+    const bool hi = ((reinterpret_cast<uintptr_t>(p) + (uintptr_t)(i * 2)) & 2) != 0;
+    const uint16_t h = static_cast<uint16_t>(hi ? (w >> 16) : w);
+    return dt == JH_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
 __device__ __forceinline__ void st_act(void* p, int64_t i, float v, int dt) {
     if (dt == JH_BF16)
         static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
@@ -438,17 +455,35 @@ __global__ __launch_bounds__(128 * kMergeGroups) void sdpa_decode_merge_kernel(c
 }
 
 // Per-head RMSNorm of one 128-feature head held as lane i: (a, b) = features
-// (i, i + 64) of a wave; w == nullptr skips the norm (heads without QNorm/KNorm).
-__device__ __forceinline__ void head_rms_norm(float& a, float& b, const void* w, int w_dt, float eps, int i) {
-    if (!w) return;
+// (i, i + 64) of a wave, with the lane's weights (w0, w1) = (w[i], w[i + 64]).
+__device__ __forceinline__ void head_rms_norm_w(float& a, float& b, float w0, float w1, float eps) {
     const float ss = wave_sum(fmaf(a, a, b * b));
     const float inv = 1.0f / (float)sqrt((double)(ss / 128.0f + eps));
-    a = (a * inv) * ld_act(w, i, w_dt);
-    b = (b * inv) * ld_act(w, i + 64, w_dt);
+    a = (a * inv) * w0;
+    b = (b * inv) * w1;
 }
 
-// Non-traditional RoPE of the pair (i, i + 64) of a 128-feature head at `pos`:
-// angle pos * scale * base^(-2i/128), cos/sin/pow in double.
+// w == nullptr skips the norm (heads without QNorm/KNorm).
+__device__ __forceinline__ void head_rms_norm(float& a, float& b, const void* w, int w_dt, float eps, int i) {
+    if (!w) return;
+    head_rms_norm_w(a, b, ld_act(w, i, w_dt), ld_act(w, i + 64, w_dt), eps);
+}
+
+// Non-traditional RoPE factors of the pair (i, i + 64) of a 128-feature head at
+// `pos`: angle pos * scale * base^(-2i/128), cos/sin/pow in double.
+__device__ __forceinline__ void head_rope_factors(float base, float scale, int64_t pos, int i, float& c, float& sn) {
+    const float fi = (float)pow((double)base, -(double)(2 * i) / 128.0);
+    const float theta = (float)pos * scale * fi;
+    c = (float)cos((double)theta);
+    sn = (float)sin((double)theta);
+}
+
+__device__ __forceinline__ void rotate_pair(float& a, float& b, float c, float sn) {
+    const float ra = a * c - b * sn, rb = a * sn + b * c;
+    a = ra;
+    b = rb;
+}
+
 // With `cs` (rope_table_kernel's output for this position) the factors are read.
 __device__ __forceinline__ void head_rope(float& a, float& b, float base, float scale, int64_t pos, int i,
                                           const float* cs = nullptr) {
@@ -457,14 +492,9 @@ __device__ __forceinline__ void head_rope(float& a, float& b, float base, float 
         c = cs[i];
         sn = cs[64 + i];
     } else {
-        const float fi = (float)pow((double)base, -(double)(2 * i) / 128.0);
-        const float theta = (float)pos * scale * fi;
-        c = (float)cos((double)theta);
-        sn = (float)sin((double)theta);
+        head_rope_factors(base, scale, pos, i, c, sn);
     }
-    const float ra = a * c - b * sn, rb = a * sn + b * c;
-    a = ra;
-    b = rb;
+    rotate_pair(a, b, c, sn);
 }
 
 // ---- Qwen3 attention prologue: per-head q/k RMSNorm, RoPE, KV append ------------
@@ -558,39 +588,82 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
     const int64_t cs = a.owner_alone ? (int64_t)split - 1 : split;  // -1: the new key's own block
     const int64_t j_begin = cs < 0 ? 0 : cs * a.kps;
     const int64_t jc_end = cs < 0 ? 0 : min(a.pos, j_begin + a.kps);  // cache rows scored by this block
-    const uint16_t* kb = a.kc + (int64_t)hk * a.cap * Dh + 8 * kl;
-    const uint16_t* vb = a.vc + (int64_t)hk * a.cap * Dh + 8 * kl;
+    // This block's cache rows as buffer resources over rows [0, jc_end) of the
+    // head: a row past jc_end reads as zeros, with no branch around the load.
+    const __amdgpu_buffer_rsrc_t kb = make_rsrc(a.kc + (int64_t)hk * a.cap * Dh, (uint32_t)(jc_end * Dh * 2));
+    const __amdgpu_buffer_rsrc_t vb = make_rsrc(a.vc + (int64_t)hk * a.cap * Dh, (uint32_t)(jc_end * Dh * 2));
     const int slot = wave * 4 + kg;
 
-    // 1. the first batch of K/V rows, then the query heads (and the new key)
+    // 1. The prologue's inputs (this wave's query heads, the norm weights, the
+    // RoPE factors; the new key and value in the new key's block) are requested
+    // first and the block's K/V rows after them: loads complete in order, so the
+    // prologue waits for its own inputs alone while the K/V rows stream in.
+    constexpr int QPW = (G + 3) / 4;  // query heads per wave
+    const bool qn = a.qn_w != nullptr, kn = a.kn_w != nullptr, table = a.rope_cs != nullptr;
+    const bool kv_wave = owner && wave == 3;
+    // Absent inputs read a valid stand-in (the qkv row) and are replaced after.
+    const void* qwp = qn ? a.qn_w : a.qkv;
+    const void* kwp = kn ? a.kn_w : a.qkv;
+    const float* csp = table ? a.rope_cs : static_cast<const float*>(a.qkv);
+    const int qw_dt = qn ? a.w_dt : a.qkv_dt, kw_dt = kn ? a.w_dt : a.qkv_dt;
+    uint32_t qraw[QPW][2], kvraw[6], wraw[2];
+#pragma unroll
+    for (int i = 0; i < QPW; i++) {
+        const int g = min(wave + 4 * i, G - 1);
+        const int64_t o = (int64_t)(hk * G + g) * Dh;
+        qraw[i][0] = ld_word(a.qkv, o + lane, a.qkv_dt);
+        qraw[i][1] = ld_word(a.qkv, o + lane + 64, a.qkv_dt);
+    }
+    wraw[0] = ld_word(qwp, lane, qw_dt);
+    wraw[1] = ld_word(qwp, lane + 64, qw_dt);
+    const float rc_raw = csp[lane], rs_raw = csp[64 + lane];
+    // Every wave issues the new key's loads (the same addresses in all blocks);
+    // only the owner's wave 3 uses them.
+    const int64_t ok = (int64_t)(Hq + hk) * Dh, ov = (int64_t)(Hq + a.Hk + hk) * Dh;
+    kvraw[0] = ld_word(a.qkv, ok + lane, a.qkv_dt);
+    kvraw[1] = ld_word(a.qkv, ok + lane + 64, a.qkv_dt);
+    kvraw[2] = ld_word(a.qkv, ov + lane, a.qkv_dt);
+    kvraw[3] = ld_word(a.qkv, ov + lane + 64, a.qkv_dt);
+    kvraw[4] = ld_word(kwp, lane, kw_dt);
+    kvraw[5] = ld_word(kwp, lane + 64, kw_dt);
     uint4 kr[U], vr[U];  // raw bf16 rows, unpacked one key at a time
-    auto load_rows = [&](uint4 (&r)[U], const uint16_t* src, int64_t j0) {
+    auto load_rows = [&](uint4 (&r)[U], __amdgpu_buffer_rsrc_t src, int64_t j0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int64_t j = j0 + 16 * u;
-            r[u] = j < jc_end ? *reinterpret_cast<const uint4*>(src + j * Dh) : make_uint4(0, 0, 0, 0);
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(src, (uint32_t)((j0 + 16 * u) * Dh * 2 + 16 * kl), 0, 0);
+            r[u] = make_uint4(v.x, v.y, v.z, v.w);
         }
     };
     int64_t j0 = j_begin + slot;
     load_rows(kr, kb, j0);
     load_rows(vr, vb, j0);
 
+    float rc = rc_raw, rsn = rs_raw;
+    if (!table) head_rope_factors(a.base, a.rscale, a.pos, lane, rc, rsn);
+    const float qw0 = qn ? word_to_f32(wraw[0], qwp, lane, qw_dt) : 1.0f;
+    const float qw1 = qn ? word_to_f32(wraw[1], qwp, lane + 64, qw_dt) : 1.0f;
     __shared__ float q_s[G][Dh];
     __shared__ float kn_s[Dh], vn_s[Dh];
-    for (int g = wave; g < G; g += 4) {
+#pragma unroll
+    for (int i = 0; i < QPW; i++) {
+        const int g = wave + 4 * i;
+        if (g >= G) break;
         const int64_t o = (int64_t)(hk * G + g) * Dh;
-        float x0 = ld_act(a.qkv, o + lane, a.qkv_dt), x1 = ld_act(a.qkv, o + lane + 64, a.qkv_dt);
-        head_rms_norm(x0, x1, a.qn_w, a.w_dt, a.eps, lane);
-        head_rope(x0, x1, a.base, a.rscale, a.pos, lane, a.rope_cs);
+        float x0 = word_to_f32(qraw[i][0], a.qkv, o + lane, a.qkv_dt);
+        float x1 = word_to_f32(qraw[i][1], a.qkv, o + lane + 64, a.qkv_dt);
+        if (qn) head_rms_norm_w(x0, x1, qw0, qw1, a.eps);
+        rotate_pair(x0, x1, rc, rsn);
         q_s[g][lane] = x0 * a.scale;
         q_s[g][lane + 64] = x1 * a.scale;
     }
-    if (owner && wave == 3) {
-        const int64_t ok = (int64_t)(Hq + hk) * Dh, ov = (int64_t)(Hq + a.Hk + hk) * Dh;
-        float k0 = ld_act(a.qkv, ok + lane, a.qkv_dt), k1 = ld_act(a.qkv, ok + lane + 64, a.qkv_dt);
-        const float v0 = ld_act(a.qkv, ov + lane, a.qkv_dt), v1 = ld_act(a.qkv, ov + lane + 64, a.qkv_dt);
-        head_rms_norm(k0, k1, a.kn_w, a.w_dt, a.eps, lane);
-        head_rope(k0, k1, a.base, a.rscale, a.pos, lane, a.rope_cs);
+    if (kv_wave) {
+        float k0 = word_to_f32(kvraw[0], a.qkv, ok + lane, a.qkv_dt);
+        float k1 = word_to_f32(kvraw[1], a.qkv, ok + lane + 64, a.qkv_dt);
+        const float v0 = word_to_f32(kvraw[2], a.qkv, ov + lane, a.qkv_dt);
+        const float v1 = word_to_f32(kvraw[3], a.qkv, ov + lane + 64, a.qkv_dt);
+        if (kn) head_rms_norm_w(k0, k1, word_to_f32(kvraw[4], kwp, lane, kw_dt),
+                                word_to_f32(kvraw[5], kwp, lane + 64, kw_dt), a.eps);
+        rotate_pair(k0, k1, rc, rsn);
         const uint16_t bk0 = f32_to_bf16(k0), bk1 = f32_to_bf16(k1);
         const uint16_t bv0 = f32_to_bf16(v0), bv1 = f32_to_bf16(v1);
         const int64_t row = ((int64_t)hk * a.cap + a.pos) * Dh;
@@ -1030,6 +1103,8 @@ Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const voi
     const AttnSplit sp = attn_split(Hk, pos, num_cus);
     const int64_t kps = sp.kps, nsplit = sp.nsplit;
     if (nsplit > kMaxSplits || kps > 0x7fffffff) return Status::fail(JH_ERR_UNSUPPORTED, "attention: cache too long");
+    // cache rows are addressed with 32-bit byte offsets within a head
+    if (cap > ((int64_t)1 << 23) - 1024) return Status::fail(JH_ERR_UNSUPPORTED, "attention: capacity above 8M tokens");
     AttnArgs a{qkv, qkv_dt, qn_w, kn_w, w_dt, eps, base, rscale, scale, rope_cs, pos,
                static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), cap, Hk, (int)nsplit, (int)kps,
                sp.owner_alone ? 1 : 0, static_cast<float*>(workspace), out, out_dt};
