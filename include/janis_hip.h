@@ -202,6 +202,17 @@ JH_API int jh_elementwise(jh_ctx *ctx, jh_op op, const void *a, jh_dtype a_dtype
  * of the maximum of each of `rows` rows of n; int32 out. */
 JH_API int jh_argmax(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t rows, int64_t n, int32_t *out);
 
+/* RowScatterer.ScatterRows (engine/backend.go:95-105; CPU semantics
+ * cpu/cpu_ops.go:215-233): out = dst with out[indices[i]] = updates[i] along
+ * the leading axis, for a dst of `rows` rows of row_bytes bytes and updates of
+ * n_indices rows. indices are host memory, as the interface passes them; a
+ * repeated index keeps the last of its updates; an index outside [0, rows) is
+ * JH_ERR_INVALID, before anything is written. out == dst updates in place;
+ * any other out (rows * row_bytes, not overlapping dst) receives a copy of dst
+ * first. */
+JH_API int jh_scatter_rows(jh_ctx *ctx, const void *dst, void *out, int64_t rows, int64_t row_bytes,
+                           const int32_t *indices, int64_t n_indices, const void *updates);
+
 /* The data movement behind Slice, Transpose, Concat, Cast and making a view
  * contiguous (engine/backend.go: Slice, Transpose, Concat, Cast; CPU semantics
  * cpu/cpu.go, cpu/cpu_misc.go): for every index of shape[ndim] (ndim <= 8),

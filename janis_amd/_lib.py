@@ -25,7 +25,7 @@ EXPORTS = [
     "jh_h2d", "jh_d2h", "jh_dequantize", "jh_quant_matmul", "jh_gather_quant_matmul",
     "jh_moe_route", "jh_moe_swiglu", "jh_rms_norm", "jh_rope", "jh_sdpa", "jh_elementwise", "jh_argmax",
     "jh_take_rows", "jh_kv_append", "jh_qk_norm_rope_append", "jh_quant_matvec_fused",
-    "jh_attention_decode", "jh_rope_table", "jh_norm_prepare", "jh_copy_strided",
+    "jh_attention_decode", "jh_rope_table", "jh_norm_prepare", "jh_copy_strided", "jh_scatter_rows",
 ]
 
 _lib = None
@@ -99,9 +99,10 @@ def load() -> ctypes.CDLL:
     L.jh_quant_matvec_fused.argtypes = [c_ctx, i, p, i, p, i, f32, p, p, p, i, i64, i64, i, i, i, p, p, i, p, p]
     L.jh_norm_prepare.argtypes = [c_ctx, p, i, i64, p, i, p, p]
     L.jh_copy_strided.argtypes = [c_ctx, p, i, i, p, p, p, i, p]
+    L.jh_scatter_rows.argtypes = [c_ctx, p, p, i64, i64, p, i64, p]
     for name in ("jh_rms_norm", "jh_rope", "jh_sdpa", "jh_elementwise", "jh_argmax", "jh_take_rows", "jh_kv_append",
                  "jh_qk_norm_rope_append", "jh_quant_matvec_fused", "jh_attention_decode", "jh_rope_table",
-                 "jh_norm_prepare", "jh_copy_strided"):
+                 "jh_norm_prepare", "jh_copy_strided", "jh_scatter_rows"):
         getattr(L, name).restype = i
     L.jh_moe_route.argtypes = [c_ctx, p, i, i64, i64, i64, i, p, p]
     L.jh_moe_route.restype = i

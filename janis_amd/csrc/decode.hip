@@ -952,6 +952,27 @@ __global__ __launch_bounds__(256) void take_rows_kernel(const uint8_t* __restric
         out[k * row_bytes + i] = ok ? table[(int64_t)id * row_bytes + i] : (uint8_t)0;
 }
 
+// Row copies of a scatter: block (x, y) copies bytes [x * kScatterChunk, ...)
+// of update row l.src[y] into out row l.dst[y], in `vec`-byte words (16 when
+// the row length and both bases allow it, else 4, else 1).
+__global__ __launch_bounds__(256) void scatter_rows_kernel(ScatterList l, const uint8_t* __restrict__ upd,
+                                                           uint8_t* __restrict__ out, int64_t row_bytes, int vec) {
+    const int e = blockIdx.y;
+    const uint8_t* s = upd + (int64_t)l.src[e] * row_bytes;
+    uint8_t* d = out + (int64_t)l.dst[e] * row_bytes;
+    const int64_t lo = (int64_t)blockIdx.x * kScatterChunk;
+    const int64_t hi = min(row_bytes, lo + (int64_t)kScatterChunk);
+    if (vec == 16) {
+        for (int64_t i = lo + 16 * threadIdx.x; i < hi; i += 16 * 256)
+            *reinterpret_cast<uint4*>(d + i) = *reinterpret_cast<const uint4*>(s + i);
+    } else if (vec == 4) {
+        for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 4 * 256)
+            *reinterpret_cast<uint32_t*>(d + i) = *reinterpret_cast<const uint32_t*>(s + i);
+    } else {
+        for (int64_t i = lo + threadIdx.x; i < hi; i += 256) d[i] = s[i];
+    }
+}
+
 __global__ __launch_bounds__(256) void kv_append_kernel(void* __restrict__ kc, void* __restrict__ vc, int c_dt,
                                                         const void* __restrict__ kn, const void* __restrict__ vn,
                                                         int n_dt, int64_t BH, int64_t cap, int64_t pos, int64_t L,
@@ -1179,6 +1200,20 @@ Status launch_copy_strided(const void* src, int sdt, int nd, const int64_t* shap
     }
     if (n == 0) return Status::ok();
     hipLaunchKernelGGL(copy_strided_kernel, dim3(grid_for(n, 256, 16384)), dim3(256), 0, st, src, sdt, dst, ddt, n, d);
+    return Status::ok();
+}
+
+Status launch_scatter_rows(const ScatterList& l, const void* updates, void* out, int64_t row_bytes,
+                           hipStream_t st) {
+    if (l.n <= 0 || row_bytes <= 0) return Status::ok();
+    const int64_t chunks = (row_bytes + kScatterChunk - 1) / kScatterChunk;
+    if (chunks > 0x7fffffff) return Status::fail(JH_ERR_UNSUPPORTED, "scatter_rows: rows too long");
+    const auto aligned = [](const void* p, int a) { return reinterpret_cast<uintptr_t>(p) % a == 0; };
+    const int vec = row_bytes % 16 == 0 && aligned(updates, 16) && aligned(out, 16) ? 16
+                    : row_bytes % 4 == 0 && aligned(updates, 4) && aligned(out, 4)  ? 4
+                                                                                      : 1;
+    hipLaunchKernelGGL(scatter_rows_kernel, dim3((unsigned)chunks, (unsigned)l.n), dim3(256), 0, st, l,
+                       static_cast<const uint8_t*>(updates), static_cast<uint8_t*>(out), row_bytes, vec);
     return Status::ok();
 }
 

@@ -259,6 +259,17 @@ constexpr int kMaxCopyDims = 8;
 // contiguous), converting between F32/F16/BF16 (other types: same-type copies).
 Status launch_copy_strided(const void* src, int sdt, int nd, const int64_t* shape, const int64_t* strides, void* dst,
                            int ddt, const int64_t* dst_strides, hipStream_t st);
+// One batch of a row scatter: update row src[i] goes to row dst[i], i < n
+// (passed by value, so a launch needs no device copy of the indices).
+constexpr int kScatterBatch = 256;
+constexpr int kScatterChunk = 64 * 1024;  // bytes of a row per block
+struct ScatterList {
+    int32_t dst[kScatterBatch];
+    int32_t src[kScatterBatch];
+    int n;
+};
+Status launch_scatter_rows(const ScatterList& l, const void* updates, void* out, int64_t row_bytes,
+                           hipStream_t st);
 Status launch_take_rows(const void* table, int64_t row_bytes, int64_t n_rows, const int32_t* ids, int64_t n_ids,
                         void* out, hipStream_t st);
 Status launch_kv_append(void* kc, void* vc, int c_dt, const void* kn, const void* vn, int n_dt, int64_t BH,

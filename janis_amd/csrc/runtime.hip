@@ -586,6 +586,42 @@ int jh_take_rows(jh_ctx* c, const void* table, int64_t row_bytes, int64_t n_rows
     return finish(c, jh::launch_take_rows(table, row_bytes, n_rows, ids, n_ids, out, c->stream), op);
 }
 
+int jh_scatter_rows(jh_ctx* c, const void* dst, void* out, int64_t rows, int64_t row_bytes, const int32_t* indices,
+                    int64_t n_indices, const void* updates) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_scatter_rows";
+    if (rows < 0 || row_bytes < 0 || n_indices < 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape");
+    if (rows > 0x7fffffff || n_indices > 0x7fffffff)
+        return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": more than 2^31 rows");
+    if (n_indices > 0 && !indices) return fail(c, JH_ERR_INVALID, std::string(op) + ": null indices");
+    // every index is checked before anything is written
+    for (int64_t i = 0; i < n_indices; i++)
+        if (indices[i] < 0 || indices[i] >= rows)
+            return fail(c, JH_ERR_INVALID, std::string(op) + ": index " + std::to_string(indices[i]) + " at " +
+                                               std::to_string(i) + " outside [0, " + std::to_string(rows) + ")");
+    if (rows == 0 || row_bytes == 0) return JH_OK;
+    if (!dst || !out || (n_indices > 0 && !updates)) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    if (out != dst)
+        JH_HIP(c, hipMemcpyAsync(out, dst, (size_t)(rows * row_bytes), hipMemcpyDeviceToDevice, c->stream));
+    // a repeated index keeps its last update (the order the updates are applied
+    // in), so each destination row is written once and the launches cannot race
+    std::vector<char> seen((size_t)rows, 0);
+    jh::ScatterList l;
+    l.n = 0;
+    for (int64_t i = n_indices - 1; i >= 0; i--) {
+        const int32_t r = indices[i];
+        if (seen[(size_t)r]) continue;
+        seen[(size_t)r] = 1;
+        l.dst[l.n] = r;
+        l.src[l.n] = (int32_t)i;
+        if (++l.n == jh::kScatterBatch) {
+            if (int e = finish(c, jh::launch_scatter_rows(l, updates, out, row_bytes, c->stream), op)) return e;
+            l.n = 0;
+        }
+    }
+    return finish(c, jh::launch_scatter_rows(l, updates, out, row_bytes, c->stream), op);
+}
+
 int jh_kv_append(jh_ctx* c, void* k_cache, void* v_cache, jh_dtype cache_dtype, int64_t BH, int64_t capacity,
                  int64_t pos, const void* k_new, const void* v_new, jh_dtype new_dtype, int64_t L, int64_t Dh) {
     if (int r = enter(c)) return r;

@@ -564,6 +564,24 @@ class HipBackend:
         check(self._ctx, self._L.jh_take_rows(self._ctx, a.ptr, row_bytes, rows, indices.ptr, indices.numel, out.ptr))
         return out
 
+    def ScatterRows(self, dst: Tensor, indices, updates: Tensor) -> Tensor:
+        """engine.RowScatterer (engine/backend.go:95-105; CPU semantics
+        cpu/cpu_ops.go:215-233): a new tensor equal to dst with row indices[i]
+        (axis 0) replaced by updates[i]; updates is [len(indices), *dst.shape[1:]]
+        of dst's dtype, indices host int32 as the interface passes them. A
+        repeated index keeps its last update; one outside [0, rows) raises."""
+        idx = np.ascontiguousarray(np.asarray(indices, dtype=np.int32).reshape(-1))
+        if updates.dtype != dst.dtype or tuple(updates.shape) != (idx.size, *dst.shape[1:]):
+            raise JanisHipError(_lib.JH_ERR_INVALID,
+                                f"ScatterRows: updates {DTYPE_NAME[updates.dtype]}{list(updates.shape)} for dst "
+                                f"{DTYPE_NAME[dst.dtype]}{list(dst.shape)} and {idx.size} indices")
+        dst, updates = self._c(dst), self._c(updates)
+        rows = dst.shape[0]
+        out = self.empty(dst.dtype, *dst.shape)
+        check(self._ctx, self._L.jh_scatter_rows(self._ctx, dst.ptr, out.ptr, rows, dst.nbytes // rows if rows else 0,
+                                                 idx.ctypes.data, idx.size, updates.ptr))
+        return out
+
     KV_STEP = 256  # cache capacity granularity (tokens)
     KV_AHEAD = 2048  # at most this many tokens of room beyond what a request needs now
 

@@ -249,3 +249,18 @@ def argmax(x) -> np.ndarray:
     lib().or_argmax(x, x.size // n, n, out)
     return out
 
+
+def scatter_rows(dst, indices, updates) -> np.ndarray:
+    """cpu/cpu_ops.go:215-233 (RowScatterer.ScatterRows): a copy of dst whose
+    row indices[i] (axis 0) is replaced by updates[i], applied in index order
+    (so a repeated index keeps its last update); any dtype, rows compared as
+    bytes. Raises IndexError for an index outside [0, rows), where the
+    reference's slice copy panics."""
+    dst = np.asarray(dst)
+    out = dst.copy()
+    upd = np.asarray(updates).reshape((len(indices),) + dst.shape[1:])
+    for i, r in enumerate(np.asarray(indices, dtype=np.int64).reshape(-1)):
+        if r < 0 or r >= dst.shape[0]:
+            raise IndexError(f"scatter_rows: index {r} outside [0, {dst.shape[0]})")
+        out[r] = upd[i]
+    return out

@@ -8,7 +8,7 @@ import pytest
 
 from janis_amd import synth
 from janis_amd.engine import BF16, F16, F32, I32, U32, JanisHipError
-from tests.conftest import step
+from tests.conftest import rel_ok, step
 
 pytestmark = pytest.mark.gpu
 
@@ -113,3 +113,98 @@ def test_sweeper_and_free():
         assert b.ptr == 0 and w.ptr != 0
     finally:
         hb.Close()
+
+
+def _raw(hip, t, dtype, shape):
+    return np.frombuffer(hip.Bytes(t), dtype=dtype).reshape(shape)
+
+
+@pytest.mark.parametrize("dt,np_dt,shape,n_idx", [
+    (U32, np.uint32, (37, 129), 11),          # 516-byte rows: 4-byte words
+    (BF16, np.uint16, (16, 24), 20),          # 48-byte rows: 16-byte words
+    (F32, np.float32, (5, 70001), 7),         # rows over several 64 KiB chunks
+    (U32, np.uint32, (600, 8), 700),          # more indices than one launch takes
+])
+def test_scatter_rows_matches_oracle(hip, oracle, dt, np_dt, shape, n_idx):
+    """RowScatterer.ScatterRows (engine/backend.go:95-105) against the CPU
+    semantics (cpu/cpu_ops.go:215-233), bit-exact, with repeated indices (the
+    last update stays) and dst left as it was."""
+    rng = np.random.default_rng(shape[0] * 7 + n_idx)
+    dst = rng.integers(0, 2**16 if np_dt == np.uint16 else 2**31, shape).astype(np_dt)
+    idx = rng.integers(0, shape[0], n_idx).astype(np.int32)
+    upd = rng.integers(0, 2**16 if np_dt == np.uint16 else 2**31, (n_idx,) + shape[1:]).astype(np_dt)
+    td, tu = hip.FromRaw(dt, dst, *shape), hip.FromRaw(dt, upd, n_idx, *shape[1:])
+    step(f"jh_scatter_rows {shape} n_idx={n_idx}")
+    out = hip.ScatterRows(td, idx, tu)
+    assert tuple(out.shape) == shape
+    assert np.array_equal(_raw(hip, out, np_dt, shape), oracle.scatter_rows(dst, idx, upd))
+    assert np.array_equal(_raw(hip, td, np_dt, shape), dst)
+
+
+def test_scatter_rows_edges(hip, oracle):
+    """No indices (a copy), a U8 tensor (1-byte words), in place through the
+    C ABI (out == dst), and out-of-range indices rejected before any write."""
+    import ctypes
+
+    from janis_amd.engine import U8
+    rng = np.random.default_rng(5)
+    dst = rng.integers(0, 255, (9, 7)).astype(np.uint8)
+    td = hip.FromRaw(U8, dst, 9, 7)
+    step("jh_scatter_rows empty / u8 / in place / out of range")
+    assert np.array_equal(_raw(hip, hip.ScatterRows(td, [], hip.FromRaw(U8, np.zeros((0, 7), np.uint8), 0, 7)),
+                               np.uint8, (9, 7)), dst)
+    upd = rng.integers(0, 255, (3, 7)).astype(np.uint8)
+    got = _raw(hip, hip.ScatterRows(td, [8, 0, 4], hip.FromRaw(U8, upd, 3, 7)), np.uint8, (9, 7))
+    assert np.array_equal(got, oracle.scatter_rows(dst, [8, 0, 4], upd))
+    idx = np.array([3, 3, 1], np.int32)
+    tu = hip.FromRaw(U8, upd, 3, 7)
+    rc = hip._L.jh_scatter_rows(hip._ctx, td.ptr, td.ptr, 9, 7, idx.ctypes.data_as(ctypes.c_void_p), 3, tu.ptr)
+    assert rc == 0
+    assert np.array_equal(_raw(hip, td, np.uint8, (9, 7)), oracle.scatter_rows(dst, idx, upd))
+    before = _raw(hip, td, np.uint8, (9, 7)).copy()
+    for bad in ([9], [-1], [0, 2, 12]):
+        with pytest.raises(JanisHipError):
+            hip.ScatterRows(td, bad, hip.FromRaw(U8, upd[:len(bad)], len(bad), 7))
+    with pytest.raises(JanisHipError):
+        hip.ScatterRows(td, [1, 2], tu)  # 3 update rows for 2 indices
+    assert np.array_equal(_raw(hip, td, np.uint8, (9, 7)), before)
+
+
+def test_slot_cache_scatter_then_gather(hip, oracle):
+    """The MoE slot cache's use of ScatterRows (qwen/slotcache.go:60-186): the
+    missed experts' W / scales / biases rows land in victim slots of persistent
+    [slots, ...] stacks, and GatherQuantMatmul over the slot stacks with slot
+    indices equals the gather over the full expert stacks with expert indices."""
+    E, S, n, k = 12, 5, 64, 512
+    q = synth.quant_linear(81, n, k, lead=(E,))
+    w, s, b = (hip.FromRaw(U32, q.w, *q.w.shape), hip.FromBF16Bits(q.s_bits, *q.s_bits.shape),
+               hip.FromBF16Bits(q.b_bits, *q.b_bits.shape))
+    slots = [hip.FromRaw(U32, np.zeros((S,) + q.w.shape[1:], np.uint32), S, *q.w.shape[1:]),
+             hip.FromBF16Bits(np.zeros((S,) + q.s_bits.shape[1:], np.uint16), S, *q.s_bits.shape[1:]),
+             hip.FromBF16Bits(np.zeros((S,) + q.b_bits.shape[1:], np.uint16), S, *q.b_bits.shape[1:])]
+    slot_of = {}
+    xb, x = synth.activations(82, (1, 1, 1, k))
+    for tok, experts in enumerate(([3, 7, 1], [7, 9, 3], [11, 0, 9])):
+        miss = [e for e in experts if e not in slot_of]
+        held = {slot_of[e] for e in experts if e in slot_of}
+        free = [v for v in range(S) if v not in slot_of.values()] + \
+               [v for v in range(S) if v in slot_of.values() and v not in held]
+        victims = free[:len(miss)]
+        for v in victims:
+            slot_of = {e: sl for e, sl in slot_of.items() if sl != v}
+        for e, v in zip(miss, victims):
+            slot_of[e] = v
+        ids = np.array(miss, np.int32)
+        step(f"slot cache token {tok}: miss {miss} -> slots {victims}")
+        slots = [hip.ScatterRows(t, victims, hip.TakeAxis(src, hip.FromInt32(ids), 0))
+                 for t, src in zip(slots, (w, s, b))]
+        sidx = np.array([[slot_of[e] for e in experts]], np.int32)
+        y = hip.Floats(hip.GatherQuantMatmul(hip.FromBF16Bits(xb, 1, 1, 1, k), *slots, hip.FromInt32(sidx),
+                                             True, 64, 4, out_dtype=F32))
+        full = hip.Floats(hip.GatherQuantMatmul(hip.FromBF16Bits(xb, 1, 1, 1, k), w, s, b,
+                                                hip.FromInt32(np.array([experts], np.int32)), True, 64, 4,
+                                                out_dtype=F32))
+        assert np.array_equal(y, full), tok
+        want = oracle.gather_quant_matmul(x, q.w, q.s, q.b, np.array([experts], np.int32), 64)
+        ok, d, sc = rel_ok(y, want, 1e-3)
+        assert ok, (tok, d, sc)

@@ -462,3 +462,17 @@ def test_silu_and_argmax(oracle):
     assert ok, (d, sc)
     t = np.array([[1, 5, 5, 2], [-np.inf, -np.inf, -np.inf, -np.inf], [np.nan, 1, 3, 3]], np.float32)
     assert list(oracle.argmax(t)) == [1, 0, 2]
+
+
+def test_scatter_rows_known_answer(oracle):
+    """ScatterRows (cpu/cpu_ops.go:215-233) on a hand-worked case: rows 2 and 0
+    replaced, row 2 twice (the later update stays), rows 1 and 3 untouched."""
+    dst = np.arange(12, dtype=np.uint32).reshape(4, 3)
+    upd = np.array([[100, 101, 102], [200, 201, 202], [300, 301, 302]], dtype=np.uint32)
+    want = np.array([[200, 201, 202], [3, 4, 5], [300, 301, 302], [9, 10, 11]], dtype=np.uint32)
+    got = oracle.scatter_rows(dst, [2, 0, 2], upd)
+    assert np.array_equal(got, want)
+    assert np.array_equal(dst, np.arange(12, dtype=np.uint32).reshape(4, 3))  # dst itself unchanged
+    assert np.array_equal(oracle.scatter_rows(dst, [], np.zeros((0, 3), np.uint32)), dst)
+    with pytest.raises(IndexError):
+        oracle.scatter_rows(dst, [4], upd[:1])
