@@ -41,9 +41,9 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0
 HIDDEN, INTER, VOCAB, LAYERS, GS = 4096, 12288, 151936, 36, 64
 
 
-def qbytes(n: int, k: int) -> int:
-    """Algorithmic bytes of one 4-bit g64 qmv: codes + bf16 scales/biases + x + y."""
-    return n * k // 2 + 4 * n * (k // GS) + 2 * k + 2 * n
+def qbytes(n: int, k: int, bits: int = 4) -> int:
+    """Algorithmic bytes of one g64 qmv: codes + bf16 scales/biases + x + y."""
+    return n * k * bits // 8 + 4 * n * (k // GS) + 2 * k + 2 * n
 
 
 def log(*a):
@@ -80,11 +80,12 @@ def main() -> int:
     hip = HipBackend(0)
     log("device:", hip.EngineInfo())
 
-    def qweight(n, k, lead=()):
-        shape = (*lead, n, k // 8)
+    def qweight(n, k, lead=(), bits=4):
+        shape = (*lead, n, k * bits // 32)
         w = torch.randint(-2**31, 2**31 - 1, shape, dtype=torch.int32, device=dev)
         s = (torch.randn((*lead, n, k // GS), device=dev).abs() * 0.02).to(torch.bfloat16)
-        b = (-8.0 * s.float() + torch.randn((*lead, n, k // GS), device=dev) * 1e-3).to(torch.bfloat16)
+        b = (-float(1 << (bits - 1)) * s.float() + torch.randn((*lead, n, k // GS), device=dev) * 1e-3
+             ).to(torch.bfloat16)
         return (hip.Wrap(w.data_ptr(), shape, U32, keep=w),
                 hip.Wrap(s.data_ptr(), s.shape, BF16, keep=s),
                 hip.Wrap(b.data_ptr(), b.shape, BF16, keep=b))
@@ -192,6 +193,19 @@ def main() -> int:
     del g
     log("per shape:", per_shape)
 
+    # ---- the same shapes with 8-bit codes (MLX's other affine width), 8 copies each -----
+    per_shape_8 = {}
+    for name, (n, k) in shapes.items():
+        copies = [qweight(n, k, bits=8) for _ in range(8)]
+        g = capture(lambda name=name, copies=copies: [
+            hip.QuantMatmul(xin[name], w, s_, b_, True, GS, 8, out=ys[name]) for (w, s_, b_) in copies])
+        ms = time_graph(g, max(5, args.steps // 2), 3) / len(copies)
+        per_shape_8[name] = {"N": n, "K": k, "us": round(ms * 1e3, 2),
+                             "GB_s": round(qbytes(n, k, 8) / (ms * 1e-3) / 1e9, 1)}
+        del g, copies
+    torch.cuda.synchronize()
+    log("per shape, 8-bit:", per_shape_8)
+
     # ---- dominant kernel: the K=4096 GEMV tile (qkv, o, gate_up; 74% of the step) -------
     # Events bracket a graph of exactly that kernel's launches, back to back, in the
     # sequence's order; achieved = their algorithmic bytes / their time per launch.
@@ -216,7 +230,8 @@ def main() -> int:
                 "launches_per_step": n_dom, "avg_launch_us": round(ms_dom * 1e3 / n_dom, 3),
                 "algorithmic_bytes_per_launch": bytes_dom // n_dom}
 
-    extra = {"per_shape": per_shape, "launches_per_token": n_launch, "bytes_per_token": bytes_token}
+    extra = {"per_shape": per_shape, "per_shape_8bit": per_shape_8, "launches_per_token": n_launch,
+             "bytes_per_token": bytes_token}
 
     if not args.quick:
         extra.update(prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args))

@@ -172,7 +172,8 @@ struct QmvFusion {
     uint16_t* nout = nullptr;      // bf16 [N] (EPI_RESID_NORM)
 };
 
-template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int PRO = PRO_NONE, int EPI = EPI_STORE>
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int PRO = PRO_NONE, int EPI = EPI_STORE,
+          int BITS = 4>
 __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     const uint32_t* __restrict__ W, const uint16_t* __restrict__ S,
     const uint16_t* __restrict__ B, const void* __restrict__ Xv, void* Y,
@@ -185,25 +186,32 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     constexpr int ROWS_PER_WAVE = SLICES * RO;
     constexpr int ROWS_PER_BLOCK = RGROUPS * ROWS_PER_WAVE;
     static_assert(EPI != EPI_SWIGLU || RPW % 2 == 0, "SwiGLU pairs gate and up rows");
+    static_assert(BITS == 4 || (BITS == 8 && PRO != PRO_RMSNORM), "8-bit tiles take a bf16 x");
+    // 8-bit codes are read as two 4-bit halves, q = lo + 16 hi, against a virtual
+    // input that holds each x twice: (x, 16x) for the (lo, hi) nibbles of its
+    // byte. 16x is exact in bf16, so the word dots are the 4-bit ones, and the
+    // offset 128 of each nibble sums to 128 * 17 per element.
+    constexpr uint32_t EPW = 32 / BITS;                 // elements per word
+    constexpr float OFF = BITS == 4 ? kCodeOffset : 17.0f * kCodeOffset;
     const uint32_t NW = EPI == EPI_SWIGLU ? 2 * N : N;     // rows of W
     const int lane = threadIdx.x & 63;
     const int wv_id = threadIdx.x >> 6;
     const int ks = wv_id % KSPLIT, rg = wv_id / KSPLIT;
     const int sl = lane % LPR;
     const int slice = lane / LPR;
-    const uint32_t G = (P * 8) >> gs_log2;
+    const uint32_t G = (P * EPW) >> gs_log2;  // groups per row
     const auto rw = make_rsrc(W, NW * P * 4);
     const auto rs = make_rsrc(S, NW * G * 2);
     const auto rb = make_rsrc(B, NW * G * 2);
     __shared__ float red[(KSPLIT > 1) ? (KSPLIT - 1) * RGROUPS * SLICES * RPW : 1];
     __shared__ float ssq[4];
-    constexpr uint32_t K = 8 * P;
+    constexpr uint32_t K = EPW * P;
 
     uint32_t gi[ITERS], wo[ITERS];
 #pragma unroll
     for (int it = 0; it < ITERS; it++) {
         wo[it] = ks * PK + it * 4 * LPR + 4 * sl;   // word offset inside a row
-        gi[it] = (8u * wo[it]) >> gs_log2;
+        gi[it] = (EPW * wo[it]) >> gs_log2;
     }
     uint4 wv[RPW][ITERS];
     uint16_t sh[RPW][ITERS], bh[RPW][ITERS];
@@ -241,13 +249,14 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
 #pragma unroll
             for (int r = 0; r < RPW; r++) nv[r] = buf_load2(rn, (row0 + r) * 2);
     };
-    // raw x: 32 elements per lane per ITER (bf16, or fp32 for the norm)
-    constexpr int XW = PRO == PRO_RMSNORM ? 8 : 4;  // 16-byte chunks per 32 elements
+    // raw x: 32 (4-bit) or 16 (8-bit) elements per lane per ITER (bf16, or fp32
+    // for the norm)
+    constexpr int XW = PRO == PRO_RMSNORM ? 8 : (int)EPW / 2;  // 16-byte chunks of them
     uint4 xraw[ITERS][XW];
     uint4 xaux[ITERS][4];  // norm weights (PRO_RMSNORM)
 #pragma unroll
     for (int it = 0; it < ITERS; it++) {
-        const uint32_t e0 = 8u * wo[it];
+        const uint32_t e0 = EPW * wo[it];
         if constexpr (PRO == PRO_RMSNORM) {
             const uint4* xv = reinterpret_cast<const uint4*>(static_cast<const float*>(Xv) + e0);
 #pragma unroll
@@ -255,7 +264,7 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
         } else {
             const uint4* xv = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(Xv) + e0);
 #pragma unroll
-            for (int j = 0; j < 4; j++) xraw[it][j] = xv[j];
+            for (int j = 0; j < XW; j++) xraw[it][j] = xv[j];
         }
     }
     // the norm weights go with x, ahead of the weights, so the normalisation
@@ -291,7 +300,28 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
         if constexpr (KSPLIT > 1)
             if (lane == 0) ssq[wv_id] = ss_part;
     }
-    if constexpr (PRO == PRO_NONE || PRO == PRO_NORMED) {
+    float xs8[ITERS];  // 8-bit: the sum of the real inputs
+    if constexpr (BITS == 8) {
+        // word j of a 16-byte chunk holds elements 4j..4j+3: its virtual input is
+        // (x, 16x) per element, 8 bf16 in one uint4
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+            const uint32_t xr[8] = {xraw[it][0].x, xraw[it][0].y, xraw[it][0].z, xraw[it][0].w,
+                                    xraw[it][1].x, xraw[it][1].y, xraw[it][1].z, xraw[it][1].w};
+            float sum = 0.0f;
+            uint32_t v[16];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const float a = __uint_as_float(xr[q] << 16), b = __uint_as_float(xr[q] & 0xFFFF0000u);
+                sum += a + b;
+                v[2 * q] = (xr[q] & 0xFFFFu) | ((uint32_t)f32_to_bf16_hw(16.0f * a) << 16);
+                v[2 * q + 1] = (xr[q] >> 16) | ((uint32_t)f32_to_bf16_hw(16.0f * b) << 16);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) xin[it][j] = make_uint4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+            xs8[it] = sum;
+        }
+    } else if constexpr (PRO == PRO_NONE || PRO == PRO_NORMED) {
 #pragma unroll
         for (int it = 0; it < ITERS; it++)
 #pragma unroll
@@ -333,7 +363,7 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
         float sum = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; j++) sum += pair_up(xin[it][j], &xp[it][4 * j]);
-        xs[it] = sum;
+        xs[it] = BITS == 8 ? xs8[it] : sum;
     }
 
     for (uint32_t bbase = blockIdx.x * ROWS_PER_BLOCK; bbase < N; bbase += gridDim.x * ROWS_PER_BLOCK) {
@@ -353,7 +383,7 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
                 d = word_dot(wv[r][it].z, &xp[it][8], d);
                 d = word_dot(wv[r][it].w, &xp[it][12], d);
                 part[r] = fmaf(sc, d, part[r]);
-                part[r] = fmaf(fmaf(-kCodeOffset, sc, bi), xs[it], part[r]);
+                part[r] = fmaf(fmaf(-OFF, sc, bi), xs[it], part[r]);
             }
         }
         slice_sums_last<LPR, RPW>(part);
@@ -487,12 +517,17 @@ __global__ __launch_bounds__(256) void qmv_generic_kernel(
 
 namespace {
 
-template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int PRO = PRO_NONE, int EPI = EPI_STORE>
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int PRO = PRO_NONE, int EPI = EPI_STORE,
+          int BITS = 4>
 Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gs_log2,
                    int num_cus, hipStream_t st, const QmvFusion& fu = QmvFusion{}) {
     constexpr int64_t rows_per_block = (4 / KSPLIT) * (64 / LPR) * (EPI == EPI_SWIGLU ? RPW / 2 : RPW);
+    // the tile's row length must be the matrix's: the kernel sizes its buffer
+    // resources and group offsets from it
+    constexpr int64_t k_tile = 4LL * LPR * ITERS * KSPLIT * (32 / BITS);
+    if (k_tile != m.in || m.bits != BITS) return Status::fail(JH_ERR_UNSUPPORTED, "qmv: tile does not fit the matrix");
     const int64_t n_out = EPI == EPI_SWIGLU ? m.rows / 2 : m.rows;
-    auto kern = qmv_bf16x_kernel<LPR, ITERS, RPW, KSPLIT, SB_F16, PRO, EPI>;
+    auto kern = qmv_bf16x_kernel<LPR, ITERS, RPW, KSPLIT, SB_F16, PRO, EPI, BITS>;
     // persistent-style grid: at most what is resident at once, so multi-pass
     // shapes reuse the x registers instead of queueing more blocks
     static int resident = 0;
@@ -538,32 +573,46 @@ namespace {
 // One tile of the table. Fused prologues/epilogues are built for bf16 scales
 // only (the checkpoints' format); an f16-scale fused call returns false and is
 // composed from separate launches by the caller.
+template <int LPR, int ITERS, int RPW, int KSPLIT, int PRO, int EPI, int BITS>
+bool tile_bits(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gl, int num_cus, hipStream_t st,
+               const QmvFusion& fu) {
+    if (m.sb_dtype == JH_F16) {
+        if constexpr (PRO == PRO_NONE && EPI == EPI_STORE)
+            return run_fast_sb<LPR, ITERS, RPW, KSPLIT, true, PRO, EPI, BITS>(m, x, y, y_dtype, gl, num_cus, st, fu)
+                       .code == JH_OK;
+        else
+            return false;
+    }
+    return run_fast_sb<LPR, ITERS, RPW, KSPLIT, false, PRO, EPI, BITS>(m, x, y, y_dtype, gl, num_cus, st, fu).code ==
+           JH_OK;
+}
+
+// 8-bit weights have tiles for a plain or prepared-norm bf16 input.
 template <int LPR, int ITERS, int RPW, int KSPLIT, int PRO, int EPI>
 bool tile(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gl, int num_cus, hipStream_t st,
           const QmvFusion& fu) {
-    if (m.sb_dtype == JH_F16) {
-        if constexpr (PRO == PRO_NONE && EPI == EPI_STORE) {
-            run_fast_sb<LPR, ITERS, RPW, KSPLIT, true, PRO, EPI>(m, x, y, y_dtype, gl, num_cus, st, fu);
-            return true;
-        } else {
-            return false;
-        }
+    if (m.bits == 8) {
+        if constexpr (PRO == PRO_RMSNORM) return false;
+        else return tile_bits<LPR, ITERS, RPW, KSPLIT, PRO, EPI, 8>(m, x, y, y_dtype, gl, num_cus, st, fu);
     }
-    run_fast_sb<LPR, ITERS, RPW, KSPLIT, false, PRO, EPI>(m, x, y, y_dtype, gl, num_cus, st, fu);
-    return true;
+    return tile_bits<LPR, ITERS, RPW, KSPLIT, PRO, EPI, 4>(m, x, y, y_dtype, gl, num_cus, st, fu);
 }
 
-// The register tiles take 4-bit weights, groups of 32/64/128 dividing K, 16-bit
-// scales, matrices under 2 GiB and the row lengths P = K/8 of the table below.
+// The register tiles take 4- and 8-bit weights, groups of 32/64/128 dividing K,
+// 16-bit scales, matrices under 2 GiB and the row lengths P (words) of the
+// table below: K = 8P for 4-bit, 4P for 8-bit.
+int64_t row_words(const QuantMatrix& m) { return m.in * m.bits / 32; }
+
 bool qmv_fast_shape(const QuantMatrix& m) {
     const int gl = log2_exact(m.group_size);
-    if (!(m.bits == 4 && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0 &&
-          (m.sb_dtype == JH_BF16 || m.sb_dtype == JH_F16) && (m.rows + 64) * (m.in / 2) < ((int64_t)1 << 31)))
+    if (!((m.bits == 4 || m.bits == 8) && gl >= 5 && gl <= 7 && (m.in % m.group_size) == 0 &&
+          (m.in % (32 / m.bits)) == 0 && (m.sb_dtype == JH_BF16 || m.sb_dtype == JH_F16) &&
+          (m.rows + 64) * row_words(m) * 4 < ((int64_t)1 << 31)))
         return false;
-    switch (m.in / 8) {
-        case 512: case 1024: case 1536: case 2048: case 256: case 768:
+    switch (row_words(m)) {
+        case 512: case 1024: case 1536: case 2048: case 3072: case 256: case 768:
         case 128: case 384: case 64: case 192: case 32: case 96:
-            return (m.in % 8) == 0;
+            return true;
         default:
             return false;
     }
@@ -578,12 +627,13 @@ bool launch_tiles(const QuantMatrix& m, const void* x, void* y, int y_dtype, int
     if (!qmv_fast_shape(m)) return false;
     const int gl = log2_exact(m.group_size);
 #define JH_TILE(L, I, R, KS) return tile<L, I, R, KS, PRO, EPI>(m, x, y, y_dtype, gl, num_cus, st, fu)
-    if (m.in == 4096 && m.rows >= 65536) JH_TILE(64, 1, 8, 2);
-    switch (m.in / 8) {
+    if (m.bits == 4 && m.in == 4096 && m.rows >= 65536) JH_TILE(64, 1, 8, 2);
+    switch (row_words(m)) {
         case 512 * 1: JH_TILE(32, 1, 4, 4);
         case 512 * 2: JH_TILE(32, 2, 2, 4);
         case 512 * 3: JH_TILE(32, 3, 2, 4);
         case 512 * 4: JH_TILE(32, 4, 2, 4);
+        case 512 * 6: JH_TILE(64, 3, 2, 4);  // 8-bit K = 12288
         case 256 * 1: JH_TILE(32, 1, 4, 2);
         case 256 * 3: JH_TILE(32, 3, 2, 2);
         case 128 * 1: JH_TILE(16, 1, 4, 2);
@@ -614,6 +664,7 @@ bool qmv_fused_single(const QuantMatrix& m, int pro, int x_dtype, int nw_dtype, 
     if ((epi == EPI_RESID || epi == EPI_RESID_NORM) && y_dtype != JH_F32) return false;
     if (epi == EPI_RESID_NORM && nw_dtype != JH_BF16) return false;
     if (!qmv_fast_shape(m)) return false;
+    if (m.bits == 8 && pro == PRO_RMSNORM) return false;
     if (m.sb_dtype != JH_BF16 && (pro != PRO_NONE || epi != EPI_STORE)) return false;
     if (pro == PRO_NONE) return epi == EPI_STORE || epi == EPI_RESID || epi == EPI_RESID_NORM;
     return epi == EPI_STORE || epi == EPI_SWIGLU;

@@ -82,11 +82,12 @@ class QuantLinear:
     b_bits  uint16 [N, K/group_size]   bf16 biases
     """
 
-    def __init__(self, w: np.ndarray, s_bits: np.ndarray, b_bits: np.ndarray, group_size: int):
+    def __init__(self, w: np.ndarray, s_bits: np.ndarray, b_bits: np.ndarray, group_size: int, bits: int = 4):
         self.w = np.ascontiguousarray(w, dtype=np.uint32)
         self.s_bits = np.ascontiguousarray(s_bits, dtype=np.uint16)
         self.b_bits = np.ascontiguousarray(b_bits, dtype=np.uint16)
         self.group_size = group_size
+        self.bits = bits
 
     @property
     def out_features(self) -> int:
@@ -94,7 +95,7 @@ class QuantLinear:
 
     @property
     def in_features(self) -> int:
-        return self.w.shape[-1] * 8
+        return self.w.shape[-1] * (32 // self.bits)
 
     @property
     def s(self) -> np.ndarray:
@@ -105,19 +106,22 @@ class QuantLinear:
         return bf16_bits_to_f32(self.b_bits)
 
 
-def quant_linear(seed: int, n: int, k: int, group_size: int = 64, lead: tuple = ()) -> QuantLinear:
-    """Random 4-bit weights [*lead, n, k] with the scale/bias distributions above."""
-    if k % group_size or group_size % 8:
-        raise ValueError("in_features must be a multiple of group_size, group_size of 8")
+def quant_linear(seed: int, n: int, k: int, group_size: int = 64, lead: tuple = (), bits: int = 4) -> QuantLinear:
+    """Random `bits`-wide weights [*lead, n, k] (uniform words: uniform codes of
+    any width) with the scale/bias distributions above; the bias centres the
+    codes, -2^(bits-1) * scale."""
+    vpw = 32 // bits
+    if bits not in (2, 4, 8) or k % group_size or group_size % vpw:
+        raise ValueError("bits 2/4/8, in_features a multiple of group_size, group_size of 32/bits")
     rows = int(np.prod(lead, dtype=np.int64)) * n
     g = k // group_size
-    w = uniform_u32(stream_seed(seed, 0), rows * (k // 8)).reshape(*lead, n, k // 8)
+    w = uniform_u32(stream_seed(seed, 0), rows * (k // vpw)).reshape(*lead, n, k // vpw)
     s32 = (np.abs(normal(stream_seed(seed, 1), rows * g)) * 0.02).astype(np.float32)
     s_bits = f32_to_bf16_bits(s32)
     s = bf16_bits_to_f32(s_bits).astype(np.float64)
-    b64 = -8.0 * s + normal(stream_seed(seed, 2), rows * g) * 1e-3
+    b64 = -float(1 << (bits - 1)) * s + normal(stream_seed(seed, 2), rows * g) * 1e-3
     b_bits = f32_to_bf16_bits(b64.astype(np.float32))
-    return QuantLinear(w, s_bits.reshape(*lead, n, g), b_bits.reshape(*lead, n, g), group_size)
+    return QuantLinear(w, s_bits.reshape(*lead, n, g), b_bits.reshape(*lead, n, g), group_size, bits)
 
 
 def activations(seed: int, shape: tuple) -> tuple[np.ndarray, np.ndarray]:

@@ -210,37 +210,39 @@ def test_qk_norm_rope_append_matches_separate_ops(hip, oracle):
     assert np.array_equal(gv[:, :, pos:pos + 1], _bf16(vh))
 
 
-def _fused_case(rng, N, K, gs=64, seed=0):
-    q = synth.quant_linear(seed or N + K, N, K, gs)
+def _fused_case(rng, N, K, gs=64, seed=0, bits=4):
+    q = synth.quant_linear(seed or N + K, N, K, gs, bits=bits)
     h = (3.0 * rng.standard_normal((1, K))).astype(np.float32)
     nw = _bf16(1 + 0.1 * rng.standard_normal(K))
     return q, h, nw
 
 
-@pytest.mark.parametrize("N,K", [(6144, 4096), (70000, 4096), (4096, 12288), (300, 960)])
-def test_quant_matvec_fused_rmsnorm(hip, oracle, N, K):
+@pytest.mark.parametrize("N,K,bits", [(6144, 4096, 4), (70000, 4096, 4), (4096, 12288, 4), (300, 960, 4),
+                                      (6144, 4096, 8)])
+def test_quant_matvec_fused_rmsnorm(hip, oracle, N, K, bits):
     """RMSNorm -> QuantMatmul in one call (the norm feeding q/k/v, gate/up and
     the LM head): against the oracle's RMSNorm, bf16 rounding, QuantMatmul, and
     against the backend's own two-launch composition. (300, 960) is outside the
-    register tiles and takes the composed path."""
+    register tiles and takes the composed path, as do 8-bit weights with this
+    prologue."""
     from janis_amd import _lib
     rng = np.random.default_rng(N + K)
-    q, h, nw = _fused_case(rng, N, K)
+    q, h, nw = _fused_case(rng, N, K, bits=bits)
     w, s, b = upload_quant(hip, q)
     hd, nwd = hip.FromFloats(h), _put(hip, nw, BF16)
-    step(f"jh_quant_matvec_fused RMSNorm N={N} K={K}")
-    got = hip.Floats(hip.QuantMatvecFused(hd, w, s, b, 64, 4, _lib.JH_PRO_RMSNORM, nwd, 1e-6, out_dtype=F32))
+    step(f"jh_quant_matvec_fused RMSNorm N={N} K={K} bits={bits}")
+    got = hip.Floats(hip.QuantMatvecFused(hd, w, s, b, 64, bits, _lib.JH_PRO_RMSNORM, nwd, 1e-6, out_dtype=F32))
     xn = _bf16(oracle.rms_norm(h, nw, 1e-6))
-    want = oracle.quant_matmul(xn, q.w, q.s, q.b, 64)
+    want = oracle.quant_matmul(xn, q.w, q.s, q.b, 64, bits=bits)
     ok, dd, sc = rel_ok(got, want, 1e-2)
     assert ok, (dd, sc)
-    comp = hip.Floats(hip.QuantMatmul(hip.RMSNorm(hd, nwd, 1e-6, out_dtype=BF16), w, s, b, True, 64, 4,
+    comp = hip.Floats(hip.QuantMatmul(hip.RMSNorm(hd, nwd, 1e-6, out_dtype=BF16), w, s, b, True, 64, bits,
                                       out_dtype=F32))
     # the one-launch path rounds x*w (not x*w/rms) to bf16: a different rounding
     # of the same input, about 2^-9 / sqrt(3) of the product's spread apart
     ok, dd, sc = rel_ok(got, comp, 5e-3)
     assert ok, (dd, sc)
-    gb = hip.Floats(hip.QuantMatvecFused(hd, w, s, b, 64, 4, _lib.JH_PRO_RMSNORM, nwd, 1e-6, out_dtype=BF16))
+    gb = hip.Floats(hip.QuantMatvecFused(hd, w, s, b, 64, bits, _lib.JH_PRO_RMSNORM, nwd, 1e-6, out_dtype=BF16))
     ok, dd, sc = rel_ok(gb, want, 1e-2)
     assert ok, (dd, sc)
 
@@ -416,19 +418,21 @@ def test_rope_table(hip, oracle, dims, pos, freqs):
     assert np.array_equal(got, r)
 
 
-@pytest.mark.parametrize("N1,K1,N2", [(4096, 4096, 6144), (4096, 12288, 24576), (4096, 4096, 70000),
-                                      (960, 512, 300), (512, 1024, 512)])
-def test_split_rmsnorm_producer_consumer(hip, oracle, N1, K1, N2):
+@pytest.mark.parametrize("N1,K1,N2,bits", [(4096, 4096, 6144, 4), (4096, 12288, 24576, 4), (4096, 4096, 70000, 4),
+                                           (960, 512, 300, 4), (512, 1024, 512, 4), (4096, 4096, 6144, 8),
+                                           (2048, 4096, 12288, 8)])
+def test_split_rmsnorm_producer_consumer(hip, oracle, N1, K1, N2, bits):
     """JH_EPI_RESID_NORM then JH_PRO_NORMED: h = resid + x.W1^T (fp32, in place),
     u = bf16(h * w) written by the producer with per-block sums of h^2, and the
     consumer's (u.W2^T) / rms(h) equals RMSNorm(h, w) -> QuantMatmul(W2) within the
     bf16 rounding of the product's input. With N2 = 24576 the consumer also
     takes the SwiGLU epilogue. (960, 512, 300) is outside the register tiles
-    (composed launches)."""
+    (composed launches). bits = 8: the 8-bit tiles with both fusions (and the
+    SwiGLU epilogue at N2 = 12288)."""
     from janis_amd import _lib
     rng = np.random.default_rng(N1 + K1 + N2)
-    q1 = synth.quant_linear(N1 + 5, N1, K1, 64)
-    q2 = synth.quant_linear(N2 + 9, N2, N1, 64)
+    q1 = synth.quant_linear(N1 + 5, N1, K1, 64, bits=bits)
+    q2 = synth.quant_linear(N2 + 9, N2, N1, 64, bits=bits)
     w1, s1, b1 = upload_quant(hip, q1)
     w2, s2, b2 = upload_quant(hip, q2)
     x = _bf16(rng.standard_normal((1, K1)))
@@ -436,23 +440,23 @@ def test_split_rmsnorm_producer_consumer(hip, oracle, N1, K1, N2):
     nw = _bf16(1 + 0.1 * rng.standard_normal(N1))
     h_d, u_d = hip.FromFloats(resid), hip.empty(BF16, 1, N1)
     st = hip.empty(F32, _lib.JH_NORM_STATS)
-    step(f"split RMSNorm producer N={N1} K={K1}")
-    hip.QuantMatvecFused(_put(hip, x, BF16), w1, s1, b1, 64, 4, norm=_put(hip, nw, BF16),
+    step(f"split RMSNorm producer N={N1} K={K1} bits={bits}")
+    hip.QuantMatvecFused(_put(hip, x, BF16), w1, s1, b1, 64, bits, norm=_put(hip, nw, BF16),
                          epilogue=_lib.JH_EPI_RESID_NORM, resid=h_d, out=h_d, stats=st, norm_out=u_d)
     h = hip.Floats(h_d)
-    want_h = resid + oracle.quant_matmul(x, q1.w, q1.s, q1.b, 64)
+    want_h = resid + oracle.quant_matmul(x, q1.w, q1.s, q1.b, 64, bits=bits)
     ok, dd, sc = rel_ok(h, want_h, 1e-3)
     assert ok, (dd, sc)
     assert np.array_equal(hip.Floats(u_d), _bf16(h * nw))  # exactly bf16(h * w) of the stored h
     stats = hip.Floats(st)
     assert abs(float(stats.astype(np.float64).sum()) - float((h.astype(np.float64) ** 2).sum())) <= \
         1e-5 * float((h.astype(np.float64) ** 2).sum())
-    swiglu = N2 == 24576
-    step(f"split RMSNorm consumer N={N2} swiglu={swiglu}")
-    got = hip.Floats(hip.QuantMatvecFused(u_d, w2, s2, b2, 64, 4, _lib.JH_PRO_NORMED, eps=1e-6, stats=st,
+    swiglu = N2 in (24576, 12288)
+    step(f"split RMSNorm consumer N={N2} swiglu={swiglu} bits={bits}")
+    got = hip.Floats(hip.QuantMatvecFused(u_d, w2, s2, b2, 64, bits, _lib.JH_PRO_NORMED, eps=1e-6, stats=st,
                                           epilogue=_lib.JH_EPI_SWIGLU if swiglu else _lib.JH_EPI_STORE,
                                           out_dtype=F32))
-    y = oracle.quant_matmul(_bf16(oracle.rms_norm(h, nw, 1e-6)), q2.w, q2.s, q2.b, 64)[0]
+    y = oracle.quant_matmul(_bf16(oracle.rms_norm(h, nw, 1e-6)), q2.w, q2.s, q2.b, 64, bits=bits)[0]
     if swiglu:
         y = oracle.silu(y[:N2 // 2]) * y[N2 // 2:]
     ok, dd, sc = rel_ok(got[0], y, 1e-2)

@@ -552,6 +552,32 @@ def test_quant_matmul_other_widths(hip, oracle, bits, rows):
     assert ok, ("bf16 y", d, sc)
 
 
+@pytest.mark.parametrize("K,gs,sb", [(128, 32, BF16), (256, 64, BF16), (384, 128, "f16"), (512, 32, BF16),
+                                     (768, 64, BF16), (1024, 128, BF16), (1536, 64, "f16"), (2048, 64, BF16),
+                                     (3072, 32, BF16), (4096, 64, BF16), (6144, 128, BF16), (8192, 64, "f16"),
+                                     (12288, 64, BF16)])
+def test_quant_matvec_8bit_tiles(hip, oracle, K, gs, sb):
+    """The 8-bit register tiles (each code as two nibbles against (x, 16x), the
+    4-bit word dots): every row length of the tile table (P = K/4 words), groups
+    of 32/64/128, bf16 and f16 scales, a ragged row count, fp32 and bf16 y."""
+    N = 517
+    q = synth.quant_linear(K + gs, N, K, gs, bits=8)
+    w, s, b = upload_quant(hip, q)
+    sc_, bi_ = q.s, q.b
+    if sb == "f16":
+        sc_, bi_ = (a.astype(np.float16).astype(np.float32) for a in (q.s, q.b))
+        s, b = hip.FromRaw(F16, sc_.astype(np.float16), *q.s.shape), hip.FromRaw(F16, bi_.astype(np.float16), *q.b.shape)
+    xb, x = synth.activations(K + 3, (1, K))
+    step(f"jh_quant_matmul 8-bit tile K={K} gs={gs} scales={sb}")
+    y = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, 1, K), w, s, b, True, gs, 8, out_dtype=F32))
+    want = oracle.quant_matmul(x, q.w, sc_, bi_, gs, bits=8)
+    ok, d, sc = rel_ok(y, want, F32_TOL)
+    assert ok, (d, sc)
+    yb = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, 1, K), w, s, b, True, gs, 8))
+    ok, d, sc = rel_ok(yb, want, BF16_TOL)
+    assert ok, ("bf16 y", d, sc)
+
+
 def test_gather_8bit(hip, oracle):
     E, N, K, gs, T, Kk = 5, 64, 512, 64, 3, 4
     w, s, b = _width_case(8, N, K, gs, E=E, seed=99)
