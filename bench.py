@@ -338,8 +338,8 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
         ms = time_graph(g, 10, 3) / nl
         byt = U * per_expert + 2 * T * H + 2 * 2 * T * K * I + 4 * T * H
         moe[f"T{T}_swiglu"] = {"unique_experts": U, "us_per_layer": round(ms * 1e3, 2),
-                               "GB_s": round(byt / (ms * 1e-3) / 1e9, 1), "launches_per_layer": 3,
-                               "note": "jh_moe_swiglu: out clear + gate/up SwiGLU + down combine"}
+                               "GB_s": round(byt / (ms * 1e-3) / 1e9, 1), "launches_per_layer": 2,
+                               "note": "jh_moe_swiglu: gate/up SwiGLU (clearing out) + down combine"}
         del g
     res["moe_gather"] = moe
     log("moe:", moe)

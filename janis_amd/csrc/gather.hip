@@ -188,6 +188,11 @@ struct MoeArgs {
     int n_pairs;
     int64_t E, k_slots, a_vectors;
     const float* scores;   // COMBINE: [n_lead, k_slots]
+    // SWIGLU of jh_moe_swiglu: the combine's fp32 output [n_lead, init_h] is
+    // cleared here (NaN rows for a token with an index outside [0, E)), so the
+    // combine launch that follows can add into it with no launch of its own
+    float* init_out = nullptr;
+    int64_t init_n = 0, init_h = 1;
 };
 
 // Expert-slot GEMV (see the file comment). LPR lanes per row, each lane ITERS
@@ -208,6 +213,21 @@ __global__ __launch_bounds__(256) void moe_qmv_kernel(MoeArgs a) {
     __shared__ uint32_t pres[FUSED ? kMaxExperts / 32 : 1];
     __shared__ int np_s, sel_s;
     __shared__ float red[KSPLIT > 1 ? (KSPLIT - 1) * NSTK * ROWS_PER_BLOCK : 1];
+
+    if constexpr (EPI == EPI_SWIGLU) {
+        if (a.init_out) {  // before any block returns: the whole grid shares the clearing
+            const int64_t nb = (int64_t)gridDim.x * gridDim.y, b = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+            for (int64_t i = b * blockDim.x + threadIdx.x; i < a.init_n; i += nb * blockDim.x) {
+                const int64_t t = i / a.init_h;
+                bool bad = false;
+                for (int64_t k = 0; k < a.k_slots; k++) {
+                    const int32_t ei = a.idx[t * a.k_slots + k];
+                    bad |= ei < 0 || ei >= a.E;
+                }
+                a.init_out[i] = bad ? __uint_as_float(0x7fc00000u) : 0.0f;
+            }
+        }
+    }
 
     int64_t e;
     int p_begin, p_end;
@@ -621,9 +641,10 @@ Status launch_moe_mlp(const MoeMlpArgs& a, void* workspace, hipStream_t st) {
 
     const int64_t n_out = a.n_tok * H;
     const unsigned init_blocks = (unsigned)std::min<int64_t>((n_out + 255) / 256, 4096);
-    hipLaunchKernelGGL(moe_init_out_kernel, dim3(init_blocks), dim3(256), 0, st, acc, a.n_tok, H, a.idx,
-                       a.k_slots, a.n_experts);
-    if (n_pairs > 0) {  // with no slots, out is the empty sum
+    if (n_pairs == 0)  // out is the empty sum; otherwise the gate/up launch clears it
+        hipLaunchKernelGGL(moe_init_out_kernel, dim3(init_blocks), dim3(256), 0, st, acc, a.n_tok, H, a.idx,
+                           a.k_slots, a.n_experts);
+    if (n_pairs > 0) {
         if (!fused)
             hipLaunchKernelGGL(moe_bucket_kernel, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.n_experts, buckets,
                                static_cast<void*>(nullptr), (int)JH_BF16, (int64_t)0);
@@ -641,6 +662,9 @@ Status launch_moe_mlp(const MoeMlpArgs& a, void* workspace, hipStream_t st) {
         g.E = a.n_experts;
         g.k_slots = a.k_slots;
         g.a_vectors = 1;
+        g.init_out = acc;
+        g.init_n = n_out;
+        g.init_h = H;
         if (!run_fast<EPI_SWIGLU>(g, a.gate.in / 8, f16, fused, max_u, st))
             return Status::fail(JH_ERR_UNSUPPORTED, "moe_swiglu: no tile for the gate/up shape");
 

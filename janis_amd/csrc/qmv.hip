@@ -432,7 +432,10 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
             } else if constexpr (EPI == EPI_SWIGLU) {
                 float act[RO];
 #pragma unroll
-                for (int r = 0; r < RO; r++) act[r] = part[r] / (1.0f + (float)exp((double)(-part[r]))) * part[RO + r];
+                // SiLU with the hardware exp (v_exp_f32, a few ulp, far inside the
+                // product's tolerance): a double exp's dependent chain held the
+                // storing lanes up longer than the rest of the epilogue
+                for (int r = 0; r < RO; r++) act[r] = part[r] / (1.0f + __expf(-part[r])) * part[RO + r];
                 store_rows<RO>(Y, y_dt, row0, N, act);
             } else {
                 store_rows<RPW>(Y, y_dt, row0, N, part);
