@@ -318,8 +318,9 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
         ms = time_graph(g, 10, 3) / nl
         per_expert = 3 * (I * H // 2 + 4 * I * (H // GS))  # packed codes + scales/biases of one expert
         byt = U * per_expert + 2 * T * H + 2 * T * K * (2 * I + H) + 2 * T * K * I
+        bucketing = T * K > 32  # past 32 pairs each call buckets in a launch of its own
         moe[f"T{T}"] = {"unique_experts": U, "us_per_layer": round(ms * 1e3, 2),
-                        "GB_s": round(byt / (ms * 1e-3) / 1e9, 1), "launches_per_layer": 3}
+                        "GB_s": round(byt / (ms * 1e-3) / 1e9, 1), "launches_per_layer": 6 if bucketing else 3}
         del g
 
         # the whole expert MLP (gate+up SwiGLU, down with the score-weighted sum)
@@ -338,8 +339,8 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
         ms = time_graph(g, 10, 3) / nl
         byt = U * per_expert + 2 * T * H + 2 * 2 * T * K * I + 4 * T * H
         moe[f"T{T}_swiglu"] = {"unique_experts": U, "us_per_layer": round(ms * 1e3, 2),
-                               "GB_s": round(byt / (ms * 1e-3) / 1e9, 1), "launches_per_layer": 2,
-                               "note": "jh_moe_swiglu: gate/up SwiGLU (clearing out) + down combine"}
+                               "GB_s": round(byt / (ms * 1e-3) / 1e9, 1), "launches_per_layer": 3 if bucketing else 2,
+                               "note": "jh_moe_swiglu: [bucketing] + gate/up SwiGLU (clearing out) + down combine"}
         del g
     res["moe_gather"] = moe
     log("moe:", moe)

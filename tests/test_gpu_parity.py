@@ -314,6 +314,15 @@ def test_gather_out_of_range_index(hip):
             hip.GatherQuantMatmul(hip.FromBF16Bits(xb, 1, 1, 1, 512), w, s, b, idx, True, 64, 4)
     finally:
         hip.SetChecks(False)
+    # past 32 pairs the buckets come from the bucketing launch: same NaN rows
+    ids = np.random.default_rng(3).integers(0, 4, (10, 4)).astype(np.int32)
+    ids[2, 1], ids[7, 3] = 4, -5
+    xb10, _ = synth.activations(4, (10, 1, 1, 512))
+    step("jh_gather_quant_matmul bad index, 40 pairs")
+    y = hip.Floats(hip.GatherQuantMatmul(hip.FromBF16Bits(xb10, 10, 1, 1, 512), w, s, b, hip.FromInt32(ids),
+                                         True, 64, 4, out_dtype=F32))
+    bad = (ids < 0) | (ids >= 4)
+    assert np.isnan(y[bad]).all() and np.isfinite(y[~bad]).all()
 
 
 # -- MoE expert MLP (moeApply as one operator) ----------------------------------------
@@ -393,7 +402,7 @@ def test_moe_swiglu_matches_gather_composition(hip):
     assert ok, (dd, s)
 
 
-def test_moe_swiglu_out_of_range_and_unsupported(hip):
+def test_moe_swiglu_out_of_range_and_unsupported(hip, oracle):
     E, H, I = 4, 512, 256
     qs = [synth.quant_linear(700 + i, *(I, H) if i < 2 else (H, I), lead=(E,)) for i in range(3)]
     st = _moe_upload(hip, qs)
@@ -411,6 +420,20 @@ def test_moe_swiglu_out_of_range_and_unsupported(hip):
             hip.MoeSwiGLU(x, *st, idx, sc, 64, 4)
     finally:
         hip.SetChecks(False)
+    # past 32 pairs the buckets come from the bucketing launch: same NaN row, and
+    # the other tokens as the oracle has them
+    ids = np.random.default_rng(5).integers(0, E, (9, 4)).astype(np.int32)
+    ids[6, 2] = E
+    scn = np.random.default_rng(6).random((9, 4)).astype(np.float32)
+    step("jh_moe_swiglu bad index, 36 pairs")
+    xb9, x9 = synth.activations(702, (9, H))
+    got = hip.Floats(hip.MoeSwiGLU(hip.FromBF16Bits(xb9, 9, H), *st, hip.FromInt32(ids), hip.FromFloats(scn), 64, 4,
+                                   out_dtype=F32))
+    assert np.isnan(got[6]).all()
+    good = [t for t in range(9) if t != 6]
+    want = oracle.moe_apply(x9[good], *[(q.w, q.s, q.b) for q in qs], ids[good], scn[good])
+    ok, d, sc_ = rel_ok(got[good], want, BF16_TOL)  # h is bf16 between the launches
+    assert ok, (d, sc_)
     step("jh_moe_swiglu no slots -> zeros")
     z = hip.Floats(hip.MoeSwiGLU(x, *st, hip.FromInt32(np.zeros((2, 0), np.int32)),
                                  hip.FromFloats(np.zeros((2, 0), np.float32)), 64, 4))
