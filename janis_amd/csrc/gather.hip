@@ -40,7 +40,6 @@ __global__ __launch_bounds__(256) void qmv_generic_kernel(
 
 namespace {
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 constexpr int kMaxExperts = 4096;
 // Up to this many pairs every product block buckets the indices itself; beyond
 // it one bucketing launch serves the call (and both products of jh_moe_swiglu):
@@ -167,43 +166,6 @@ __device__ int bucket_in_block(const int32_t* __restrict__ idx, int n_pairs, int
             if (sidx[p] == e) plist[atomicAdd(np, 1)] = p;
     __syncthreads();
     return e;
-}
-
-constexpr uint32_t kBf16Bytes = 0x43434343u;  // 0x43 = high byte of bf16(128.0)
-constexpr uint32_t kSelB0B2 = 0x04020400u;
-constexpr uint32_t kSelB1B3 = 0x04030401u;
-constexpr float kCodeOffset = 128.0f;
-
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                           __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
-// acc + sum_l (128 + q_l) * x_l over the 8 codes of `word`, with
-// xp[p] = (x_p, x_{p+4}) as bf16 pairs (see pair_up). v_perm_b32 places code
-// bytes under the high byte 0x43, giving bf16 128 + q exactly.
-__device__ __forceinline__ float word_dot(uint32_t word, const uint32_t* xp, float acc) {
-    const uint32_t lo = word & 0x0F0F0F0Fu;
-    const uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB0B2), xp[0], acc);
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB0B2), xp[1], acc);
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB1B3), xp[2], acc);
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB1B3), xp[3], acc);
-    return acc;
-}
-
-// The 8 bf16 inputs (x0,x1) (x2,x3) (x4,x5) (x6,x7) of one word regrouped as
-// (x0,x4) (x1,x5) (x2,x6) (x3,x7); returns their fp32 sum.
-__device__ __forceinline__ float pair_up(uint4 v, uint32_t* xp) {
-    xp[0] = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
-    xp[1] = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
-    xp[2] = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
-    xp[3] = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
-    const float a = __uint_as_float(v.x << 16) + __uint_as_float(v.x & 0xFFFF0000u);
-    const float b = __uint_as_float(v.y << 16) + __uint_as_float(v.y & 0xFFFF0000u);
-    const float c = __uint_as_float(v.z << 16) + __uint_as_float(v.z & 0xFFFF0000u);
-    const float d = __uint_as_float(v.w << 16) + __uint_as_float(v.w & 0xFFFF0000u);
-    return (a + b) + (c + d);
 }
 
 // SiLU as the reference defines it (cpu/cpu.go:327-329): v / (1 + exp(-v)).

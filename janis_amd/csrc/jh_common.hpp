@@ -131,6 +131,54 @@ __device__ __forceinline__ float rows4_max(float v) { return pair32<true>(pair16
 __device__ __forceinline__ float wave_sum(float v) { return rows4_sum(row16_reduce<false>(v)); }
 __device__ __forceinline__ float wave_max(float v) { return rows4_max(row16_reduce<true>(v)); }
 
+// ---- 4-bit word dot products ------------------------------------------------------
+// Codes become bf16 without conversion instructions: a code q in the low 4
+// mantissa bits of bf16(128.0) = 0x4300 is exactly 128 + q. Two masks split a
+// word into its even and odd codes (one per byte) and v_perm_b32 builds the bf16
+// pairs (128 + q_p, 128 + q_{p+4}); v_dot2_f32_bf16 multiplies them with the
+// input pairs (x_p, x_{p+4}) and accumulates in fp32. The 128 is removed per
+// group through the input sum:
+//   scale*sum(x*(128+q)) + (bias - 128*scale)*sum(x) = scale*sum(x*q) + bias*sum(x).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+constexpr uint32_t kBf16Bytes = 0x43434343u;  // 0x43 = high byte of bf16(128.0)
+// v_perm_b32 selectors over {src0 = kBf16Bytes (bytes 4..7), src1 = codes (bytes 0..3)}:
+// result bytes (low to high) = code byte 0, 0x43, code byte 2, 0x43  /  byte 1, 0x43, byte 3, 0x43
+constexpr uint32_t kSelB0B2 = 0x04020400u;
+constexpr uint32_t kSelB1B3 = 0x04030401u;
+constexpr float kCodeOffset = 128.0f;
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// acc + sum_l (128 + q_l) * x_l over the 8 codes of `word`; xp[p] = (x_p, x_{p+4}).
+// lo = word & 0x0F0F0F0F holds codes 0,2,4,6 one per byte, hi = (word >> 4) &
+// 0x0F0F0F0F codes 1,3,5,7: 7 integer ops and 4 dot2 per word.
+__device__ __forceinline__ float word_dot(uint32_t word, const uint32_t* xp, float acc) {
+    const uint32_t lo = word & 0x0F0F0F0Fu;
+    const uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB0B2), xp[0], acc);  // (q0, q4)
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB0B2), xp[1], acc);  // (q1, q5)
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB1B3), xp[2], acc);  // (q2, q6)
+    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB1B3), xp[3], acc);  // (q3, q7)
+    return acc;
+}
+
+// The 8 bf16 inputs (x0,x1) (x2,x3) (x4,x5) (x6,x7) of one word regrouped as
+// (x0,x4) (x1,x5) (x2,x6) (x3,x7); returns their fp32 sum.
+__device__ __forceinline__ float pair_up(uint4 v, uint32_t* xp) {
+    xp[0] = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+    xp[1] = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+    xp[2] = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+    xp[3] = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+    const float a = __uint_as_float(v.x << 16) + __uint_as_float(v.x & 0xFFFF0000u);
+    const float b = __uint_as_float(v.y << 16) + __uint_as_float(v.y & 0xFFFF0000u);
+    const float c = __uint_as_float(v.z << 16) + __uint_as_float(v.z & 0xFFFF0000u);
+    const float d = __uint_as_float(v.w << 16) + __uint_as_float(v.w & 0xFFFF0000u);
+    return (a + b) + (c + d);
+}
+
 // Load element i of a scale/bias array of the given dtype as fp32 (exact).
 __device__ __forceinline__ float load_sb(const void* p, int64_t i, int dt) {
     if (dt == JH_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);

@@ -59,7 +59,6 @@ __device__ __forceinline__ float widen_sb(uint32_t bits) {
         return bf16_to_f32((uint16_t)bits);
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 // One packed word -> 8 bf16 weights fl32(q*s + b) rounded to nearest even, in

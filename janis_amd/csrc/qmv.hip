@@ -26,49 +26,6 @@
 namespace jh {
 namespace {
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-constexpr uint32_t kBf16Bytes = 0x43434343u;  // 0x43 = high byte of bf16(128.0)
-// v_perm_b32 selectors over {src0 = kBf16Bytes (bytes 4..7), src1 = codes (bytes 0..3)}:
-// result bytes (low to high) = code byte 0, 0x43, code byte 2, 0x43  /  byte 1, 0x43, byte 3, 0x43
-constexpr uint32_t kSelB0B2 = 0x04020400u;
-constexpr uint32_t kSelB1B3 = 0x04030401u;
-constexpr float kCodeOffset = 128.0f;
-
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                           __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
-// acc + sum_l (128 + q_l) * x_l over the 8 codes of `word`; xp[p] = (x_p, x_{p+4}).
-// lo = word & 0x0F0F0F0F holds codes 0,2,4,6 one per byte, hi = (word >> 4) &
-// 0x0F0F0F0F codes 1,3,5,7; v_perm_b32 then builds each bf16 pair by taking two
-// code bytes and filling the high byte of each half with 0x43 from kBf16Bytes:
-// 7 integer ops and 4 dot2 per word.
-__device__ __forceinline__ float word_dot(uint32_t word, const uint32_t* xp, float acc) {
-    const uint32_t lo = word & 0x0F0F0F0Fu;
-    const uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB0B2), xp[0], acc);  // (q0, q4)
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB0B2), xp[1], acc);  // (q1, q5)
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, lo, kSelB1B3), xp[2], acc);  // (q2, q6)
-    acc = dot2_bf16(__builtin_amdgcn_perm(kBf16Bytes, hi, kSelB1B3), xp[3], acc);  // (q3, q7)
-    return acc;
-}
-
-// The 8 bf16 inputs of one word, (x0..x7) in 4 dwords, regrouped as the pairs
-// (x0,x4) (x1,x5) (x2,x6) (x3,x7); returns their fp32 sum.
-__device__ __forceinline__ float pair_up(uint4 v, uint32_t* xp) {
-    xp[0] = (v.x & 0xFFFFu) | (v.z << 16);
-    xp[1] = (v.x >> 16) | (v.z & 0xFFFF0000u);
-    xp[2] = (v.y & 0xFFFFu) | (v.w << 16);
-    xp[3] = (v.y >> 16) | (v.w & 0xFFFF0000u);
-    const float a = __uint_as_float(v.x << 16) + __uint_as_float(v.x & 0xFFFF0000u);
-    const float b = __uint_as_float(v.y << 16) + __uint_as_float(v.y & 0xFFFF0000u);
-    const float c = __uint_as_float(v.z << 16) + __uint_as_float(v.z & 0xFFFF0000u);
-    const float d = __uint_as_float(v.w << 16) + __uint_as_float(v.w & 0xFFFF0000u);
-    return (a + b) + (c + d);
-}
-
 // The slice sums of RPW values at once: each DPP step is applied to all RPW
 // values before the next, so the DPP read-after-write waits are filled with
 // useful work. Totals land in the last lane of each slice (see slice_sum_last).
