@@ -447,6 +447,103 @@ def test_moe_swiglu_out_of_range_and_unsupported(hip, oracle):
         hip.MoeSwiGLU(hip.FromBF16Bits(xb6, 2, 640), *_moe_upload(hip, q6), idx, sc, 64, 4)
 
 
+# -- MoE expert MLP, one decode token ----------------------------------------------------
+
+def _t1_stacks(hip):
+    qs = [_qwen3_moe_stack(p) for p in ("gate", "up", "down")]
+    if "_dev" not in _STACKS:
+        _STACKS["_dev"] = _moe_upload(hip, qs)
+    return qs, _STACKS["_dev"]
+
+
+def _t1_call(hip, st, xb, idx, sc, out_dtype=F32):
+    return hip.Floats(hip.MoeSwiGLU(hip.FromBF16Bits(xb, 1, 2048), *st, hip.FromInt32(idx), hip.FromFloats(sc),
+                                    64, 4, out_dtype=out_dtype))
+
+
+@pytest.mark.parametrize("k,out_dtype,collide", [(8, F32, True), (2, F32, False), (5, BF16, False),
+                                                 (8, BF16, True)])
+def test_moe_swiglu_one_token(hip, oracle, k, out_dtype, collide):
+    """A decode token at the Qwen3-30B-A3B expert shapes: fewer slots than 8, a
+    repeated expert, bf16 output, against the oracle's moeApply
+    (qwen/moe.go:501-511)."""
+    qs, st = _t1_stacks(hip)
+    rng = np.random.default_rng(9400 + k)
+    idx = rng.choice(128, k, replace=False).astype(np.int32)[None, :]
+    if collide:
+        idx[0, 1] = idx[0, 0]
+        idx[0, k - 1] = idx[0, 0]
+    sc = rng.random((1, k)).astype(np.float32)
+    xb, x = synth.activations(9401 + k, (1, 2048))
+    step(f"jh_moe_swiglu one token k={k} out={out_dtype} collide={collide}")
+    got = _t1_call(hip, st, xb, idx, sc, out_dtype)
+    want = oracle.moe_apply(x, *[(q.w, q.s, q.b) for q in qs], idx, sc)
+    ok, d, s_ = rel_ok(got, want, BF16_TOL)
+    assert ok, (d, s_)
+
+
+def test_moe_swiglu_one_token_graph_replays(hip, oracle):
+    """Captured once into a HIP graph and replayed on new tokens and routes
+    (written into the captured buffers between replays): every replay matches
+    the oracle on its inputs, so no replay reuses an earlier call's state."""
+    import ctypes
+    import subprocess
+
+    from janis_amd import _lib as jl
+
+    out = subprocess.run(["ldd", jl.LIB_PATH], capture_output=True, text=True).stdout
+    rt = ctypes.CDLL(next(ln.split("=>")[1].split()[0] for ln in out.splitlines() if "libamdhip64" in ln))
+    for name in ("hipStreamCreate", "hipStreamSynchronize", "hipStreamBeginCapture", "hipStreamEndCapture",
+                 "hipGraphInstantiate", "hipGraphLaunch", "hipGraphExecDestroy", "hipGraphDestroy",
+                 "hipStreamDestroy"):
+        getattr(rt, name).restype = ctypes.c_int
+    qs, st = _t1_stacks(hip)
+    xt, it, sct = hip.empty(BF16, 1, 2048), hip.empty(I32, 1, 8), hip.empty(F32, 1, 8)
+    outt = hip.empty(F32, 1, 2048)
+
+    def put(t, a):
+        a = np.ascontiguousarray(a)
+        hip.Sync()
+        hip._L.jh_h2d(hip._ctx, ctypes.c_void_p(t.ptr), a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
+        hip.Sync()
+
+    cases = []
+    for i in range(3):
+        idx, sc = synth.route(9800 + i, 1, 128, 8)
+        xb, x = synth.activations(9810 + i, (1, 2048))
+        cases.append((xb, x, idx, sc, oracle.moe_apply(x, *[(q.w, q.s, q.b) for q in qs], idx, sc)))
+
+    def load(i):
+        xb, _, idx, sc, _ = cases[i]
+        put(xt, xb), put(it, idx.astype(np.int32)), put(sct, sc.astype(np.float32))
+
+    load(0)
+    hip.MoeSwiGLU(xt, *st, it, sct, 64, 4, out=outt)  # warm outside the capture
+    stream, graph, exe = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    assert rt.hipStreamCreate(ctypes.byref(stream)) == 0
+    try:
+        hip.SetStream(stream.value)
+        step("capture jh_moe_swiglu (one token)")
+        assert rt.hipStreamBeginCapture(stream, 0) == 0
+        hip.MoeSwiGLU(xt, *st, it, sct, 64, 4, out=outt)
+        assert rt.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+        assert rt.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for rep, i in enumerate((1, 2, 0, 1, 1)):
+            step(f"graph replay {rep} on case {i}")
+            load(i)
+            assert rt.hipGraphLaunch(exe, stream) == 0
+            assert rt.hipStreamSynchronize(stream) == 0
+            ok, d, s_ = rel_ok(hip.Floats(outt), cases[i][4], BF16_TOL)
+            assert ok, (rep, d, s_)
+    finally:
+        hip.SetStream(None)
+        if exe.value:
+            rt.hipGraphExecDestroy(exe)
+        if graph.value:
+            rt.hipGraphDestroy(graph)
+        rt.hipStreamDestroy(stream)
+
+
 # -- MoE router on the device ------------------------------------------------------------
 
 def _route_oracle(oracle, logits, k, norm):
