@@ -717,7 +717,7 @@ class HipBackend:
     def AttentionDecode(self, qkv: Tensor, n_heads: int, n_kv_heads: int, q_norm: Tensor | None,
                         k_norm: Tensor | None, eps: float, base: float, rope_scale: float, pos: int,
                         k_cache: Tensor, v_cache: Tensor, scale: float, out_dtype: int | None = None,
-                        rope_cs: Tensor | None = None) -> Tensor:
+                        rope_cs: Tensor | None = None, out: Tensor | None = None) -> Tensor:
         """Attention.ForwardCached for one token after the q/k/v product
         (qwen/attention.go:98-128) in one launch: q/k RMSNorm (when the weights
         are given), RoPE at pos, the KV append at row pos, and SDPA over keys
@@ -734,7 +734,10 @@ class HipBackend:
         k_norm = self._c(k_norm) if k_norm is not None else None
         Dh = 128
         cap = k_cache.shape[-2]
-        out = self.empty(out_dtype if out_dtype is not None else qkv.dtype, 1, n_heads * Dh)
+        if out is None:
+            out = self.empty(out_dtype if out_dtype is not None else qkv.dtype, 1, n_heads * Dh)
+        elif out.numel != n_heads * Dh or out.dtype not in (F32, BF16):
+            raise JanisHipError(_lib.JH_ERR_INVALID, "AttentionDecode: out must be F32/BF16 [1, Hq*128]")
         wd = q_norm.dtype if q_norm is not None else (k_norm.dtype if k_norm is not None else BF16)
         check(self._ctx, self._L.jh_attention_decode(
             self._ctx, qkv.ptr, qkv.dtype, n_heads, n_kv_heads, Dh, q_norm.ptr if q_norm is not None else None,

@@ -403,6 +403,95 @@ def test_attention_decode_consecutive_tokens(hip, oracle):
         hip.AttentionDecode(hip.FromFloats(qkv), Hq, Hk, None, None, 1e-6, 1e6, 1.0, cap, kc, vc, scale)
 
 
+def test_attention_decode_consecutive_short_cache(hip, oracle):
+    """Tokens in a row through a short cache (positions 500 to 503), where the
+    launch merges its own splits: every token sees the rows the previous ones
+    appended and none reads an earlier call's partials."""
+    rng = np.random.default_rng(98)
+    Hq, Hk, Dh, cap, pos0 = 32, 8, 128, 600, 500
+    scale = Dh ** -0.5
+    _, qn, kn, k_old, v_old = _attention_case(rng, Hq, Hk, cap, pos0, True)
+    kc, vc = _put(hip, k_old, BF16), _put(hip, v_old, BF16)
+    kh, vh = k_old.copy(), v_old.copy()
+    qnd, knd = _put(hip, qn, BF16), _put(hip, kn, BF16)
+    for t in range(4):
+        pos = pos0 + t
+        qkv = rng.standard_normal((1, (Hq + 2 * Hk) * Dh)).astype(np.float32)
+        step(f"jh_attention_decode short cache, token {t} pos={pos}")
+        got = hip.Floats(hip.AttentionDecode(hip.FromFloats(qkv), Hq, Hk, qnd, knd, 1e-6, 1e6, 1.0, pos, kc, vc, scale,
+                                             out_dtype=F32))
+        want, kh, vh = _attention_oracle(oracle, qkv, qn, kn, kh, vh, Hq, Hk, pos, scale)
+        ok, dd, sc = rel_ok(got, want, 1e-3)
+        assert ok, (t, dd, sc)
+
+
+def test_attention_decode_graph_replays(hip, oracle):
+    """A short-cache attention captured into a HIP graph and replayed on new
+    q/k/v rows: every replay matches the eager call on the same inputs bit for
+    bit (the merge's call tags come from device state, not from captured
+    arguments) and the oracle within 1e-3."""
+    import ctypes
+    import subprocess
+
+    from janis_amd import _lib as jl
+
+    out = subprocess.run(["ldd", jl.LIB_PATH], capture_output=True, text=True).stdout
+    rt = ctypes.CDLL(next(ln.split("=>")[1].split()[0] for ln in out.splitlines() if "libamdhip64" in ln))
+    for name in ("hipStreamCreate", "hipStreamSynchronize", "hipStreamBeginCapture", "hipStreamEndCapture",
+                 "hipGraphInstantiate", "hipGraphLaunch", "hipGraphExecDestroy", "hipGraphDestroy",
+                 "hipStreamDestroy"):
+        getattr(rt, name).restype = ctypes.c_int
+    rng = np.random.default_rng(97)
+    Hq, Hk, Dh, cap, pos = 32, 8, 128, 300, 255
+    scale = Dh ** -0.5
+    _, qn, kn, k_old, v_old = _attention_case(rng, Hq, Hk, cap, pos, True)
+    kc, vc = _put(hip, k_old, BF16), _put(hip, v_old, BF16)
+    qnd, knd = _put(hip, qn, BF16), _put(hip, kn, BF16)
+    qkvs = [rng.standard_normal((1, (Hq + 2 * Hk) * Dh)).astype(np.float32) for _ in range(3)]
+    xt = hip.empty(F32, 1, (Hq + 2 * Hk) * Dh)
+    ot = hip.empty(F32, 1, Hq * Dh)
+
+    def put(a):
+        hip.Sync()
+        hip._L.jh_h2d(hip._ctx, ctypes.c_void_p(xt.ptr), a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
+        hip.Sync()
+
+    def call():
+        return hip.AttentionDecode(xt, Hq, Hk, qnd, knd, 1e-6, 1e6, 1.0, pos, kc, vc, scale, out=ot)
+
+    eager = []
+    for a in qkvs:
+        put(a)
+        call()
+        eager.append(hip.Floats(ot).copy())
+    stream, graph, exe = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    assert rt.hipStreamCreate(ctypes.byref(stream)) == 0
+    try:
+        hip.SetStream(stream.value)
+        step("capture jh_attention_decode pos=255")
+        assert rt.hipStreamBeginCapture(stream, 0) == 0
+        call()
+        assert rt.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+        assert rt.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for rep, i in enumerate((1, 2, 0, 1, 1)):
+            step(f"graph replay {rep} on q/k/v {i}")
+            put(qkvs[i])
+            assert rt.hipGraphLaunch(exe, stream) == 0
+            assert rt.hipStreamSynchronize(stream) == 0
+            got = hip.Floats(ot)
+            assert np.array_equal(got.view(np.uint32), eager[i].view(np.uint32)), rep
+            want, _, _ = _attention_oracle(oracle, qkvs[i], qn, kn, k_old, v_old, Hq, Hk, pos, scale)
+            ok, dd, sc = rel_ok(got, want, 1e-3)
+            assert ok, (rep, dd, sc)
+    finally:
+        hip.SetStream(None)
+        if exe.value:
+            rt.hipGraphExecDestroy(exe)
+        if graph.value:
+            rt.hipGraphDestroy(graph)
+        rt.hipStreamDestroy(stream)
+
+
 @pytest.mark.parametrize("dims,pos,freqs", [(128, 0, False), (128, 8191, False), (64, 77, True)])
 def test_rope_table(hip, oracle, dims, pos, freqs):
     """jh_rope_table: the oracle's RoPE applied to (1, 0) pairs gives exactly
