@@ -371,7 +371,8 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_wreg_kernel(
     uint32_t k_per_split, float* __restrict__ acc_out) {
     constexpr int NTH = 64 * NW;
     constexpr int RBN = 32 * WNF * NW;
-    constexpr int XCH = RBM * 8 / NTH;  // 16-byte X chunks per thread per step
+    constexpr int XCH = (RBM * 8 + NTH - 1) / NTH;  // 16-byte X chunks per thread per step
+    constexpr bool XPART = RBM * 8 % NTH != 0;        // 6 waves: the last chunk is held by part of the block
     constexpr int XL = XCH * (XF32 ? 2 : 1);
     constexpr uint32_t SBB = SBT == 2 ? 4 : 2;
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * RXT];
@@ -422,7 +423,8 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_wreg_kernel(
         const uint32_t k0 = ksup(step / SPS) + 32 * (step % SPS);
 #pragma unroll
         for (int q = 0; q < XCH; q++) {
-            const uint32_t c = NTH * q + tid;
+            const uint32_t c0 = NTH * q + tid;
+            const uint32_t c = XPART && c0 >= RBM * 8 ? 0 : c0;  // past the tile: a repeat of chunk 0, never stored
             const uint32_t kc = k0 + (SUP / 2) * ((c >> 2) & 1) + 8 * (c & 3);
             const uint32_t off = ((m0 + (c >> 3)) * K + kc) * (XF32 ? 4 : 2);
             if constexpr (XF32) {
@@ -438,6 +440,7 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_wreg_kernel(
     };
     auto store_xq = [&](const XRegs& xr, uint8_t* buf, int q) {
         const int c = NTH * q + tid;
+        if (XPART && c >= RBM * 8) return;
         uint4 v;
         if constexpr (XF32) {
             const uint4 a = xr.v[2 * q], b = xr.v[2 * q + 1];
@@ -565,11 +568,16 @@ Status launch_generic(const QuantMatrix& m, const void* x, int x_dtype, int64_t 
 constexpr int kBM = BM, kBN = BN;  // the LDS tile
 
 // How one prefill product is launched. K divisible by 256 takes the W-in-
-// registers tile: 8 waves (128 x 256 of Y per block, one block per CU) when that
-// already gives every CU a block, else 4 waves (128 x 128, two blocks per CU)
-// with K split until the grid covers the CUs' block slots (at most 8 ways).
-// Other K (multiples of 64) take the LDS tile. Measured on MI355X for the
-// Qwen3-8B MLP shapes at M = 128, 512 and 2048.
+// registers tile with 4, 6 or 8 waves (128 x 32·waves of Y per block; two
+// 4-wave blocks or one 6- or 8-wave block per CU) and K split 1, 2, 4 or 8 ways
+// (fp32 atomics into an fp32 buffer). The pair is the one with the least
+// modelled time: the busiest CU's blocks, each costing its columns x K super-
+// steps at the CU's measured rate for that wave count, plus a fixed and a per-
+// element cost of the split (zero fill, atomics, conversion). The rates and
+// split costs are a least-squares fit (5.7 % rms) to 320 timed plans of the
+// Qwen3-8B projections (N x K = 12288/6144/4096 x 4096, 4096 x 12288) at
+// M = 128 .. 2048 on MI355X; the fitted choice came within 1 % of the best
+// plan in total. Other K (multiples of 64) take the LDS tile.
 struct QmmPlan {
     bool wreg;
     int nw;
@@ -578,21 +586,41 @@ struct QmmPlan {
     dim3 grid;
 };
 
+// Modelled microseconds of one W-in-registers plan (see above).
+double qmm_wreg_cost(int64_t M, int64_t N, int64_t nsup, int nw, int64_t split, int num_cus) {
+    constexpr double kRate4 = 35.3;      // column·super-steps per µs, one 4-wave block on a CU
+    constexpr double kRate4x2 = 46.3;    // two 4-wave blocks on a CU
+    constexpr double kRate6 = 40.1;      // one 6-wave block
+    constexpr double kRate8 = 46.5;      // one 8-wave block
+    constexpr double kSplitFixed = 10.5;  // µs: fill + conversion launches
+    constexpr double kSplitElem = 2.38;   // µs per 10^6 partial sums
+    const int64_t rbn = 32 * nw, mt = (M + RBM - 1) / RBM;
+    const int64_t blocks = ((N + rbn - 1) / rbn) * mt * split;
+    const int64_t per_cu = (blocks + num_cus - 1) / num_cus;
+    const double u = (double)rbn * (double)((nsup + split - 1) / split);
+    double t;
+    if (nw == 4)
+        t = (double)(per_cu / 2) * 2.0 * u / kRate4x2 + (double)(per_cu % 2) * u / kRate4;
+    else
+        t = (double)per_cu * u / (nw == 6 ? kRate6 : kRate8);
+    if (split > 1) t += kSplitFixed + kSplitElem * (double)(M * N * split) * 1e-6;
+    return t;
+}
+
 QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus) {
     QmmPlan p{};
-    const int64_t mt = (rows + RBM - 1) / RBM;
     if (m.in % 256 == 0) {
         p.wreg = true;
-        const int64_t tiles8 = ((m.rows + 255) / 256) * mt;
-        p.nw = tiles8 >= num_cus ? 8 : 4;
-        const int64_t rbn = 32 * p.nw;
-        const int64_t tiles = ((m.rows + rbn - 1) / rbn) * mt;
-        const int64_t slots = (int64_t)num_cus * (p.nw == 8 ? 1 : 2);
         const int64_t nsup = m.in / 256;
-        p.split = 1;
-        while (p.split < 8 && tiles * p.split * 2 <= slots && nsup / (p.split * 2) >= 2) p.split *= 2;
+        double best = 0;
+        for (int nw : {8, 4, 6})
+            for (int64_t split = 1; split <= 8 && (split == 1 || nsup / split >= 2); split *= 2) {
+                const double t = qmm_wreg_cost(rows, m.rows, nsup, nw, split, num_cus);
+                if (p.nw == 0 || t < best) best = t, p.nw = nw, p.split = split;
+            }
+        const int64_t rbn = 32 * p.nw;
         p.k_per_split = (uint32_t)(((nsup + p.split - 1) / p.split) * 256);
-        p.grid = dim3((unsigned)((m.rows + rbn - 1) / rbn), (unsigned)mt, (unsigned)p.split);
+        p.grid = dim3((unsigned)((m.rows + rbn - 1) / rbn), (unsigned)((rows + RBM - 1) / RBM), (unsigned)p.split);
         return p;
     }
     p.wreg = false;
@@ -664,7 +692,10 @@ Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows
     auto tile = [&](auto split_c, float* acc) {
         constexpr bool SPLIT = decltype(split_c)::value;
         if (p.wreg) {
-            if (p.nw == 8) {
+            if (p.nw == 6) {
+                if (xf32) launch_tile_wreg<6, 1, 256, SPLIT, true>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+                else launch_tile_wreg<6, 1, 256, SPLIT, false>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+            } else if (p.nw == 8) {
                 if (xf32) launch_tile_wreg<8, 1, 256, SPLIT, true>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
                 else launch_tile_wreg<8, 1, 256, SPLIT, false>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
             } else {

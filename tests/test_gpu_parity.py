@@ -211,6 +211,43 @@ def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
     assert ok, (d, sc)
 
 
+@pytest.mark.parametrize("m,n,k,gs,sb,xf32,out_dtype", [
+    (500, 12288, 4096, 64, "bf16", False, BF16),   # 6 waves, K whole, M ragged
+    (640, 8000, 2048, 32, "f16", False, BF16),     # 6 waves, N ragged (8000 = 41.7 tiles of 192)
+    (1000, 6000, 1024, 128, "f32", True, F32),     # 6 waves, fp32 x and scales
+    (300, 2784, 2048, 64, "bf16", False, BF16),    # 6 waves, K split 4, bf16 out via the fp32 buffer
+    (300, 2784, 2048, 64, "bf16", True, F32),      # 6 waves, K split 4, atomics straight into y
+    (768, 6144, 4096, 64, "bf16", False, BF16),    # qkv at M=768: 6 waves
+    (384, 6144, 4096, 64, "f16", False, F32),      # qkv at M=384: 4 waves, K whole
+    (1536, 4096, 12288, 64, "bf16", False, BF16),  # down at M=1536: 4 waves, K split 2
+])
+def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
+    """Every tile/split pair the prefill planner picks on a 256-CU MI355X (4/6/8
+    waves, K whole or split, ragged M and N, fp32 x, bf16/f16/fp32 scales and
+    both outputs): the oracle on a random 48x96 block of the output."""
+    q = synth.quant_linear(9000 + m + n, n, k, gs)
+    xb, x = synth.activations(9500 + m, (m, k))
+    w = hip.FromRaw(U32, q.w, *q.w.shape)
+    if sb == "bf16":
+        s_np, b_np = q.s, q.b
+        s, b = hip.FromBF16Bits(q.s_bits, *q.s_bits.shape), hip.FromBF16Bits(q.b_bits, *q.b_bits.shape)
+    elif sb == "f16":
+        s_np, b_np = (v.astype(np.float16).astype(np.float32) for v in (q.s, q.b))
+        s, b = hip.FromRaw(F16, q.s.astype(np.float16), *q.s.shape), hip.FromRaw(F16, q.b.astype(np.float16), *q.b.shape)
+    else:
+        s_np, b_np = q.s, q.b
+        s, b = hip.FromFloats(q.s), hip.FromFloats(q.b)
+    xt = hip.FromFloats(x) if xf32 else hip.FromBF16Bits(xb, m, k)
+    step(f"jh_quant_matmul planner M={m} N={n} K={k} gs={gs} sb={sb} xf32={xf32} out={out_dtype}")
+    y = hip.Floats(hip.QuantMatmul(xt, w, s, b, True, gs, 4, out_dtype=out_dtype))
+    rng = np.random.default_rng(m * 7 + n)
+    rs = np.sort(np.concatenate([rng.choice(m - 1, size=47, replace=False), [m - 1]]))
+    cs = np.sort(np.concatenate([rng.choice(n - 1, size=95, replace=False), [n - 1]]))
+    want = oracle.quant_matmul(x[rs], q.w[cs], s_np[cs], b_np[cs], gs)
+    ok, d, sc = rel_ok(y[np.ix_(rs, cs)], want, BF16_TOL if out_dtype == BF16 else 5e-3)
+    assert ok, (d, sc)
+
+
 def test_qmm_rows_are_independent(hip):
     """Row r of a prefill product equals the decode product of x[r] (fp32 out, 1e-3)."""
     q = synth.quant_linear(11, 512, 4096)
