@@ -169,6 +169,10 @@ __device__ __forceinline__ void store_stage(const Stage<XF32>& st, uint8_t* buf,
 // 32x32 MFMA tiles. Each dequantized W element feeds 256 rows of X, and every
 // thread dequantizes 16 codes per step, so the dequant's VALU work stays below
 // the MFMA time; LDS (2 x 48 KiB) leaves room for one block of 8 waves per CU.
+// Floats between the split-K partial slices of an M x N product (a multiple of
+// 4, so every slice starts 16-byte aligned).
+__host__ __device__ inline size_t split_stride(uint32_t M, uint32_t N) { return ((size_t)M * N + 3) & ~(size_t)3; }
+
 template <bool SPLIT, bool XF32, int SBT>
 __global__ __launch_bounds__(NT, 1) void qmm_mfma_kernel(
     const uint32_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ B,
@@ -266,7 +270,7 @@ __global__ __launch_bounds__(NT, 1) void qmm_mfma_kernel(
                 const uint32_t m = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < M && n < N) {
                     if constexpr (SPLIT)
-                        atomicAdd(acc_out + (size_t)m * N + n, acc[i][j][r]);
+                        acc_out[blockIdx.z * split_stride(M, N) + (size_t)m * N + n] = acc[i][j][r];
                     else
                         store_y(Y, (int64_t)m * N + n, acc[i][j][r], y_dt);
                 }
@@ -274,14 +278,34 @@ __global__ __launch_bounds__(NT, 1) void qmm_mfma_kernel(
         }
 }
 
-__global__ void zero_f32_kernel(float* __restrict__ p, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-        p[i] = 0.0f;
-}
-
-__global__ void f32_to_y_kernel(const float* __restrict__ a, void* __restrict__ y, int y_dt, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-        store_y(y, i, a[i], y_dt);
+// y = the sum of the `split` partial products in ws (each M x N fp32, slices
+// split_stride apart), added in split order: the result does not depend on
+// which block ran first. Four elements per thread (16-byte loads), then a
+// scalar tail.
+__global__ void split_sum_kernel(const float* __restrict__ ws, int split, int64_t n, void* __restrict__ y,
+                                 int y_dt) {
+    const int64_t n4 = n >> 2;
+    const size_t ss = (size_t)(n + 3) & ~(size_t)3;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        float4 a = reinterpret_cast<const float4*>(ws)[i];
+        for (int s = 1; s < split; s++) {
+            const float4 b = reinterpret_cast<const float4*>(ws + s * ss)[i];
+            a.x += b.x, a.y += b.y, a.z += b.z, a.w += b.w;
+        }
+        if (y_dt == JH_F32) {
+            reinterpret_cast<float4*>(y)[i] = a;
+        } else {
+            const uint32_t lo = (uint32_t)f32_to_bf16_hw(a.x) | ((uint32_t)f32_to_bf16_hw(a.y) << 16);
+            const uint32_t hi = (uint32_t)f32_to_bf16_hw(a.z) | ((uint32_t)f32_to_bf16_hw(a.w) << 16);
+            reinterpret_cast<uint2*>(y)[i] = make_uint2(lo, hi);
+        }
+    }
+    for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        float a = ws[i];
+        for (int s = 1; s < split; s++) a += ws[s * ss + i];
+        store_y(y, i, a, y_dt);
+    }
 }
 
 int log2_exact(int v) {
@@ -552,7 +576,7 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_wreg_kernel(
                 const uint32_t m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (m < M && n < N) {
                     if constexpr (SPLIT)
-                        atomicAdd(acc_out + (size_t)m * N + n, acc[i][j][r]);
+                        acc_out[blockIdx.z * split_stride(M, N) + (size_t)m * N + n] = acc[i][j][r];
                     else
                         store_y(Y, (int64_t)m * N + n, acc[i][j][r], y_dt);
                 }
@@ -570,14 +594,16 @@ constexpr int kBM = BM, kBN = BN;  // the LDS tile
 // How one prefill product is launched. K divisible by 256 takes the W-in-
 // registers tile with 4, 6 or 8 waves (128 x 32·waves of Y per block; two
 // 4-wave blocks or one 6- or 8-wave block per CU) and K split 1, 2, 4 or 8 ways
-// (fp32 atomics into an fp32 buffer). The pair is the one with the least
-// modelled time: the busiest CU's blocks, each costing its columns x K super-
-// steps at the CU's measured rate for that wave count, plus a fixed and a per-
-// element cost of the split (zero fill, atomics, conversion). The rates and
-// split costs are a least-squares fit (5.7 % rms) to 320 timed plans of the
+// (8 for 4 waves only). Each K range stores its fp32 partial tile, and one
+// pass sums them in order. The pair is the one with the least modelled time:
+// the busiest CU's blocks, each costing a fixed start plus its columns x K
+// super-steps at the CU's measured rate for that wave count, plus a fixed and
+// a per-element cost of the split (partial stores, the summing pass). The
+// constants are a least-squares fit (4.8 % rms) to 320 timed plans of the
 // Qwen3-8B projections (N x K = 12288/6144/4096 x 4096, 4096 x 12288) at
-// M = 128 .. 2048 on MI355X; the fitted choice came within 1 % of the best
-// plan in total. Other K (multiples of 64) take the LDS tile.
+// M = 128 .. 2048 on MI355X; over those 32 cases the fitted choice took
+// 3079 us against 3075 us for the best plan of each. Other K (multiples of
+// 64) take the LDS tile.
 struct QmmPlan {
     bool wreg;
     int nw;
@@ -588,21 +614,22 @@ struct QmmPlan {
 
 // Modelled microseconds of one W-in-registers plan (see above).
 double qmm_wreg_cost(int64_t M, int64_t N, int64_t nsup, int nw, int64_t split, int num_cus) {
-    constexpr double kRate4 = 35.3;      // column·super-steps per µs, one 4-wave block on a CU
-    constexpr double kRate4x2 = 46.3;    // two 4-wave blocks on a CU
-    constexpr double kRate6 = 40.1;      // one 6-wave block
-    constexpr double kRate8 = 46.5;      // one 8-wave block
-    constexpr double kSplitFixed = 10.5;  // µs: fill + conversion launches
-    constexpr double kSplitElem = 2.38;   // µs per 10^6 partial sums
+    constexpr double kRate4 = 37.0;      // column·super-steps per µs, one 4-wave block on a CU
+    constexpr double kRate4x2 = 44.0;    // two 4-wave blocks on a CU
+    constexpr double kRate6 = 43.0;      // one 6-wave block
+    constexpr double kRate8 = 49.9;      // one 8-wave block
+    constexpr double kBlockStart = 3.9;  // µs per block (per pair of 4-wave blocks) a CU runs in turn
+    constexpr double kSplitFixed = 5.9;  // µs: the summing launch
+    constexpr double kSplitElem = 1.04;  // µs per 10^6 partial sums
     const int64_t rbn = 32 * nw, mt = (M + RBM - 1) / RBM;
     const int64_t blocks = ((N + rbn - 1) / rbn) * mt * split;
     const int64_t per_cu = (blocks + num_cus - 1) / num_cus;
     const double u = (double)rbn * (double)((nsup + split - 1) / split);
     double t;
     if (nw == 4)
-        t = (double)(per_cu / 2) * 2.0 * u / kRate4x2 + (double)(per_cu % 2) * u / kRate4;
+        t = (double)(per_cu / 2) * (2.0 * u / kRate4x2 + kBlockStart) + (double)(per_cu % 2) * (u / kRate4 + kBlockStart);
     else
-        t = (double)per_cu * u / (nw == 6 ? kRate6 : kRate8);
+        t = (double)per_cu * (u / (nw == 6 ? kRate6 : kRate8) + kBlockStart);
     if (split > 1) t += kSplitFixed + kSplitElem * (double)(M * N * split) * 1e-6;
     return t;
 }
@@ -614,7 +641,7 @@ QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus) {
         const int64_t nsup = m.in / 256;
         double best = 0;
         for (int nw : {8, 4, 6})
-            for (int64_t split = 1; split <= 8 && (split == 1 || nsup / split >= 2); split *= 2) {
+            for (int64_t split = 1; split <= (nw == 4 ? 8 : 4) && (split == 1 || nsup / split >= 2); split *= 2) {
                 const double t = qmm_wreg_cost(rows, m.rows, nsup, nw, split, num_cus);
                 if (p.nw == 0 || t < best) best = t, p.nw = nw, p.split = split;
             }
@@ -643,8 +670,10 @@ bool qmm_uses_mfma(const QuantMatrix& m, int64_t rows, int x_dtype) {
 }
 
 size_t qmm_workspace_bytes(const QuantMatrix& m, int64_t rows, int x_dtype, int y_dtype, int num_cus) {
-    if (!qmm_uses_mfma(m, rows, x_dtype) || qmm_plan(m, rows, num_cus).split == 1 || y_dtype == JH_F32) return 0;
-    return sizeof(float) * (size_t)(rows * m.rows);
+    (void)y_dtype;
+    if (!qmm_uses_mfma(m, rows, x_dtype)) return 0;
+    const int64_t split = qmm_plan(m, rows, num_cus).split;
+    return split == 1 ? 0 : sizeof(float) * (size_t)split * split_stride((uint32_t)rows, (uint32_t)m.rows);
 }
 
 template <int NW, int WNF, int SUP, bool SPLIT, bool XF32>
@@ -711,16 +740,14 @@ Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows
         tile(std::false_type{}, nullptr);
         return Status::ok();
     }
-    // split K: fp32 partial tiles meet by atomic adds (in y itself when y is fp32)
-    float* acc = y_dtype == JH_F32 ? static_cast<float*>(y) : static_cast<float*>(workspace);
+    // split K: each K range stores its fp32 partial tile into its own slice of
+    // the workspace, and one pass adds the slices in order into y
+    float* acc = static_cast<float*>(workspace);
     if (!acc) return Status::fail(JH_ERR_INVALID, "qmm: split-K needs a workspace");
     const int64_t n = rows * m.rows;
-    hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256),
-                       0, st, acc, n);
     tile(std::true_type{}, acc);
-    if (y_dtype != JH_F32)
-        hipLaunchKernelGGL(f32_to_y_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)),
-                           dim3(256), 0, st, acc, y, y_dtype, n);
+    hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)std::min<int64_t>((n / 4 + 255) / 256 + 1, 4096)), dim3(256),
+                       0, st, acc, (int)p.split, n, y, y_dtype);
     return Status::ok();
 }
 

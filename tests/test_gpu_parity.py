@@ -217,9 +217,10 @@ def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
     (1000, 6000, 1024, 128, "f32", True, F32),     # 6 waves, fp32 x and scales
     (300, 2784, 2048, 64, "bf16", False, BF16),    # 6 waves, K split 4, bf16 out via the fp32 buffer
     (300, 2784, 2048, 64, "bf16", True, F32),      # 6 waves, K split 4, atomics straight into y
-    (768, 6144, 4096, 64, "bf16", False, BF16),    # qkv at M=768: 6 waves
-    (384, 6144, 4096, 64, "f16", False, F32),      # qkv at M=384: 4 waves, K whole
-    (1536, 4096, 12288, 64, "bf16", False, BF16),  # down at M=1536: 4 waves, K split 2
+    (384, 6144, 4096, 64, "f16", False, F32),      # qkv at M=384: 6 waves, K split 2
+    (260, 9000, 4096, 64, "bf16", False, BF16),    # 8 waves, K split 2, M ragged
+    (1536, 4096, 12288, 64, "bf16", False, BF16),  # down at M=1536: 8 waves, K split 4
+    (1100, 3000, 2048, 64, "bf16", True, BF16),    # 4 waves, K whole
 ])
 def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
     """Every tile/split pair the prefill planner picks on a 256-CU MI355X (4/6/8
@@ -246,6 +247,21 @@ def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
     want = oracle.quant_matmul(x[rs], q.w[cs], s_np[cs], b_np[cs], gs)
     ok, d, sc = rel_ok(y[np.ix_(rs, cs)], want, BF16_TOL if out_dtype == BF16 else 5e-3)
     assert ok, (d, sc)
+
+
+@pytest.mark.parametrize("out_dtype", [BF16, F32])
+def test_qmm_split_k_is_deterministic(hip, out_dtype):
+    """K split 4 ways (M=128, 12288 x 4096): the partial products are added in a
+    fixed order, so repeated calls give identical bits."""
+    q = synth.quant_linear(31, 12288, 4096)
+    xb, _ = synth.activations(32, (128, 4096))
+    w, s, b = upload_quant(hip, q)
+    xt = hip.FromBF16Bits(xb, 128, 4096)
+    step(f"jh_quant_matmul split-K determinism out={out_dtype}")
+    y0 = hip.Floats(hip.QuantMatmul(xt, w, s, b, True, 64, 4, out_dtype=out_dtype))
+    for _ in range(3):
+        y1 = hip.Floats(hip.QuantMatmul(xt, w, s, b, True, 64, 4, out_dtype=out_dtype))
+        assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
 
 
 def test_qmm_rows_are_independent(hip):
