@@ -179,7 +179,10 @@ def test_qmv_linearity_full_lm_head(hip):
 
 @pytest.mark.parametrize("m,n,k,gs", [(2, 64, 512, 64), (3, 130, 1024, 64), (13, 256, 2048, 64),
                                       (128, 384, 4096, 64), (77, 200, 1024, 32), (40, 96, 768, 128),
-                                      (5, 24, 1032, 8)])
+                                      (5, 24, 1032, 8),
+                                      # K a multiple of 64 but not of 256: the LDS tile, K whole
+                                      # (704 = 11 steps) and K split 2 (1088 = 17 steps)
+                                      (100, 300, 704, 64), (100, 300, 1088, 64)])
 def test_qmm_matches_oracle(hip, oracle, m, n, k, gs):
     q = synth.quant_linear(5000 + m + n, n, k, gs)
     xb, x = synth.activations(6000 + m, (m, k))
