@@ -140,7 +140,10 @@ JH_API int jh_dequantize(jh_ctx *ctx, const uint32_t *w, const void *scales, con
  * use; transpose == 0 returns JH_ERR_UNSUPPORTED):
  *   y[rows, out_features] = x[rows, in_features] . W^T
  * x_dtype and y_dtype are JH_BF16 or JH_F32; accumulation is fp32. rows == 1
- * runs the decode GEMV, rows > 1 the MFMA prefill GEMM. rows == 0 is a no-op.
+ * runs the decode GEMV; 2..8 bf16 rows (2..4 for in_features 768, 1536, 3072,
+ * 6144, 12288 and 16384) run the decode GEMV's tiles with every row's x in
+ * registers, so each row's result has the bits of a one-row call; more rows
+ * run the MFMA prefill GEMM. rows == 0 is a no-op.
  * When the prefill GEMM splits K, its fp32 partial products go to the
  * context's workspace (grown to split * rows * out_features floats) and are
  * added in a fixed order: results are the same bits on every call. */

@@ -242,6 +242,12 @@ Status launch_norm_prepare(const void* x, int x_dt, int64_t d, const void* w, in
                            hipStream_t st);
 // out = bf16(u / sqrt(sum(stats) / d + eps)).
 Status launch_norm_apply(const uint16_t* u, int64_t d, const float* stats, float eps, uint16_t* out, hipStream_t st);
+// A few bf16 x rows (2..kQmvRowsMax, fewer for long rows) through the decode
+// tiles, the weights read once per launch of 2, 4 or 8 rows.
+constexpr int64_t kQmvRowsMax = 8;
+bool qmv_rows_ok(const QuantMatrix& m, int64_t rows, int x_dtype);
+Status launch_qmv_rows(const QuantMatrix& m, const void* x, int64_t rows, void* y, int y_dtype, int num_cus,
+                       hipStream_t st);
 Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y,
                   int y_dtype, int num_cus, hipStream_t st, void* workspace);
 // fp32 accumulation buffer a split-K prefill needs (0 when none).

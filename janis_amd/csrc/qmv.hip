@@ -411,6 +411,141 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     }
 }
 
+
+// A few rows of x (2..MR) through the decode tile: each weight word is loaded
+// and split into (128 + q) bf16 pairs once and applied to every row's x, so
+// the weights stream from HBM once for all rows. The lanes, words, dot order
+// and reductions are those of qmv_bf16x_kernel with the same tile, so row m of
+// y has the bits a one-row call on x[m] gives. bf16 x and y rows of N (bf16 or
+// fp32); rows past `rows` read as zero and are not stored.
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int MR>
+__global__ __launch_bounds__(256) void qmv_rows_kernel(
+    const uint32_t* __restrict__ W, const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
+    const uint16_t* __restrict__ X, void* Y, int y_dt, uint32_t N, int gs_log2, int rows) {
+    constexpr int SLICES = 64 / LPR;
+    constexpr int RGROUPS = 4 / KSPLIT;
+    constexpr uint32_t PK = 4 * LPR * ITERS;
+    constexpr uint32_t P = PK * KSPLIT;
+    constexpr uint32_t K = 8 * P;
+    constexpr int ROWS_PER_WAVE = SLICES * RPW;
+    constexpr int ROWS_PER_BLOCK = RGROUPS * ROWS_PER_WAVE;
+    const int lane = threadIdx.x & 63;
+    const int wv_id = threadIdx.x >> 6;
+    const int ks = wv_id % KSPLIT, rg = wv_id / KSPLIT;
+    const int sl = lane % LPR, slice = lane / LPR;
+    const uint32_t G = K >> gs_log2;
+    const auto rw = make_rsrc(W, N * P * 4);
+    const auto rs = make_rsrc(S, N * G * 2);
+    const auto rb = make_rsrc(B, N * G * 2);
+    const auto rx = make_rsrc(X, (uint32_t)rows * K * 2);
+    __shared__ float red[(KSPLIT > 1) ? (KSPLIT - 1) * RGROUPS * SLICES * RPW * MR : 1];
+
+    uint32_t gi[ITERS], wo[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; it++) {
+        wo[it] = ks * PK + it * 4 * LPR + 4 * sl;
+        gi[it] = (8 * wo[it]) >> gs_log2;
+    }
+    // every row's part of x as (x_p, x_{p+4}) pairs, and its group sums
+    uint32_t xp[MR][ITERS][16];
+    float xs[MR][ITERS];
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+            const uint32_t off = (m * K + 8 * wo[it]) * 2;
+            float sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16 * j, 0, 0);
+                sum += pair_up(make_uint4(v.x, v.y, v.z, v.w), &xp[m][it][4 * j]);
+            }
+            xs[m][it] = sum;
+        }
+
+    const uint32_t lane_row = rg * ROWS_PER_WAVE + (uint32_t)slice * RPW;
+    for (uint32_t bbase = blockIdx.x * ROWS_PER_BLOCK; bbase < N; bbase += gridDim.x * ROWS_PER_BLOCK) {
+        const uint32_t row0 = bbase + lane_row;
+        uint4 wv[RPW][ITERS];
+        uint16_t sh[RPW][ITERS], bh[RPW][ITERS];
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int it = 0; it < ITERS; it++) wv[r][it] = buf_load16_nt(rw, ((row0 + r) * P + wo[it]) * 4);
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int it = 0; it < ITERS; it++) {
+                const uint32_t off = ((row0 + r) * G + gi[it]) * 2;
+                sh[r][it] = buf_load2(rs, off);
+                bh[r][it] = buf_load2(rb, off);
+            }
+        float part[MR * RPW];
+#pragma unroll
+        for (int i = 0; i < MR * RPW; i++) part[i] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int it = 0; it < ITERS; it++) {
+                const float sc = SB_F16 ? f16_to_f32(sh[r][it]) : bf16_to_f32(sh[r][it]);
+                const float bi = SB_F16 ? f16_to_f32(bh[r][it]) : bf16_to_f32(bh[r][it]);
+                const float bo = fmaf(-kCodeOffset, sc, bi);
+                float d[MR];
+#pragma unroll
+                for (int m = 0; m < MR; m++) d[m] = 0.0f;
+                const uint32_t words[4] = {wv[r][it].x, wv[r][it].y, wv[r][it].z, wv[r][it].w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t lo = words[q] & 0x0F0F0F0Fu;
+                    const uint32_t hi = (words[q] >> 4) & 0x0F0F0F0Fu;
+                    const uint32_t c0 = __builtin_amdgcn_perm(kBf16Bytes, lo, kSelB0B2);
+                    const uint32_t c1 = __builtin_amdgcn_perm(kBf16Bytes, hi, kSelB0B2);
+                    const uint32_t c2 = __builtin_amdgcn_perm(kBf16Bytes, lo, kSelB1B3);
+                    const uint32_t c3 = __builtin_amdgcn_perm(kBf16Bytes, hi, kSelB1B3);
+#pragma unroll
+                    for (int m = 0; m < MR; m++) {
+                        d[m] = dot2_bf16(c0, xp[m][it][4 * q + 0], d[m]);
+                        d[m] = dot2_bf16(c1, xp[m][it][4 * q + 1], d[m]);
+                        d[m] = dot2_bf16(c2, xp[m][it][4 * q + 2], d[m]);
+                        d[m] = dot2_bf16(c3, xp[m][it][4 * q + 3], d[m]);
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    part[m * RPW + r] = fmaf(sc, d[m], part[m * RPW + r]);
+                    part[m * RPW + r] = fmaf(bo, xs[m][it], part[m * RPW + r]);
+                }
+            }
+        slice_sums_last<LPR, MR * RPW>(part);
+        if constexpr (KSPLIT > 1) {
+            const int slot = (rg * SLICES + slice) * RPW * MR;
+            if (ks > 0 && sl == LPR - 1)
+#pragma unroll
+                for (int i = 0; i < MR * RPW; i++) red[((ks - 1) * RGROUPS * SLICES * RPW * MR) + slot + i] = part[i];
+            __syncthreads();
+            if (ks == 0 && sl == LPR - 1)
+#pragma unroll
+                for (int k = 1; k < KSPLIT; k++)
+#pragma unroll
+                    for (int i = 0; i < MR * RPW; i++) part[i] += red[((k - 1) * RGROUPS * SLICES * RPW * MR) + slot + i];
+            __syncthreads();
+        }
+        if (ks == 0 && sl == LPR - 1) {
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+                if (m < rows)
+#pragma unroll
+                    for (int r = 0; r < RPW; r++)
+                        if (row0 + r < N) {
+                            const size_t o = (size_t)m * N + row0 + r;
+                            if (y_dt == JH_BF16)
+                                static_cast<uint16_t*>(Y)[o] = f32_to_bf16_hw(part[m * RPW + r]);
+                            else
+                                static_cast<float*>(Y)[o] = part[m * RPW + r];
+                        }
+        }
+    }
+}
 }  // namespace
 
 // Generic kernel: any x dtype (bf16/f32), any K % 8 == 0 and group size dividing
@@ -614,6 +749,97 @@ Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int
     if (x_dtype == JH_BF16 && launch_tiles<PRO_NONE, EPI_STORE>(m, x, y, y_dtype, num_cus, st, QmvFusion{}))
         return Status::ok();
     return launch_generic(m, x, x_dtype, 1, y, y_dtype, num_cus, st);
+}
+
+
+namespace {
+
+// Rows of x per launch of the multi-row tile: x of MR rows lives in registers
+// (16 VGPRs per row and 32 elements of a lane's K part), so long K parts take
+// fewer rows per launch.
+template <int ITERS>
+constexpr int rows_mr() { return ITERS == 1 ? 8 : (ITERS == 2 ? 4 : 2); }
+
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int MR>
+Status run_rows_mr(const QuantMatrix& m, const uint16_t* x, int64_t rows, void* y, int y_dtype, int gl,
+                   int num_cus, hipStream_t st) {
+    constexpr int64_t rows_per_block = (4 / KSPLIT) * (64 / LPR) * RPW;
+    auto kern = qmv_rows_kernel<LPR, ITERS, RPW, KSPLIT, SB_F16, MR>;
+    static int per_cu = 0;  // resident blocks per CU, asked once per instantiation
+    if (per_cu == 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) != hipSuccess || per_cu < 1))
+        per_cu = 1;
+    int64_t blocks = (m.rows + rows_per_block - 1) / rows_per_block;
+    blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, (int64_t)num_cus * per_cu));
+    const size_t ysz = y_dtype == JH_BF16 ? 2 : 4;
+    for (int64_t r0 = 0; r0 < rows; r0 += MR) {
+        const int n = (int)std::min<int64_t>(MR, rows - r0);
+        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, st, m.w,
+                           static_cast<const uint16_t*>(m.scales), static_cast<const uint16_t*>(m.biases),
+                           x + r0 * m.in, static_cast<char*>(y) + (size_t)r0 * m.rows * ysz, y_dtype,
+                           (uint32_t)m.rows, gl, n);
+    }
+    return Status::ok();
+}
+
+// The kernel computes all MR rows whatever the count, so the smallest of 2, 4
+// and 8 rows per launch that covers the call (up to the tile's limit) is used.
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16>
+Status run_rows(const QuantMatrix& m, const uint16_t* x, int64_t rows, void* y, int y_dtype, int gl, int num_cus,
+                hipStream_t st) {
+    constexpr int MRMAX = rows_mr<ITERS>();
+    if constexpr (MRMAX >= 8)
+        if (rows > 4) return run_rows_mr<LPR, ITERS, RPW, KSPLIT, SB_F16, 8>(m, x, rows, y, y_dtype, gl, num_cus, st);
+    if constexpr (MRMAX >= 4)
+        if (rows > 2) return run_rows_mr<LPR, ITERS, RPW, KSPLIT, SB_F16, 4>(m, x, rows, y, y_dtype, gl, num_cus, st);
+    return run_rows_mr<LPR, ITERS, RPW, KSPLIT, SB_F16, 2>(m, x, rows, y, y_dtype, gl, num_cus, st);
+}
+
+// 16-byte weight loads per lane and row of the decode tile for a row length.
+int tile_iters(int64_t row_words) {
+    switch (row_words) {
+        case 512 * 2: return 2;
+        case 512 * 3: case 256 * 3: case 128 * 3: case 64 * 3: case 32 * 3: return 3;
+        case 512 * 4: return 4;
+        default: return 1;
+    }
+}
+
+}  // namespace
+
+// Up to 8 rows (4 for tiles whose lanes hold 96 or 128 elements of each row):
+// beyond that the prefill GEMM is faster (measured on MI355X for the Qwen3-8B
+// shapes: gate/up 12288 x 4096 at 8 rows 23.5 us against 28.4 for the GEMM;
+// down 4096 x 12288 at 4 rows 20.9 against 32.2, at 8 rows 42.2).
+bool qmv_rows_ok(const QuantMatrix& m, int64_t rows, int x_dtype) {
+    if (x_dtype != JH_BF16 || m.bits != 4 || rows < 2 || !qmv_fast_shape(m) || rows * m.in * 2 >= ((int64_t)1 << 31))
+        return false;
+    return rows <= (tile_iters(row_words(m)) >= 3 ? 4 : kQmvRowsMax);
+}
+
+Status launch_qmv_rows(const QuantMatrix& m, const void* x, int64_t rows, void* y, int y_dtype, int num_cus,
+                       hipStream_t st) {
+    if (!qmv_rows_ok(m, rows, JH_BF16)) return Status::fail(JH_ERR_UNSUPPORTED, "qmv_rows: shape outside the tiles");
+    const int gl = log2_exact(m.group_size);
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+#define JH_ROWS(L, I, R, KS)                                                                   \
+    return m.sb_dtype == JH_F16 ? run_rows<L, I, R, KS, true>(m, xb, rows, y, y_dtype, gl, num_cus, st) \
+                                : run_rows<L, I, R, KS, false>(m, xb, rows, y, y_dtype, gl, num_cus, st)
+    switch (row_words(m)) {
+        case 512 * 1: JH_ROWS(32, 1, 4, 4);
+        case 512 * 2: JH_ROWS(32, 2, 2, 4);
+        case 512 * 3: JH_ROWS(32, 3, 2, 4);
+        case 512 * 4: JH_ROWS(32, 4, 2, 4);
+        case 256 * 1: JH_ROWS(32, 1, 4, 2);
+        case 256 * 3: JH_ROWS(32, 3, 2, 2);
+        case 128 * 1: JH_ROWS(16, 1, 4, 2);
+        case 128 * 3: JH_ROWS(16, 3, 2, 2);
+        case 64 * 1: JH_ROWS(16, 1, 4, 1);
+        case 64 * 3: JH_ROWS(16, 3, 2, 1);
+        case 32 * 1: JH_ROWS(8, 1, 4, 1);
+        case 32 * 3: JH_ROWS(8, 3, 2, 1);
+        default: return Status::fail(JH_ERR_UNSUPPORTED, "qmv_rows: no tile for the row length");
+    }
+#undef JH_ROWS
 }
 
 // True when one register-tile launch takes the fused call (no workspace).

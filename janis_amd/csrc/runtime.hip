@@ -275,6 +275,8 @@ int jh_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, co
     jh::QuantMatrix m{w, scales, biases, sb_dtype, out_features, in_features, group_size, bits};
     if (rows == 1)
         return finish(c, jh::launch_qmv(m, x, x_dtype, y, y_dtype, c->num_cus, c->stream), "qmv");
+    if (jh::qmv_rows_ok(m, rows, x_dtype))
+        return finish(c, jh::launch_qmv_rows(m, x, rows, y, y_dtype, c->num_cus, c->stream), "qmv_rows");
     const size_t need = jh::qmm_workspace_bytes(m, rows, x_dtype, y_dtype, c->num_cus);
     if (need)
         if (int r = ensure_workspace(c, need, "jh_quant_matmul")) return r;

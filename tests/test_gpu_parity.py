@@ -197,6 +197,42 @@ def test_qmm_matches_oracle(hip, oracle, m, n, k, gs):
     assert ok, ("f32 out", d, sc)
 
 
+@pytest.mark.parametrize("n,k,rows,gs,sb", [
+    (4096, 4096, 8, 64, "bf16"),    # 8 rows per launch
+    (4096, 4096, 5, 64, "bf16"),    # 8 rows per launch, 5 used
+    (4096, 4096, 3, 64, "f16"),     # 4 rows per launch, 3 used
+    (1000, 12288, 4, 64, "bf16"),   # 2 rows per launch, two launches, ragged N
+    (1000, 12288, 3, 64, "bf16"),   # two launches, the second with one row
+    (257, 8192, 3, 32, "f16"),      # 4 rows per launch
+    (300, 2048, 7, 128, "bf16"),
+    (33, 768, 2, 64, "bf16"),
+    (70, 3072, 3, 64, "f16"),
+    (100, 16384, 4, 64, "bf16"),
+])
+def test_qmv_rows_match_one_row_calls(hip, oracle, n, k, rows, gs, sb):
+    """2..8 rows (2..4 for long rows) take the decode tiles with every row's x
+    in registers: each row of y has the bits of a one-row call on that row
+    (fp32 out), and the bf16 output is within the bar of the oracle."""
+    q = synth.quant_linear(12000 + n + k, n, k, gs)
+    xb, x = synth.activations(13000 + rows, (rows, k))
+    w = hip.FromRaw(U32, q.w, *q.w.shape)
+    if sb == "f16":
+        s_np, b_np = (v.astype(np.float16).astype(np.float32) for v in (q.s, q.b))
+        s, b = hip.FromRaw(F16, q.s.astype(np.float16), *q.s.shape), hip.FromRaw(F16, q.b.astype(np.float16), *q.b.shape)
+    else:
+        s_np, b_np = q.s, q.b
+        s, b = hip.FromBF16Bits(q.s_bits, *q.s_bits.shape), hip.FromBF16Bits(q.b_bits, *q.b_bits.shape)
+    step(f"jh_quant_matmul rows={rows} N={n} K={k} gs={gs} sb={sb} (multi-row decode tile)")
+    y32 = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, rows, k), w, s, b, True, gs, 4, out_dtype=F32))
+    for r in range(rows):
+        y1 = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb[r:r + 1], 1, k), w, s, b, True, gs, 4, out_dtype=F32))
+        assert np.array_equal(y32[r].view(np.uint32), y1[0].view(np.uint32)), r
+    y16 = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, rows, k), w, s, b, True, gs, 4))
+    cs = np.sort(np.random.default_rng(n).choice(n, size=min(n, 96), replace=False))
+    ok, d, sc = rel_ok(y16[:, cs], oracle.quant_matmul(x, q.w[cs], s_np[cs], b_np[cs], gs), BF16_TOL)
+    assert ok, (d, sc)
+
+
 @pytest.mark.parametrize("m", [128, 512, 2048])
 @pytest.mark.parametrize("name,n,k", [("gate_up", 12288, 4096), ("down", 4096, 12288)])
 def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
