@@ -288,6 +288,18 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
             pre[f"{name}_M{m}"] = {"us": round(ms * 1e3, 1), "TFLOP_s": round(fl / (ms * 1e-3) / 1e12, 1),
                                    "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)}
             del g
+        # a few rows (batched decode of several sequences): the multi-row decode
+        # GEMV up to 8 rows (4 for down), HBM-bound on the weights
+        few = {}
+        for m in ((2, 4, 8) if k == 4096 else (2, 4)):
+            x = bf16((m, k))
+            y = bf16((m, n), randn=False)
+            g = capture(lambda: [hip.QuantMatmul(x, *c, True, GS, 4, out=y) for c in copies])
+            ms = time_graph(g, 5, 2) / len(copies)
+            byts = 0.5625 * n * k + 2 * m * (n + k)
+            few[f"M{m}"] = {"us": round(ms * 1e3, 2), "GB_s": round(byts / (ms * 1e-3) / 1e9, 1)}
+            del g
+        pre[f"{name}_few_rows"] = few
         del copies
     res["prefill_qmm"] = pre
     log("prefill:", pre)
