@@ -20,8 +20,8 @@
 // Operand layout of v_mfma_f32_32x32x16_bf16: lane l supplies
 //   A[i = l % 32][k = 8*(l/32) .. +8]  and  B[k = 8*(l/32) .. +8][j = l % 32],
 // and accumulator register r of lane l holds D[8*(r/4) + 4*(l/32) + r%4][l % 32].
-// When the tile grid is too small to fill the GPU, K is split over blockIdx.z
-// and the partial tiles are added with fp32 atomics into an fp32 buffer.
+// When the tile grid is too small to fill the GPU, K is split over blockIdx.z:
+// each K range stores its fp32 partial tile and one pass adds them in order.
 #include "jh_common.hpp"
 
 namespace jh {
