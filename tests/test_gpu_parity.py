@@ -303,6 +303,74 @@ def test_qmm_split_k_is_deterministic(hip, out_dtype):
         assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
 
 
+@pytest.mark.parametrize("rows,n,k", [(128, 12288, 4096), (4, 4096, 4096)])
+def test_quant_matmul_graph_replays(hip, oracle, rows, n, k):
+    """Captured once into a HIP graph (after one eager call, which sizes the
+    workspace) and replayed on new x written into the captured buffer: every
+    replay matches the eager call on the same x bit for bit. 128 rows take the
+    K-split prefill tile (partial tiles, then the ordered sum, no fill), 4 rows
+    the multi-row decode tile."""
+    import ctypes
+    import subprocess
+
+    from janis_amd import _lib as jl
+
+    out = subprocess.run(["ldd", jl.LIB_PATH], capture_output=True, text=True).stdout
+    rt = ctypes.CDLL(next(ln.split("=>")[1].split()[0] for ln in out.splitlines() if "libamdhip64" in ln))
+    for name in ("hipStreamCreate", "hipStreamSynchronize", "hipStreamBeginCapture", "hipStreamEndCapture",
+                 "hipGraphInstantiate", "hipGraphLaunch", "hipGraphExecDestroy", "hipGraphDestroy",
+                 "hipStreamDestroy"):
+        getattr(rt, name).restype = ctypes.c_int
+    q = synth.quant_linear(41 + rows, n, k)
+    w, s, b = upload_quant(hip, q)
+    xs = [synth.activations(42 + i, (rows, k)) for i in range(3)]
+    xt = hip.empty(BF16, rows, k)
+    yt = hip.empty(BF16, rows, n)
+
+    def put(a):
+        a = np.ascontiguousarray(a)
+        hip.Sync()
+        hip._L.jh_h2d(hip._ctx, ctypes.c_void_p(xt.ptr), a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
+        hip.Sync()
+
+    def call():
+        return hip.QuantMatmul(xt, w, s, b, True, 64, 4, out=yt)
+
+    eager = []
+    for xb, _ in xs:
+        put(xb)
+        call()
+        eager.append(hip.Floats(yt).copy())
+    stream, graph, exe = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    assert rt.hipStreamCreate(ctypes.byref(stream)) == 0
+    try:
+        hip.SetStream(stream.value)
+        step(f"capture jh_quant_matmul rows={rows} N={n} K={k}")
+        assert rt.hipStreamBeginCapture(stream, 0) == 0
+        call()
+        assert rt.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+        assert rt.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for rep, i in enumerate((1, 2, 0, 1, 1)):
+            step(f"graph replay {rep} on x {i}")
+            put(xs[i][0])
+            assert rt.hipGraphLaunch(exe, stream) == 0
+            assert rt.hipStreamSynchronize(stream) == 0
+            got = hip.Floats(yt)
+            assert np.array_equal(got.view(np.uint32), eager[i].view(np.uint32)), rep
+        cs = np.sort(np.random.default_rng(rows).choice(n, size=64, replace=False))
+        rs = np.arange(min(rows, 16))
+        ok, d, sc = rel_ok(got[np.ix_(rs, cs)], oracle.quant_matmul(xs[1][1][rs], q.w[cs], q.s[cs], q.b[cs], 64),
+                           BF16_TOL)
+        assert ok, (d, sc)
+    finally:
+        hip.SetStream(None)
+        if exe.value:
+            rt.hipGraphExecDestroy(exe)
+        if graph.value:
+            rt.hipGraphDestroy(graph)
+        rt.hipStreamDestroy(stream)
+
+
 def test_qmm_rows_are_independent(hip):
     """Row r of a prefill product equals the decode product of x[r] (fp32 out, 1e-3)."""
     q = synth.quant_linear(11, 512, 4096)
