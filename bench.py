@@ -64,6 +64,12 @@ def main() -> int:
     ap.add_argument("--pmc-workload", action="store_true",
                     help="eager launches for rocprofv3 --pmc: a 256 MiB copy (counter calibration), "
                          "then one pass of the dominant kernel's launches; prints nothing else")
+    ap.add_argument("--shapes-workload", action="store_true",
+                    help="eager launches for rocprofv3: each decode shape (qkv, o, gate_up, down, lm_head) "
+                         "3 times on distinct weights, in that order")
+    ap.add_argument("--prefill-workload", type=int, default=0, metavar="M",
+                    help="eager launches for rocprofv3: the config-2 prefill products (gate_up 12288x4096, "
+                         "down 4096x12288) at M rows, 3 times each")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this backend is measured on one GPU; --gpus N > 1 is not "
@@ -156,6 +162,36 @@ def main() -> int:
         hip.Close()
         return 0
 
+    if args.shapes_workload:
+        # calibration for FETCH_SIZE/WRITE_SIZE: a plain copy of 256 MiB first
+        src = torch.empty(1 << 28, dtype=torch.uint8, device=dev).fill_(1)
+        torch.empty_like(src).copy_(src)
+        torch.cuda.synchronize()
+        hip.SetStream(torch.cuda.current_stream().cuda_stream)
+        for name in ("qkv", "o", "gate_up", "down"):
+            for L in layers[:3]:
+                launch(name, L[name], xin[name], ys[name])
+        for _ in range(3):
+            launch("lm_head", head, x_h, y_head)
+        torch.cuda.synchronize()
+        log("shapes workload done")
+        hip.Close()
+        return 0
+
+    if args.prefill_workload:
+        hip.SetStream(torch.cuda.current_stream().cuda_stream)
+        m = args.prefill_workload
+        for n, k in ((12288, HIDDEN), (HIDDEN, INTER)):
+            copies = [qweight(n, k) for _ in range(3)]
+            x, y = bf16((m, k)), bf16((m, n), randn=False)
+            for c in copies:
+                hip.QuantMatmul(x, *c, True, GS, 4, out=y)
+            torch.cuda.synchronize()
+            del copies
+        log(f"prefill workload M={m} done")
+        hip.Close()
+        return 0
+
     if args.pmc_workload:
         # calibration: a plain copy of known size (reads and writes 256 MiB)
         src = torch.empty(1 << 28, dtype=torch.uint8, device=dev).fill_(1)
@@ -191,6 +227,24 @@ def main() -> int:
     per_shape["lm_head"] = {"N": VOCAB, "K": HIDDEN, "us": round(ms * 1e3, 2),
                             "GB_s": round(qbytes(VOCAB, HIDDEN) / (ms * 1e-3) / 1e9, 1)}
     del g
+    # q_proj and k_proj / v_proj as the reference's separate linears (config 1 times
+    # each shape separately), 36 copies each
+    for name, (n, k) in {"q_proj": (HIDDEN, HIDDEN), "k_proj": (1024, HIDDEN)}.items():
+        copies = [qweight(n, k) for _ in range(LAYERS)]
+        yq = bf16((1, n), randn=False)
+        g = capture(lambda copies=copies, yq=yq: [hip.QuantMatmul(x_h, *c, True, GS, 4, out=yq) for c in copies])
+        ms = time_graph(g, max(5, args.steps // 2), 3) / LAYERS
+        per_shape[name] = {"N": n, "K": k, "us": round(ms * 1e3, 2),
+                           "GB_s": round(qbytes(n, k) / (ms * 1e-3) / 1e9, 1)}
+        if name == "k_proj":
+            per_shape[name]["note"] = "v_proj has the same shape"
+        del g, copies
+    # the plain-read floor of each shape's bytes (one launch reading them, nothing else)
+    floors = memory_floors(torch, dev, capture, time_graph, {nm: qbytes(v["N"], v["K"]) for nm, v in per_shape.items()})
+    for nm, v in per_shape.items():
+        f = floors["floors"][nm]
+        v["floor_us"] = f["us"]
+        v["vs_floor"] = round(v["us"] / f["us"], 3)
     log("per shape:", per_shape)
 
     # ---- the same shapes with 8-bit codes (MLX's other affine width), 8 copies each -----
@@ -231,7 +285,8 @@ def main() -> int:
                 "algorithmic_bytes_per_launch": bytes_dom // n_dom}
 
     extra = {"per_shape": per_shape, "per_shape_8bit": per_shape_8, "launches_per_token": n_launch,
-             "bytes_per_token": bytes_token}
+             "bytes_per_token": bytes_token, "hbm_measured": floors["hbm"],
+             "read_floors": floors["floors"]}
 
     if not args.quick:
         extra.update(prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args))
@@ -406,30 +461,144 @@ def decode_step_figures(hip, torch, dev, capture, time_graph, args, contexts=(51
     return {"qwen3_8b_decode_step": res}
 
 
+def memory_floors(torch, dev, capture, time_graph, sizes):
+    """Measured HBM figures from bench.py's own kernels (janis_amd/libjanis_bench.so):
+    a 1 GiB device copy and a 2 GiB read (the device's bandwidth beside the 8 TB/s
+    specification), and for each byte count in `sizes` the fastest single launch that
+    only reads that many bytes -- a graph of launches over distinct windows of a 2 GiB
+    buffer (no window re-read while in the 256 MB last-level cache), best of 1/2/4
+    blocks per CU and 4/8/16 loads per lane in flight. That is the floor a decode
+    product of those bytes can reach in one launch."""
+    import ctypes
+
+    from janis_amd import build as jb
+
+    L = ctypes.CDLL(jb.BENCH_LIB)
+    L.jhb_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                           ctypes.c_void_p]
+    L.jhb_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    L.jhb_read.restype = L.jhb_copy.restype = ctypes.c_int
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    pool_bytes = 2 << 30
+    pool = torch.empty(pool_bytes, dtype=torch.uint8, device=dev).fill_(7)
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+
+    def reads(nb, blocks, unroll, n):
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(n):
+            rc = L.jhb_read(pool.data_ptr() + i * nb, nb, sink.data_ptr(), blocks, unroll, st)
+            if rc != 0:
+                raise RuntimeError(f"jhb_read: {rc}")
+
+    floors = {}
+    for name, nbytes in sizes.items():
+        nb = (int(nbytes) + 255) // 256 * 256
+        n = max(1, min(36, pool_bytes // nb))
+        best = None
+        for bpc in (1, 2, 4):
+            for unroll in (4, 8, 16):
+                g = capture(lambda: reads(nb, bpc * cus, unroll, n))
+                ms = time_graph(g, 10, 3) / n
+                del g
+                if best is None or ms < best[0]:
+                    best = (ms, bpc, unroll)
+        floors[name] = {"bytes": nb, "us": round(best[0] * 1e3, 2), "GB_s": round(nb / (best[0] * 1e-3) / 1e9, 1),
+                        "blocks_per_cu": best[1], "loads_in_flight_per_lane": best[2], "launches_timed": n}
+    # whole-buffer read and copy
+    g = capture(lambda: reads(pool_bytes, 4 * cus, 8, 1))
+    ms_read = time_graph(g, 10, 3)
+    del g
+    half = pool_bytes // 2
+
+    def copy():
+        rc = L.jhb_copy(pool.data_ptr() + half, pool.data_ptr(), half, 4 * cus, torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"jhb_copy: {rc}")
+
+    g = capture(copy)
+    ms_copy = time_graph(g, 10, 3)
+    del g, pool
+    torch.cuda.empty_cache()
+    hbm = {"copy_GB_s": round(2 * half / (ms_copy * 1e-3) / 1e9, 1),
+           "read_GB_s": round(pool_bytes / (ms_read * 1e-3) / 1e9, 1),
+           "note": "1 GiB device copy (read + write bytes / time) and a 2 GiB read, one launch each, "
+                   "janis_amd/csrc/bench_kernels.hip; the roofline's peak stays the 8 TB/s specification"}
+    log("hbm measured:", hbm, "read floors:", floors)
+    return {"hbm": hbm, "floors": floors}
+
+
+def host_info() -> dict:
+    """nproc, the cores this process may use, the CPU model and the L3 size."""
+    info = {"nproc": os.cpu_count(),
+            "affinity": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    info["cpu_model"] = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    # total L3: the size of each distinct L3 instance (by the CPUs sharing it)
+    seen, total = set(), 0
+    base = "/sys/devices/system/cpu"
+    try:
+        for cpu in sorted(os.listdir(base)):
+            d = os.path.join(base, cpu, "cache", "index3")
+            if not cpu.startswith("cpu") or not os.path.isdir(d):
+                continue
+            with open(os.path.join(d, "shared_cpu_list")) as f:
+                key = f.read().strip()
+            if key in seen:
+                continue
+            seen.add(key)
+            with open(os.path.join(d, "size")) as f:
+                sz = f.read().strip()
+            mult = {"K": 1 << 10, "M": 1 << 20}.get(sz[-1:], 1)
+            total += int(sz.rstrip("KM")) * mult
+    except (OSError, ValueError):
+        pass
+    if total:
+        info["l3_bytes"] = total
+        info["l3_instances"] = len(seen)
+    return info
+
+
 def cpu_baseline(seconds: float, bytes_token: int):
     """janis's amd64 decode path -- the AVX2 per-channel kernel over parallelFor
-    chunks (cpu/qmv_amd64.s, cpu/cpu.go:37-79), restated in oracle/ -- timed on all
-    host cores over one layer of the same shapes plus a 1/8 slice of lm_head."""
+    chunks (cpu/qmv_amd64.s, cpu/cpu.go:37-79), restated in oracle/ -- timed on
+    the host cores of the GPU box over the same decode shapes: whole layers
+    (qkv, o, gate_up, down) plus slices of lm_head, distinct random matrices
+    totalling at least 4x the host's L3 (so every pass streams from DRAM, as
+    the reference does on a real model), each read once per pass."""
     import numpy as np
 
-    from janis_amd import synth
     from oracle import oracle
 
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = min(cores, 16)  # the GPU box's CPU share
-    shapes = [(6144, HIDDEN), (HIDDEN, HIDDEN), (2 * INTER, HIDDEN), (HIDDEN, INTER), (VOCAB // 8, HIDDEN)]
-    mats = [synth.quant_linear(500 + i, n, k) for i, (n, k) in enumerate(shapes)]
-    xs = {k: synth.activations(900 + k, (k,))[1] for k in (HIDDEN, INTER)}
-    sb = [(q.w, q.s, q.b) for q in mats]
-    byt = sum(qbytes(n, k) for n, k in shapes)
-    # one untimed pass, then as many passes as fit in `seconds`
-    for (w, s, b), (n, k) in zip(sb, shapes):
-        oracle.qmv_avx2_parallel(xs[k], w, s, b, GS, cores)
+    info = host_info()
+    # 16 cores: the GPU box's CPU share for one GPU (its scheduler allots 16 per
+    # GPU whatever nproc shows), so the parallelFor split runs over 16 workers
+    cores = min(info["affinity"], 16)
+    target = max(4 * info.get("l3_bytes", 256 << 20), 1 << 30)
+    layer = [(6144, HIDDEN), (HIDDEN, HIDDEN), (2 * INTER, HIDDEN), (HIDDEN, INTER)]
+    rng = np.random.default_rng(77)
+    mats, byt = [], 0
+    while byt < target:
+        for n, k in layer + [(VOCAB // 8, HIDDEN)]:
+            w = rng.integers(0, 1 << 32, size=(n, k // 8), dtype=np.uint32)
+            sc = (np.abs(rng.standard_normal((n, k // GS))) * 0.02).astype(np.float32)
+            bi = (-8.0 * sc + rng.standard_normal((n, k // GS)) * 1e-3).astype(np.float32)
+            mats.append((w, sc, bi, k))
+            byt += qbytes(n, k)
+    xs = {k: rng.standard_normal(k).astype(np.float32) for k in (HIDDEN, INTER)}
+    for w, sc, bi, k in mats[:5]:  # untimed warm-up (page faults, thread start)
+        oracle.qmv_avx2_parallel(xs[k], w, sc, bi, GS, cores)
     t0 = time.perf_counter()
     passes = 0
+    used = cores
     while True:
-        for (w, s, b), (n, k) in zip(sb, shapes):
-            _, used = oracle.qmv_avx2_parallel(xs[k], w, s, b, GS, cores)
+        for w, sc, bi, k in mats:
+            _, used = oracle.qmv_avx2_parallel(xs[k], w, sc, bi, GS, cores)
         passes += 1
         el = time.perf_counter() - t0
         if el >= seconds:
@@ -438,8 +607,10 @@ def cpu_baseline(seconds: float, bytes_token: int):
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": int(used), "kind": "port",
             "avx2": bool(oracle.have_avx2_fma()),
             "tok_s_equiv": round(gbs * 1e9 / bytes_token, 2),
-            "sample": f"{passes} passes over one layer (qkv, o, gate_up, down) + 1/8 of lm_head "
-                      f"({byt / 1e6:.0f} MB), fp32 x, {el:.1f}s"}
+            "host": info,
+            "sample": f"{passes} passes over {len(mats)} distinct matrices (whole Qwen3-8B decode layers + "
+                      f"lm_head slices, {byt / 1e6:.0f} MB >= 4x L3), fp32 x, {el:.1f}s; "
+                      f"{int(used)} workers = the box's 16-core share for one GPU"}
 
 
 if __name__ == "__main__":

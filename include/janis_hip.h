@@ -18,6 +18,15 @@
  * Threading: one context is used by one thread at a time, as janis drives its
  * backend from one engine thread (serve/serve.go:94-105). Distinct contexts are
  * independent.
+ *
+ * Workspace: operators that need device scratch memory (split-K prefill
+ * partials, expert buckets, attention partials, argmax partials) take it from
+ * one per-context workspace that grows on demand. A buffer the workspace grows
+ * out of is kept until jh_destroy, so a HIP graph captured before the growth
+ * still replays into valid memory; growth itself is refused (JH_ERR_INVALID)
+ * while the context's stream is being captured, so make each captured call
+ * once, eagerly, before the capture. Graphs captured on one context share its
+ * workspace: replay them on one stream, not concurrently.
  */
 #ifndef JANIS_HIP_H
 #define JANIS_HIP_H
@@ -51,7 +60,8 @@ enum {
     JH_ERR_INVALID = 1,     /* bad shape, dtype, pointer or argument */
     JH_ERR_UNSUPPORTED = 2, /* valid for the reference, not implemented here */
     JH_ERR_HIP = 3,         /* the HIP runtime reported an error */
-    JH_ERR_OOM = 4          /* device allocation failed */
+    JH_ERR_OOM = 4,         /* device allocation failed */
+    JH_ERR_NONFINITE = 5    /* value checks on (JH_CHECK_VALUES): the result holds NaN/Inf */
 };
 
 typedef struct jh_ctx jh_ctx;
@@ -84,12 +94,33 @@ JH_API int jh_set_stream(jh_ctx *ctx, void *hip_stream);
 /* The hipStream_t operators are enqueued on. */
 JH_API void *jh_get_stream(const jh_ctx *ctx);
 
-/* When on, jh_gather_quant_matmul copies the expert indices to the host and
- * rejects out-of-range ones with JH_ERR_INVALID before launching, as
- * JANIS_GGML_CHECK turns on read-back checks (ggml/ggml.go:622-677). When off
- * (default) an out-of-range index yields a row of NaN and no memory outside
- * the expert stack is read. */
-JH_API int jh_set_checks(jh_ctx *ctx, int on);
+/* Check flags of jh_set_checks. */
+#define JH_CHECK_INDICES 1 /* device indices (expert ids, row ids) read back and range-checked */
+#define JH_CHECK_VALUES 2  /* every float result read back and counted for NaN/Inf */
+
+/* Read-back checks, the equivalent of janis's JANIS_GGML_CHECK
+ * (ggml/ggml.go:622-677), off by default. flags is a combination of:
+ *   JH_CHECK_INDICES  jh_gather_quant_matmul, jh_moe_swiglu and jh_take_rows
+ *                     copy their indices to the host and reject an out-of-range
+ *                     one with JH_ERR_INVALID before launching. When off, an
+ *                     out-of-range expert index yields a row of NaN (a row id,
+ *                     a row of zeros) and no memory outside the table is read.
+ *   JH_CHECK_VALUES   after each operator with a float result (the quantized
+ *                     products, the fused products, the decode-step operators,
+ *                     Softmax/Mean/Scalar), the result is counted for NaN/Inf
+ *                     on the device and any found is JH_ERR_NONFINITE naming
+ *                     the operator, the count and the first index. The
+ *                     reference reports the same and exits; here the caller
+ *                     decides.
+ * Both wait for the stream, so they refuse (JH_ERR_INVALID) a stream under
+ * graph capture. jh_set_checks(ctx, 1) keeps its earlier meaning. */
+JH_API int jh_set_checks(jh_ctx *ctx, int flags);
+
+/* Counts the NaN/Inf among n device values of dtype (JH_F32, JH_BF16, JH_F16):
+ * *count, and *first = the first index of one (n when none). Waits for the
+ * stream. The check a caller can run on any tensor before Floats. */
+JH_API int jh_check_finite(jh_ctx *ctx, const void *x, jh_dtype dtype, int64_t n, int64_t *count,
+                           int64_t *first);
 
 /* Waits for every operator enqueued on the context's stream. */
 JH_API int jh_sync(jh_ctx *ctx);
@@ -135,10 +166,14 @@ JH_API int jh_dequantize(jh_ctx *ctx, const uint32_t *w, const void *scales, con
                   jh_dtype sb_dtype, int64_t rows, int64_t in_features, int group_size, int bits,
                   void *out, jh_dtype out_dtype);
 
-/* Backend.QuantMatmul (engine/backend.go:265-267; cpu/cpu_misc.go:232-400)
- * with transpose != 0 (the QuantizedLinear convention, the only one the models
- * use; transpose == 0 returns JH_ERR_UNSUPPORTED):
+/* Backend.QuantMatmul (engine/backend.go:265-267; cpu/cpu_misc.go:232-400).
+ * transpose != 0 (the QuantizedLinear convention, the one the models use):
  *   y[rows, out_features] = x[rows, in_features] . W^T
+ * transpose == 0 (the CPU backend's MatMul(x, Dequantize(w)), :233-236):
+ *   y[rows, in_features] = x[rows, out_features] . Dequantize(W)
+ *   with the CPU backend's order (each output a sum over the out_features rows
+ *   in increasing order, terms rounded then added, zero x terms skipped), so its
+ *   fp32 results have the CPU backend's bits; a slow path, off the models' path.
  * x_dtype and y_dtype are JH_BF16 or JH_F32; accumulation is fp32. rows == 1
  * runs the decode GEMV; 2..8 bf16 rows (2..4 for in_features 768, 1536, 3072,
  * 6144, 12288 and 16384) run the decode GEMV's tiles with every row's x in
@@ -153,7 +188,7 @@ JH_API int jh_quant_matmul(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t
                     jh_dtype y_dtype);
 
 /* Backend.GatherQuantMatmul (engine/backend.go:269-274; cpu/cpu_misc.go:178-230),
- * the MoE expert product, with transpose != 0:
+ * the MoE expert product. transpose != 0:
  *   x            [n_lead, a_vectors, in_features]  (the reference's [lead.., A, 1, in]);
  *                a_vectors == 1 shares one vector across the k_slots experts,
  *                a_vectors == k_slots gives each slot its own vector;
@@ -163,7 +198,12 @@ JH_API int jh_quant_matmul(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t
  * Slots are bucketed by expert on the device, so each routed expert's packed
  * weights are read once per call whatever the number of slots routed to it,
  * and experts nobody routed to are not read. One call = one bucketing launch
- * plus one product launch. */
+ * plus one product launch.
+ * transpose == 0: each slot is the transposed product of jh_quant_matmul with
+ * its expert's matrix (cpu/cpu_misc.go:224 with :233-236): x [n_lead,
+ * a_vectors, out_features], y [n_lead, k_slots, in_features]. (The reference
+ * sizes that result's rows by the stack's out_features, which agrees when the
+ * experts are square.) */
 JH_API int jh_gather_quant_matmul(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t n_lead,
                            int64_t a_vectors, const uint32_t *w, const void *scales,
                            const void *biases, jh_dtype sb_dtype, int64_t n_experts,
@@ -338,6 +378,29 @@ JH_API int jh_moe_swiglu(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t n
                   jh_dtype sb_dtype, int64_t n_experts, int64_t hidden, int64_t intermediate,
                   const int32_t *rhs_indices, const float *scores, int64_t k_slots,
                   int group_size, int bits, void *out, jh_dtype out_dtype);
+
+/* Backend.Softmax (engine/backend.go:241-242; cpu/cpu.go:461-499) along the
+ * middle axis of x viewed as [outer, len, inner] (axis a of a shape d: outer =
+ * d0..d(a-1), len = d(a), inner = d(a+1)..): the maximum, e = exp(x - max) in
+ * double rounded to fp32, e / sum(e), with the CPU backend's sequential fp32
+ * sum for len <= 8192 (bit-identical; longer lines sum in a tree). y is fp32
+ * of x's shape. The router softmax of MoEBlock.Forward (qwen/moe.go:458). */
+JH_API int jh_softmax(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t outer, int64_t len, int64_t inner,
+                      float *y);
+
+/* Backend.Mean (engine/backend.go:186; cpu/cpu_ops.go:113-142) over the middle
+ * axis of [outer, len, inner]: y [outer, inner] fp32, each the sequential fp32
+ * sum along the axis divided by len (bit-identical to the CPU backend). */
+JH_API int jh_mean(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t outer, int64_t len, int64_t inner,
+                   float *y);
+
+/* Backend.ScalarMul / ScalarAdd (engine/backend.go:250-252; cpu/cpu_misc.go:24-30). */
+typedef enum {
+    JH_SCALAR_MUL = 0, /* y = x * v */
+    JH_SCALAR_ADD = 1  /* y = x + v */
+} jh_scalar_op;
+JH_API int jh_scalar(jh_ctx *ctx, jh_scalar_op op, const void *x, jh_dtype x_dtype, int64_t n, float v, void *y,
+                     jh_dtype y_dtype);
 
 /* Prologues and epilogues of jh_quant_matvec_fused. */
 typedef enum {

@@ -13,7 +13,9 @@ LIB_PATH = os.path.join(HERE, "libjanis_hip.so")
 
 # engine.DType (engine/backend.go:11-21)
 F32, F16, BF16, I32, U32, U8 = range(6)
-JH_OK, JH_ERR_INVALID, JH_ERR_UNSUPPORTED, JH_ERR_HIP, JH_ERR_OOM = range(5)
+JH_OK, JH_ERR_INVALID, JH_ERR_UNSUPPORTED, JH_ERR_HIP, JH_ERR_OOM, JH_ERR_NONFINITE = range(6)
+JH_CHECK_INDICES, JH_CHECK_VALUES = 1, 2  # jh_set_checks flags
+JH_SCALAR_MUL, JH_SCALAR_ADD = 0, 1  # jh_scalar_op
 JH_OP_ADD, JH_OP_MUL, JH_OP_SILU, JH_OP_SILU_MUL = range(4)  # jh_op
 JH_PRO_NONE, JH_PRO_RMSNORM, JH_PRO_SILU_MUL, JH_PRO_NORMED = range(4)  # jh_prologue
 JH_EPI_STORE, JH_EPI_RESID, JH_EPI_SWIGLU, JH_EPI_RESID_NORM = range(4)  # jh_epilogue
@@ -26,6 +28,7 @@ EXPORTS = [
     "jh_moe_route", "jh_moe_swiglu", "jh_rms_norm", "jh_rope", "jh_sdpa", "jh_elementwise", "jh_argmax",
     "jh_take_rows", "jh_kv_append", "jh_qk_norm_rope_append", "jh_quant_matvec_fused",
     "jh_attention_decode", "jh_rope_table", "jh_norm_prepare", "jh_copy_strided", "jh_scatter_rows",
+    "jh_softmax", "jh_mean", "jh_scalar", "jh_check_finite",
 ]
 
 _lib = None
@@ -103,6 +106,12 @@ def load() -> ctypes.CDLL:
     for name in ("jh_rms_norm", "jh_rope", "jh_sdpa", "jh_elementwise", "jh_argmax", "jh_take_rows", "jh_kv_append",
                  "jh_qk_norm_rope_append", "jh_quant_matvec_fused", "jh_attention_decode", "jh_rope_table",
                  "jh_norm_prepare", "jh_copy_strided", "jh_scatter_rows"):
+        getattr(L, name).restype = i
+    L.jh_softmax.argtypes = [c_ctx, p, i, i64, i64, i64, p]
+    L.jh_mean.argtypes = [c_ctx, p, i, i64, i64, i64, p]
+    L.jh_scalar.argtypes = [c_ctx, i, p, i, i64, f32, p, i]
+    L.jh_check_finite.argtypes = [c_ctx, p, i, i64, ctypes.POINTER(i64), ctypes.POINTER(i64)]
+    for name in ("jh_softmax", "jh_mean", "jh_scalar", "jh_check_finite"):
         getattr(L, name).restype = i
     L.jh_moe_route.argtypes = [c_ctx, p, i, i64, i64, i64, i, p, p]
     L.jh_moe_route.restype = i

@@ -3,8 +3,9 @@
     python -m janis_amd.build
 
 Every HIP source under janis_amd/csrc/ is compiled separately (in parallel)
-and linked into janis_amd/libjanis_hip.so. The library exports only the C ABI
-declared in include/janis_hip.h.
+and linked into janis_amd/libjanis_hip.so, which exports only the C ABI
+declared in include/janis_hip.h; bench_kernels.hip (bench.py's plain-read and
+copy kernels) becomes janis_amd/libjanis_bench.so.
 """
 from __future__ import annotations
 
@@ -18,7 +19,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libjanis_hip.so")
-SOURCES = ["runtime.hip", "qmv.hip", "qmm.hip", "gather.hip", "dequant.hip", "decode.hip"]
+SOURCES = ["runtime.hip", "qmv.hip", "qmm.hip", "gather.hip", "dequant.hip", "decode.hip", "ops.hip"]
+# bench.py's measurement kernels (plain read, copy): a library of their own,
+# outside the backend's C ABI
+BENCH_SOURCE = "bench_kernels.hip"
+BENCH_LIB = os.path.join(HERE, "libjanis_bench.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -40,20 +45,24 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compile and link; always rebuilds. Returns the library path."""
-    os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", tmp, *objs,
-           "-Wl,--version-script=" + os.path.join(CSRC, "exports.map")]
+def _link(objs, out, extra=()) -> None:
+    tmp = out + ".tmp"
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", tmp, *objs, *extra]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile and link both libraries; always rebuilds. Returns the backend's path."""
+    os.makedirs(BUILD, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES) + 1, os.cpu_count() or 4)) as ex:
+        objs = list(ex.map(_compile, SOURCES + [BENCH_SOURCE]))
+    _link(objs[:-1], LIB, ["-Wl,--version-script=" + os.path.join(CSRC, "exports.map")])
+    _link(objs[-1:], BENCH_LIB)
     if verbose:
-        print("built", LIB)
+        print("built", LIB, "and", BENCH_LIB)
     return LIB
 
 

@@ -1,0 +1,86 @@
+// Measurement kernels for bench.py (libjanis_bench.so; not part of the
+// backend's C ABI): a plain streaming read and a copy of device memory. They do
+// nothing but move bytes, so their time for a given byte count is the floor a
+// decode product reading that many bytes in one launch can reach, and the copy
+// gives the device's measured bandwidth beside the 8 TB/s specification.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Every block reads UNROLL 16-byte chunks per lane per step, all issued before
+// any is used (the way the decode tiles issue a pass's weight loads), and
+// strides over the buffer by the grid. The loaded words are folded into one
+// value that is stored only if it equals a constant, so the loads stay.
+template <int UNROLL>
+__global__ __launch_bounds__(256) void read_kernel(const u32x4* __restrict__ src, int64_t n16,
+                                                   uint32_t* __restrict__ sink) {
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    const int64_t step = (int64_t)gridDim.x * 256 * UNROLL;
+    for (int64_t base = (int64_t)blockIdx.x * 256 * UNROLL + threadIdx.x; base < n16; base += step) {
+        u32x4 v[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; u++) {
+            const int64_t i = base + (int64_t)u * 256;
+            v[u] = i < n16 ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; u++) acc ^= v[u];
+    }
+    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9e3779b9u) sink[0] = acc.x;
+}
+
+template <int UNROLL>
+__global__ __launch_bounds__(256) void copy_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ src,
+                                                   int64_t n16) {
+    const int64_t step = (int64_t)gridDim.x * 256 * UNROLL;
+    for (int64_t base = (int64_t)blockIdx.x * 256 * UNROLL + threadIdx.x; base < n16; base += step) {
+        u32x4 v[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; u++) {
+            const int64_t i = base + (int64_t)u * 256;
+            if (i < n16) v[u] = __builtin_nontemporal_load(src + i);
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; u++) {
+            const int64_t i = base + (int64_t)u * 256;
+            if (i < n16) __builtin_nontemporal_store(v[u], dst + i);
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+// Reads `bytes` (a multiple of 16, 16-byte aligned) at src with `blocks`
+// blocks of 256 threads and `unroll` (4, 8 or 16) loads per lane in flight, on
+// `stream`. Returns 0, or the HIP error code.
+__attribute__((visibility("default"))) int jhb_read(const void* src, int64_t bytes, void* sink, int blocks,
+                                                    int unroll, void* stream) {
+    if (bytes <= 0 || (bytes & 15) || ((uintptr_t)src & 15) || blocks <= 0) return (int)hipErrorInvalidValue;
+    const int64_t n16 = bytes / 16;
+    auto st = static_cast<hipStream_t>(stream);
+    auto s = static_cast<const u32x4*>(src);
+    auto k = static_cast<uint32_t*>(sink);
+    if (unroll == 4) hipLaunchKernelGGL(read_kernel<4>, dim3(blocks), dim3(256), 0, st, s, n16, k);
+    else if (unroll == 8) hipLaunchKernelGGL(read_kernel<8>, dim3(blocks), dim3(256), 0, st, s, n16, k);
+    else if (unroll == 16) hipLaunchKernelGGL(read_kernel<16>, dim3(blocks), dim3(256), 0, st, s, n16, k);
+    else return (int)hipErrorInvalidValue;
+    return (int)hipGetLastError();
+}
+
+// Copies `bytes` (a multiple of 16, both pointers 16-byte aligned) src -> dst.
+__attribute__((visibility("default"))) int jhb_copy(void* dst, const void* src, int64_t bytes, int blocks,
+                                                    void* stream) {
+    if (bytes <= 0 || (bytes & 15) || ((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || blocks <= 0)
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(copy_kernel<4>, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<u32x4*>(dst), static_cast<const u32x4*>(src), bytes / 16);
+    return (int)hipGetLastError();
+}
+
+}  // extern "C"

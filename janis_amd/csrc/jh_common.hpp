@@ -337,4 +337,17 @@ const char* moe_unsupported(const MoeMlpArgs& a);
 size_t moe_workspace_bytes(const MoeMlpArgs& a);
 Status launch_moe_mlp(const MoeMlpArgs& a, void* workspace, hipStream_t st);
 
+// ---- operators around the products (ops.hip) ----
+// QuantMatmul with transpose = false: y [rows, m.in] = x [rows, m.rows] . Dequantize(W);
+// with idx, the gather form over a stack of n_experts (rows = the slot pairs).
+Status launch_quant_matmul_t(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y, int y_dtype,
+                             const int32_t* idx, int64_t n_experts, int64_t k_slots, int64_t a_vectors,
+                             hipStream_t st);
+// Softmax / Mean along the middle axis of an [outer, len, inner] view, fp32 out.
+Status launch_softmax(const void* x, int x_dt, float* y, int64_t outer, int64_t len, int64_t inner, hipStream_t st);
+Status launch_mean(const void* x, int x_dt, float* y, int64_t outer, int64_t len, int64_t inner, hipStream_t st);
+Status launch_scalar(int op, const void* x, int x_dt, float v, void* y, int y_dt, int64_t n, hipStream_t st);
+// res[0] += NaN/Inf count, res[1] = min(res[1], first index of one).
+Status launch_nonfinite(const void* x, int x_dt, int64_t n, unsigned long long* res, hipStream_t st);
+
 }  // namespace jh

@@ -794,13 +794,15 @@ Status run_rows(const QuantMatrix& m, const uint16_t* x, int64_t rows, void* y, 
     return run_rows_mr<LPR, ITERS, RPW, KSPLIT, SB_F16, 2>(m, x, rows, y, y_dtype, gl, num_cus, st);
 }
 
-// 16-byte weight loads per lane and row of the decode tile for a row length.
+// 16-byte weight loads per lane and row of the multi-row tile for a 4-bit row
+// length, or 0 when no multi-row tile takes it.
 int tile_iters(int64_t row_words) {
     switch (row_words) {
+        case 512 * 1: case 256 * 1: case 128 * 1: case 64 * 1: case 32 * 1: return 1;
         case 512 * 2: return 2;
-        case 512 * 3: case 256 * 3: case 128 * 3: case 64 * 3: case 32 * 3: return 3;
+        case 512 * 3: case 256 * 3: case 128 * 3: case 64 * 3: case 32 * 3: case 512 * 6: return 3;
         case 512 * 4: return 4;
-        default: return 1;
+        default: return 0;
     }
 }
 
@@ -809,11 +811,13 @@ int tile_iters(int64_t row_words) {
 // Up to 8 rows (4 for tiles whose lanes hold 96 or 128 elements of each row):
 // beyond that the prefill GEMM is faster (measured on MI355X for the Qwen3-8B
 // shapes: gate/up 12288 x 4096 at 8 rows 23.5 us against 28.4 for the GEMM;
-// down 4096 x 12288 at 4 rows 20.9 against 32.2, at 8 rows 42.2).
+// down 4096 x 12288 at 4 rows 20.9 against 32.2, at 8 rows 42.2). Only row
+// lengths with a case in launch_qmv_rows are accepted (tile_iters > 0).
 bool qmv_rows_ok(const QuantMatrix& m, int64_t rows, int x_dtype) {
     if (x_dtype != JH_BF16 || m.bits != 4 || rows < 2 || !qmv_fast_shape(m) || rows * m.in * 2 >= ((int64_t)1 << 31))
         return false;
-    return rows <= (tile_iters(row_words(m)) >= 3 ? 4 : kQmvRowsMax);
+    const int it = tile_iters(row_words(m));
+    return it > 0 && rows <= (it >= 3 ? 4 : kQmvRowsMax);
 }
 
 Status launch_qmv_rows(const QuantMatrix& m, const void* x, int64_t rows, void* y, int y_dtype, int num_cus,
@@ -824,11 +828,18 @@ Status launch_qmv_rows(const QuantMatrix& m, const void* x, int64_t rows, void* 
 #define JH_ROWS(L, I, R, KS)                                                                   \
     return m.sb_dtype == JH_F16 ? run_rows<L, I, R, KS, true>(m, xb, rows, y, y_dtype, gl, num_cus, st) \
                                 : run_rows<L, I, R, KS, false>(m, xb, rows, y, y_dtype, gl, num_cus, st)
+    // Each case keeps the one-row tile's lanes per row (L), loads per lane (I)
+    // and K split (KS) for that row length, so a row's reduction order -- and
+    // its bits -- are those of a one-row call; only the rows per slice (R) may
+    // differ. The lm_head-sized matrix takes the one-row special case's 64-lane,
+    // 2-way split (4 rows per slice instead of 8, for registers).
+    if (m.in == 4096 && m.rows >= 65536) JH_ROWS(64, 1, 4, 2);
     switch (row_words(m)) {
         case 512 * 1: JH_ROWS(32, 1, 4, 4);
         case 512 * 2: JH_ROWS(32, 2, 2, 4);
         case 512 * 3: JH_ROWS(32, 3, 2, 4);
         case 512 * 4: JH_ROWS(32, 4, 2, 4);
+        case 512 * 6: JH_ROWS(64, 3, 2, 4);
         case 256 * 1: JH_ROWS(32, 1, 4, 2);
         case 256 * 3: JH_ROWS(32, 3, 2, 2);
         case 128 * 1: JH_ROWS(16, 1, 4, 2);

@@ -21,8 +21,13 @@ struct jh_ctx {
     int checks = 0;
     char name[256] = {0};
     std::string err;
-    void* ws = nullptr;  // gather bucketing workspace, grown on demand
+    void* ws = nullptr;  // operator workspace, grown on demand
     size_t ws_bytes = 0;
+    // Workspaces replaced by a larger one. They stay allocated until jh_destroy:
+    // a HIP graph captured earlier holds their address in its launches, and
+    // replaying it must not touch memory that was freed (or reused since).
+    std::vector<void*> retired;
+    unsigned long long* check_buf = nullptr;  // 2 counters of the value checks
 };
 
 namespace {
@@ -55,21 +60,32 @@ int enter(jh_ctx* c) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Grows the context's workspace to at least `need` bytes (power of two, >= 4 KiB).
+// The old buffer is retired, not freed (graphs captured before may replay into
+// it), so growth never waits for the stream. Growth while the context's stream
+// is being captured is refused: an allocation is not a stream operation, and a
+// graph must not depend on one made during its capture; one eager call of the
+// same operator and size before the capture sizes the workspace.
 int ensure_workspace(jh_ctx* c, size_t need, const char* op) {
     if (need <= c->ws_bytes) return JH_OK;
-    if (c->ws) {
-        JH_HIP(c, hipStreamSynchronize(c->stream));
-        JH_HIP(c, hipFree(c->ws));
-        c->ws = nullptr;
-        c->ws_bytes = 0;
-    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    JH_HIP(c, hipStreamIsCapturing(c->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(c, JH_ERR_INVALID,
+                    std::string(op) + ": needs a workspace of " + std::to_string(need) + " bytes while the stream is " +
+                        "being captured (the context holds " + std::to_string(c->ws_bytes) +
+                        "); make the same call once before the capture");
+    if (need > ((size_t)1 << 62)) return fail(c, JH_ERR_OOM, std::string(op) + ": workspace size overflows");
     size_t cap = 4096;
     while (cap < need) cap *= 2;
-    if (hipMalloc(&c->ws, cap) != hipSuccess) {
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, cap);
+    if (e != hipSuccess) {
         (void)hipGetLastError();
-        c->ws = nullptr;
-        return fail(c, JH_ERR_OOM, std::string(op) + ": workspace allocation failed");
+        return fail(c, JH_ERR_OOM, std::string(op) + ": workspace allocation of " + std::to_string(cap) +
+                                       " bytes failed (" + hipGetErrorString(e) + ")");
     }
+    if (c->ws) c->retired.push_back(c->ws);
+    c->ws = p;
     c->ws_bytes = cap;
     return JH_OK;
 }
@@ -109,6 +125,97 @@ int finish(jh_ctx* c, const jh::Status& s, const char* op) {
     if (s.code != JH_OK) return fail(c, s.code, s.msg);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(c, e, op);
+    return JH_OK;
+}
+
+// Read-back checks wait for the stream, which a stream under capture cannot do.
+int checks_not_capturing(jh_ctx* c, const char* op) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    JH_HIP(c, hipStreamIsCapturing(c->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(c, JH_ERR_INVALID,
+                    std::string(op) + ": checks read results back to the host; turn them off (jh_set_checks) "
+                                      "while capturing a graph");
+    return JH_OK;
+}
+
+// With JH_CHECK_INDICES: device int32 indices copied to the host and each
+// checked against [0, limit) before anything is launched.
+int check_indices(jh_ctx* c, const char* op, const int32_t* idx, int64_t n, int64_t limit, const char* what) {
+    if (!(c->checks & JH_CHECK_INDICES) || n <= 0) return JH_OK;
+    if (int r = checks_not_capturing(c, op)) return r;
+    std::vector<int32_t> h((size_t)n);
+    JH_HIP(c, hipMemcpyAsync(h.data(), idx, h.size() * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+    JH_HIP(c, hipStreamSynchronize(c->stream));
+    for (size_t i = 0; i < h.size(); i++)
+        if (h[i] < 0 || h[i] >= limit)
+            return fail(c, JH_ERR_INVALID, std::string(op) + ": " + what + " " + std::to_string(h[i]) + " at " +
+                                               std::to_string(i) + " outside [0, " + std::to_string(limit) + ")");
+    return JH_OK;
+}
+
+// Counts the NaN/Inf among n values of a float type on the device: count and
+// the first index (n when none). Waits for the stream.
+int count_nonfinite(jh_ctx* c, const char* op, const void* p, int dt, int64_t n, int64_t* count, int64_t* first) {
+    if (int r = checks_not_capturing(c, op)) return r;
+    if (!c->check_buf) {
+        void* b = nullptr;
+        if (hipMalloc(&b, 2 * sizeof(unsigned long long)) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(c, JH_ERR_OOM, std::string(op) + ": no room for the check counters");
+        }
+        c->check_buf = static_cast<unsigned long long*>(b);
+    }
+    const unsigned long long init[2] = {0ull, (unsigned long long)n};
+    unsigned long long res[2] = {0ull, 0ull};
+    JH_HIP(c, hipMemcpyAsync(c->check_buf, init, sizeof(init), hipMemcpyHostToDevice, c->stream));
+    if (int r = finish(c, jh::launch_nonfinite(p, dt, n, c->check_buf, c->stream), "nonfinite_kernel")) return r;
+    JH_HIP(c, hipMemcpyAsync(res, c->check_buf, sizeof(res), hipMemcpyDeviceToHost, c->stream));
+    JH_HIP(c, hipStreamSynchronize(c->stream));
+    *count = (int64_t)res[0];
+    *first = (int64_t)res[1];
+    return JH_OK;
+}
+
+// With JH_CHECK_VALUES, an operator's result is counted for NaN/Inf after it
+// runs, as JANIS_GGML_CHECK reads every fp32 result back (ggml/ggml.go:622-677);
+// any found is JH_ERR_NONFINITE, naming the operator, the count and the first
+// index. The reference exits the process there; here the caller decides.
+int check_values(jh_ctx* c, const char* op, const void* y, int dt, int64_t n) {
+    if (!(c->checks & JH_CHECK_VALUES) || n <= 0) return JH_OK;
+    int64_t bad = 0, first = 0;
+    if (int r = count_nonfinite(c, op, y, dt, n, &bad, &first)) return r;
+    if (bad)
+        return fail(c, JH_ERR_NONFINITE, std::string(op) + ": " + std::to_string(bad) + " of " + std::to_string(n) +
+                                             " values NaN/Inf in the result, the first at index " +
+                                             std::to_string(first));
+    return JH_OK;
+}
+
+}  // namespace
+
+namespace {
+
+int check_attention(jh_ctx* c, const char* op, const void* qkv, jh_dtype qkv_dtype, int64_t n_heads,
+                    int64_t n_kv_heads, int64_t head_dim, const void* q_norm_w, const void* k_norm_w,
+                    jh_dtype w_dtype, int64_t pos, const void* k_cache, const void* v_cache, jh_dtype cache_dtype,
+                    int64_t capacity, const void* out, jh_dtype out_dtype) {
+    if (int r = check_act_dtype(c, op, "qkv", qkv_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "out", out_dtype)) return r;
+    if (head_dim != 128) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": head_dim must be 128");
+    if (cache_dtype != JH_BF16) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": the caches must be bf16");
+    if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads || n_heads > 65536)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad head counts");
+    const int64_t G = n_heads / n_kv_heads;
+    if (G != 1 && G != 2 && G != 4 && G != 8)
+        return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": n_heads / n_kv_heads must be 1, 2, 4 or 8");
+    if ((q_norm_w || k_norm_w) && w_dtype != JH_BF16 && w_dtype != JH_F16 && w_dtype != JH_F32)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": norm weights must be bf16, f16 or f32");
+    if (pos < 0 || pos >= capacity || capacity > 0x7fffffff)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": pos " + std::to_string(pos) + " outside the cache capacity " +
+                                           std::to_string(capacity));
+    if (!qkv || !out || !k_cache || !v_cache || !aligned16(k_cache) || !aligned16(v_cache))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer, or caches not 16-byte aligned");
     return JH_OK;
 }
 
@@ -164,6 +271,8 @@ void jh_destroy(jh_ctx* c) {
     if (c->own_stream) (void)hipStreamSynchronize(c->own_stream);
     if (c->stream && c->stream != c->own_stream) (void)hipStreamSynchronize(c->stream);
     if (c->ws) (void)hipFree(c->ws);
+    for (void* p : c->retired) (void)hipFree(p);
+    if (c->check_buf) (void)hipFree(c->check_buf);
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     delete c;
 }
@@ -188,10 +297,25 @@ int jh_set_stream(jh_ctx* c, void* s) {
 
 void* jh_get_stream(const jh_ctx* c) { return c ? static_cast<void*>(c->stream) : nullptr; }
 
-int jh_set_checks(jh_ctx* c, int on) {
+int jh_set_checks(jh_ctx* c, int flags) {
     if (int r = enter(c)) return r;
-    c->checks = on != 0;
+    if (flags & ~(JH_CHECK_INDICES | JH_CHECK_VALUES))
+        return fail(c, JH_ERR_INVALID, "jh_set_checks: unknown check flags " + std::to_string(flags));
+    c->checks = flags;
     return JH_OK;
+}
+
+int jh_check_finite(jh_ctx* c, const void* x, jh_dtype dtype, int64_t n, int64_t* count, int64_t* first) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_check_finite";
+    if (dtype != JH_F32 && dtype != JH_BF16 && dtype != JH_F16)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": dtype must be f32, bf16 or f16");
+    if (n < 0 || !count || !first) return fail(c, JH_ERR_INVALID, std::string(op) + ": bad arguments");
+    *count = 0;
+    *first = n;
+    if (n == 0) return JH_OK;
+    if (!x) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    return count_nonfinite(c, op, x, dtype, n, count, first);
 }
 
 int jh_sync(jh_ctx* c) {
@@ -251,7 +375,8 @@ int jh_dequantize(jh_ctx* c, const uint32_t* w, const void* scales, const void* 
     if (rows == 0) return JH_OK;
     if (!out || !aligned16(out)) return fail(c, JH_ERR_INVALID, "jh_dequantize: out must be 16-byte aligned");
     jh::QuantMatrix m{w, scales, biases, sb_dtype, rows, in_features, group_size, bits};
-    return finish(c, jh::launch_dequantize(m, out, out_dtype, c->stream), "dequant_kernel");
+    if (int r = finish(c, jh::launch_dequantize(m, out, out_dtype, c->stream), "dequant_kernel")) return r;
+    return check_values(c, "jh_dequantize", out, out_dtype, rows * in_features);
 }
 
 int jh_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, const uint32_t* w,
@@ -259,28 +384,40 @@ int jh_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, co
                     int64_t in_features, int transpose, int group_size, int bits, void* y,
                     jh_dtype y_dtype) {
     if (int r = enter(c)) return r;
-    if (!transpose)
-        return fail(c, JH_ERR_UNSUPPORTED,
-                    "jh_quant_matmul: transpose=false (x @ Dequantize(w)) is not implemented; "
-                    "the models only use transpose=true");
-    if (int r = check_quant(c, "jh_quant_matmul", w, scales, biases, sb_dtype, out_features,
-                            in_features, group_size, bits))
+    const char* op = "jh_quant_matmul";
+    if (int r = check_quant(c, op, w, scales, biases, sb_dtype, out_features, in_features, group_size, bits))
         return r;
-    if (int r = check_act_dtype(c, "jh_quant_matmul", "x", x_dtype)) return r;
-    if (int r = check_act_dtype(c, "jh_quant_matmul", "y", y_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "y", y_dtype)) return r;
     if (rows < 0) return fail(c, JH_ERR_INVALID, "jh_quant_matmul: rows < 0");
+    jh::QuantMatrix m{w, scales, biases, sb_dtype, out_features, in_features, group_size, bits};
+    if (!transpose) {
+        // MatMul(x, Dequantize(w)) (cpu/cpu_misc.go:233-236): x [rows, out_features],
+        // y [rows, in_features]
+        if (rows == 0 || in_features == 0) return JH_OK;
+        if (!x || !y || (out_features > 0 && !w)) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+        if (rows > 0x7fffffff) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": too many rows");
+        if (int r = finish(c, jh::launch_quant_matmul_t(m, x, x_dtype, rows, y, y_dtype, nullptr, 1, 1, 1, c->stream),
+                           "qmt"))
+            return r;
+        return check_values(c, op, y, y_dtype, rows * in_features);
+    }
     if (rows == 0 || out_features == 0) return JH_OK;
     if (!x || !y || !aligned16(x) || !aligned16(y))
         return fail(c, JH_ERR_INVALID, "jh_quant_matmul: x and y must be non-null and 16-byte aligned");
-    jh::QuantMatrix m{w, scales, biases, sb_dtype, out_features, in_features, group_size, bits};
+    int r;
     if (rows == 1)
-        return finish(c, jh::launch_qmv(m, x, x_dtype, y, y_dtype, c->num_cus, c->stream), "qmv");
-    if (jh::qmv_rows_ok(m, rows, x_dtype))
-        return finish(c, jh::launch_qmv_rows(m, x, rows, y, y_dtype, c->num_cus, c->stream), "qmv_rows");
-    const size_t need = jh::qmm_workspace_bytes(m, rows, x_dtype, y_dtype, c->num_cus);
-    if (need)
-        if (int r = ensure_workspace(c, need, "jh_quant_matmul")) return r;
-    return finish(c, jh::launch_qmm(m, x, x_dtype, rows, y, y_dtype, c->num_cus, c->stream, c->ws), "qmm");
+        r = finish(c, jh::launch_qmv(m, x, x_dtype, y, y_dtype, c->num_cus, c->stream), "qmv");
+    else if (jh::qmv_rows_ok(m, rows, x_dtype))
+        r = finish(c, jh::launch_qmv_rows(m, x, rows, y, y_dtype, c->num_cus, c->stream), "qmv_rows");
+    else {
+        const size_t need = jh::qmm_workspace_bytes(m, rows, x_dtype, y_dtype, c->num_cus);
+        if (need)
+            if (int e = ensure_workspace(c, need, op)) return e;
+        r = finish(c, jh::launch_qmm(m, x, x_dtype, rows, y, y_dtype, c->num_cus, c->stream, c->ws), "qmm");
+    }
+    if (r) return r;
+    return check_values(c, op, y, y_dtype, rows * out_features);
 }
 
 int jh_quant_matvec_fused(jh_ctx* c, jh_prologue pro, const void* x, jh_dtype x_dtype, const void* norm_w,
@@ -324,9 +461,10 @@ int jh_quant_matvec_fused(jh_ctx* c, jh_prologue pro, const void* x, jh_dtype x_
     jh::NormSplit ns;
     ns.stats = norm_stats;
     ns.out = static_cast<uint16_t*>(norm_out);
-    return finish(c, jh::launch_qmv_fused(m, (int)pro, x, x_dtype, norm_w, norm_w_dtype, eps, (int)epi, resid, y,
+    if (int r = finish(c, jh::launch_qmv_fused(m, (int)pro, x, x_dtype, norm_w, norm_w_dtype, eps, (int)epi, resid, y,
                                           y_dtype, ns, c->num_cus, c->stream, c->ws),
-                  op);
+                  op)) return r;
+    return check_values(c, op, y, y_dtype, out_features);
 }
 
 int jh_norm_prepare(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t d, const void* norm_w, jh_dtype norm_w_dtype,
@@ -351,7 +489,6 @@ int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n
                            jh_dtype y_dtype) {
     if (int r = enter(c)) return r;
     const char* op = "jh_gather_quant_matmul";
-    if (!transpose) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": transpose=false is not implemented");
     if (int r = check_quant(c, op, w, scales, biases, sb_dtype, out_features, in_features,
                             group_size, bits))
         return r;
@@ -367,17 +504,17 @@ int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n
     if (n_pairs > (int64_t)1 << 30) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": too many slots");
     if (!x || !y || !rhs_indices || !aligned16(x) || !aligned16(y))
         return fail(c, JH_ERR_INVALID, std::string(op) + ": null or unaligned x / y / indices");
-    if (c->checks) {
-        std::vector<int32_t> h((size_t)n_pairs);
-        JH_HIP(c, hipMemcpyAsync(h.data(), rhs_indices, h.size() * sizeof(int32_t),
-                                 hipMemcpyDeviceToHost, c->stream));
-        JH_HIP(c, hipStreamSynchronize(c->stream));
-        for (size_t i = 0; i < h.size(); i++)
-            if (h[i] < 0 || h[i] >= n_experts)
-                return fail(c, JH_ERR_INVALID,
-                            std::string(op) + ": expert index " + std::to_string(h[i]) +
-                                " at slot " + std::to_string(i) + " outside [0, " +
-                                std::to_string(n_experts) + ")");
+    if (int r = check_indices(c, op, rhs_indices, n_pairs, n_experts, "expert index")) return r;
+    if (!transpose) {
+        // per slot MatMul(x_slot, Dequantize(W_e)) (cpu/cpu_misc.go:224 with
+        // :233-236): x [n_lead, a_vectors, out_features], y [n_pairs, in_features]
+        if (n_pairs > 0x7fffffff) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": too many slots");
+        jh::QuantMatrix m{w, scales, biases, sb_dtype, out_features, in_features, group_size, bits};
+        if (int r = finish(c, jh::launch_quant_matmul_t(m, x, x_dtype, n_pairs, y, y_dtype, rhs_indices, n_experts,
+                                                        k_slots, a_vectors, c->stream),
+                           "qmt"))
+            return r;
+        return check_values(c, op, y, y_dtype, n_pairs * in_features);
     }
     jh::GatherArgs a;
     a.m = jh::QuantMatrix{w, scales, biases, sb_dtype, out_features, in_features, group_size, bits};
@@ -395,7 +532,8 @@ int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n
         if (int r = ensure_workspace(c, jh::gather_workspace_bytes(n_experts, n_pairs), op)) return r;
         a.workspace = c->ws;
     }
-    return finish(c, jh::launch_gather(a, c->num_cus, c->stream), "gather");
+    if (int r = finish(c, jh::launch_gather(a, c->num_cus, c->stream), "gather")) return r;
+    return check_values(c, op, y, y_dtype, n_pairs * out_features);
 }
 
 int jh_rms_norm(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, int64_t d, const void* w,
@@ -409,7 +547,8 @@ int jh_rms_norm(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, int64_
     if (rows < 0 || d <= 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape");
     if (rows == 0) return JH_OK;
     if (!x || !w || !out) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
-    return finish(c, jh::launch_rms_norm(x, x_dtype, w, w_dtype, eps, out, out_dtype, rows, d, c->stream), op);
+    if (int r = finish(c, jh::launch_rms_norm(x, x_dtype, w, w_dtype, eps, out, out_dtype, rows, d, c->stream), op)) return r;
+    return check_values(c, op, out, out_dtype, rows * d);
 }
 
 int jh_rope(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, int64_t L, int64_t D, int dims,
@@ -423,9 +562,10 @@ int jh_rope(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, int64_t L,
         return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape (need 0 < dims <= D, dims even)");
     if (rows == 0) return JH_OK;
     if (!x || !out) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
-    return finish(c, jh::launch_rope(x, x_dtype, out, out_dtype, rows, L, D, dims, traditional != 0, base, scale,
+    if (int r = finish(c, jh::launch_rope(x, x_dtype, out, out_dtype, rows, L, D, dims, traditional != 0, base, scale,
                                      offset, freqs, c->stream),
-                  op);
+                  op)) return r;
+    return check_values(c, op, out, out_dtype, rows * D);
 }
 
 int jh_sdpa(jh_ctx* c, const void* q, jh_dtype q_dtype, const void* k, const void* v, jh_dtype kv_dtype, int64_t B,
@@ -448,9 +588,10 @@ int jh_sdpa(jh_ctx* c, const void* q, jh_dtype q_dtype, const void* k, const voi
     const size_t need = jh::sdpa_workspace_bytes(q_dtype, kv_dtype, B, Hq, Hk, Lq, Lk, Dh, c->num_cus);
     if (need)
         if (int r = ensure_workspace(c, need, op)) return r;
-    return finish(c, jh::launch_sdpa(q, q_dtype, k, v, kv_dtype, out, out_dtype, B, Hq, Hk, Lq, Lk, kv_capacity, Dh,
+    if (int r = finish(c, jh::launch_sdpa(q, q_dtype, k, v, kv_dtype, out, out_dtype, B, Hq, Hk, Lq, Lk, kv_capacity, Dh,
                                      scale, causal != 0, c->ws, c->num_cus, c->stream),
-                  op);
+                  op)) return r;
+    return check_values(c, op, out, out_dtype, B * Hq * Lq * Dh);
 }
 
 int jh_elementwise(jh_ctx* c, jh_op opk, const void* a, jh_dtype a_dtype, const void* b, jh_dtype b_dtype, int64_t n,
@@ -466,7 +607,8 @@ int jh_elementwise(jh_ctx* c, jh_op opk, const void* a, jh_dtype a_dtype, const 
     if (n < 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": n < 0");
     if (n == 0) return JH_OK;
     if (!a || !out || (opk != JH_OP_SILU && !b)) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
-    return finish(c, jh::launch_elementwise((int)opk, a, a_dtype, b, b_dtype, out, out_dtype, n, c->stream), op);
+    if (int r = finish(c, jh::launch_elementwise((int)opk, a, a_dtype, b, b_dtype, out, out_dtype, n, c->stream), op)) return r;
+    return check_values(c, op, out, out_dtype, n);
 }
 
 int jh_argmax(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, int64_t n, int32_t* out) {
@@ -512,6 +654,7 @@ int jh_rope_table(jh_ctx* c, int dims, float base, float scale, int64_t pos, con
     return finish(c, jh::launch_rope_table(dims, base, scale, pos, freqs, out, c->stream), op);
 }
 
+
 int jh_attention_decode(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t n_heads, int64_t n_kv_heads,
                         int64_t head_dim, const void* q_norm_w, const void* k_norm_w, jh_dtype w_dtype, float eps,
                         float rope_base, float rope_scale, const float* rope_cs, int64_t pos, void* k_cache,
@@ -519,30 +662,18 @@ int jh_attention_decode(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t 
                         jh_dtype cache_dtype, int64_t capacity, float scale, void* out, jh_dtype out_dtype) {
     if (int r = enter(c)) return r;
     const char* op = "jh_attention_decode";
-    if (int r = check_act_dtype(c, op, "qkv", qkv_dtype)) return r;
-    if (int r = check_act_dtype(c, op, "out", out_dtype)) return r;
-    if (head_dim != 128) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": head_dim must be 128");
-    if (cache_dtype != JH_BF16) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": the caches must be bf16");
-    if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads || n_heads > 65536)
-        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad head counts");
-    const int64_t G = n_heads / n_kv_heads;
-    if (G != 1 && G != 2 && G != 4 && G != 8)
-        return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": n_heads / n_kv_heads must be 1, 2, 4 or 8");
-    if ((q_norm_w || k_norm_w) && w_dtype != JH_BF16 && w_dtype != JH_F16 && w_dtype != JH_F32)
-        return fail(c, JH_ERR_INVALID, std::string(op) + ": norm weights must be bf16, f16 or f32");
-    if (pos < 0 || pos >= capacity || capacity > 0x7fffffff)
-        return fail(c, JH_ERR_INVALID, std::string(op) + ": pos " + std::to_string(pos) + " outside the cache capacity " +
-                                           std::to_string(capacity));
-    if (!qkv || !out || !k_cache || !v_cache || !aligned16(k_cache) || !aligned16(v_cache))
-        return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer, or caches not 16-byte aligned");
+    if (int r = check_attention(c, op, qkv, qkv_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, w_dtype, pos,
+                                k_cache, v_cache, cache_dtype, capacity, out, out_dtype))
+        return r;
     const size_t need = jh::attn_decode_workspace_bytes(n_heads, n_kv_heads, pos, c->num_cus);
     if (need)
         if (int r = ensure_workspace(c, need, op)) return r;
-    return finish(c, jh::launch_attn_decode(qkv, qkv_dtype, (int)n_heads, (int)n_kv_heads, q_norm_w, k_norm_w, w_dtype,
-                                            eps, rope_base, rope_scale, rope_cs, pos, k_cache, v_cache, capacity, scale,
-                                            out,
-                                            out_dtype, c->ws, c->num_cus, c->stream),
-                  op);
+    if (int r = finish(c, jh::launch_attn_decode(qkv, qkv_dtype, (int)n_heads, (int)n_kv_heads, q_norm_w, k_norm_w,
+                                                 w_dtype, eps, rope_base, rope_scale, rope_cs, pos, k_cache, v_cache,
+                                                 capacity, scale, out, out_dtype, c->ws, c->num_cus, c->stream),
+                       op))
+        return r;
+    return check_values(c, op, out, out_dtype, n_heads * head_dim);
 }
 
 int jh_copy_strided(jh_ctx* c, const void* src, jh_dtype src_dtype, int ndim, const int64_t* shape,
@@ -576,15 +707,7 @@ int jh_take_rows(jh_ctx* c, const void* table, int64_t row_bytes, int64_t n_rows
     if (n_ids == 0 || row_bytes == 0) return JH_OK;
     if (n_ids > 0x7fffffff) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": too many ids");
     if (!table || !ids || !out) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
-    if (c->checks) {
-        std::vector<int32_t> h((size_t)n_ids);
-        JH_HIP(c, hipMemcpyAsync(h.data(), ids, h.size() * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
-        JH_HIP(c, hipStreamSynchronize(c->stream));
-        for (size_t i = 0; i < h.size(); i++)
-            if (h[i] < 0 || h[i] >= n_rows)
-                return fail(c, JH_ERR_INVALID, std::string(op) + ": id " + std::to_string(h[i]) + " at " +
-                                                   std::to_string(i) + " outside [0, " + std::to_string(n_rows) + ")");
-    }
+    if (int r = check_indices(c, op, ids, n_ids, n_rows, "id")) return r;
     return finish(c, jh::launch_take_rows(table, row_bytes, n_rows, ids, n_ids, out, c->stream), op);
 }
 
@@ -693,20 +816,46 @@ int jh_moe_swiglu(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n_tok, con
     a.out_dtype = out_dtype;
     if (const char* why = jh::moe_unsupported(a))
         return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": " + why);
-    if (c->checks && n_pairs > 0) {
-        std::vector<int32_t> h((size_t)n_pairs);
-        JH_HIP(c, hipMemcpyAsync(h.data(), rhs_indices, h.size() * sizeof(int32_t),
-                                 hipMemcpyDeviceToHost, c->stream));
-        JH_HIP(c, hipStreamSynchronize(c->stream));
-        for (size_t i = 0; i < h.size(); i++)
-            if (h[i] < 0 || h[i] >= n_experts)
-                return fail(c, JH_ERR_INVALID,
-                            std::string(op) + ": expert index " + std::to_string(h[i]) +
-                                " at slot " + std::to_string(i) + " outside [0, " +
-                                std::to_string(n_experts) + ")");
-    }
+    if (int r = check_indices(c, op, rhs_indices, n_pairs, n_experts, "expert index")) return r;
     if (int r = ensure_workspace(c, jh::moe_workspace_bytes(a), op)) return r;
-    return finish(c, jh::launch_moe_mlp(a, c->ws, c->stream), "moe_swiglu");
+    if (int r = finish(c, jh::launch_moe_mlp(a, c->ws, c->stream), "moe_swiglu")) return r;
+    return check_values(c, op, out, out_dtype, n_tok * hidden);
+}
+
+int jh_softmax(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t outer, int64_t len, int64_t inner, float* y) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_softmax";
+    if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
+    if (outer < 0 || len < 0 || inner < 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape");
+    if (outer * len * inner == 0) return JH_OK;
+    if (!x || !y) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    if (int r = finish(c, jh::launch_softmax(x, x_dtype, y, outer, len, inner, c->stream), op)) return r;
+    return check_values(c, op, y, JH_F32, outer * len * inner);
+}
+
+int jh_mean(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t outer, int64_t len, int64_t inner, float* y) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_mean";
+    if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
+    if (outer < 0 || len < 0 || inner < 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape");
+    if (outer * inner == 0) return JH_OK;
+    if (!y || (len > 0 && !x)) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    if (int r = finish(c, jh::launch_mean(x, x_dtype, y, outer, len, inner, c->stream), op)) return r;
+    return check_values(c, op, y, JH_F32, outer * inner);
+}
+
+int jh_scalar(jh_ctx* c, jh_scalar_op sop, const void* x, jh_dtype x_dtype, int64_t n, float v, void* y,
+              jh_dtype y_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_scalar";
+    if (sop != JH_SCALAR_MUL && sop != JH_SCALAR_ADD) return fail(c, JH_ERR_INVALID, std::string(op) + ": unknown op");
+    if (int r = check_act_dtype(c, op, "x", x_dtype)) return r;
+    if (int r = check_act_dtype(c, op, "y", y_dtype)) return r;
+    if (n < 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": n < 0");
+    if (n == 0) return JH_OK;
+    if (!x || !y) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    if (int r = finish(c, jh::launch_scalar((int)sop, x, x_dtype, v, y, y_dtype, n, c->stream), op)) return r;
+    return check_values(c, op, y, y_dtype, n);
 }
 
 }  // extern "C"

@@ -196,8 +196,20 @@ class HipBackend:
                 continue
             t.free()
 
-    def SetChecks(self, on: bool) -> None:
-        check(self._ctx, self._L.jh_set_checks(self._ctx, int(bool(on))))
+    def SetChecks(self, on) -> None:
+        """Read-back checks like JANIS_GGML_CHECK (ggml/ggml.go:622-677): True or
+        JH_CHECK_INDICES range-checks device indices, JH_CHECK_VALUES counts
+        every float result for NaN/Inf (JH_ERR_NONFINITE); flags combine."""
+        flags = _lib.JH_CHECK_INDICES if on is True else int(on)
+        check(self._ctx, self._L.jh_set_checks(self._ctx, flags))
+
+    def CheckFinite(self, t: Tensor) -> tuple:
+        """(count of NaN/Inf values in t, index of the first, or numel when none)."""
+        t = self._c(t)
+        cnt, first = ctypes.c_int64(), ctypes.c_int64()
+        check(self._ctx, self._L.jh_check_finite(self._ctx, t.ptr, t.dtype, t.numel, ctypes.byref(cnt),
+                                                 ctypes.byref(first)))
+        return cnt.value, first.value
 
     # -- creation ----------------------------------------------------------------
     def make_arena(self, nbytes: int) -> Tensor:
@@ -287,11 +299,36 @@ class HipBackend:
         return a.reshape(t.shape).copy()
 
     def Ints(self, t: Tensor) -> np.ndarray:
+        """engine/backend.go:282-283: I32/U32 copied out as they are; a float
+        tensor rounded half away from zero, as the CPU backend rounds its fp32
+        data (cpu/cpu_misc.go:15-22)."""
         t = self._c(t)
-        raw = np.frombuffer(self.Bytes(t), dtype=np.uint8)
         if t.dtype not in (I32, U32):
-            raise JanisHipError(_lib.JH_ERR_INVALID, "Ints: tensor is not I32/U32")
+            f = self.Floats(t).astype(np.float64)
+            return (np.sign(f) * np.floor(np.abs(f) + 0.5)).astype(np.int32)
+        raw = np.frombuffer(self.Bytes(t), dtype=np.uint8)
         return raw.view(np.int32).reshape(t.shape).copy()
+
+    def _result(self, op: str, out: Tensor | None, out_dtype: int | None, default_dtype: int, shape,
+                dtypes=(F32, BF16)) -> Tensor:
+        """The result buffer of an operator: `out` when given (checked: dense,
+        exactly the result's element count, a dtype the operator writes and, when
+        out_dtype is also given, that dtype), else a new tensor of `shape`."""
+        n = int(np.prod(shape, dtype=np.int64)) if len(shape) else 1
+        if out is None:
+            dt = out_dtype if out_dtype is not None else default_dtype
+            if dt not in dtypes:
+                raise JanisHipError(_lib.JH_ERR_INVALID, f"{op}: result dtype {DTYPE_NAME.get(dt, dt)} not in "
+                                                         f"{[DTYPE_NAME[d] for d in dtypes]}")
+            return self.empty(dt, *shape)
+        self._live(out)
+        if out.numel != n or not out.contiguous:
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"{op}: out {list(out.shape)} must be a dense buffer of "
+                                                     f"{n} elements ({list(shape)})")
+        if out.dtype not in dtypes or (out_dtype is not None and out_dtype != out.dtype):
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"{op}: out is {DTYPE_NAME[out.dtype]}, needs "
+                                                     f"{DTYPE_NAME.get(out_dtype, out_dtype) if out_dtype is not None else [DTYPE_NAME[d] for d in dtypes]}")
+        return out
 
     # -- quantized operators ------------------------------------------------------------
     @staticmethod
@@ -325,11 +362,13 @@ class HipBackend:
         x, w, scales, biases = self._c(x), self._c(w), self._c(scales), self._c(biases)
         n, P = w.shape[-2], w.shape[-1]
         k = P * (32 // bits)
-        if x.shape[-1] != k:
-            raise JanisHipError(_lib.JH_ERR_INVALID, f"QuantMatmul: x has {x.shape[-1]} features, W has {k}")
-        rows = x.numel // k
-        yd = out_dtype if out_dtype is not None else (out.dtype if out is not None else x.dtype)
-        y = out if out is not None else self.empty(yd, *x.shape[:-1], n)
+        # transpose=false is MatMul(x, Dequantize(w)) (cpu/cpu_misc.go:233-236):
+        # x [..., n] -> [..., k]
+        x_feat, y_feat = (k, n) if transpose else (n, k)
+        if x.shape[-1] != x_feat:
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"QuantMatmul: x has {x.shape[-1]} features, needs {x_feat}")
+        rows = x.numel // x_feat
+        y = self._result("QuantMatmul", out, out_dtype, x.dtype, (*x.shape[:-1], y_feat))
         check(self._ctx, self._L.jh_quant_matmul(self._ctx, x.ptr, x.dtype, rows, w.ptr, scales.ptr,
                                                  biases.ptr, self._sb_dtype(scales, biases), n, k,
                                                  int(bool(transpose)), groupSize, bits, y.ptr, y.dtype))
@@ -350,13 +389,14 @@ class HipBackend:
         rs = rhsIndices.shape
         K = rs[-1]
         n_lead = int(np.prod(rs[:-1], dtype=np.int64)) if len(rs) > 1 else 1
-        if x.shape[-1] != k or len(x.shape) < 3:
-            raise JanisHipError(_lib.JH_ERR_INVALID, f"GatherQuantMatmul: x {list(x.shape)} vs in={k}")
+        # transpose=false: each slot's MatMul(x, Dequantize(W_e)), x features = n
+        x_feat, y_feat = (k, n) if transpose else (n, k)
+        if x.shape[-1] != x_feat or len(x.shape) < 3:
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"GatherQuantMatmul: x {list(x.shape)} vs {x_feat} features")
         A = x.shape[-3]
-        if x.numel != n_lead * A * k:
+        if x.numel != n_lead * A * x_feat:
             raise JanisHipError(_lib.JH_ERR_INVALID, "GatherQuantMatmul: x lead dims do not match indices")
-        yd = out_dtype if out_dtype is not None else (out.dtype if out is not None else x.dtype)
-        y = out if out is not None else self.empty(yd, *rs, 1, n)
+        y = self._result("GatherQuantMatmul", out, out_dtype, x.dtype, (*rs, 1, y_feat))
         check(self._ctx, self._L.jh_gather_quant_matmul(
             self._ctx, x.ptr, x.dtype, n_lead, A, w.ptr, scales.ptr, biases.ptr,
             self._sb_dtype(scales, biases), E, n, k, rhsIndices.ptr, K, int(bool(transpose)),
@@ -520,11 +560,49 @@ class HipBackend:
         return t, L
 
 
+    def _broadcast(self, x: Tensor, shape) -> Tensor:
+        """x expanded to `shape` by numpy broadcasting (length-1 or missing
+        leading axes repeat), as the CPU backend's elementwise ops read their
+        operands (cpu/cpu.go:290-298): a zero-stride view copied dense."""
+        shape = tuple(shape)
+        if tuple(x.shape) == shape:
+            return x
+        lead = len(shape) - len(x.shape)
+        if lead < 0:
+            raise JanisHipError(_lib.JH_ERR_INVALID, f"broadcast: {list(x.shape)} to {list(shape)}")
+        st = []
+        for ax, n in enumerate(shape):
+            if ax < lead:
+                st.append(0)
+                continue
+            d, s_ = x.shape[ax - lead], x.strides[ax - lead]
+            if d == n:
+                st.append(s_)
+            elif d == 1:
+                st.append(0)
+            else:
+                raise JanisHipError(_lib.JH_ERR_INVALID, f"broadcast: {list(x.shape)} to {list(shape)}")
+        out = self.empty(x.dtype, *shape)
+        self._copy(self._view(x, shape, st), out)
+        return out
+
+    @staticmethod
+    def _broadcast_shape(a, b) -> tuple:
+        n = max(len(a), len(b))
+        a, b = (1,) * (n - len(a)) + tuple(a), (1,) * (n - len(b)) + tuple(b)
+        out = []
+        for x, y in zip(a, b):
+            if x != y and x != 1 and y != 1:
+                raise JanisHipError(_lib.JH_ERR_INVALID, f"shapes {list(a)} and {list(b)} do not broadcast")
+            out.append(max(x, y) if x and y else 0)
+        return tuple(out)
+
     def _elementwise(self, op, a, b, out_dtype):
+        if b is not None and tuple(a.shape) != tuple(b.shape):
+            shape = self._broadcast_shape(a.shape, b.shape)
+            a, b = self._broadcast(a, shape), self._broadcast(b, shape)
         a = self._c(a)
         b = self._c(b) if b is not None else None
-        if b is not None and b.numel != a.numel:
-            raise JanisHipError(_lib.JH_ERR_UNSUPPORTED, "elementwise: operands must have the same size")
         out = self.empty(out_dtype if out_dtype is not None else a.dtype, *a.shape)
         check(self._ctx, self._L.jh_elementwise(self._ctx, op, a.ptr, a.dtype, b.ptr if b is not None else None,
                                                 b.dtype if b is not None else a.dtype, a.numel, out.ptr, out.dtype))
@@ -542,6 +620,43 @@ class HipBackend:
     def SiLUMul(self, gate: Tensor, up: Tensor, out_dtype: int | None = None) -> Tensor:
         """Mul(SiLU(gate), up) in one pass (qwen/mlp.go:33-35)."""
         return self._elementwise(_lib.JH_OP_SILU_MUL, gate, up, out_dtype)
+
+    @staticmethod
+    def _axis_view(x: Tensor, axis: int) -> tuple:
+        axis = axis % len(x.shape)
+        outer = int(np.prod(x.shape[:axis], dtype=np.int64))
+        inner = int(np.prod(x.shape[axis + 1:], dtype=np.int64))
+        return axis, outer, x.shape[axis], inner
+
+    def Softmax(self, x: Tensor, axis: int) -> Tensor:
+        """engine.Backend.Softmax (cpu/cpu.go:461-499): F32 of x's shape."""
+        x = self._c(x)
+        _, outer, n, inner = self._axis_view(x, axis)
+        out = self.empty(F32, *x.shape)
+        check(self._ctx, self._L.jh_softmax(self._ctx, x.ptr, x.dtype, outer, n, inner, out.ptr))
+        return out
+
+    def Mean(self, x: Tensor, axis: int) -> Tensor:
+        """engine.Backend.Mean (cpu/cpu_ops.go:113-142): the axis removed, F32."""
+        x = self._c(x)
+        ax, outer, n, inner = self._axis_view(x, axis)
+        out = self.empty(F32, *x.shape[:ax], *x.shape[ax + 1:])
+        check(self._ctx, self._L.jh_mean(self._ctx, x.ptr, x.dtype, outer, n, inner, out.ptr))
+        return out
+
+    def _scalar(self, op, x, v, out_dtype):
+        x = self._c(x)
+        out = self.empty(out_dtype if out_dtype is not None else x.dtype, *x.shape)
+        check(self._ctx, self._L.jh_scalar(self._ctx, op, x.ptr, x.dtype, x.numel, float(v), out.ptr, out.dtype))
+        return out
+
+    def ScalarMul(self, x: Tensor, v: float, out_dtype: int | None = None) -> Tensor:
+        """engine.Backend.ScalarMul (cpu/cpu_misc.go:24-26): x * v."""
+        return self._scalar(_lib.JH_SCALAR_MUL, x, v, out_dtype)
+
+    def ScalarAdd(self, x: Tensor, v: float, out_dtype: int | None = None) -> Tensor:
+        """engine.Backend.ScalarAdd (cpu/cpu_misc.go:28-30): x + v."""
+        return self._scalar(_lib.JH_SCALAR_ADD, x, v, out_dtype)
 
     def Argmax(self, x: Tensor, axis: int = -1) -> Tensor:
         """cpu/cpu_misc.go:91-121, last axis only."""
@@ -681,9 +796,10 @@ class HipBackend:
         if (prologue == _lib.JH_PRO_NORMED or epilogue == _lib.JH_EPI_RESID_NORM) and (
                 stats is None or stats.dtype != F32 or stats.numel != _lib.JH_NORM_STATS):
             raise JanisHipError(_lib.JH_ERR_INVALID, "QuantMatvecFused: stats must be F32 [JH_NORM_STATS]")
-        yd = F32 if residual else (
-            out_dtype if out_dtype is not None else (out.dtype if out is not None else x.dtype))
-        y = out if out is not None else self.empty(yd, 1, n)
+        if residual:
+            y = self._result("QuantMatvecFused", out, out_dtype, F32, (1, n), dtypes=(F32,))
+        else:
+            y = self._result("QuantMatvecFused", out, out_dtype, x.dtype, (1, n))
         check(self._ctx, self._L.jh_quant_matvec_fused(
             self._ctx, int(prologue), x.ptr, x.dtype, norm.ptr if norm is not None else None,
             norm.dtype if norm is not None else BF16, float(eps), w.ptr, scales.ptr, biases.ptr,
@@ -784,8 +900,7 @@ class HipBackend:
         n_tok = int(np.prod(rs[:-1], dtype=np.int64)) if len(rs) > 1 else 1
         if x.shape[-1] != H or x.numel != n_tok * H:
             raise JanisHipError(_lib.JH_ERR_INVALID, f"MoeSwiGLU: x {list(x.shape)} vs hidden={H}")
-        od = out_dtype if out_dtype is not None else (out.dtype if out is not None else F32)
-        y = out if out is not None else self.empty(od, *rs[:-1], H)
+        y = self._result("MoeSwiGLU", out, out_dtype, F32, (*rs[:-1], H))
         check(self._ctx, self._L.jh_moe_swiglu(
             self._ctx, x.ptr, x.dtype, n_tok, wg.ptr, sg.ptr, bg.ptr, wu.ptr, su.ptr, bu.ptr,
             wd.ptr, sd.ptr, bd.ptr, self._sb_dtype(sg, bg), E, H, I, rhsIndices.ptr, scores.ptr, K,

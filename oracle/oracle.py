@@ -264,3 +264,83 @@ def scatter_rows(dst, indices, updates) -> np.ndarray:
             raise IndexError(f"scatter_rows: index {r} outside [0, {dst.shape[0]})")
         out[r] = upd[i]
     return out
+
+
+# -- engine operators around the products ---------------------------------------------
+
+def matmul_dequant(x, w, s, b, group_size: int, bits: int = 4) -> np.ndarray:
+    """QuantMatmul with transpose=false: MatMul(x, Dequantize(w))
+    (cpu/cpu_misc.go:233-236). Dequantize is cpu/cpu_misc.go:154-156; the
+    product follows cpu/cpu_ops.go:33-48 -- per output row, over k in
+    increasing order, a zero x[i, k] skipped, the term x[i, k] * W[k, :]
+    rounded to fp32 and then added in fp32. x [..., N] with N the rows of w;
+    returns [..., K]."""
+    wd = dequantize(w, s, b, group_size, bits)  # [N, K]
+    x = _f32(x)
+    N, K = wd.shape
+    assert x.shape[-1] == N, (x.shape, wd.shape)
+    xr = x.reshape(-1, N)
+    out = np.zeros((xr.shape[0], K), dtype=np.float32)
+    for i in range(xr.shape[0]):
+        o = out[i]
+        for k in range(N):
+            a = xr[i, k]
+            if a == 0:
+                continue
+            o += (np.float32(a) * wd[k]).astype(np.float32)  # float32 * float32 -> rounded, then added
+    return out.reshape(x.shape[:-1] + (K,))
+
+
+def gather_matmul_dequant(x, w, s, b, idx, group_size: int, bits: int = 4) -> np.ndarray:
+    """GatherQuantMatmul with transpose=false (cpu/cpu_misc.go:178-230 with
+    :233-236): slot (l, k) is MatMul(x[l, a], Dequantize(W[idx[l, k]])) with a
+    = 0 when x has one vector per lead (A = 1), else k. x [n_lead, A, N];
+    returns [n_lead, K, Kin]. Raises IndexError for an index outside the stack."""
+    x = _f32(x)
+    idx = np.asarray(idx, dtype=np.int64)
+    n_lead, kk = idx.shape
+    A = x.shape[1]
+    E = w.shape[0]
+    kin = w.shape[-1] * (32 // bits)
+    out = np.empty((n_lead, kk, kin), dtype=np.float32)
+    for l in range(n_lead):
+        for k in range(kk):
+            e = int(idx[l, k])
+            if e < 0 or e >= E:
+                raise IndexError(f"expert index {e} outside [0, {E})")
+            out[l, k] = matmul_dequant(x[l, 0 if A == 1 else k][None], w[e], s[e], b[e], group_size, bits)[0]
+    return out
+
+
+def softmax(x, axis: int) -> np.ndarray:
+    """Backend.Softmax (cpu/cpu.go:461-499) along any axis: each line through
+    softmax_row (max, fp32(exp(double(x - max))), the sequential fp32 sum, then
+    the fp32 division)."""
+    x = _f32(x)
+    xm = np.moveaxis(x, axis, -1)
+    flat = np.ascontiguousarray(xm.reshape(-1, xm.shape[-1]))
+    out = np.stack([softmax_row(r) for r in flat]) if flat.shape[0] else flat.copy()
+    return np.ascontiguousarray(np.moveaxis(out.reshape(xm.shape), -1, axis))
+
+
+def mean(x, axis: int) -> np.ndarray:
+    """Backend.Mean (cpu/cpu_ops.go:113-142): per output the fp32 sum along
+    the axis in increasing index order, then divided by the axis length in
+    fp32. (numpy's own reductions sum pairwise; this loop keeps the order.)"""
+    x = _f32(x)
+    xm = np.moveaxis(x, axis, -1)
+    n = xm.shape[-1]
+    s = np.zeros(xm.shape[:-1], dtype=np.float32)
+    for i in range(n):
+        s = (s + xm[..., i]).astype(np.float32)
+    return (s / np.float32(n)).astype(np.float32)
+
+
+def scalar_mul(x, v: float) -> np.ndarray:
+    """Backend.ScalarMul (cpu/cpu_misc.go:24-26): x * v in fp32."""
+    return (_f32(x) * np.float32(v)).astype(np.float32)
+
+
+def scalar_add(x, v: float) -> np.ndarray:
+    """Backend.ScalarAdd (cpu/cpu_misc.go:28-30): x + v in fp32."""
+    return (_f32(x) + np.float32(v)).astype(np.float32)

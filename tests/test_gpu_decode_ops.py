@@ -11,7 +11,7 @@ import pytest
 
 from janis_amd import synth
 from janis_amd.engine import BF16, F16, F32, I32, U32, JanisHipError
-from tests.conftest import rel_ok, step, upload_quant
+from tests.conftest import hip_runtime, rel_ok, step, upload_quant
 
 pytestmark = pytest.mark.gpu
 
@@ -431,16 +431,8 @@ def test_attention_decode_graph_replays(hip, oracle):
     bit (the merge's call tags come from device state, not from captured
     arguments) and the oracle within 1e-3."""
     import ctypes
-    import subprocess
 
-    from janis_amd import _lib as jl
-
-    out = subprocess.run(["ldd", jl.LIB_PATH], capture_output=True, text=True).stdout
-    rt = ctypes.CDLL(next(ln.split("=>")[1].split()[0] for ln in out.splitlines() if "libamdhip64" in ln))
-    for name in ("hipStreamCreate", "hipStreamSynchronize", "hipStreamBeginCapture", "hipStreamEndCapture",
-                 "hipGraphInstantiate", "hipGraphLaunch", "hipGraphExecDestroy", "hipGraphDestroy",
-                 "hipStreamDestroy"):
-        getattr(rt, name).restype = ctypes.c_int
+    rt = hip_runtime()
     rng = np.random.default_rng(97)
     Hq, Hk, Dh, cap, pos = 32, 8, 128, 300, 255
     scale = Dh ** -0.5

@@ -12,7 +12,7 @@ import pytest
 
 from janis_amd import synth
 from janis_amd.engine import BF16, F16, F32, I32, U32, JanisHipError
-from tests.conftest import rel_ok, step, upload_quant
+from tests.conftest import hip_runtime, rel_ok, step, upload_quant
 
 pytestmark = pytest.mark.gpu
 
@@ -197,6 +197,18 @@ def test_qmm_matches_oracle(hip, oracle, m, n, k, gs):
     assert ok, ("f32 out", d, sc)
 
 
+_ROWS_W = {}
+
+
+def _rows_weights(seed, n, k, gs):
+    """Weights of the multi-row cases, made once per shape (lm_head-sized ones
+    take seconds)."""
+    if (seed, gs) not in _ROWS_W:
+        _ROWS_W.clear()
+        _ROWS_W[(seed, gs)] = synth.quant_linear(seed, n, k, gs)
+    return _ROWS_W[(seed, gs)]
+
+
 @pytest.mark.parametrize("n,k,rows,gs,sb", [
     (4096, 4096, 8, 64, "bf16"),    # 8 rows per launch
     (4096, 4096, 5, 64, "bf16"),    # 8 rows per launch, 5 used
@@ -208,12 +220,17 @@ def test_qmm_matches_oracle(hip, oracle, m, n, k, gs):
     (33, 768, 2, 64, "bf16"),
     (70, 3072, 3, 64, "f16"),
     (100, 16384, 4, 64, "bf16"),
+    (1000, 24576, 2, 64, "bf16"),   # the 64-lane 3-load tile (one launch)
+    (1000, 24576, 4, 64, "f16"),    # two launches of 2 rows
+    (151936, 4096, 2, 64, "bf16"),  # lm_head: the one-row call's 64-lane, 2-way split
+    (151936, 4096, 5, 64, "bf16"),
+    (151936, 4096, 8, 64, "bf16"),
 ])
 def test_qmv_rows_match_one_row_calls(hip, oracle, n, k, rows, gs, sb):
     """2..8 rows (2..4 for long rows) take the decode tiles with every row's x
     in registers: each row of y has the bits of a one-row call on that row
     (fp32 out), and the bf16 output is within the bar of the oracle."""
-    q = synth.quant_linear(12000 + n + k, n, k, gs)
+    q = _rows_weights(12000 + n + k, n, k, gs)
     xb, x = synth.activations(13000 + rows, (rows, k))
     w = hip.FromRaw(U32, q.w, *q.w.shape)
     if sb == "f16":
@@ -311,16 +328,8 @@ def test_quant_matmul_graph_replays(hip, oracle, rows, n, k):
     K-split prefill tile (partial tiles, then the ordered sum, no fill), 4 rows
     the multi-row decode tile."""
     import ctypes
-    import subprocess
 
-    from janis_amd import _lib as jl
-
-    out = subprocess.run(["ldd", jl.LIB_PATH], capture_output=True, text=True).stdout
-    rt = ctypes.CDLL(next(ln.split("=>")[1].split()[0] for ln in out.splitlines() if "libamdhip64" in ln))
-    for name in ("hipStreamCreate", "hipStreamSynchronize", "hipStreamBeginCapture", "hipStreamEndCapture",
-                 "hipGraphInstantiate", "hipGraphLaunch", "hipGraphExecDestroy", "hipGraphDestroy",
-                 "hipStreamDestroy"):
-        getattr(rt, name).restype = ctypes.c_int
+    rt = hip_runtime()
     q = synth.quant_linear(41 + rows, n, k)
     w, s, b = upload_quant(hip, q)
     xs = [synth.activations(42 + i, (rows, k)) for i in range(3)]
@@ -647,16 +656,8 @@ def test_moe_swiglu_one_token_graph_replays(hip, oracle):
     (written into the captured buffers between replays): every replay matches
     the oracle on its inputs, so no replay reuses an earlier call's state."""
     import ctypes
-    import subprocess
 
-    from janis_amd import _lib as jl
-
-    out = subprocess.run(["ldd", jl.LIB_PATH], capture_output=True, text=True).stdout
-    rt = ctypes.CDLL(next(ln.split("=>")[1].split()[0] for ln in out.splitlines() if "libamdhip64" in ln))
-    for name in ("hipStreamCreate", "hipStreamSynchronize", "hipStreamBeginCapture", "hipStreamEndCapture",
-                 "hipGraphInstantiate", "hipGraphLaunch", "hipGraphExecDestroy", "hipGraphDestroy",
-                 "hipStreamDestroy"):
-        getattr(rt, name).restype = ctypes.c_int
+    rt = hip_runtime()
     qs, st = _t1_stacks(hip)
     xt, it, sct = hip.empty(BF16, 1, 2048), hip.empty(I32, 1, 8), hip.empty(F32, 1, 8)
     outt = hip.empty(F32, 1, 2048)
@@ -881,7 +882,7 @@ def test_bad_arguments_raise(hip):
     x = hip.FromBF16Bits(xb, 1, 256)
     with pytest.raises(JanisHipError):  # 3-bit codes do not divide a word
         hip.Dequantize(w, s, b, 64, 3)
-    with pytest.raises(JanisHipError):  # transpose=false
+    with pytest.raises(JanisHipError):  # transpose=false takes x of out_features (16) features
         hip.QuantMatmul(x, w, s, b, False, 64, 4)
     with pytest.raises(JanisHipError):  # group does not divide K
         hip.QuantMatmul(x, w, s, b, True, 96, 4)

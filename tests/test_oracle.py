@@ -476,3 +476,84 @@ def test_scatter_rows_known_answer(oracle):
     assert np.array_equal(oracle.scatter_rows(dst, [], np.zeros((0, 3), np.uint32)), dst)
     with pytest.raises(IndexError):
         oracle.scatter_rows(dst, [4], upd[:1])
+
+
+# -- the operators around the products: transpose=false, Softmax, Mean, Scalar ------------
+
+@pytest.mark.parametrize("rows,n,k,gs,bits", [(1, 64, 256, 64, 4), (3, 40, 64, 16, 2), (2, 32, 128, 32, 8),
+                                              (2, 8, 16, 8, 4)])
+def test_matmul_dequant_matches_float64(oracle, rows, n, k, gs, bits):
+    """MatMul(x, Dequantize(w)) (cpu/cpu_misc.go:233-236) against the float64
+    product with the exactly dequantized matrix: x [rows, n] . W [n, k]."""
+    q = synth.quant_linear(3100 + n, n, k, gs, bits=bits)
+    _, x = synth.activations(3101 + rows, (rows, n))
+    got = oracle.matmul_dequant(x, q.w, q.s, q.b, gs, bits)
+    wd = oracle.dequantize(q.w, q.s, q.b, gs, bits).astype(np.float64)
+    ok, d, sc = rel_ok(got, x.astype(np.float64) @ wd, 1e-5)
+    assert ok, (d, sc)
+
+
+def test_matmul_dequant_catches_transposed_operand(oracle):
+    """A planted mistake -- the matrix used transposed, as the transpose=true
+    path reads it -- fails the float64 check on a square matrix."""
+    q = synth.quant_linear(3110, 64, 64, 32)
+    _, x = synth.activations(3111, (2, 64))
+    wd = oracle.dequantize(q.w, q.s, q.b, 32).astype(np.float64)
+    wrong = oracle.quant_matmul(x, q.w, q.s, q.b, 32)  # x . W^T
+    assert not rel_ok(wrong, x.astype(np.float64) @ wd, 1e-2)[0]
+    assert rel_ok(oracle.matmul_dequant(x, q.w, q.s, q.b, 32), x.astype(np.float64) @ wd, 1e-5)[0]
+
+
+def test_matmul_dequant_skips_zero_inputs(oracle):
+    """cpu/cpu_ops.go:41-43 skips a zero x term, so a NaN weight row met only by
+    x == 0 leaves the result finite (the float64 product would be NaN)."""
+    q = synth.quant_linear(3120, 16, 64, 64)
+    q.s_bits[5, 0] = 0x7FC0
+    _, x = synth.activations(3121, (2, 16))
+    x[:, 5] = 0
+    got = oracle.matmul_dequant(x, q.w, q.s, q.b, 64)
+    assert np.isfinite(got).all()
+    x[1, 5] = 1.0
+    assert np.isnan(oracle.matmul_dequant(x, q.w, q.s, q.b, 64)[1, :64]).all()
+
+
+def test_gather_matmul_dequant_is_per_slot(oracle):
+    q = synth.quant_linear(3130, 48, 64, 32, lead=(4,))
+    idx = np.array([[0, 3, 3], [2, 1, 0]], np.int32)
+    _, x = synth.activations(3131, (2, 3, 48))
+    got = oracle.gather_matmul_dequant(x, q.w, q.s, q.b, idx, 32)
+    for l in range(2):
+        for k in range(3):
+            e = idx[l, k]
+            assert np.array_equal(got[l, k], oracle.matmul_dequant(x[l, k][None], q.w[e], q.s[e], q.b[e], 32)[0])
+    with pytest.raises(IndexError):
+        oracle.gather_matmul_dequant(x, q.w, q.s, q.b, np.array([[0, 4, 1], [0, 0, 0]], np.int32), 32)
+
+
+@pytest.mark.parametrize("shape,axis", [((6, 128), -1), ((3, 7, 5), 1), ((4, 3), 0)])
+def test_softmax_along_axis_float64(oracle, shape, axis):
+    _, x = synth.activations(3140 + len(shape), shape)
+    got = oracle.softmax(x, axis)
+    e = np.exp(x.astype(np.float64) - x.max(axis=axis, keepdims=True))
+    ok, d, sc = rel_ok(got, e / e.sum(axis=axis, keepdims=True), 1e-6)
+    assert ok, (d, sc)
+    # each line through the pinned softmax_row
+    assert np.array_equal(np.moveaxis(got, axis, -1)[0, ...].reshape(-1, shape[axis])[0],
+                          oracle.softmax_row(np.moveaxis(x, axis, -1)[0, ...].reshape(-1, shape[axis])[0]))
+
+
+def test_mean_sequential_order_known_answer(oracle):
+    """cpu/cpu_ops.go:136-140 sums in index order in fp32: 1e8 + 1 rounds back
+    to 1e8, so [1e8, 1, -1e8, 1] averages to 0.25 (the exact mean is 0.5, a
+    pairwise sum gives 0)."""
+    assert oracle.mean(np.array([1e8, 1, -1e8, 1], np.float32), 0) == np.float32(0.25)
+    _, x = synth.activations(3150, (4, 9, 33))
+    for ax in (0, 1, 2):
+        ok, d, sc = rel_ok(oracle.mean(x, ax), x.astype(np.float64).mean(axis=ax), 1e-6)
+        assert ok, (ax, d, sc)
+
+
+def test_scalar_ops_closed_form(oracle):
+    x = np.array([1.5, -2.0, 3.0e38, 0.1], np.float32)
+    assert np.array_equal(oracle.scalar_mul(x, 2.0), np.array([3.0, -4.0, np.inf, 0.2], np.float32))
+    assert np.array_equal(oracle.scalar_add(x, 1.0), np.array([2.5, -1.0, 3.0e38, 1.1], np.float32))
