@@ -320,6 +320,27 @@ JH_API int jh_attention_decode(jh_ctx *ctx, const void *qkv, jh_dtype qkv_dtype,
                         void *v_cache, jh_dtype cache_dtype, int64_t capacity, float scale, void *out,
                         jh_dtype out_dtype);
 
+/* jh_attention_decode for callers that cannot allocate device memory (code
+ * under HIP graph capture on a context whose workspace was never sized, tight
+ * serving loops, harnesses that forbid hipMalloc). It has no counterpart in the
+ * reference. Same arguments, arithmetic and results (bit for bit) as
+ * jh_attention_decode, but the split partials go to a fixed 4 MiB device array
+ * of the library (one per GPU, held until the process ends) instead of the
+ * context's workspace, and nothing is allocated. The partials take
+ * n_kv_heads * splits * (n_heads / n_kv_heads) * 130 floats, and the split
+ * count is bounded by the CU count, so on a 256-CU MI355X every call fits (at
+ * most ~3.2 MiB: 3 * CUs * 8 * 130 floats); a call that needs more than the
+ * array (a part with more CUs) returns JH_ERR_UNSUPPORTED. Every call on one
+ * GPU shares that array, from any
+ * context: calls that overlap on one GPU (other streams, other threads) race
+ * and must be ordered by the caller. No value checks (JH_CHECK_VALUES) run here. */
+JH_API int jh_attention_decode_noalloc(jh_ctx *ctx, const void *qkv, jh_dtype qkv_dtype, int64_t n_heads,
+                                       int64_t n_kv_heads, int64_t head_dim, const void *q_norm_w,
+                                       const void *k_norm_w, jh_dtype w_dtype, float eps, float rope_base,
+                                       float rope_scale, const float *rope_cs, int64_t pos, void *k_cache,
+                                       void *v_cache, jh_dtype cache_dtype, int64_t capacity, float scale,
+                                       void *out, jh_dtype out_dtype);
+
 /* The RoPE factors at one position, for callers that rotate many heads there
  * (the RoPE angles of cpu/cpu_attn.go:13-34): out[i] = cos(theta_i) and
  * out[dims/2 + i] = sin(theta_i), theta_i = pos * scale * inv_i, inv_i =

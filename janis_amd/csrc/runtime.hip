@@ -8,6 +8,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -28,11 +29,39 @@ struct jh_ctx {
     // replaying it must not touch memory that was freed (or reused since).
     std::vector<void*> retired;
     unsigned long long* check_buf = nullptr;  // 2 counters of the value checks
+    void* scratch = nullptr;  // this device's copy of `scratch` (jh_attention_decode_noalloc)
 };
 
 namespace {
 
 thread_local std::string g_create_error;
+
+// Scratch memory of jh_attention_decode_noalloc: a fixed device array, so that
+// entry point never allocates. Each GPU the library runs on holds its own copy
+// until the process ends. Its device address is taken once per device, with
+// that device current, by hipGetSymbolAddress (in jh_create); host code uses
+// that address only -- the array's name in host code is a host-side stand-in.
+constexpr size_t kScratchBytes = (size_t)4 << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch` (device current on this thread), or nullptr.
+void* scratch_address(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        g_scratch_ptr[device] = p;
+    }
+    return g_scratch_ptr[device];
+}
 
 int fail(jh_ctx* c, int code, const std::string& msg) {
     if (c) c->err = msg;
@@ -260,6 +289,9 @@ int jh_create(int device, jh_ctx** out) {
     }
     c->stream = c->own_stream;
     c->num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    // the no-allocation entry point's scratch, located once per device now, with
+    // the device current (a failure here only disables that entry point)
+    c->scratch = scratch_address(device);
     std::snprintf(c->name, sizeof(c->name), "%s (%s, %d CUs)", prop.name, prop.gcnArchName, c->num_cus);
     *out = c;
     return JH_OK;
@@ -674,6 +706,31 @@ int jh_attention_decode(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t 
                        op))
         return r;
     return check_values(c, op, out, out_dtype, n_heads * head_dim);
+}
+
+int jh_attention_decode_noalloc(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t n_heads, int64_t n_kv_heads,
+                                int64_t head_dim, const void* q_norm_w, const void* k_norm_w, jh_dtype w_dtype,
+                                float eps, float rope_base, float rope_scale, const float* rope_cs, int64_t pos,
+                                void* k_cache, void* v_cache, jh_dtype cache_dtype, int64_t capacity, float scale,
+                                void* out, jh_dtype out_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_attention_decode_noalloc";
+    if (int r = check_attention(c, op, qkv, qkv_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, w_dtype, pos,
+                                k_cache, v_cache, cache_dtype, capacity, out, out_dtype))
+        return r;
+    if (!c->scratch)
+        return fail(c, JH_ERR_HIP, std::string(op) + ": the device scratch array could not be located");
+    const size_t need = jh::attn_decode_workspace_bytes(n_heads, n_kv_heads, pos, c->num_cus);
+    if (need > kScratchBytes)
+        return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": needs " + std::to_string(need) +
+                                               " bytes of partials, more than the " + std::to_string(kScratchBytes) +
+                                               "-byte scratch (use jh_attention_decode)");
+    // every split block writes all of its partials before the merge reads them,
+    // so the scratch needs no clearing
+    return finish(c, jh::launch_attn_decode(qkv, qkv_dtype, (int)n_heads, (int)n_kv_heads, q_norm_w, k_norm_w,
+                                            w_dtype, eps, rope_base, rope_scale, rope_cs, pos, k_cache, v_cache,
+                                            capacity, scale, out, out_dtype, c->scratch, c->num_cus, c->stream),
+                  op);
 }
 
 int jh_copy_strided(jh_ctx* c, const void* src, jh_dtype src_dtype, int ndim, const int64_t* shape,

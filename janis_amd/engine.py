@@ -833,12 +833,14 @@ class HipBackend:
     def AttentionDecode(self, qkv: Tensor, n_heads: int, n_kv_heads: int, q_norm: Tensor | None,
                         k_norm: Tensor | None, eps: float, base: float, rope_scale: float, pos: int,
                         k_cache: Tensor, v_cache: Tensor, scale: float, out_dtype: int | None = None,
-                        rope_cs: Tensor | None = None, out: Tensor | None = None) -> Tensor:
+                        rope_cs: Tensor | None = None, out: Tensor | None = None, noalloc: bool = False) -> Tensor:
         """Attention.ForwardCached for one token after the q/k/v product
         (qwen/attention.go:98-128) in one launch: q/k RMSNorm (when the weights
         are given), RoPE at pos, the KV append at row pos, and SDPA over keys
         0..pos. qkv [.., (Hq+2Hk)*128]; caches bf16 [1, Hk, cap, 128]; rope_cs
-        optionally RoPETable(128, base, rope_scale, pos). Returns [1, Hq*128]."""
+        optionally RoPETable(128, base, rope_scale, pos). Returns [1, Hq*128].
+        noalloc=True takes jh_attention_decode_noalloc (partials in the
+        library's fixed device scratch instead of the context's workspace)."""
         if q_norm is not None and k_norm is not None and q_norm.dtype != k_norm.dtype:
             raise JanisHipError(_lib.JH_ERR_INVALID, "AttentionDecode: norm weights differ in dtype")
         if k_cache.dtype != v_cache.dtype or k_cache.shape != v_cache.shape:
@@ -855,7 +857,8 @@ class HipBackend:
         elif out.numel != n_heads * Dh or out.dtype not in (F32, BF16):
             raise JanisHipError(_lib.JH_ERR_INVALID, "AttentionDecode: out must be F32/BF16 [1, Hq*128]")
         wd = q_norm.dtype if q_norm is not None else (k_norm.dtype if k_norm is not None else BF16)
-        check(self._ctx, self._L.jh_attention_decode(
+        fn = self._L.jh_attention_decode_noalloc if noalloc else self._L.jh_attention_decode
+        check(self._ctx, fn(
             self._ctx, qkv.ptr, qkv.dtype, n_heads, n_kv_heads, Dh, q_norm.ptr if q_norm is not None else None,
             k_norm.ptr if k_norm is not None else None, wd, float(eps), float(base), float(rope_scale),
             rope_cs.ptr if rope_cs is not None else None, int(pos),
