@@ -375,9 +375,12 @@ JH_API int jh_moe_route(jh_ctx *ctx, const void *logits, jh_dtype logits_dtype, 
  *   h = SiLU(g) * u                              SiLU(v) = v / (1 + exp(-v))
  *   d = gather(h, down)                          one vector per slot (A = k_slots)
  *   out[t, :] = mean_k(d[t, k, :] * scores[t, k]) * k_slots
- * Here it is two product launches (gate+up with the SiLU*mul epilogue; down with
- * the score-weighted sum done as fp32 atomics into out) plus one clearing
- * launch, and h stays on the device in bf16.
+ * Here it is two launches: gate+up with the SiLU*mul epilogue (h stays on the
+ * device in bf16), then the down product with the score-weighted sum taken in
+ * a fixed order (slot order, then a fixed tree of four partial sums) and
+ * written once; calls of more than 32 (token, slot) pairs add a bucketing
+ * launch and a launch that sums each token's weighted slot rows in slot order.
+ * No atomics: repeated calls give the same bits.
  *   x            bf16 [n_tok, hidden] (x_dtype must be JH_BF16)
  *   gate, up     stacked [n_experts, intermediate, hidden * bits / 32] with
  *                scales/biases [n_experts, intermediate, hidden / group_size]
@@ -385,8 +388,7 @@ JH_API int jh_moe_route(jh_ctx *ctx, const void *logits, jh_dtype logits_dtype, 
  *                scales/biases [n_experts, hidden, intermediate / group_size]
  *   rhs_indices  int32 [n_tok, k_slots] and scores fp32 [n_tok, k_slots], device memory
  *   out          [n_tok, hidden] of out_dtype (JH_F32 or JH_BF16)
- * The score-weighted sum is accumulated with atomics, so its fp32 rounding
- * order varies from run to run. A token with an index outside [0, n_experts)
+ * A token with an index outside [0, n_experts)
  * gets a row of NaN (or JH_ERR_INVALID when jh_set_checks is on). Shapes
  * outside the expert tiles (hidden and intermediate in {256, 512, 768, 1024,
  * 1536, 2048, 3072, 4096, 6144, 8192, 12288}, group_size 32/64/128, 16-bit

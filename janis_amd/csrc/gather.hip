@@ -22,12 +22,19 @@
 // v_perm_b32 and meet bf16 x pairs in v_dot2_f32_bf16; the 128 is removed
 // through the group's sum of x) run per expert bucket: block (rb, u) loads its
 // rows of expert u into registers once, then applies them to the x vector of
-// every pair in the bucket. Its epilogue is one of
+// every pair in the bucket. One token's slots (a single token routed to its
+// top-k) skip the bucketing: block (rb, p) takes pair p's expert directly.
+// Its epilogue is one of
 //    EPI_PLAIN    y[pair, row]    = dot                      (GatherQuantMatmul)
 //    EPI_SWIGLU   y[pair, row]    = SiLU(dot_gate) * dot_up  (two stacks, one launch)
-//    EPI_COMBINE  out[lead, row] += score[pair] * dot        (fp32 atomics)
-// so a whole moeApply is one SWIGLU launch over gate+up and one COMBINE launch
-// over down, with the hidden activations h kept in bf16 between them.
+//    EPI_PARTIAL  y[pair, row]    = score[pair] * dot        (fp32, the down product)
+// The score-weighted sum over a token's slots (moeApply's Mean * K,
+// qwen/moe.go:510) is taken in slot order, never by atomics, so results repeat
+// bit for bit: up to 32 pairs moe_down_combine_kernel computes a token's rows
+// for all its slots in one block and sums them there; beyond, EPI_PARTIAL
+// products go to a workspace and moe_combine_kernel sums each token's slots.
+// A whole moeApply is one SWIGLU launch over gate+up and one down launch (two
+// plus the bucketing beyond 32 pairs), with h kept in bf16 between them.
 #include "jh_common.hpp"
 
 namespace jh {
@@ -48,7 +55,12 @@ constexpr int kMaxExperts = 4096;
 // 34.8 -> 32.4 us with the buckets precomputed).
 constexpr int kInBlockMaxPairs = 32;
 constexpr int kMaxRouteExperts = 4096;
-enum { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_COMBINE = 2 };
+enum { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_PARTIAL = 2 };
+// How a product block finds its expert and pairs: the workspace buckets of
+// moe_bucket_kernel, buckets made inside the block, or one pair per block.
+enum { MODE_WS = 0, MODE_IN_BLOCK = 1, MODE_PAIR = 2 };
+// Up to this many pairs (one token's top-8) each product block takes one pair.
+constexpr int kPerPairMaxPairs = 8;
 
 __device__ __forceinline__ void nan_row(void* Y, int y_dt, int64_t p, int64_t N, int tid, int nthreads) {
     const float nan = __uint_as_float(0x7fc00000u);
@@ -184,18 +196,13 @@ struct MoeArgs {
     const int32_t* idx;    // [n_lead, k_slots]
     int n_pairs;
     int64_t E, k_slots, a_vectors;
-    const float* scores;   // COMBINE: [n_lead, k_slots]
-    // SWIGLU of jh_moe_swiglu: the combine's fp32 output [n_lead, init_h] is
-    // cleared here (NaN rows for a token with an index outside [0, E)), so the
-    // combine launch that follows can add into it with no launch of its own
-    float* init_out = nullptr;
-    int64_t init_n = 0, init_h = 1;
+    const float* scores;   // PARTIAL: [n_lead, k_slots]
 };
 
 // Expert-slot GEMV (see the file comment). LPR lanes per row, each lane ITERS
 // 16-byte words per K-part; K split over KSPLIT waves that meet in LDS. Rows per
 // block = (4 / KSPLIT) * (64 / LPR) * RPW.
-template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int EPI, bool FUSED>
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int EPI, int MODE>
 __global__ __launch_bounds__(256) void moe_qmv_kernel(MoeArgs a) {
     constexpr int NSTK = EPI == EPI_SWIGLU ? 2 : 1;
     constexpr int SLICES = 64 / LPR;
@@ -205,32 +212,29 @@ __global__ __launch_bounds__(256) void moe_qmv_kernel(MoeArgs a) {
     constexpr uint32_t K = 8 * P;
     constexpr int ROWS_PER_WAVE = SLICES * RPW;
     constexpr int ROWS_PER_BLOCK = RGROUPS * ROWS_PER_WAVE;
-    __shared__ int sidx[FUSED ? kInBlockMaxPairs : 1];
-    __shared__ int plist_s[FUSED ? kInBlockMaxPairs : 1];
-    __shared__ uint32_t pres[FUSED ? kMaxExperts / 32 : 1];
+    constexpr bool IN_BLOCK = MODE == MODE_IN_BLOCK;
+    __shared__ int sidx[IN_BLOCK ? kInBlockMaxPairs : 1];
+    __shared__ int plist_s[IN_BLOCK ? kInBlockMaxPairs : 1];
+    __shared__ uint32_t pres[IN_BLOCK ? kMaxExperts / 32 : 1];
     __shared__ int np_s, sel_s;
     __shared__ float red[KSPLIT > 1 ? (KSPLIT - 1) * NSTK * ROWS_PER_BLOCK : 1];
-
-    if constexpr (EPI == EPI_SWIGLU) {
-        if (a.init_out) {  // before any block returns: the whole grid shares the clearing
-            const int64_t nb = (int64_t)gridDim.x * gridDim.y, b = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
-            for (int64_t i = b * blockDim.x + threadIdx.x; i < a.init_n; i += nb * blockDim.x) {
-                const int64_t t = i / a.init_h;
-                bool bad = false;
-                for (int64_t k = 0; k < a.k_slots; k++) {
-                    const int32_t ei = a.idx[t * a.k_slots + k];
-                    bad |= ei < 0 || ei >= a.E;
-                }
-                a.init_out[i] = bad ? __uint_as_float(0x7fc00000u) : 0.0f;
-            }
-        }
-    }
 
     int64_t e;
     int p_begin, p_end;
     const int* pairs;
-    if constexpr (FUSED) {
-        if (EPI != EPI_COMBINE && blockIdx.x == 0 && blockIdx.y == 0)
+    int pair_self = 0;
+    if constexpr (MODE == MODE_PAIR) {
+        pair_self = blockIdx.y;
+        e = a.idx[pair_self];
+        if (e < 0 || e >= a.E) {  // this block's rows of the pair's output are NaN
+            if (EPI != EPI_PARTIAL && blockIdx.x == 0) nan_row(a.y, a.y_dt, pair_self, a.N, threadIdx.x, blockDim.x);
+            return;  // block-uniform
+        }
+        p_begin = 0;
+        p_end = 1;
+        pairs = &pair_self;
+    } else if constexpr (IN_BLOCK) {
+        if (EPI != EPI_PARTIAL && blockIdx.x == 0 && blockIdx.y == 0)
             for (int p = 0; p < a.n_pairs; p++) {
                 const int ei = a.idx[p];
                 if (ei < 0 || ei >= a.E) nan_row(a.y, a.y_dt, p, a.N, threadIdx.x, blockDim.x);
@@ -353,8 +357,8 @@ __global__ __launch_bounds__(256) void moe_qmv_kernel(MoeArgs a) {
             for (int r = 0; r < RPW; r++) {
                 const uint32_t row = row0 + r;
                 if (row >= N) continue;
-                if constexpr (EPI == EPI_COMBINE) {
-                    atomicAdd(static_cast<float*>(a.y) + l * N + row, a.scores[pair] * part[0][r]);
+                if constexpr (EPI == EPI_PARTIAL) {
+                    static_cast<float*>(a.y)[pair * N + row] = a.scores[pair] * part[0][r];
                 } else {
                     const float v = EPI == EPI_SWIGLU ? silu(part[0][r]) * part[NSTK - 1][r] : part[0][r];
                     if (a.y_dt == JH_BF16)
@@ -367,28 +371,144 @@ __global__ __launch_bounds__(256) void moe_qmv_kernel(MoeArgs a) {
     }
 }
 
-// out[t, :] = 0, or NaN for a token with an expert index outside [0, E).
-__global__ __launch_bounds__(256) void moe_init_out_kernel(float* __restrict__ out, int64_t n_tok, int64_t H,
-                                                           const int32_t* __restrict__ idx, int64_t K,
-                                                           int64_t E) {
-    const int64_t n = n_tok * H;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t t = i / H;
-        bool bad = false;
-        for (int64_t k = 0; k < K; k++) {
-            const int32_t e = idx[t * K + k];
-            bad |= e < 0 || e >= E;
+__device__ __forceinline__ void store_out(void* y, int dt, int64_t i, float v) {
+    if (dt == JH_BF16)
+        static_cast<uint16_t*>(y)[i] = f32_to_bf16_hw(v);
+    else
+        static_cast<float*>(y)[i] = v;
+}
+
+// The down product and the score-weighted sum of one token's slots in one
+// block (calls of up to 32 pairs): block (rb, t) has 4 waves; wave w computes
+// rows rb of the experts of slots w*SPW .. w*SPW+SPW-1 against their h rows
+// (all its loads issued before any is used), weights each by its score and
+// adds them in slot order; the 4 waves' sums meet in LDS and are added in wave
+// order. Out is written once (fp32 or bf16), so nothing clears it first, and
+// the order is fixed. A token with an expert index outside [0, E) gets NaN.
+// Rows per block = (64 / LPR) * RPW; K (the down's in_features) = 32 * LPR * ITERS.
+template <int LPR, int ITERS, int RPW, bool SB_F16, int SPW>
+__global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeArgs a, void* __restrict__ out, int out_dt) {
+    constexpr int NW = 4;
+    constexpr int SLICES = 64 / LPR;
+    constexpr int ROWS = SLICES * RPW;
+    constexpr uint32_t P = 4 * LPR * ITERS;
+    constexpr uint32_t K = 8 * P;
+    __shared__ float red[NW][ROWS];
+    __shared__ int bad_s[NW];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int sl = lane % LPR, slice = lane / LPR;
+    const int64_t t = blockIdx.y;
+    const uint32_t N = a.N, G = K >> a.gs_log2;
+    const uint32_t row0 = blockIdx.x * ROWS + slice * RPW;
+    uint32_t wo[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; it++) wo[it] = it * 4 * LPR + 4 * sl;
+    int64_t es[SPW];
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < SPW; j++) {
+        const int64_t k = (int64_t)w * SPW + j;
+        es[j] = -1;
+        if (k < a.k_slots) {
+            const int64_t e = a.idx[t * a.k_slots + k];
+            if (e < 0 || e >= a.E) bad = true;
+            else es[j] = e;
         }
-        out[i] = bad ? __uint_as_float(0x7fc00000u) : 0.0f;
+    }
+    // every slot's weights, scales and biases, then its h
+    uint4 wv[SPW][RPW][ITERS];
+    uint16_t sh[SPW][RPW][ITERS], bh[SPW][RPW][ITERS];
+#pragma unroll
+    for (int j = 0; j < SPW; j++) {
+        const int64_t e = es[j] < 0 ? 0 : es[j];
+        const auto rw = make_rsrc(a.w[0] + e * (int64_t)N * P, es[j] < 0 ? 0u : N * P * 4);
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int it = 0; it < ITERS; it++) wv[j][r][it] = buf_load16_nt(rw, ((row0 + r) * P + wo[it]) * 4);
+    }
+#pragma unroll
+    for (int j = 0; j < SPW; j++) {
+        const int64_t e = es[j] < 0 ? 0 : es[j];
+        const auto rs = make_rsrc(a.s[0] + e * (int64_t)N * G, es[j] < 0 ? 0u : N * G * 2);
+        const auto rb = make_rsrc(a.b[0] + e * (int64_t)N * G, es[j] < 0 ? 0u : N * G * 2);
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int it = 0; it < ITERS; it++) {
+                const uint32_t off = ((row0 + r) * G + ((8u * wo[it]) >> a.gs_log2)) * 2;
+                sh[j][r][it] = buf_load2(rs, off);
+                bh[j][r][it] = buf_load2(rb, off);
+            }
+    }
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SPW; j++) {
+        const int64_t k = (int64_t)w * SPW + j;
+        if (es[j] < 0) continue;  // wave-uniform
+        const int64_t pair = t * a.k_slots + k;
+        const uint16_t* xr = a.x + pair * K;
+        float part[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; r++) part[r] = 0.0f;
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+            const uint4* xv = reinterpret_cast<const uint4*>(xr + 8 * wo[it]);
+            uint32_t xp[16];
+            const uint4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
+            const float xs = (pair_up(x0, &xp[0]) + pair_up(x1, &xp[4])) + (pair_up(x2, &xp[8]) + pair_up(x3, &xp[12]));
+#pragma unroll
+            for (int r = 0; r < RPW; r++) {
+                const float sc = SB_F16 ? f16_to_f32(sh[j][r][it]) : bf16_to_f32(sh[j][r][it]);
+                const float bi = SB_F16 ? f16_to_f32(bh[j][r][it]) : bf16_to_f32(bh[j][r][it]);
+                float d = 0.0f;
+                d = word_dot(wv[j][r][it].x, &xp[0], d);
+                d = word_dot(wv[j][r][it].y, &xp[4], d);
+                d = word_dot(wv[j][r][it].z, &xp[8], d);
+                d = word_dot(wv[j][r][it].w, &xp[12], d);
+                part[r] = fmaf(sc, d, part[r]);
+                part[r] = fmaf(fmaf(-kCodeOffset, sc, bi), xs, part[r]);
+            }
+        }
+        const float score = a.scores[pair];
+#pragma unroll
+        for (int r = 0; r < RPW; r++) acc[r] += score * slice_sum_last<LPR>(part[r]);
+    }
+    if (sl == LPR - 1)
+#pragma unroll
+        for (int r = 0; r < RPW; r++) red[w][slice * RPW + r] = acc[r];
+    if (lane == 0) bad_s[w] = bad;
+    __syncthreads();
+    if (threadIdx.x < ROWS) {
+        const uint32_t row = blockIdx.x * ROWS + threadIdx.x;
+        if (row < N) {
+            float v = ((red[0][threadIdx.x] + red[1][threadIdx.x]) + red[2][threadIdx.x]) + red[3][threadIdx.x];
+            if (bad_s[0] | bad_s[1] | bad_s[2] | bad_s[3]) v = __uint_as_float(0x7fc00000u);
+            store_out(out, out_dt, t * N + row, v);
+        }
     }
 }
 
-__global__ __launch_bounds__(256) void moe_narrow_kernel(const float* __restrict__ acc, void* __restrict__ out,
-                                                         int dt, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (int64_t)gridDim.x * blockDim.x)
-        store_y(out, i, acc[i], dt);
+// out[t, :] = the sum over slots k = 0.. of part[t * K + k, :] in slot order,
+// NaN for a token with an expert index outside [0, E) (its partial rows were
+// never written).
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ part, const int32_t* __restrict__ idx,
+                                                          int64_t n_tok, int64_t K, int64_t E, int64_t H,
+                                                          void* __restrict__ out, int out_dt) {
+    const int64_t n = n_tok * H;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = i / H, h = i - t * H;
+        float v = 0.0f;
+        bool bad = false;
+        for (int64_t k = 0; k < K; k++) {
+            const int32_t e = idx[t * K + k];
+            if (e < 0 || e >= E) bad = true;
+            else v += part[(t * K + k) * H + h];
+        }
+        store_out(out, out_dt, i, bad ? __uint_as_float(0x7fc00000u) : v);
+    }
 }
 
 int log2_exact(int v) {
@@ -398,40 +518,41 @@ int log2_exact(int v) {
 }
 
 template <int LPR, int ITERS, int RPW, int KSPLIT, int EPI>
-void run_tile(const MoeArgs& a, bool sb_f16, bool fused, int64_t max_u, hipStream_t st) {
+void run_tile(const MoeArgs& a, bool sb_f16, int mode, int64_t max_u, hipStream_t st) {
     constexpr int64_t rows_per_block = (4 / KSPLIT) * (64 / LPR) * RPW;
     const dim3 grid((unsigned)((a.N + rows_per_block - 1) / rows_per_block), (unsigned)max_u);
-    if (fused) {
-        if (sb_f16)
-            hipLaunchKernelGGL((moe_qmv_kernel<LPR, ITERS, RPW, KSPLIT, true, EPI, true>), grid, dim3(256), 0, st, a);
-        else
-            hipLaunchKernelGGL((moe_qmv_kernel<LPR, ITERS, RPW, KSPLIT, false, EPI, true>), grid, dim3(256), 0, st, a);
-    } else {
-        if (sb_f16)
-            hipLaunchKernelGGL((moe_qmv_kernel<LPR, ITERS, RPW, KSPLIT, true, EPI, false>), grid, dim3(256), 0, st, a);
-        else
-            hipLaunchKernelGGL((moe_qmv_kernel<LPR, ITERS, RPW, KSPLIT, false, EPI, false>), grid, dim3(256), 0, st, a);
-    }
+    auto go = [&](auto sb, auto md) {
+        hipLaunchKernelGGL((moe_qmv_kernel<LPR, ITERS, RPW, KSPLIT, decltype(sb)::value, EPI, decltype(md)::value>),
+                           grid, dim3(256), 0, st, a);
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    using M0 = std::integral_constant<int, MODE_WS>;
+    using M1 = std::integral_constant<int, MODE_IN_BLOCK>;
+    using M2 = std::integral_constant<int, MODE_PAIR>;
+    if (mode == MODE_PAIR) sb_f16 ? go(T{}, M2{}) : go(F{}, M2{});
+    else if (mode == MODE_IN_BLOCK) sb_f16 ? go(T{}, M1{}) : go(F{}, M1{});
+    else sb_f16 ? go(T{}, M0{}) : go(F{}, M0{});
 }
 
 // Tile per row length P (32-bit words). SWIGLU holds two stacks' rows, so it
 // takes half the rows per wave of the single-stack epilogues.
 template <int EPI>
-bool run_fast(const MoeArgs& a, int64_t P, bool sb_f16, bool fused, int64_t max_u, hipStream_t st) {
+bool run_fast(const MoeArgs& a, int64_t P, bool sb_f16, int mode, int64_t max_u, hipStream_t st) {
     constexpr int R4 = EPI == EPI_SWIGLU ? 2 : 4;
     constexpr int R2 = EPI == EPI_SWIGLU ? 1 : 2;
     switch (P) {
-        case 256 * 1: run_tile<64, 1, R4, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
-        case 256 * 2: run_tile<64, 2, R2, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
-        case 256 * 3: run_tile<64, 3, R2, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
-        case 256 * 4: run_tile<64, 4, 1, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
-        case 256 * 6: run_tile<64, 6, 1, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
-        case 128 * 1: run_tile<32, 1, R4, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
-        case 128 * 3: run_tile<32, 3, R2, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
-        case 64 * 1: run_tile<16, 1, R4, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
-        case 64 * 3: run_tile<16, 3, R2, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
-        case 32 * 1: run_tile<8, 1, R4, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
-        case 32 * 3: run_tile<8, 3, R2, 1, EPI>(a, sb_f16, fused, max_u, st); return true;
+        case 256 * 1: run_tile<64, 1, R4, 1, EPI>(a, sb_f16, mode, max_u, st); return true;
+        case 256 * 2: run_tile<64, 2, R2, 1, EPI>(a, sb_f16, mode, max_u, st); return true;
+        case 256 * 3: run_tile<64, 3, R2, 1, EPI>(a, sb_f16, mode, max_u, st); return true;
+        case 256 * 4: run_tile<64, 4, 1, 1, EPI>(a, sb_f16, mode, max_u, st); return true;
+        case 256 * 6: run_tile<64, 6, 1, 1, EPI>(a, sb_f16, mode, max_u, st); return true;
+        case 128 * 1: run_tile<32, 1, R4, 1, EPI>(a, sb_f16, mode, max_u, st); return true;
+        case 128 * 3: run_tile<32, 3, R2, 1, EPI>(a, sb_f16, mode, max_u, st); return true;
+        case 64 * 1: run_tile<16, 1, R4, 1, EPI>(a, sb_f16, mode, max_u, st); return true;
+        case 64 * 3: run_tile<16, 3, R2, 1, EPI>(a, sb_f16, mode, max_u, st); return true;
+        case 32 * 1: run_tile<8, 1, R4, 1, EPI>(a, sb_f16, mode, max_u, st); return true;
+        case 32 * 3: run_tile<8, 3, R2, 1, EPI>(a, sb_f16, mode, max_u, st); return true;
         default: return false;
     }
 }
@@ -484,10 +605,11 @@ Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st) {
         return Status::fail(JH_ERR_UNSUPPORTED, "gather_quant_matmul: more than 4096 experts");
     const int64_t max_u = n_pairs < a.n_experts ? n_pairs : a.n_experts;
     if (max_u > 65535) return Status::fail(JH_ERR_UNSUPPORTED, "gather_quant_matmul: too many experts in one call");
-    const bool fused = !gather_uses_workspace(a);
-    if (!fused)
+    const bool in_launch = !gather_uses_workspace(a);
+    if (!in_launch)
         hipLaunchKernelGGL(moe_bucket_kernel, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.n_experts,
                            static_cast<int*>(a.workspace), a.y, a.y_dtype, a.m.rows);
+    const int mode = !in_launch ? MODE_WS : (n_pairs <= kPerPairMaxPairs ? MODE_PAIR : MODE_IN_BLOCK);
     if (fast_ok(a.m, a.x_dtype)) {
         MoeArgs m = single_stack(a.m);
         m.x = static_cast<const uint16_t*>(a.x);
@@ -499,7 +621,9 @@ Status launch_gather(const GatherArgs& a, int num_cus, hipStream_t st) {
         m.E = a.n_experts;
         m.k_slots = a.k_slots;
         m.a_vectors = a.a_vectors;
-        if (run_fast<EPI_PLAIN>(m, a.m.in / 8, a.m.sb_dtype == JH_F16, fused, max_u, st)) return Status::ok();
+        if (run_fast<EPI_PLAIN>(m, a.m.in / 8, a.m.sb_dtype == JH_F16, mode, mode == MODE_PAIR ? n_pairs : max_u,
+                                st))
+            return Status::ok();
     }
     int64_t blocks = (a.m.rows + 3) / 4;
     const int64_t cap = (int64_t)num_cus * 4;
@@ -610,11 +734,47 @@ const char* moe_unsupported(const MoeMlpArgs& a) {
     return nullptr;
 }
 
+// The calls whose down product and combine run as one launch per token
+// (moe_down_combine_kernel): up to 32 pairs and 16 slots per token.
+bool moe_small(const MoeMlpArgs& a) {
+    return a.n_tok * a.k_slots <= kInBlockMaxPairs && a.k_slots <= 16;
+}
+
+template <int LPR, int ITERS, int SPW>
+void run_down_combine(const MoeArgs& d, bool f16, int64_t n_tok, void* out, int out_dt, hipStream_t st) {
+    constexpr int rows = 64 / LPR;
+    const dim3 grid((unsigned)((d.N + rows - 1) / rows), (unsigned)n_tok);
+    if (f16)
+        hipLaunchKernelGGL((moe_down_combine_kernel<LPR, ITERS, 1, true, SPW>), grid, dim3(256), 0, st, d, out, out_dt);
+    else
+        hipLaunchKernelGGL((moe_down_combine_kernel<LPR, ITERS, 1, false, SPW>), grid, dim3(256), 0, st, d, out, out_dt);
+}
+
+template <int SPW>
+bool down_combine_tiles(const MoeArgs& d, int64_t P, bool f16, int64_t n_tok, void* out, int out_dt, hipStream_t st) {
+    switch (P) {
+        case 256 * 1: run_down_combine<64, 1, SPW>(d, f16, n_tok, out, out_dt, st); return true;
+        case 256 * 2: run_down_combine<64, 2, SPW>(d, f16, n_tok, out, out_dt, st); return true;
+        case 256 * 3: run_down_combine<64, 3, SPW>(d, f16, n_tok, out, out_dt, st); return true;
+        case 256 * 4: run_down_combine<64, 4, SPW>(d, f16, n_tok, out, out_dt, st); return true;
+        case 256 * 6: run_down_combine<64, 6, SPW>(d, f16, n_tok, out, out_dt, st); return true;
+        case 128 * 1: run_down_combine<32, 1, SPW>(d, f16, n_tok, out, out_dt, st); return true;
+        case 128 * 3: run_down_combine<32, 3, SPW>(d, f16, n_tok, out, out_dt, st); return true;
+        case 64 * 1: run_down_combine<16, 1, SPW>(d, f16, n_tok, out, out_dt, st); return true;
+        case 64 * 3: run_down_combine<16, 3, SPW>(d, f16, n_tok, out, out_dt, st); return true;
+        case 32 * 1: run_down_combine<8, 1, SPW>(d, f16, n_tok, out, out_dt, st); return true;
+        case 32 * 3: run_down_combine<8, 3, SPW>(d, f16, n_tok, out, out_dt, st); return true;
+        default: return false;
+    }
+}
+
 size_t moe_workspace_bytes(const MoeMlpArgs& a) {
     const int64_t n_pairs = a.n_tok * a.k_slots;
     size_t b = align256(sizeof(uint16_t) * (size_t)(n_pairs * a.gate.rows));  // h
-    if (a.out_dtype != JH_F32) b += align256(sizeof(float) * (size_t)(a.n_tok * a.down.rows));
-    if (n_pairs > kInBlockMaxPairs) b += gather_workspace_bytes(a.n_experts, n_pairs);
+    if (!moe_small(a)) {
+        b += align256(sizeof(float) * (size_t)(n_pairs * a.down.rows));  // weighted down partials
+        b += gather_workspace_bytes(a.n_experts, n_pairs);
+    }
     return b;
 }
 
@@ -624,63 +784,69 @@ Status launch_moe_mlp(const MoeMlpArgs& a, void* workspace, hipStream_t st) {
     if (const char* why = moe_unsupported(a)) return Status::fail(JH_ERR_UNSUPPORTED, std::string("moe_swiglu: ") + why);
     const int64_t H = a.down.rows, I = a.gate.rows;
     const int64_t max_u = std::min<int64_t>(n_pairs, a.n_experts);
-    const bool fused = n_pairs <= kInBlockMaxPairs;
+    const bool small = moe_small(a);
     const bool f16 = a.gate.sb_dtype == JH_F16;
     char* wsp = static_cast<char*>(workspace);
     uint16_t* h = reinterpret_cast<uint16_t*>(wsp);
     wsp += align256(sizeof(uint16_t) * (size_t)(n_pairs * I));
-    float* acc = static_cast<float*>(a.out);
-    if (a.out_dtype != JH_F32) {
-        acc = reinterpret_cast<float*>(wsp);
-        wsp += align256(sizeof(float) * (size_t)(a.n_tok * H));
+    float* part = nullptr;
+    int* buckets = nullptr;
+    if (!small) {
+        part = reinterpret_cast<float*>(wsp);
+        wsp += align256(sizeof(float) * (size_t)(n_pairs * H));
+        buckets = reinterpret_cast<int*>(wsp);
     }
-    int* buckets = fused ? nullptr : reinterpret_cast<int*>(wsp);
-
     const int64_t n_out = a.n_tok * H;
-    const unsigned init_blocks = (unsigned)std::min<int64_t>((n_out + 255) / 256, 4096);
-    if (n_pairs == 0)  // out is the empty sum; otherwise the gate/up launch clears it
-        hipLaunchKernelGGL(moe_init_out_kernel, dim3(init_blocks), dim3(256), 0, st, acc, a.n_tok, H, a.idx,
-                           a.k_slots, a.n_experts);
-    if (n_pairs > 0) {
-        if (!fused)
-            hipLaunchKernelGGL(moe_bucket_kernel, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.n_experts, buckets,
-                               static_cast<void*>(nullptr), (int)JH_BF16, (int64_t)0);
-
-        MoeArgs g = single_stack(a.gate);
-        g.w[1] = a.up.w;
-        g.s[1] = static_cast<const uint16_t*>(a.up.scales);
-        g.b[1] = static_cast<const uint16_t*>(a.up.biases);
-        g.x = static_cast<const uint16_t*>(a.x);
-        g.y = h;
-        g.y_dt = JH_BF16;
-        g.ws = buckets;
-        g.idx = a.idx;
-        g.n_pairs = (int)n_pairs;
-        g.E = a.n_experts;
-        g.k_slots = a.k_slots;
-        g.a_vectors = 1;
-        g.init_out = acc;
-        g.init_n = n_out;
-        g.init_h = H;
-        if (!run_fast<EPI_SWIGLU>(g, a.gate.in / 8, f16, fused, max_u, st))
-            return Status::fail(JH_ERR_UNSUPPORTED, "moe_swiglu: no tile for the gate/up shape");
-
-        MoeArgs d = single_stack(a.down);
-        d.x = h;
-        d.y = acc;
-        d.y_dt = JH_F32;
-        d.ws = buckets;
-        d.idx = a.idx;
-        d.n_pairs = (int)n_pairs;
-        d.E = a.n_experts;
-        d.k_slots = a.k_slots;
-        d.a_vectors = a.k_slots;
-        d.scores = a.scores;
-        if (!run_fast<EPI_COMBINE>(d, a.down.in / 8, f16, fused, max_u, st))
-            return Status::fail(JH_ERR_UNSUPPORTED, "moe_swiglu: no tile for the down shape");
+    const unsigned out_blocks = (unsigned)std::min<int64_t>((n_out + 255) / 256, 4096);
+    if (n_pairs == 0) {  // every token's sum is empty
+        hipLaunchKernelGGL(moe_combine_kernel, dim3(out_blocks), dim3(256), 0, st, static_cast<const float*>(nullptr),
+                           a.idx, a.n_tok, (int64_t)0, a.n_experts, H, a.out, a.out_dtype);
+        return Status::ok();
     }
-    if (a.out_dtype != JH_F32)
-        hipLaunchKernelGGL(moe_narrow_kernel, dim3(init_blocks), dim3(256), 0, st, acc, a.out, a.out_dtype, n_out);
+    if (!small)
+        hipLaunchKernelGGL(moe_bucket_kernel, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.n_experts, buckets,
+                           static_cast<void*>(nullptr), (int)JH_BF16, (int64_t)0);
+    const int gu_mode = !small ? MODE_WS : (n_pairs <= kPerPairMaxPairs ? MODE_PAIR : MODE_IN_BLOCK);
+
+    MoeArgs g = single_stack(a.gate);
+    g.w[1] = a.up.w;
+    g.s[1] = static_cast<const uint16_t*>(a.up.scales);
+    g.b[1] = static_cast<const uint16_t*>(a.up.biases);
+    g.x = static_cast<const uint16_t*>(a.x);
+    g.y = h;
+    g.y_dt = JH_BF16;
+    g.ws = buckets;
+    g.idx = a.idx;
+    g.n_pairs = (int)n_pairs;
+    g.E = a.n_experts;
+    g.k_slots = a.k_slots;
+    g.a_vectors = 1;
+    if (!run_fast<EPI_SWIGLU>(g, a.gate.in / 8, f16, gu_mode, gu_mode == MODE_PAIR ? n_pairs : max_u, st))
+        return Status::fail(JH_ERR_UNSUPPORTED, "moe_swiglu: no tile for the gate/up shape");
+
+    MoeArgs d = single_stack(a.down);
+    d.x = h;
+    d.ws = buckets;
+    d.idx = a.idx;
+    d.n_pairs = (int)n_pairs;
+    d.E = a.n_experts;
+    d.k_slots = a.k_slots;
+    d.a_vectors = a.k_slots;
+    d.scores = a.scores;
+    const int64_t Pd = a.down.in / 8;
+    if (small) {
+        const bool ok = a.k_slots <= 4   ? down_combine_tiles<1>(d, Pd, f16, a.n_tok, a.out, a.out_dtype, st)
+                        : a.k_slots <= 8 ? down_combine_tiles<2>(d, Pd, f16, a.n_tok, a.out, a.out_dtype, st)
+                                         : down_combine_tiles<4>(d, Pd, f16, a.n_tok, a.out, a.out_dtype, st);
+        if (!ok) return Status::fail(JH_ERR_UNSUPPORTED, "moe_swiglu: no tile for the down shape");
+        return Status::ok();
+    }
+    d.y = part;
+    d.y_dt = JH_F32;
+    if (!run_fast<EPI_PARTIAL>(d, Pd, f16, MODE_WS, max_u, st))
+        return Status::fail(JH_ERR_UNSUPPORTED, "moe_swiglu: no tile for the down shape");
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(out_blocks), dim3(256), 0, st, static_cast<const float*>(part),
+                       a.idx, a.n_tok, a.k_slots, a.n_experts, H, a.out, a.out_dtype);
     return Status::ok();
 }
 

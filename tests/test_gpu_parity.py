@@ -524,6 +524,24 @@ def test_moe_swiglu_qwen3_30b_a3b(hip, oracle, n_tok):
     assert ok, (d, s)
 
 
+@pytest.mark.parametrize("n_tok", [1, 4, 16])
+def test_moe_swiglu_repeats_bit_for_bit(hip, n_tok):
+    """The score-weighted sum over a token's slots is taken in a fixed order
+    (no atomics), so repeated calls on the same inputs give the same bits --
+    the one-launch-per-token combine (1 and 4 tokens) and the partials plus
+    combine launch (16 tokens) alike."""
+    qs, st = _t1_stacks(hip)
+    idx, sc = synth.route(9350 + n_tok, n_tok, 128, 8)
+    xb, _ = synth.activations(9351 + n_tok, (n_tok, 2048))
+    x, it, sct = hip.FromBF16Bits(xb, n_tok, 2048), hip.FromInt32(idx), hip.FromFloats(sc)
+    step(f"jh_moe_swiglu repeated calls T={n_tok}")
+    first = hip.Floats(hip.MoeSwiGLU(x, *st, it, sct, 64, 4, out_dtype=F32))
+    assert np.isfinite(first).all()
+    for _ in range(4):
+        again = hip.Floats(hip.MoeSwiGLU(x, *st, it, sct, 64, 4, out_dtype=F32))
+        assert np.array_equal(first.view(np.uint32), again.view(np.uint32))
+
+
 @pytest.mark.parametrize("n_tok,E,H,I,out_dtype", [(4, 6, 512, 256, F32), (3, 5, 1024, 768, BF16),
                                                     (2, 3, 256, 512, F32)])
 def test_moe_swiglu_small_with_collisions(hip, oracle, n_tok, E, H, I, out_dtype):
