@@ -184,20 +184,22 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     auto wrow = [&](uint32_t row0, int r) -> uint32_t {
         return EPI == EPI_SWIGLU ? row0 + (r % RO) + (r / RO) * N : row0 + r;
     };
+    // Row by row: a row's words, then its scales and biases, so that the first
+    // rows' dot products can start while later rows are still arriving (loads
+    // complete in issue order).
     auto load_pass = [&](uint32_t row0) {
 #pragma unroll
-        for (int r = 0; r < RPW; r++)
+        for (int r = 0; r < RPW; r++) {
 #pragma unroll
             for (int it = 0; it < ITERS; it++)
                 wv[r][it] = buf_load16_nt(rw, (wrow(row0, r) * P + wo[it]) * 4);
-#pragma unroll
-        for (int r = 0; r < RPW; r++)
 #pragma unroll
             for (int it = 0; it < ITERS; it++) {
                 const uint32_t off = (wrow(row0, r) * G + gi[it]) * 2;
                 sh[r][it] = buf_load2(rs, off);
                 bh[r][it] = buf_load2(rb, off);
             }
+        }
         if constexpr (RESID)
 #pragma unroll
             for (int r = 0; r < RPW; r++)
@@ -713,18 +715,24 @@ bool qmv_fast_shape(const QuantMatrix& m) {
     }
 }
 
-// Tile per row length, from a sweep of the Qwen3-8B shapes on MI355X: splitting
+// Tile per row length, from sweeps of the Qwen3-8B shapes on MI355X (graph
+// replays over weight copies that do not fit the last-level cache): splitting
 // K over 2-4 waves per row beats one wave per row at every shape (more waves in
-// flight, shorter per-wave dependency chains).
+// flight, shorter per-wave dependency chains). For 512-word rows, matrices of
+// up to 4096 output rows take 2 rows per slice (twice the blocks: o_proj 4.16
+// against 4.37 us) and larger ones 4 (gate+up 11.6 against 12.4 us; the
+// 151936-row lm_head 57.0 us, against 63.5 for a 64-lane 2-way tile).
 template <int PRO, int EPI>
 bool launch_tiles(const QuantMatrix& m, const void* x, void* y, int y_dtype, int num_cus, hipStream_t st,
                   const QmvFusion& fu) {
     if (!qmv_fast_shape(m)) return false;
     const int gl = log2_exact(m.group_size);
+    const int64_t n_out = EPI == EPI_SWIGLU ? m.rows / 2 : m.rows;
 #define JH_TILE(L, I, R, KS) return tile<L, I, R, KS, PRO, EPI>(m, x, y, y_dtype, gl, num_cus, st, fu)
-    if (m.bits == 4 && m.in == 4096 && m.rows >= 65536) JH_TILE(64, 1, 8, 2);
     switch (row_words(m)) {
-        case 512 * 1: JH_TILE(32, 1, 4, 4);
+        case 512 * 1:
+            if (n_out <= 4096 && EPI != EPI_SWIGLU) JH_TILE(32, 1, 2, 4);
+            JH_TILE(32, 1, 4, 4);
         case 512 * 2: JH_TILE(32, 2, 2, 4);
         case 512 * 3: JH_TILE(32, 3, 2, 4);
         case 512 * 4: JH_TILE(32, 4, 2, 4);
@@ -831,9 +839,7 @@ Status launch_qmv_rows(const QuantMatrix& m, const void* x, int64_t rows, void* 
     // Each case keeps the one-row tile's lanes per row (L), loads per lane (I)
     // and K split (KS) for that row length, so a row's reduction order -- and
     // its bits -- are those of a one-row call; only the rows per slice (R) may
-    // differ. The lm_head-sized matrix takes the one-row special case's 64-lane,
-    // 2-way split (4 rows per slice instead of 8, for registers).
-    if (m.in == 4096 && m.rows >= 65536) JH_ROWS(64, 1, 4, 2);
+    // differ.
     switch (row_words(m)) {
         case 512 * 1: JH_ROWS(32, 1, 4, 4);
         case 512 * 2: JH_ROWS(32, 2, 2, 4);
