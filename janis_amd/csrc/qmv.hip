@@ -130,7 +130,7 @@ struct QmvFusion {
 };
 
 template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int PRO = PRO_NONE, int EPI = EPI_STORE,
-          int BITS = 4>
+          int BITS = 4, bool PIPE = false>
 __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     const uint32_t* __restrict__ W, const uint16_t* __restrict__ S,
     const uint16_t* __restrict__ B, const void* __restrict__ Xv, void* Y,
@@ -170,11 +170,14 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
         wo[it] = ks * PK + it * 4 * LPR + 4 * sl;   // word offset inside a row
         gi[it] = (EPW * wo[it]) >> gs_log2;
     }
-    uint4 wv[RPW][ITERS];
-    uint16_t sh[RPW][ITERS], bh[RPW][ITERS];
+    // PIPE: two register sets; the next pass's loads are issued before this
+    // pass is computed (a persistent grid of a few blocks per CU walks the rows)
+    constexpr int NB = PIPE ? 2 : 1;
+    uint4 wv[NB][RPW][ITERS];
+    uint16_t sh[NB][RPW][ITERS], bh[NB][RPW][ITERS];
     constexpr bool RESID = EPI == EPI_RESID || EPI == EPI_RESID_NORM;
-    float rv[RESID ? RPW : 1];  // the residual rows, fetched with the pass's weights
-    uint16_t nv[EPI == EPI_RESID_NORM ? RPW : 1];  // the next norm's weights for those rows
+    float rv[NB][RESID ? RPW : 1];  // the residual rows, fetched with the pass's weights
+    uint16_t nv[NB][EPI == EPI_RESID_NORM ? RPW : 1];  // the next norm's weights for those rows
     const auto rr = make_rsrc(fu.resid, RESID ? N * 4 : 0);
     const auto rn = make_rsrc(fu.nw, EPI == EPI_RESID_NORM ? N * 2 : 0);
     // Loads complete in issue order. The raw x loads go first, then the first
@@ -187,27 +190,30 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
     // Row by row: a row's words, then its scales and biases, so that the first
     // rows' dot products can start while later rows are still arriving (loads
     // complete in issue order).
-    auto load_pass = [&](uint32_t row0) {
+    auto load_pass = [&](auto bufc, uint32_t row0) {
+        constexpr int Q = decltype(bufc)::value;
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
 #pragma unroll
             for (int it = 0; it < ITERS; it++)
-                wv[r][it] = buf_load16_nt(rw, (wrow(row0, r) * P + wo[it]) * 4);
+                wv[Q][r][it] = buf_load16_nt(rw, (wrow(row0, r) * P + wo[it]) * 4);
 #pragma unroll
             for (int it = 0; it < ITERS; it++) {
                 const uint32_t off = (wrow(row0, r) * G + gi[it]) * 2;
-                sh[r][it] = buf_load2(rs, off);
-                bh[r][it] = buf_load2(rb, off);
+                sh[Q][r][it] = buf_load2(rs, off);
+                bh[Q][r][it] = buf_load2(rb, off);
             }
         }
         if constexpr (RESID)
 #pragma unroll
             for (int r = 0; r < RPW; r++)
-                rv[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr, (row0 + r) * 4, 0, 0));
+                rv[Q][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr, (row0 + r) * 4, 0, 0));
         if constexpr (EPI == EPI_RESID_NORM)
 #pragma unroll
-            for (int r = 0; r < RPW; r++) nv[r] = buf_load2(rn, (row0 + r) * 2);
+            for (int r = 0; r < RPW; r++) nv[Q][r] = buf_load2(rn, (row0 + r) * 2);
     };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, NB - 1>;
     // raw x: 32 (4-bit) or 16 (8-bit) elements per lane per ITER (bf16, or fp32
     // for the norm)
     constexpr int XW = PRO == PRO_RMSNORM ? 8 : (int)EPW / 2;  // 16-byte chunks of them
@@ -246,7 +252,7 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
         for (int j = 0; j < SPL; j++) st4[j] = sp[j * 64 + lane];
     }
     const uint32_t lane_row = rg * ROWS_PER_WAVE + (uint32_t)slice * RO;
-    load_pass(blockIdx.x * ROWS_PER_BLOCK + lane_row);
+    load_pass(B0{}, blockIdx.x * ROWS_PER_BLOCK + lane_row);
     // the product's input as bf16, 8 per uint4
     uint4 xin[ITERS][4];
     float ss_part = 0.0f;  // PRO_RMSNORM / PRO_NORMED: sum of x^2 over this wave's share
@@ -325,22 +331,23 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
         xs[it] = BITS == 8 ? xs8[it] : sum;
     }
 
-    for (uint32_t bbase = blockIdx.x * ROWS_PER_BLOCK; bbase < N; bbase += gridDim.x * ROWS_PER_BLOCK) {
+    // one pass: the rows of bbase from register set Q
+    auto pass = [&](auto bufc, uint32_t bbase) {
+        constexpr int Q = decltype(bufc)::value;
         const uint32_t row0 = bbase + lane_row;
-        if (bbase != blockIdx.x * ROWS_PER_BLOCK) load_pass(row0);
         float part[RPW];
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
             part[r] = 0.0f;
 #pragma unroll
             for (int it = 0; it < ITERS; it++) {
-                const float sc = SB_F16 ? f16_to_f32(sh[r][it]) : bf16_to_f32(sh[r][it]);
-                const float bi = SB_F16 ? f16_to_f32(bh[r][it]) : bf16_to_f32(bh[r][it]);
+                const float sc = SB_F16 ? f16_to_f32(sh[Q][r][it]) : bf16_to_f32(sh[Q][r][it]);
+                const float bi = SB_F16 ? f16_to_f32(bh[Q][r][it]) : bf16_to_f32(bh[Q][r][it]);
                 float d = 0.0f;
-                d = word_dot(wv[r][it].x, &xp[it][0], d);
-                d = word_dot(wv[r][it].y, &xp[it][4], d);
-                d = word_dot(wv[r][it].z, &xp[it][8], d);
-                d = word_dot(wv[r][it].w, &xp[it][12], d);
+                d = word_dot(wv[Q][r][it].x, &xp[it][0], d);
+                d = word_dot(wv[Q][r][it].y, &xp[it][4], d);
+                d = word_dot(wv[Q][r][it].z, &xp[it][8], d);
+                d = word_dot(wv[Q][r][it].w, &xp[it][12], d);
                 part[r] = fmaf(sc, d, part[r]);
                 part[r] = fmaf(fmaf(-OFF, sc, bi), xs[it], part[r]);
             }
@@ -378,14 +385,14 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
             if constexpr (EPI == EPI_RESID) {
 #pragma unroll
                 for (int r = 0; r < RPW; r++)
-                    if (row0 + r < N) static_cast<float*>(Y)[row0 + r] = rv[r] + part[r];
+                    if (row0 + r < N) static_cast<float*>(Y)[row0 + r] = rv[Q][r] + part[r];
             } else if constexpr (EPI == EPI_RESID_NORM) {
 #pragma unroll
                 for (int r = 0; r < RPW; r++)
                     if (row0 + r < N) {
-                        const float h = rv[r] + part[r];
+                        const float h = rv[Q][r] + part[r];
                         static_cast<float*>(Y)[row0 + r] = h;
-                        fu.nout[row0 + r] = f32_to_bf16_hw(h * bf16_to_f32(nv[r]));
+                        fu.nout[row0 + r] = f32_to_bf16_hw(h * bf16_to_f32(nv[Q][r]));
                         sq = fmaf(h, h, sq);
                     }
             } else if constexpr (EPI == EPI_SWIGLU) {
@@ -399,6 +406,24 @@ __global__ __launch_bounds__(256) void qmv_bf16x_kernel(
             } else {
                 store_rows<RPW>(Y, y_dt, row0, N, part);
             }
+        }
+    };
+    const uint32_t stride = gridDim.x * ROWS_PER_BLOCK;
+    if constexpr (!PIPE) {
+        for (uint32_t bbase = blockIdx.x * ROWS_PER_BLOCK; bbase < N; bbase += stride) {
+            if (bbase != blockIdx.x * ROWS_PER_BLOCK) load_pass(B0{}, bbase + lane_row);
+            pass(B0{}, bbase);
+        }
+    } else {
+        // set 0 holds the first pass; each pass requests the one after it into
+        // the other set before computing (the trip count is uniform over the block)
+        for (uint32_t bbase = blockIdx.x * ROWS_PER_BLOCK; bbase < N; bbase += 2 * stride) {
+            const uint32_t b1 = bbase + stride;
+            if (b1 < N) load_pass(B1{}, b1 + lane_row);
+            pass(B0{}, bbase);
+            if (b1 >= N) break;
+            if (b1 + stride < N) load_pass(B0{}, b1 + stride + lane_row);
+            pass(B1{}, b1);
         }
     }
     if constexpr (EPI == EPI_RESID_NORM) {
@@ -614,8 +639,9 @@ __global__ __launch_bounds__(256) void qmv_generic_kernel(
 
 namespace {
 
+// BPC > 0: the pipelined kernel on a grid of at most BPC blocks per CU.
 template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int PRO = PRO_NONE, int EPI = EPI_STORE,
-          int BITS = 4>
+          int BITS = 4, int BPC = 0>
 Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gs_log2,
                    int num_cus, hipStream_t st, const QmvFusion& fu = QmvFusion{}) {
     constexpr int64_t rows_per_block = (4 / KSPLIT) * (64 / LPR) * (EPI == EPI_SWIGLU ? RPW / 2 : RPW);
@@ -624,7 +650,7 @@ Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, in
     constexpr int64_t k_tile = 4LL * LPR * ITERS * KSPLIT * (32 / BITS);
     if (k_tile != m.in || m.bits != BITS) return Status::fail(JH_ERR_UNSUPPORTED, "qmv: tile does not fit the matrix");
     const int64_t n_out = EPI == EPI_SWIGLU ? m.rows / 2 : m.rows;
-    auto kern = qmv_bf16x_kernel<LPR, ITERS, RPW, KSPLIT, SB_F16, PRO, EPI, BITS>;
+    auto kern = qmv_bf16x_kernel<LPR, ITERS, RPW, KSPLIT, SB_F16, PRO, EPI, BITS, (BPC > 0)>;
     // persistent-style grid: at most what is resident at once, so multi-pass
     // shapes reuse the x registers instead of queueing more blocks
     static int resident = 0;
@@ -635,7 +661,7 @@ Status run_fast_sb(const QuantMatrix& m, const void* x, void* y, int y_dtype, in
         resident = per_cu;
     }
     int64_t blocks = (n_out + rows_per_block - 1) / rows_per_block;
-    const int64_t cap = (int64_t)num_cus * resident;
+    const int64_t cap = (int64_t)num_cus * (BPC > 0 ? BPC : resident);
     if (blocks > cap) blocks = cap;
     if (EPI == EPI_RESID_NORM && blocks > kNormSlots) blocks = kNormSlots;  // one partial per block
     if (blocks < 1) blocks = 1;
@@ -670,29 +696,30 @@ namespace {
 // One tile of the table. Fused prologues/epilogues are built for bf16 scales
 // only (the checkpoints' format); an f16-scale fused call returns false and is
 // composed from separate launches by the caller.
-template <int LPR, int ITERS, int RPW, int KSPLIT, int PRO, int EPI, int BITS>
+template <int LPR, int ITERS, int RPW, int KSPLIT, int PRO, int EPI, int BITS, int BPC>
 bool tile_bits(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gl, int num_cus, hipStream_t st,
                const QmvFusion& fu) {
     if (m.sb_dtype == JH_F16) {
         if constexpr (PRO == PRO_NONE && EPI == EPI_STORE)
-            return run_fast_sb<LPR, ITERS, RPW, KSPLIT, true, PRO, EPI, BITS>(m, x, y, y_dtype, gl, num_cus, st, fu)
+            return run_fast_sb<LPR, ITERS, RPW, KSPLIT, true, PRO, EPI, BITS, BPC>(m, x, y, y_dtype, gl, num_cus, st,
+                                                                                 fu)
                        .code == JH_OK;
         else
             return false;
     }
-    return run_fast_sb<LPR, ITERS, RPW, KSPLIT, false, PRO, EPI, BITS>(m, x, y, y_dtype, gl, num_cus, st, fu).code ==
-           JH_OK;
+    return run_fast_sb<LPR, ITERS, RPW, KSPLIT, false, PRO, EPI, BITS, BPC>(m, x, y, y_dtype, gl, num_cus, st, fu)
+               .code == JH_OK;
 }
 
 // 8-bit weights have tiles for a plain or prepared-norm bf16 input.
-template <int LPR, int ITERS, int RPW, int KSPLIT, int PRO, int EPI>
+template <int LPR, int ITERS, int RPW, int KSPLIT, int PRO, int EPI, int BPC = 0>
 bool tile(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gl, int num_cus, hipStream_t st,
           const QmvFusion& fu) {
     if (m.bits == 8) {
         if constexpr (PRO == PRO_RMSNORM) return false;
-        else return tile_bits<LPR, ITERS, RPW, KSPLIT, PRO, EPI, 8>(m, x, y, y_dtype, gl, num_cus, st, fu);
+        else return tile_bits<LPR, ITERS, RPW, KSPLIT, PRO, EPI, 8, BPC>(m, x, y, y_dtype, gl, num_cus, st, fu);
     }
-    return tile_bits<LPR, ITERS, RPW, KSPLIT, PRO, EPI, 4>(m, x, y, y_dtype, gl, num_cus, st, fu);
+    return tile_bits<LPR, ITERS, RPW, KSPLIT, PRO, EPI, 4, BPC>(m, x, y, y_dtype, gl, num_cus, st, fu);
 }
 
 // The register tiles take 4- and 8-bit weights, groups of 32/64/128 dividing K,
@@ -721,7 +748,12 @@ bool qmv_fast_shape(const QuantMatrix& m) {
 // flight, shorter per-wave dependency chains). For 512-word rows, matrices of
 // up to 4096 output rows take 2 rows per slice (twice the blocks: o_proj 4.16
 // against 4.37 us) and larger ones 4 (gate+up 11.6 against 12.4 us; the
-// 151936-row lm_head 57.0 us, against 63.5 for a 64-lane 2-way tile).
+// 151936-row lm_head 57.0 us, against 63.5 for a 64-lane 2-way tile). Rows of
+// 1536 words (down_proj, K = 12288) take one row per slice on a grid of two
+// blocks per CU, each block walking four passes with the next pass's loads in
+// flight while it computes (7.65 against 8.29 us at 4096 rows): with a whole
+// row's three 16-byte loads per lane issued at once, the single-pass tile
+// waits for all of its loads before any dot product starts.
 template <int PRO, int EPI>
 bool launch_tiles(const QuantMatrix& m, const void* x, void* y, int y_dtype, int num_cus, hipStream_t st,
                   const QmvFusion& fu) {
@@ -734,7 +766,10 @@ bool launch_tiles(const QuantMatrix& m, const void* x, void* y, int y_dtype, int
             if (n_out <= 4096 && EPI != EPI_SWIGLU) JH_TILE(32, 1, 2, 4);
             JH_TILE(32, 1, 4, 4);
         case 512 * 2: JH_TILE(32, 2, 2, 4);
-        case 512 * 3: JH_TILE(32, 3, 2, 4);
+        case 512 * 3:
+            if constexpr (EPI != EPI_SWIGLU)
+                if (n_out >= 2048) return tile<32, 3, 1, 4, PRO, EPI, 2>(m, x, y, y_dtype, gl, num_cus, st, fu);
+            JH_TILE(32, 3, 2, 4);
         case 512 * 4: JH_TILE(32, 4, 2, 4);
         case 512 * 6: JH_TILE(64, 3, 2, 4);  // 8-bit K = 12288
         case 256 * 1: JH_TILE(32, 1, 4, 2);

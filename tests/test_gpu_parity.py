@@ -96,9 +96,11 @@ def test_inkling2_embed_golden(hip, name, tol):
 
 QMV_SHAPES = [
     # (N, K, gs): every fast-kernel tile (K = 256..16384), group sizes 32/64/128,
-    # ragged N, the lm_head-size tile, and the generic kernel (K = 1032, gs = 8)
+    # ragged N, the lm_head-size tile, and the generic kernel (K = 1032, gs = 8).
+    # K = 12288 with N >= 2048 is the two-set pipelined tile; 3001 rows leave the
+    # persistent blocks ragged pass counts and a half-filled last row pair.
     (4096, 4096, 64), (1024, 4096, 64), (33, 2048, 64), (1000, 6144, 64), (257, 8192, 64),
-    (4096, 12288, 64), (100, 16384, 64), (129, 1024, 64), (70, 3072, 64), (65, 512, 64),
+    (4096, 12288, 64), (3001, 12288, 32), (100, 16384, 64), (129, 1024, 64), (70, 3072, 64), (65, 512, 64),
     (48, 1536, 64), (31, 256, 64), (768, 768, 64), (300, 4096, 32), (300, 4096, 128),
     (50, 2048, 32), (40, 768, 128), (24, 1032, 8), (9, 96, 32), (65539, 4096, 64)]
 
@@ -875,6 +877,21 @@ def test_quant_matvec_8bit_tiles(hip, oracle, K, gs, sb):
     yb = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, 1, K), w, s, b, True, gs, 8))
     ok, d, sc = rel_ok(yb, want, BF16_TOL)
     assert ok, ("bf16 y", d, sc)
+
+
+@pytest.mark.parametrize("N,K", [(2500, 6144), (4096, 6144)])
+def test_quant_matvec_8bit_pipelined_tile(hip, oracle, N, K):
+    """8-bit rows of K = 6144 (1536 words, like the 4-bit K = 12288) at N >= 2048
+    take the pipelined tile: a persistent grid whose blocks walk several passes
+    with two register sets. N = 2500 leaves the blocks uneven pass counts."""
+    q = synth.quant_linear(K + N, N, K, 64, bits=8)
+    w, s, b = upload_quant(hip, q)
+    xb, x = synth.activations(K + 5, (1, K))
+    step(f"jh_quant_matmul 8-bit pipelined tile N={N} K={K}")
+    y = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, 1, K), w, s, b, True, 64, 8, out_dtype=F32))
+    want = oracle.quant_matmul(x, q.w, q.s, q.b, 64, bits=8)
+    ok, d, sc = rel_ok(y, want, F32_TOL)
+    assert ok, (d, sc)
 
 
 def test_gather_8bit(hip, oracle):
