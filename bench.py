@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # WRITE_SIZE over `bench.py --pmc-workload`, each scaled by what the counter reads
 # for a 256 MiB copy in the same run (FETCH_SIZE x2.0, WRITE_SIZE x1.0). Re-measure
 # after changing the kernel; the summary sits in profiles/.
-DOMINANT_TRAFFIC_BYTES = 26912362
+DOMINANT_TRAFFIC_BYTES = 26916846
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 HIDDEN, INTER, VOCAB, LAYERS, GS = 4096, 12288, 151936, 36, 64
 
@@ -70,6 +70,13 @@ def main() -> int:
     ap.add_argument("--prefill-workload", type=int, default=0, metavar="M",
                     help="eager launches for rocprofv3: the config-2 prefill products (gate_up 12288x4096, "
                          "down 4096x12288) at M rows, 3 times each")
+    ap.add_argument("--dominant-workload", action="store_true",
+                    help="profiling workload: only the roofline kernel's graph (36 layers x q/k/v, o, gate+up), "
+                         "warmup + steps replays, the same graph bench.py times for `roofline`; prints one line "
+                         "to stderr")
+    ap.add_argument("--moe-workload", type=int, default=0, metavar="T",
+                    help="eager launches for rocprofv3: the config-3 expert MLP (jh_moe_swiglu, Qwen3-30B-A3B "
+                         "experts, top-8) at T tokens over 4 layers' expert stacks, 3 passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this backend is measured on one GPU; --gpus N > 1 is not "
@@ -178,6 +185,28 @@ def main() -> int:
         hip.Close()
         return 0
 
+    if args.moe_workload:
+        from janis_amd import synth
+        from janis_amd.engine import F32, I32
+        E, H, I, K, T = 128, 2048, 768, 8, args.moe_workload
+        stacks = [{"gate": qweight(I, H, (E,)), "up": qweight(I, H, (E,)), "down": qweight(H, I, (E,))}
+                  for _ in range(4)]
+        idx_np, sc_np = synth.route(77 + T, T, E, K)
+        it, sct = torch.from_numpy(idx_np).to(dev), torch.from_numpy(sc_np).to(dev)
+        idx = hip.Wrap(it.data_ptr(), tuple(idx_np.shape), I32, keep=it)
+        scores = hip.Wrap(sct.data_ptr(), tuple(sc_np.shape), F32, keep=sct)
+        xs = bf16((T, H))
+        ot = torch.empty((T, H), device=dev, dtype=torch.float32)
+        out = hip.Wrap(ot.data_ptr(), (T, H), F32, keep=ot)
+        hip.SetStream(torch.cuda.current_stream().cuda_stream)
+        for _ in range(3):
+            for st in stacks:
+                hip.MoeSwiGLU(xs, st["gate"], st["up"], st["down"], idx, scores, GS, 4, out=out)
+        torch.cuda.synchronize()
+        log(f"moe workload T={T} done")
+        hip.Close()
+        return 0
+
     if args.prefill_workload:
         hip.SetStream(torch.cuda.current_stream().cuda_stream)
         m = args.prefill_workload
@@ -204,6 +233,17 @@ def main() -> int:
                 launch(name, L[name], xin[name], ys[name])
         torch.cuda.synchronize()
         log("pmc workload done")
+        hip.Close()
+        return 0
+
+    if args.dominant_workload:
+        def dominant_graph():
+            for L in layers:
+                for name in ("qkv", "o", "gate_up"):
+                    launch(name, L[name], xin[name], ys[name])
+        g = capture(dominant_graph)
+        ms = time_graph(g, args.steps, args.warmup)
+        log(f"dominant workload: {ms * 1e3 / (3 * LAYERS):.3f} us per launch")
         hip.Close()
         return 0
 
@@ -280,7 +320,7 @@ def main() -> int:
                 "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
                 "traffic_source": "rocprofv3 --pmc FETCH_SIZE (x2.0) + WRITE_SIZE, "
                                   "profiles/qmv_bf16x_k4096_traffic.md",
-                "kernel": "qmv_bf16x_kernel<32,1,4,4,false> (K=4096 decode GEMV: qkv, o, gate_up)",
+                "kernel": "qmv_bf16x_kernel, K=4096 decode GEMV tiles <32,1,4,4> (qkv, gate_up) and <32,1,2,4> (o)",
                 "launches_per_step": n_dom, "avg_launch_us": round(ms_dom * 1e3 / n_dom, 3),
                 "algorithmic_bytes_per_launch": bytes_dom // n_dom}
 
