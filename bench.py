@@ -135,8 +135,8 @@ def main() -> int:
     bytes_token = LAYERS * bytes_layer + qbytes(VOCAB, HIDDEN)
     n_launch = LAYERS * 4 + 1
 
-    def capture(fn):
-        g = torch.cuda.CUDAGraph()
+    def capture(fn, keep=False):
+        g = torch.cuda.CUDAGraph(keep_graph=keep)
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -147,6 +147,8 @@ def main() -> int:
             hip.SetStream(torch.cuda.current_stream().cuda_stream)
             fn()
         hip.SetStream(torch.cuda.current_stream().cuda_stream)
+        if keep:
+            g.instantiate()
         torch.cuda.synchronize()
         return g
 
@@ -456,6 +458,24 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
     return res
 
 
+def graph_kernel_nodes(graph) -> int:
+    """Kernel nodes of a captured HIP graph (hipGraphGetNodes / hipGraphNodeGetType)."""
+    import ctypes
+
+    rt = ctypes.CDLL("libamdhip64.so")
+    n = ctypes.c_size_t(0)
+    if rt.hipGraphGetNodes(ctypes.c_void_p(graph), None, ctypes.byref(n)) != 0:
+        return -1
+    nodes = (ctypes.c_void_p * n.value)()
+    if rt.hipGraphGetNodes(ctypes.c_void_p(graph), nodes, ctypes.byref(n)) != 0:
+        return -1
+    kinds = [ctypes.c_int(0) for _ in range(n.value)]
+    for i in range(n.value):
+        if rt.hipGraphNodeGetType(ctypes.c_void_p(nodes[i]), ctypes.byref(kinds[i])) != 0:
+            return -1
+    return sum(1 for k in kinds if k.value == 0)  # hipGraphNodeTypeKernel
+
+
 def decode_step_figures(hip, torch, dev, capture, time_graph, args, contexts=(512, 8192)):
     """Config 4: the whole Qwen3-8B-architecture decode step (36 layers: RMSNorm,
     q/k/v product, per-head q/k RMSNorm, RoPE, KV append, SDPA over the cache, o
@@ -481,14 +501,13 @@ def decode_step_figures(hip, torch, dev, capture, time_graph, args, contexts=(51
     H, Hq, Hk, Dh, I = cfg.hidden, cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.inter
     per_layer = (qbytes((Hq + 2 * Hk) * Dh, H) + qbytes(H, Hq * Dh) + qbytes(2 * I, H) + qbytes(H, I))
     weights = cfg.layers * per_layer + qbytes(cfg.vocab, H) + (H // 2 + 4 * (H // GS))  # + one embedding row
-    # embedding (3 row gathers + dequantize), RoPE table, first norm, 6 per layer, lm_head + 2-stage argmax
-    launches = 6 + cfg.layers * 6 + 3
     res = {}
     for ctx in contexts:
         def fn(ctx=ctx):
             with hip.use_arena(arena):
                 decode_step(hip, m, tt, ctx)
-        g = capture(fn)
+        g = capture(fn, keep=True)
+        launches = graph_kernel_nodes(g.raw_cuda_graph())
         ms = time_graph(g, max(5, args.steps // 4), 3)
         kv = cfg.layers * 2 * Hk * (ctx + 1) * Dh * 2
         res[f"ctx{ctx}"] = {"us_per_token": round(ms * 1e3, 1), "tok_s": round(1000.0 / ms, 1),

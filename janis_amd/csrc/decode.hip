@@ -552,14 +552,24 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
 //   3. the slots merge in registers (cross-row permlane swaps) and then across
 //      the 4 waves in LDS;
 //   4. with one split the block writes the output; otherwise (max, sum,
-//      weighted values) go to the workspace in sdpa_decode_split_kernel's
-//      layout and sdpa_decode_merge_kernel merges them. (A last-block merge in
-//      the same launch needs an agent-scope release per block, an L2 writeback
-//      on this multi-L2 part, which cost ten times the merge launch. Without
-//      the release -- partials as agent-scope stores, which write through, an
-//      agent-scope arrival counter, agent-scope loads in the last block -- it
-//      still measured slower than the merge launch: 9.7 against 9.1 us per
-//      layer at 512 keys, 25.4 against 17.0 us at 8192.)
+//      weighted values) go to the workspace and are merged in split order,
+//      either
+//      - in the same launch (`sync` set, kv heads a multiple of 8): the grid
+//        is 1-D and block b runs on XCD b % 8 (workgroups are dealt to the 8
+//        XCDs round-robin in launch order; jh_create checks this on the
+//        device and leaves `sync` unset otherwise), so every split of kv head
+//        hk runs on XCD hk % 8 and shares its L2. Each block stores its
+//        partials (128-byte-aligned records, plain stores: the per-CU L1 is
+//        write-through), waits for the stores, and adds one to the head's
+//        arrival counter with an L2 atomic; the block that arrives last reads
+//        the partials back from that L2 and writes the output, then clears
+//        the counter for the next call. Nothing leaves the XCD: no release to
+//        memory, no second launch. (The same protocol at agent scope -- stores
+//        written through to memory, memory atomics, 9.7 against 9.1 us per
+//        layer at 512 keys -- lost to the merge launch, and an agent-scope
+//        release per block, an L2 writeback, cost ten times it.)
+//      - or in sdpa_decode_merge_kernel, from sdpa_decode_split_kernel's
+//        layout.
 struct AttnArgs {
     const void* qkv;    // [(Hq + 2 Hk) * 128]: q heads, k heads, v heads
     int qkv_dt;
@@ -574,15 +584,26 @@ struct AttnArgs {
     int64_t cap;
     int Hk, nsplit, kps;
     int owner_alone;    // 1: split 0 takes only the new key; 0: the last split also takes it
-    float* part;        // [Hk, nsplit, G, 130]
+    float* part;        // [Hk, nsplit, G, 130], or [Hk, nsplit] records of attn_rec_floats(G) with `sync`
     void* out;          // [Hq * 128]
     int out_dt;
+    int* sync;          // [Hk] arrival counters (zero between calls), or nullptr: merge launch
 };
+
+// Floats of one split's partials in the in-launch merge layout: G x (max, sum,
+// 128 values), rounded up to whole 128-byte lines so that no two blocks' records
+// share a cache line.
+constexpr int attn_rec_floats(int G) { return (G * (kDecodeDh + 2) + 31) / 32 * 32; }
+static_assert(kDecodeDh == 128, "the in-launch merge maps 64 lanes onto G x 128 outputs");
 
 template <int G, int U>  // U: keys per slot per load batch
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
     constexpr int Dh = 128;
-    const int split = blockIdx.x, hk = blockIdx.y;
+    // 1-D grid with `sync`: block b = 8 t + x runs on XCD x and takes kv head
+    // x + 8 (t / nsplit), split t % nsplit
+    const int t8 = blockIdx.x >> 3;
+    const int split = a.sync ? t8 % a.nsplit : blockIdx.x;
+    const int hk = a.sync ? (blockIdx.x & 7) + 8 * (t8 / a.nsplit) : blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int kg = lane >> 4, kl = lane & 15;
     const int Hq = a.Hk * G;
@@ -820,16 +841,121 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
 
     // 4. partials out
     constexpr int PS = Dh + 2;
-    float* mine = a.part + ((int64_t)hk * a.nsplit + split) * G * PS;
+    if (!a.sync) {
+        float* mine = a.part + ((int64_t)hk * a.nsplit + split) * G * PS;
+#pragma unroll
+        for (int r = 0; r < PER; r++) {
+            const int t = threadIdx.x + 256 * r;
+            if (t < G * Dh) {
+                const int g = t / Dh, d = t - g * Dh;
+                mine[g * PS + 2 + d] = rA[r];
+                if (d == 0) mine[g * PS] = rM[r], mine[g * PS + 1] = rL[r];
+            }
+        }
+        return;
+    }
+    // in-launch layout: a record of REC floats per split, values [G][128]
+    // first (16-byte aligned), then max[G], sum[G]
+    constexpr int REC = attn_rec_floats(G);
+    float* mine = a.part + ((int64_t)hk * a.nsplit + split) * REC;
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int t = threadIdx.x + 256 * r;
+        if (t < G * Dh) {
+            mine[t] = rA[r];
+            if ((t & (Dh - 1)) == 0) mine[G * Dh + t / Dh] = rM[r], mine[G * Dh + G + t / Dh] = rL[r];
+        }
+    }
+
+    // 5. in-launch merge on this XCD: every wave's partial stores have reached
+    // the L2 before the block's arrival is counted there
+    __shared__ int last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(a.sync + hk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+               a.nsplit - 1;
+    __syncthreads();
+    if (!last) return;
+    // The last block: all splits' records are in this XCD's L2 (this CU's L1
+    // holds no line of another block's record: records are whole lines and no
+    // block reads them before this point). Wave w merges splits w, w + 4, ...
+    // in that order, SB splits per round trip, lane l holding VPL consecutive
+    // outputs of one query head; the 4 waves' results meet in LDS.
+    constexpr int VPL = G * Dh / 64, SB = VPL >= 16 ? 4 : (VPL >= 8 ? 8 : 16);
+    const int o0 = lane * VPL, gl = o0 / Dh;
+    const float* hb = a.part + (int64_t)hk * a.nsplit * REC;
+    float M = -__builtin_inff(), L = 0.0f, A[VPL];
+#pragma unroll
+    for (int e = 0; e < VPL; e++) A[e] = 0.0f;
+    for (int s0 = wave; s0 < a.nsplit; s0 += 4 * SB) {
+        float mv[SB], lv[SB], av[SB][VPL];
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const int sp = s0 + 4 * u;
+            const float* rec = hb + (int64_t)min(sp, a.nsplit - 1) * REC;  // in bounds either way
+            const bool in = sp < a.nsplit;
+            mv[u] = in ? rec[G * Dh + gl] : -__builtin_inff();
+            lv[u] = rec[G * Dh + G + gl];
+            if constexpr (VPL >= 4) {
+#pragma unroll
+                for (int e = 0; e < VPL; e += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(rec + o0 + e);
+                    av[u][e] = v.x, av[u][e + 1] = v.y, av[u][e + 2] = v.z, av[u][e + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < VPL; e++) av[u][e] = rec[o0 + e];
+            }
+        }
+        float mn = M;
+#pragma unroll
+        for (int u = 0; u < SB; u++) mn = fmaxf(mn, mv[u]);
+        if (mn == -__builtin_inff()) continue;  // no keys so far
+        const float corr = __expf(M - mn);
+        L *= corr;
+#pragma unroll
+        for (int e = 0; e < VPL; e++) A[e] *= corr;
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const float c = __expf(mv[u] - mn);  // 0 for splits past the end
+            L = fmaf(lv[u], c, L);
+#pragma unroll
+            for (int e = 0; e < VPL; e++) A[e] = fmaf(av[u][e], c, A[e]);
+        }
+        M = mn;
+    }
+    // the waves' results through step 3's LDS (free since the barriers above)
+#pragma unroll
+    for (int e = 0; e < VPL; e++) wacc[wave][gl][o0 - gl * Dh + e] = A[e];
+    if ((o0 & (Dh - 1)) == 0) wm[wave][gl] = M, wl[wave][gl] = L;
+    __syncthreads();
 #pragma unroll
     for (int r = 0; r < PER; r++) {
         const int t = threadIdx.x + 256 * r;
         if (t < G * Dh) {
             const int g = t / Dh, d = t - g * Dh;
-            mine[g * PS + 2 + d] = rA[r];
-            if (d == 0) mine[g * PS] = rM[r], mine[g * PS + 1] = rL[r];
+            float Mt = wm[0][g];
+#pragma unroll
+            for (int w = 1; w < 4; w++) Mt = fmaxf(Mt, wm[w][g]);
+            float Lt = 0.0f, At = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float c = wm[w][g] == -__builtin_inff() ? 0.0f : __expf(wm[w][g] - Mt);
+                Lt = fmaf(wl[w][g], c, Lt);
+                At = fmaf(wacc[w][g][d], c, At);
+            }
+            st_act(a.out, (int64_t)hk * G * Dh + t, At / Lt, a.out_dt);
         }
     }
+    if (threadIdx.x == 0) __hip_atomic_store(a.sync + hk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Workgroup -> XCD placement: out[b] = the XCD (XCC id) block b runs on.
+__global__ __launch_bounds__(64) void xcc_probe_kernel(int* out) {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    if (threadIdx.x == 0) out[blockIdx.x] = (int)(x & 0xFu);
 }
 
 // ---- elementwise -----------------------------------------------------------------
@@ -1101,8 +1227,11 @@ struct AttnSplit {
     bool owner_alone;
 };
 
-AttnSplit attn_split(int64_t Hk, int64_t pos, int num_cus) {
-    const int64_t target = std::max<int64_t>(1, 2 * (int64_t)num_cus / Hk);
+// With the in-launch merge the last block reads every split's partials, so
+// long caches take one block per CU instead of two (the attention launch alone
+// measured the same for 128 to 1024 blocks at 8192 keys).
+AttnSplit attn_split(int64_t Hk, int64_t pos, int num_cus, bool in_launch) {
+    const int64_t target = std::max<int64_t>(1, (in_launch ? 1 : 2) * (int64_t)num_cus / Hk);
     AttnSplit sp;
     sp.u = pos <= 64 * target ? 4 : 8;
     const int64_t batch = 16 * sp.u;
@@ -1116,24 +1245,36 @@ AttnSplit attn_split(int64_t Hk, int64_t pos, int num_cus) {
 }
 
 size_t attn_decode_workspace_bytes(int64_t Hq, int64_t Hk, int64_t pos, int num_cus) {
-    const AttnSplit sp = attn_split(Hk, pos, num_cus);
-    return sp.nsplit > 1 ? (size_t)(Hk * sp.nsplit * (Hq / Hk) * (kDecodeDh + 2)) * sizeof(float) : 0;
+    // the larger of the two plans' needs
+    AttnSplit sp = attn_split(Hk, pos, num_cus, false);
+    const AttnSplit sp1 = attn_split(Hk, pos, num_cus, true);
+    if (sp1.nsplit > sp.nsplit) sp = sp1;
+    if (sp.nsplit <= 1) return 0;
+    // the larger of the two layouts (records padded to whole lines for the
+    // in-launch merge)
+    const int64_t G = Hq / Hk;
+    const int64_t rec = std::max<int64_t>(G * (kDecodeDh + 2), (G * (kDecodeDh + 2) + 31) / 32 * 32);
+    return (size_t)(Hk * sp.nsplit * rec) * sizeof(float);
 }
+
+bool attn_merge_in_launch(int64_t Hk, const int* sync) { return sync != nullptr && Hk % 8 == 0 && Hk <= kAttnSyncSlots; }
 
 Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt,
                           float eps, float base, float rscale, const float* rope_cs, int64_t pos, void* kc,
                           void* vc, int64_t cap, float scale, void* out, int out_dt, void* workspace, int num_cus,
-                          hipStream_t st) {
+                          hipStream_t st, int* sync) {
     const int G = Hq / Hk;
-    const AttnSplit sp = attn_split(Hk, pos, num_cus);
+    const bool sync_ok = attn_merge_in_launch(Hk, sync);
+    const AttnSplit sp = attn_split(Hk, pos, num_cus, sync_ok);
     const int64_t kps = sp.kps, nsplit = sp.nsplit;
     if (nsplit > kMaxSplits || kps > 0x7fffffff) return Status::fail(JH_ERR_UNSUPPORTED, "attention: cache too long");
     // cache rows are addressed with 32-bit byte offsets within a head
     if (cap > ((int64_t)1 << 23) - 1024) return Status::fail(JH_ERR_UNSUPPORTED, "attention: capacity above 8M tokens");
+    const bool in_launch = nsplit > 1 && sync_ok;
     AttnArgs a{qkv, qkv_dt, qn_w, kn_w, w_dt, eps, base, rscale, scale, rope_cs, pos,
                static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), cap, Hk, (int)nsplit, (int)kps,
-               sp.owner_alone ? 1 : 0, static_cast<float*>(workspace), out, out_dt};
-    const dim3 grid((unsigned)nsplit, (unsigned)Hk);
+               sp.owner_alone ? 1 : 0, static_cast<float*>(workspace), out, out_dt, in_launch ? sync : nullptr};
+    const dim3 grid = in_launch ? dim3((unsigned)(nsplit * Hk)) : dim3((unsigned)nsplit, (unsigned)Hk);
     const bool u8 = sp.u == 8;
     auto go = [&](auto k4, auto k8) {
         if (u8)
@@ -1146,10 +1287,23 @@ Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const voi
     else if (G == 4) go(attn_decode_kernel<4, 4>, attn_decode_kernel<4, 8>);
     else if (G == 8) go(attn_decode_kernel<8, 4>, attn_decode_kernel<8, 8>);
     else return Status::fail(JH_ERR_UNSUPPORTED, "attention: n_heads / n_kv_heads must be 1, 2, 4 or 8");
-    if (nsplit > 1)
+    if (nsplit > 1 && !in_launch)
         hipLaunchKernelGGL(sdpa_decode_merge_kernel, dim3((unsigned)Hq), dim3(kDecodeDh * merge_groups(nsplit)), 0, st,
                            static_cast<const float*>(workspace), Hk, G, (int)nsplit, out, out_dt);
     return Status::ok();
+}
+
+int probe_xcd_round_robin(int* buf, hipStream_t st) {
+    constexpr int kBlocks = 64;
+    hipLaunchKernelGGL(xcc_probe_kernel, dim3(kBlocks), dim3(64), 0, st, buf);
+    int h[kBlocks];
+    if (hipMemcpyAsync(h, buf, sizeof h, hipMemcpyDeviceToHost, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    for (int b = 0; b < kBlocks; b++)
+        if (h[b] != b % 8) return 0;
+    return 8;
 }
 
 Status launch_norm_prepare(const void* x, int x_dt, int64_t d, const void* w, int w_dt, uint16_t* out, float* stats,

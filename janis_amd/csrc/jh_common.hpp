@@ -304,10 +304,19 @@ Status launch_qk_norm_rope_append(const void* qkv, int qkv_dt, int Hq, int Hk, c
 // One-token attention (q/k norm, RoPE, KV append, SDPA over keys 0..pos): one
 // launch, plus a merge launch when the keys are split over blocks.
 size_t attn_decode_workspace_bytes(int64_t Hq, int64_t Hk, int64_t pos, int num_cus);
+// `sync` (kAttnSyncSlots zeroed ints per context, or nullptr) lets the split
+// partials be merged inside the attention launch when the GPU deals workgroups
+// to its 8 XCDs round-robin (probe_xcd_round_robin) and the kv heads are a
+// multiple of 8; otherwise a merge launch follows.
+constexpr int kAttnSyncSlots = 1024;
+bool attn_merge_in_launch(int64_t Hk, const int* sync);
 Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt,
                           float eps, float base, float rscale, const float* rope_cs, int64_t pos, void* kc,
                           void* vc, int64_t cap, float scale, void* out, int out_dt, void* workspace, int num_cus,
-                          hipStream_t st);
+                          hipStream_t st, int* sync);
+// 8 when block b of a launch runs on XCD b % 8 (checked on a 64-block launch;
+// buf: 64 ints of device memory), else 0.
+int probe_xcd_round_robin(int* buf, hipStream_t st);
 Status launch_rope_table(int dims, float base, float scale, int64_t pos, const float* freqs, float* out,
                          hipStream_t st);
 constexpr int kMaxCopyDims = 8;

@@ -30,6 +30,10 @@ struct jh_ctx {
     std::vector<void*> retired;
     unsigned long long* check_buf = nullptr;  // 2 counters of the value checks
     void* scratch = nullptr;  // this device's copy of `scratch` (jh_attention_decode_noalloc)
+    // Arrival counters of the in-launch attention merge (jh::kAttnSyncSlots
+    // ints, zero between calls), or nullptr when the GPU does not deal
+    // workgroups to its XCDs round-robin: then the merge is a second launch.
+    int* attn_sync = nullptr;
 };
 
 namespace {
@@ -292,6 +296,22 @@ int jh_create(int device, jh_ctx** out) {
     // the no-allocation entry point's scratch, located once per device now, with
     // the device current (a failure here only disables that entry point)
     c->scratch = scratch_address(device);
+    // counters of the in-launch attention merge, after checking on the device
+    // that block b of a launch runs on XCD b % 8 (a failure only keeps the
+    // merge a launch of its own)
+    if (hipMalloc(&c->attn_sync, jh::kAttnSyncSlots * sizeof(int)) == hipSuccess) {
+        if (hipMemsetAsync(c->attn_sync, 0, jh::kAttnSyncSlots * sizeof(int), c->own_stream) != hipSuccess ||
+            jh::probe_xcd_round_robin(c->attn_sync, c->own_stream) != 8 ||
+            hipMemsetAsync(c->attn_sync, 0, jh::kAttnSyncSlots * sizeof(int), c->own_stream) != hipSuccess ||
+            hipStreamSynchronize(c->own_stream) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipFree(c->attn_sync);
+            c->attn_sync = nullptr;
+        }
+    } else {
+        (void)hipGetLastError();
+        c->attn_sync = nullptr;
+    }
     std::snprintf(c->name, sizeof(c->name), "%s (%s, %d CUs)", prop.name, prop.gcnArchName, c->num_cus);
     *out = c;
     return JH_OK;
@@ -305,6 +325,7 @@ void jh_destroy(jh_ctx* c) {
     if (c->ws) (void)hipFree(c->ws);
     for (void* p : c->retired) (void)hipFree(p);
     if (c->check_buf) (void)hipFree(c->check_buf);
+    if (c->attn_sync) (void)hipFree(c->attn_sync);
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     delete c;
 }
@@ -702,7 +723,8 @@ int jh_attention_decode(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t 
         if (int r = ensure_workspace(c, need, op)) return r;
     if (int r = finish(c, jh::launch_attn_decode(qkv, qkv_dtype, (int)n_heads, (int)n_kv_heads, q_norm_w, k_norm_w,
                                                  w_dtype, eps, rope_base, rope_scale, rope_cs, pos, k_cache, v_cache,
-                                                 capacity, scale, out, out_dtype, c->ws, c->num_cus, c->stream),
+                                                 capacity, scale, out, out_dtype, c->ws, c->num_cus, c->stream,
+                                                 c->attn_sync),
                        op))
         return r;
     return check_values(c, op, out, out_dtype, n_heads * head_dim);
@@ -729,7 +751,8 @@ int jh_attention_decode_noalloc(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, 
     // so the scratch needs no clearing
     return finish(c, jh::launch_attn_decode(qkv, qkv_dtype, (int)n_heads, (int)n_kv_heads, q_norm_w, k_norm_w,
                                             w_dtype, eps, rope_base, rope_scale, rope_cs, pos, k_cache, v_cache,
-                                            capacity, scale, out, out_dtype, c->scratch, c->num_cus, c->stream),
+                                            capacity, scale, out, out_dtype, c->scratch, c->num_cus, c->stream,
+                                            c->attn_sync),
                   op);
 }
 

@@ -68,7 +68,9 @@ def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bo
     and the sum of h^2) and the product that reads it (which applies the
     1/rms factor to its output), SiLU*mul in the gate/up product's epilogue,
     the residual adds in the o/down products' epilogues, and the q/k norms,
-    RoPE, KV append and SDPA in one launch plus a merge (6 launches per layer).
+    RoPE, KV append and SDPA in one launch, whose split partials are merged
+    inside it (5 launches per layer; a merge launch follows on GPUs that do not
+    deal workgroups to their XCDs round-robin).
     fused=False makes the reference's calls one for one (qwen/block.go,
     qwen/attention.go, qwen/mlp.go, qwen/cache.go): separate q/k/v and gate/up
     products on row views of the stacked matrices, Reshape/Transpose views, the

@@ -347,7 +347,9 @@ def _attention_oracle(oracle, qkv, qn, kn, k_old, v_old, Hq, Hk, pos, scale):
                                                        (32, 8, 16, True, False), (32, 8, 512, True, True),
                                                        (32, 8, 8192, True, True), (8, 8, 300, False, False),
                                                        (16, 8, 1000, True, True), (64, 8, 777, True, False),
-                                                       (32, 8, 64, True, True), (32, 8, 65, True, False)])
+                                                       (32, 8, 64, True, True), (32, 8, 65, True, False),
+                                                       (32, 4, 600, True, True), (64, 16, 900, True, False),
+                                                       (32, 8, 3000, True, True)])
 def test_attention_decode(hip, oracle, Hq, Hk, pos, with_norm, table):
     """jh_attention_decode (q/k norm, RoPE, KV append, SDPA in one launch)
     against the oracle's RMSNorm + RoPE + SDPA over the updated cache, and
