@@ -320,6 +320,31 @@ JH_API int jh_attention_decode(jh_ctx *ctx, const void *qkv, jh_dtype qkv_dtype,
                         void *v_cache, jh_dtype cache_dtype, int64_t capacity, float scale, void *out,
                         jh_dtype out_dtype);
 
+/* The q/k/v product of one token and its attention in one launch: exactly
+ * jh_quant_matvec_fused(JH_PRO_NORMED, x, norm_stats, norm_eps, w/scales/biases
+ * with (n_heads + 2 n_kv_heads) * head_dim rows, JH_EPI_STORE, y = qkv of
+ * qkv_dtype bf16 or f32) followed by jh_attention_decode(qkv, qkv_dtype, ...),
+ * with the same results bit
+ * for bit: Attention.Forward's QuantLinear calls, QNorm/KNorm, RoPE, the KV
+ * append and SDPA of one token (qwen/attention.go:98-128) after the block's
+ * input RMSNorm (qwen/block.go:59). An optional capability in the pattern of
+ * engine/backend.go:38-112 (the reference makes these calls one by one).
+ * On MI355X with 8 kv heads, head_dim 128, in_features 4096 and 4-bit codes in
+ * groups of 64 with bf16 scales, the kv head h's rows are computed on XCD h and
+ * its attention follows there in the same launch (workgroups are dealt to the
+ * XCDs round-robin; jh_create checks this); any other call runs the two
+ * operators. The fused launch keeps all its blocks resident and must not share
+ * the GPU's CUs with other long-running kernels (it waits for its own blocks). */
+JH_API int jh_qkv_attention_decode(jh_ctx *ctx, const void *x, const float *norm_stats, float norm_eps,
+                                   const uint32_t *w, const void *scales, const void *biases, jh_dtype sb_dtype,
+                                   int64_t in_features, int group_size, int bits, void *qkv,
+                                   jh_dtype qkv_dtype, int64_t n_heads,
+                                   int64_t n_kv_heads, int64_t head_dim, const void *q_norm_w,
+                                   const void *k_norm_w, jh_dtype w_dtype, float eps, float rope_base,
+                                   float rope_scale, const float *rope_cs, int64_t pos, void *k_cache,
+                                   void *v_cache, jh_dtype cache_dtype, int64_t capacity, float scale, void *out,
+                                   jh_dtype out_dtype);
+
 /* jh_attention_decode for callers that cannot allocate device memory (code
  * under HIP graph capture on a context whose workspace was never sized, tight
  * serving loops, harnesses that forbid hipMalloc). It has no counterpart in the

@@ -15,6 +15,7 @@
 // weighted values); a second launch merges the splits. Other shapes take a
 // per-query-row kernel with the offset causal mask.
 #include "jh_common.hpp"
+#include "qmv_tile.hpp"
 
 namespace jh {
 namespace {
@@ -588,6 +589,9 @@ struct AttnArgs {
     void* out;          // [Hq * 128]
     int out_dt;
     int* sync;          // [Hk] arrival counters (zero between calls), or nullptr: merge launch
+    int* flags;         // fused q/k/v + attention launch: this XCD's arrival flags, cleared by its
+                        // last attention block; nullptr otherwise
+    int nflags;
 };
 
 // Floats of one split's partials in the in-launch merge layout: G x (max, sum,
@@ -596,14 +600,13 @@ struct AttnArgs {
 constexpr int attn_rec_floats(int G) { return (G * (kDecodeDh + 2) + 31) / 32 * 32; }
 static_assert(kDecodeDh == 128, "the in-launch merge maps 64 lanes onto G x 128 outputs");
 
-template <int G, int U>  // U: keys per slot per load batch
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+// One block's share of a one-token attention: split `split` of kv head hk.
+// FUSED (the q/k/v product ran earlier in the same launch, on this XCD): the
+// block's K/V rows are requested first, then wait() returns once the product's
+// rows are all stored, and q/k/v are read device-coherently from the L2.
+template <int G, int U, bool FUSED, class Wait>  // U: keys per slot per load batch
+__device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, const int hk, Wait wait) {
     constexpr int Dh = 128;
-    // 1-D grid with `sync`: block b = 8 t + x runs on XCD x and takes kv head
-    // x + 8 (t / nsplit), split t % nsplit
-    const int t8 = blockIdx.x >> 3;
-    const int split = a.sync ? t8 % a.nsplit : blockIdx.x;
-    const int hk = a.sync ? (blockIdx.x & 7) + 8 * (t8 / a.nsplit) : blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int kg = lane >> 4, kl = lane & 15;
     const int Hq = a.Hk * G;
@@ -631,26 +634,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
     const void* kwp = kn ? a.kn_w : a.qkv;
     const float* csp = table ? a.rope_cs : static_cast<const float*>(a.qkv);
     const int qw_dt = qn ? a.w_dt : a.qkv_dt, kw_dt = kn ? a.w_dt : a.qkv_dt;
-    uint32_t qraw[QPW][2], kvraw[6], wraw[2];
-#pragma unroll
-    for (int i = 0; i < QPW; i++) {
-        const int g = min(wave + 4 * i, G - 1);
-        const int64_t o = (int64_t)(hk * G + g) * Dh;
-        qraw[i][0] = ld_word(a.qkv, o + lane, a.qkv_dt);
-        qraw[i][1] = ld_word(a.qkv, o + lane + 64, a.qkv_dt);
-    }
-    wraw[0] = ld_word(qwp, lane, qw_dt);
-    wraw[1] = ld_word(qwp, lane + 64, qw_dt);
-    const float rc_raw = csp[lane], rs_raw = csp[64 + lane];
-    // Every wave issues the new key's loads (the same addresses in all blocks);
-    // only the owner's wave 3 uses them.
-    const int64_t ok = (int64_t)(Hq + hk) * Dh, ov = (int64_t)(Hq + a.Hk + hk) * Dh;
-    kvraw[0] = ld_word(a.qkv, ok + lane, a.qkv_dt);
-    kvraw[1] = ld_word(a.qkv, ok + lane + 64, a.qkv_dt);
-    kvraw[2] = ld_word(a.qkv, ov + lane, a.qkv_dt);
-    kvraw[3] = ld_word(a.qkv, ov + lane + 64, a.qkv_dt);
-    kvraw[4] = ld_word(kwp, lane, kw_dt);
-    kvraw[5] = ld_word(kwp, lane + 64, kw_dt);
     uint4 kr[U], vr[U];  // raw bf16 rows, unpacked one key at a time
     auto load_rows = [&](uint4 (&r)[U], __amdgpu_buffer_rsrc_t src, int64_t j0) {
 #pragma unroll
@@ -660,8 +643,45 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
         }
     };
     int64_t j0 = j_begin + slot;
-    load_rows(kr, kb, j0);
-    load_rows(vr, vb, j0);
+    if constexpr (FUSED) {
+        // the K/V rows do not depend on the product: in flight while it finishes
+        load_rows(kr, kb, j0);
+        load_rows(vr, vb, j0);
+        wait();
+    }
+    // q/k/v words (FUSED: bf16 or f32, stored by other CUs of this XCD, read from L2)
+    const bool qf32 = a.qkv_dt == JH_F32;
+    const auto rq = make_rsrc(a.qkv, (uint32_t)((Hq + 2 * a.Hk) * Dh * (qf32 ? 4 : 2)));
+    auto ldq = [&](int64_t i) -> uint32_t {
+        if constexpr (FUSED)
+            return __builtin_amdgcn_raw_buffer_load_b32(rq, (uint32_t)(qf32 ? i : i >> 1) * 4, 0, kAuxSc1);
+        else
+            return ld_word(a.qkv, i, a.qkv_dt);
+    };
+    uint32_t qraw[QPW][2], kvraw[6], wraw[2];
+#pragma unroll
+    for (int i = 0; i < QPW; i++) {
+        const int g = min(wave + 4 * i, G - 1);
+        const int64_t o = (int64_t)(hk * G + g) * Dh;
+        qraw[i][0] = ldq(o + lane);
+        qraw[i][1] = ldq(o + lane + 64);
+    }
+    wraw[0] = ld_word(qwp, lane, qw_dt);
+    wraw[1] = ld_word(qwp, lane + 64, qw_dt);
+    const float rc_raw = csp[lane], rs_raw = csp[64 + lane];
+    // Every wave issues the new key's loads (the same addresses in all blocks);
+    // only the owner's wave 3 uses them.
+    const int64_t ok = (int64_t)(Hq + hk) * Dh, ov = (int64_t)(Hq + a.Hk + hk) * Dh;
+    kvraw[0] = ldq(ok + lane);
+    kvraw[1] = ldq(ok + lane + 64);
+    kvraw[2] = ldq(ov + lane);
+    kvraw[3] = ldq(ov + lane + 64);
+    kvraw[4] = ld_word(kwp, lane, kw_dt);
+    kvraw[5] = ld_word(kwp, lane + 64, kw_dt);
+    if constexpr (!FUSED) {
+        load_rows(kr, kb, j0);
+        load_rows(vr, vb, j0);
+    }
 
     float rc = rc_raw, rsn = rs_raw;
     if (!table) head_rope_factors(a.base, a.rscale, a.pos, lane, rc, rsn);
@@ -836,6 +856,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
             const int t = threadIdx.x + 256 * r;
             if (t < G * Dh) st_act(a.out, (int64_t)hk * G * Dh + t, rA[r] / rL[r], a.out_dt);
         }
+        // the XCD's only attention block: every block has arrived, the call is over
+        if (FUSED)
+            for (int i = threadIdx.x; i < a.nflags; i += 256) a.flags[i] = 0;
         return;
     }
 
@@ -877,14 +900,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
                a.nsplit - 1;
     __syncthreads();
     if (!last) return;
-    // The last block: all splits' records are in this XCD's L2 (this CU's L1
-    // holds no line of another block's record: records are whole lines and no
-    // block reads them before this point). Wave w merges splits w, w + 4, ...
-    // in that order, SB splits per round trip, lane l holding VPL consecutive
+    // The last block: all splits' records are in this XCD's L2. Wave w merges
+    // splits w, w + 4, ... in that order, SB splits per round trip, lane l holding VPL consecutive
     // outputs of one query head; the 4 waves' results meet in LDS.
     constexpr int VPL = G * Dh / 64, SB = VPL >= 16 ? 4 : (VPL >= 8 ? 8 : 16);
     const int o0 = lane * VPL, gl = o0 / Dh;
-    const float* hb = a.part + (int64_t)hk * a.nsplit * REC;
+    // Reads are device-coherent (sc1): they miss this CU's L1, which could hold a
+    // stale copy of a line another CU wrote, and are served by the shared L2.
+    const auto hb = make_rsrc(a.part + (int64_t)hk * a.nsplit * REC, (uint32_t)(a.nsplit * REC * 4));
     float M = -__builtin_inff(), L = 0.0f, A[VPL];
 #pragma unroll
     for (int e = 0; e < VPL; e++) A[e] = 0.0f;
@@ -893,19 +916,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int u = 0; u < SB; u++) {
             const int sp = s0 + 4 * u;
-            const float* rec = hb + (int64_t)min(sp, a.nsplit - 1) * REC;  // in bounds either way
+            const uint32_t rec = (uint32_t)min(sp, a.nsplit - 1) * REC * 4;  // in bounds either way
             const bool in = sp < a.nsplit;
-            mv[u] = in ? rec[G * Dh + gl] : -__builtin_inff();
-            lv[u] = rec[G * Dh + G + gl];
+            const float m_ = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(hb, rec + (G * Dh + gl) * 4, 0, kAuxSc1));
+            mv[u] = in ? m_ : -__builtin_inff();
+            lv[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(hb, rec + (G * Dh + G + gl) * 4, 0, kAuxSc1));
             if constexpr (VPL >= 4) {
 #pragma unroll
                 for (int e = 0; e < VPL; e += 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(rec + o0 + e);
-                    av[u][e] = v.x, av[u][e + 1] = v.y, av[u][e + 2] = v.z, av[u][e + 3] = v.w;
+                    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(hb, rec + (o0 + e) * 4, 0, kAuxSc1);
+                    av[u][e] = __uint_as_float(v.x), av[u][e + 1] = __uint_as_float(v.y);
+                    av[u][e + 2] = __uint_as_float(v.z), av[u][e + 3] = __uint_as_float(v.w);
                 }
             } else {
 #pragma unroll
-                for (int e = 0; e < VPL; e++) av[u][e] = rec[o0 + e];
+                for (int e = 0; e < VPL; e++)
+                    av[u][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(hb, rec + (o0 + e) * 4, 0, kAuxSc1));
             }
         }
         float mn = M;
@@ -948,7 +974,99 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
             st_act(a.out, (int64_t)hk * G * Dh + t, At / Lt, a.out_dt);
         }
     }
-    if (threadIdx.x == 0) __hip_atomic_store(a.sync + hk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(a.sync + hk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    // every block of the XCD has arrived and every attention block has passed
+    // its wait: the flags start the next call at zero
+    if (FUSED)
+        for (int i = threadIdx.x; i < a.nflags; i += 256) a.flags[i] = 0;
+}
+
+template <int G, int U>
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+    // 1-D grid with `sync`: block b = 8 t + x runs on XCD x and takes kv head
+    // x + 8 (t / nsplit), split t % nsplit
+    const int t8 = blockIdx.x >> 3;
+    const int split = a.sync ? t8 % a.nsplit : blockIdx.x;
+    const int hk = a.sync ? (blockIdx.x & 7) + 8 * (t8 / a.nsplit) : blockIdx.y;
+    attn_body<G, U, false>(a, split, hk, [] {});
+}
+
+// ---- the q/k/v product and the attention of one token in one launch ----------------
+// Block b = 8 t + x runs on XCD x (workgroups are dealt round-robin) and owns kv
+// head x (8 kv heads): first its share of the q/k/v rows of that head (the G
+// query heads, the key head and the value head: (G + 2) x 128 rows of the
+// stacked matrix, 8 rows per block pass, the decode GEMV tile <32,1,4,4> with
+// the prepared-norm prologue, so the rows are bit for bit those of the plain
+// product), stored (bf16 or f32); then it sets its own arrival flag. Blocks
+// t < nsplit then run split t of the head's attention (attn_body): their K/V
+// rows are requested at once, and the q/k/v rows are read device-coherently
+// once one wave has seen every flag of the XCD set; the splits merge in the
+// launch, whose last block clears the flags for the next call.
+// (One arrival counter per XCD, 96 atomics on one L2 line, took 3-11 us to be
+// seen by the pollers on MI355X; per-block flags, about 1 us.) Every block of the grid is resident at once
+// (the launcher sizes the grid to the occupancy), so the wait ends; its bound
+// is a safety net only.
+struct QkvRows {
+    uint32_t qbase, kbase, vbase, g128, nblk, past;
+    __device__ uint32_t base(uint32_t blk) const {
+        if (blk >= nblk) return past;
+        const uint32_t i = blk * 8;
+        return i < g128 ? qbase + i : (i < g128 + 128 ? kbase + (i - g128) : vbase + (i - g128 - 128));
+    }
+};
+
+struct QkvAttnArgs {
+    AttnArgs a;                 // a.qkv: the product's output (bf16 or f32); a.flags: set below per XCD
+    int* flags;                 // per XCD kAttnMaxBlocksPerXcd arrival flags
+    const uint32_t* w;          // stacked q/k/v rows [(Hq + 2 Hk) * 128, K / 8]
+    const uint16_t* s;
+    const uint16_t* b;
+    const uint16_t* x;          // bf16 prepared norm input [K]
+    float* stats;               // its sum-of-squares partials (kNormSlots)
+    float norm_eps;
+    int gs_log2;
+    int bpx;                    // blocks per XCD
+};
+
+constexpr uint32_t kPhaseSpin = 1u << 22;
+
+template <int G, int U>
+__global__ __launch_bounds__(256) void qkv_attn_kernel(QkvAttnArgs f) {
+    const int x = blockIdx.x & 7, t = blockIdx.x >> 3;
+    int* flags = f.flags + kAttnMaxBlocksPerXcd * x;
+    AttnArgs a = f.a;
+    a.flags = flags;
+    const int Hq = a.Hk * G;
+    const uint32_t rows = (uint32_t)(Hq + 2 * a.Hk) * 128;
+    const QkvRows map{(uint32_t)(x * G * 128), (uint32_t)((Hq + x) * 128), (uint32_t)((Hq + a.Hk + x) * 128),
+                      (uint32_t)(G * 128), (uint32_t)((G + 2) * 16), rows};
+    qmvt::QmvFusion fu;
+    fu.eps = f.norm_eps;
+    fu.stats = f.stats;
+    qmvt::qmv_tile<32, 1, 4, 4, false, qmvt::PRO_NORMED, qmvt::EPI_STORE, 4, false>(
+        f.w, f.s, f.b, f.x, const_cast<void*>(a.qkv), a.qkv_dt, rows, f.gs_log2, fu, (uint32_t)t, (uint32_t)f.bpx,
+        map.nblk, map);
+    // the block's rows are in the L2 before its flag is
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(flags + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t >= a.nsplit) return;
+    attn_body<G, U, true>(a, t, x, [&] {
+        // wave 0 reads all the XCD's flags per round (device-scope atomic loads:
+        // they miss the L1, and the compiler keeps them in the loop)
+        if (threadIdx.x < 64) {
+            const int l = threadIdx.x;
+            for (uint32_t n = 0; n < kPhaseSpin; n++) {
+                const int f0 = l < f.bpx ? __hip_atomic_load(flags + l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1;
+                const int f1 =
+                    l + 64 < f.bpx ? __hip_atomic_load(flags + l + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1;
+                if (__all(f0 == 1 && f1 == 1)) break;
+            }
+        }
+        __syncthreads();
+    });
 }
 
 // Workgroup -> XCD placement: out[b] = the XCD (XCC id) block b runs on.
@@ -1257,7 +1375,25 @@ size_t attn_decode_workspace_bytes(int64_t Hq, int64_t Hk, int64_t pos, int num_
     return (size_t)(Hk * sp.nsplit * rec) * sizeof(float);
 }
 
-bool attn_merge_in_launch(int64_t Hk, const int* sync) { return sync != nullptr && Hk % 8 == 0 && Hk <= kAttnSyncSlots; }
+bool attn_merge_in_launch(int64_t Hk, const int* sync) { return sync != nullptr && Hk % 8 == 0 && Hk <= kAttnFlagSlot; }
+
+namespace {
+int log2_exact(int v) {
+    int l = 0;
+    while ((1 << l) < v) l++;
+    return ((1 << l) == v) ? l : -1;
+}
+}  // namespace
+
+// The fused launch takes 8 kv heads (one per XCD) of head_dim 128, G = 1, 2, 4
+// or 8, and the q/k/v matrix the <32,1,4,4> decode tile takes: K = 4096, 4-bit
+// codes in groups of 64 with bf16 scales, (Hq + 2 Hk) x 128 rows.
+bool qkv_attn_ok(const QuantMatrix& m, int64_t Hq, int64_t Hk, const int* sync, int num_cus) {
+    const int64_t G = Hk > 0 ? Hq / Hk : 0;
+    return sync != nullptr && Hk == 8 && G * Hk == Hq && (G == 1 || G == 2 || G == 4 || G == 8) && m.bits == 4 &&
+           m.group_size == 64 && m.in == 4096 && m.sb_dtype == JH_BF16 && m.rows == (Hq + 2 * Hk) * kDecodeDh &&
+           num_cus % 8 == 0 && num_cus >= 64;
+}
 
 Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt,
                           float eps, float base, float rscale, const float* rope_cs, int64_t pos, void* kc,
@@ -1291,6 +1427,54 @@ Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const voi
         hipLaunchKernelGGL(sdpa_decode_merge_kernel, dim3((unsigned)Hq), dim3(kDecodeDh * merge_groups(nsplit)), 0, st,
                            static_cast<const float*>(workspace), Hk, G, (int)nsplit, out, out_dt);
     return Status::ok();
+}
+
+Status launch_qkv_attn(const QuantMatrix& m, const uint16_t* x, float* stats, float norm_eps, void* qkv, int qkv_dt,
+                       int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt, float eps, float base, float rscale,
+                       const float* rope_cs, int64_t pos, void* kc, void* vc, int64_t cap, float scale, void* out,
+                       int out_dt, void* workspace, int num_cus, hipStream_t st, int* sync) {
+    const int G = Hk > 0 ? Hq / Hk : 0;
+    if (!qkv_attn_ok(m, Hq, Hk, sync, num_cus)) return Status::fail(JH_ERR_UNSUPPORTED, "qkv_attn: outside the fused launch");
+    if (cap > ((int64_t)1 << 23) - 1024) return Status::fail(JH_ERR_UNSUPPORTED, "attention: capacity above 8M tokens");
+    const AttnSplit sp = attn_split(Hk, pos, num_cus, true);
+    const bool u8 = sp.u == 8;
+    // blocks per XCD: one per 8-row pass of the head's q/k/v rows, at most what
+    // is resident at once (the attention blocks wait for all of them)
+    auto go = [&](auto k4, auto k8) -> Status {
+        auto kern = u8 ? k8 : k4;
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) != hipSuccess || per_cu < 1) {
+            (void)hipGetLastError();
+            return Status::fail(JH_ERR_UNSUPPORTED, "qkv_attn: occupancy unknown");
+        }
+        // two blocks per CU at most: against three (the occupancy of the 4-key
+        // kernel) the whole decode step measured 36-44 us per token faster at 512
+        // keys and 20 us at 8192 on MI355X (the product phase's last blocks
+        // finished ~2 us later with three); one block per CU was slower than both
+        per_cu = std::min(per_cu, 2);
+        const int bpx = std::min({(G + 2) * 16, per_cu * (num_cus / 8), kAttnMaxBlocksPerXcd});
+        if (bpx < sp.nsplit) return Status::fail(JH_ERR_UNSUPPORTED, "qkv_attn: more splits than resident blocks");
+        QkvAttnArgs f{};
+        f.a = AttnArgs{qkv, qkv_dt, qn_w, kn_w, w_dt, eps, base, rscale, scale, rope_cs, pos,
+                       static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc), cap, Hk, (int)sp.nsplit, (int)sp.kps,
+                       sp.owner_alone ? 1 : 0, static_cast<float*>(workspace), out, out_dt,
+                       sp.nsplit > 1 ? sync : nullptr, nullptr, bpx};
+        f.flags = sync + kAttnFlagSlot;
+        f.w = m.w;
+        f.s = static_cast<const uint16_t*>(m.scales);
+        f.b = static_cast<const uint16_t*>(m.biases);
+        f.x = x;
+        f.stats = stats;
+        f.norm_eps = norm_eps;
+        f.gs_log2 = log2_exact(m.group_size);
+        f.bpx = bpx;
+        hipLaunchKernelGGL(kern, dim3((unsigned)(8 * bpx)), dim3(256), 0, st, f);
+        return Status::ok();
+    };
+    if (G == 1) return go(qkv_attn_kernel<1, 4>, qkv_attn_kernel<1, 8>);
+    if (G == 2) return go(qkv_attn_kernel<2, 4>, qkv_attn_kernel<2, 8>);
+    if (G == 4) return go(qkv_attn_kernel<4, 4>, qkv_attn_kernel<4, 8>);
+    return go(qkv_attn_kernel<8, 4>, qkv_attn_kernel<8, 8>);
 }
 
 int probe_xcd_round_robin(int* buf, hipStream_t st) {

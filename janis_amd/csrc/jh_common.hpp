@@ -45,6 +45,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
 constexpr int kAuxNT = 2;  // non-temporal: streamed data, read once
+// Device-coherent load (gfx950 sc1): misses the CU's L1 and is served by the
+// XCD's L2, so it sees what another CU of the same XCD stored (a plain or sc0
+// load may return the L1's stale copy; measured on MI355X).
+constexpr int kAuxSc1 = 16;
 
 __device__ __forceinline__ uint4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAuxNT);
@@ -308,12 +312,23 @@ size_t attn_decode_workspace_bytes(int64_t Hq, int64_t Hk, int64_t pos, int num_
 // partials be merged inside the attention launch when the GPU deals workgroups
 // to its 8 XCDs round-robin (probe_xcd_round_robin) and the kv heads are a
 // multiple of 8; otherwise a merge launch follows.
-constexpr int kAttnSyncSlots = 1024;
+constexpr int kAttnSyncSlots = 4096;
+// The fused q/k/v + attention launch's share of them: per XCD x, the arrival
+// flags of its blocks at kAttnFlagSlot + 128 x (zero between calls).
+constexpr int kAttnFlagSlot = 1024;
+constexpr int kAttnMaxBlocksPerXcd = 128;
 bool attn_merge_in_launch(int64_t Hk, const int* sync);
 Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt,
                           float eps, float base, float rscale, const float* rope_cs, int64_t pos, void* kc,
                           void* vc, int64_t cap, float scale, void* out, int out_dt, void* workspace, int num_cus,
                           hipStream_t st, int* sync);
+// The q/k/v product (JH_PRO_NORMED prologue, bf16 or f32 out) and the attention of one
+// token in one launch (decode.hip); JH_ERR_UNSUPPORTED outside qkv_attn_ok.
+bool qkv_attn_ok(const QuantMatrix& m, int64_t Hq, int64_t Hk, const int* sync, int num_cus);
+Status launch_qkv_attn(const QuantMatrix& m, const uint16_t* x, float* stats, float norm_eps, void* qkv, int qkv_dt,
+                       int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt, float eps, float base, float rscale,
+                       const float* rope_cs, int64_t pos, void* kc, void* vc, int64_t cap, float scale, void* out,
+                       int out_dt, void* workspace, int num_cus, hipStream_t st, int* sync);
 // 8 when block b of a launch runs on XCD b % 8 (checked on a 64-block launch;
 // buf: 64 ints of device memory), else 0.
 int probe_xcd_round_robin(int* buf, hipStream_t st);

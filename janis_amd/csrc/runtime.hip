@@ -730,6 +730,50 @@ int jh_attention_decode(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t 
     return check_values(c, op, out, out_dtype, n_heads * head_dim);
 }
 
+int jh_qkv_attention_decode(jh_ctx* c, const void* x, const float* norm_stats, float norm_eps, const uint32_t* w,
+                            const void* scales, const void* biases, jh_dtype sb_dtype, int64_t in_features,
+                            int group_size, int bits, void* qkv, jh_dtype qkv_dtype, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                            const void* q_norm_w, const void* k_norm_w, jh_dtype w_dtype, float eps, float rope_base,
+                            float rope_scale, const float* rope_cs, int64_t pos, void* k_cache, void* v_cache,
+                            jh_dtype cache_dtype, int64_t capacity, float scale, void* out, jh_dtype out_dtype) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_qkv_attention_decode";
+    if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || n_heads % n_kv_heads != 0)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad head counts");
+    const int64_t rows = (n_heads + 2 * n_kv_heads) * head_dim;
+    if (int r = check_quant(c, op, w, scales, biases, sb_dtype, rows, in_features, group_size, bits)) return r;
+    if (!x || !aligned16(x) || !norm_stats || !aligned16(norm_stats) || !qkv || !aligned16(qkv))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": x, norm_stats and qkv must be non-null and 16-byte aligned");
+    if (qkv_dtype != JH_BF16 && qkv_dtype != JH_F32)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": qkv must be bf16 or f32");
+    if (int r = check_attention(c, op, qkv, qkv_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, w_dtype, pos,
+                                k_cache, v_cache, cache_dtype, capacity, out, out_dtype))
+        return r;
+    const jh::QuantMatrix m{w, scales, biases, sb_dtype, rows, in_features, group_size, bits};
+    const size_t need = jh::attn_decode_workspace_bytes(n_heads, n_kv_heads, pos, c->num_cus);
+    if (need)
+        if (int r = ensure_workspace(c, need, op)) return r;
+    if (jh::qkv_attn_ok(m, n_heads, n_kv_heads, c->attn_sync, c->num_cus)) {
+        const jh::Status st = jh::launch_qkv_attn(m, static_cast<const uint16_t*>(x), const_cast<float*>(norm_stats),
+                                                  norm_eps, qkv, (int)qkv_dtype, (int)n_heads, (int)n_kv_heads,
+                                                  q_norm_w, k_norm_w, w_dtype, eps, rope_base, rope_scale, rope_cs, pos,
+                                                  k_cache, v_cache, capacity, scale, out, out_dtype, c->ws, c->num_cus,
+                                                  c->stream, c->attn_sync);
+        if (st.code != JH_ERR_UNSUPPORTED) {
+            if (int r = finish(c, st, op)) return r;
+            return check_values(c, op, out, out_dtype, n_heads * head_dim);
+        }
+    }
+    // otherwise the two operators it fuses, one after the other
+    if (int r = jh_quant_matvec_fused(c, JH_PRO_NORMED, x, JH_BF16, nullptr, JH_BF16, norm_eps, w, scales, biases,
+                                      sb_dtype, rows, in_features, group_size, bits, JH_EPI_STORE, nullptr, qkv,
+                                      qkv_dtype, const_cast<float*>(norm_stats), nullptr))
+        return r;
+    return jh_attention_decode(c, qkv, qkv_dtype, n_heads, n_kv_heads, head_dim, q_norm_w, k_norm_w, w_dtype, eps,
+                               rope_base, rope_scale, rope_cs, pos, k_cache, v_cache, cache_dtype, capacity, scale, out,
+                               out_dtype);
+}
+
 int jh_attention_decode_noalloc(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t n_heads, int64_t n_kv_heads,
                                 int64_t head_dim, const void* q_norm_w, const void* k_norm_w, jh_dtype w_dtype,
                                 float eps, float rope_base, float rope_scale, const float* rope_cs, int64_t pos,

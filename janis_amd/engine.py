@@ -865,6 +865,53 @@ class HipBackend:
             k_cache.ptr, v_cache.ptr, k_cache.dtype, cap, float(scale), out.ptr, out.dtype))
         return out
 
+    def QkvAttentionDecode(self, x: Tensor, stats: Tensor, norm_eps: float, w: Tensor, scales: Tensor,
+                           biases: Tensor, groupSize: int, bits: int, qkv: Tensor, n_heads: int, n_kv_heads: int,
+                           q_norm: Tensor | None, k_norm: Tensor | None, eps: float, base: float, rope_scale: float,
+                           pos: int, k_cache: Tensor, v_cache: Tensor, scale: float,
+                           rope_cs: Tensor | None = None, out: Tensor | None = None,
+                           out_dtype: int | None = None) -> Tensor:
+        """The q/k/v product of one token (JH_PRO_NORMED: x = the bf16 norm_out of
+        a split RMSNorm and `stats` its statistics; w stacks the q, k and v rows)
+        written to `qkv` (F32 or BF16 [1, (Hq+2Hk)*128]) and its attention (as
+        AttentionDecode) in one launch when the backend has it: the same results
+        as QuantMatvecFused(PRO_NORMED) then AttentionDecode, bit for bit
+        (qwen/attention.go:98-128 after qwen/block.go:59). Returns [1, Hq*128]."""
+        if w.dtype != U32:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QkvAttentionDecode: weight tensor is not packed U32")
+        if k_cache.dtype != v_cache.dtype or k_cache.shape != v_cache.shape:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QkvAttentionDecode: caches differ")
+        if not (k_cache.contiguous and v_cache.contiguous):
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QkvAttentionDecode: the caches must be whole buffers")
+        if q_norm is not None and k_norm is not None and q_norm.dtype != k_norm.dtype:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QkvAttentionDecode: norm weights differ in dtype")
+        x, w, scales, biases = self._c(x), self._c(w), self._c(scales), self._c(biases)
+        Dh = 128
+        rows, P = w.shape[-2], w.shape[-1]
+        k = P * (32 // bits)
+        if rows != (n_heads + 2 * n_kv_heads) * Dh:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QkvAttentionDecode: w must hold (Hq + 2 Hk) * 128 rows")
+        if x.dtype != BF16 or x.numel != k:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QkvAttentionDecode: x must be the BF16 norm_out [in_features]")
+        if stats.dtype != F32 or stats.numel != _lib.JH_NORM_STATS:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QkvAttentionDecode: stats must be F32 [JH_NORM_STATS]")
+        if qkv.dtype not in (F32, BF16) or qkv.numel != rows:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QkvAttentionDecode: qkv must be F32/BF16 [1, (Hq + 2 Hk) * 128]")
+        if out is None:
+            out = self.empty(out_dtype if out_dtype is not None else BF16, 1, n_heads * Dh)
+        elif out.numel != n_heads * Dh or out.dtype not in (F32, BF16):
+            raise JanisHipError(_lib.JH_ERR_INVALID, "QkvAttentionDecode: out must be F32/BF16 [1, Hq*128]")
+        q_norm = self._c(q_norm) if q_norm is not None else None
+        k_norm = self._c(k_norm) if k_norm is not None else None
+        wd = q_norm.dtype if q_norm is not None else (k_norm.dtype if k_norm is not None else BF16)
+        check(self._ctx, self._L.jh_qkv_attention_decode(
+            self._ctx, x.ptr, stats.ptr, float(norm_eps), w.ptr, scales.ptr, biases.ptr, scales.dtype, k,
+            int(groupSize), int(bits), qkv.ptr, qkv.dtype, n_heads, n_kv_heads, Dh,
+            q_norm.ptr if q_norm is not None else None, k_norm.ptr if k_norm is not None else None, wd, float(eps),
+            float(base), float(rope_scale), rope_cs.ptr if rope_cs is not None else None, int(pos),
+            k_cache.ptr, v_cache.ptr, k_cache.dtype, k_cache.shape[-2], float(scale), out.ptr, out.dtype))
+        return out
+
     def MoeRoute(self, logits: Tensor, k: int, normTopk: bool = True) -> tuple:
         """The router of MoEBlock.Forward (qwen/moe.go:455-491) on the device:
         softmax over the last axis, top-k (selection-sort ties), optional

@@ -86,11 +86,12 @@ def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bo
     if fused:
         cs = b.RoPETable(Dh, c.theta, 1.0, pos)  # shared by every layer
         u, st = b.NormPrepare(h, m.layers[0].in_norm)  # the first block's InputNorm, producer half
+        qkv_buf = b.empty(F32, 1, (Hq + 2 * Hk) * Dh)
         for li, L in enumerate(m.layers):
             nxt = m.layers[li + 1].in_norm if li + 1 < len(m.layers) else m.norm
-            qkv = b.QuantMatvecFused(u, *L.qkv, gs, bits, NORMED, eps=c.eps, stats=st, out_dtype=F32)
-            att = b.AttentionDecode(qkv, Hq, Hk, L.q_norm, L.k_norm, c.eps, c.theta, 1.0, pos, L.k_cache,
-                                    L.v_cache, Dh ** -0.5, out_dtype=BF16, rope_cs=cs)
+            att = b.QkvAttentionDecode(u, st, c.eps, *L.qkv, gs, bits, qkv_buf, Hq, Hk, L.q_norm, L.k_norm, c.eps,
+                                       c.theta, 1.0, pos, L.k_cache, L.v_cache, Dh ** -0.5, rope_cs=cs,
+                                       out_dtype=BF16)
             b.QuantMatvecFused(att, *L.o, gs, bits, norm=L.post_norm, epilogue=RESID_NORM, resid=h, out=h,
                                stats=st, norm_out=u)
             act = b.QuantMatvecFused(u, *L.gate_up, gs, bits, NORMED, eps=c.eps, stats=st, epilogue=SWIGLU,

@@ -563,3 +563,129 @@ def test_norm_prepare(hip, oracle):
         hip.QuantMatvecFused(hip.FromFloats(x), w, s_, b_, 64, 4, _lib.JH_PRO_RMSNORM, _put(hip, nw, BF16), 1e-6,
                              epilogue=_lib.JH_EPI_RESID_NORM, resid=hip.FromFloats(np.zeros((1, 256), np.float32)),
                              stats=st, norm_out=hip.empty(BF16, 1, 256))
+
+
+def _qkv_attn_case(hip, rng, seed, Hq, Hk, K, cap, pos):
+    from janis_amd import _lib
+    Dh = 128
+    q = synth.quant_linear(seed, (Hq + 2 * Hk) * Dh, K, 64)
+    w, s, b = upload_quant(hip, q)
+    h = (2.0 * rng.standard_normal((1, K))).astype(np.float32)
+    nw = _bf16(1 + 0.1 * rng.standard_normal(K))
+    qn, kn = _bf16(1 + 0.1 * rng.standard_normal(Dh)), _bf16(1 + 0.1 * rng.standard_normal(Dh))
+    k_old, v_old = _cache(rng, 1, Hk, cap, Dh)
+    u, st = hip.NormPrepare(hip.FromFloats(h), _put(hip, nw, BF16))
+    return q, (w, s, b), h, nw, qn, kn, k_old, v_old, u, st
+
+
+@pytest.mark.parametrize("Hq,Hk,K,pos,qdt", [(32, 8, 4096, 0, F32), (32, 8, 4096, 15, F32), (32, 8, 4096, 512, F32),
+                                             (32, 8, 4096, 512, BF16), (32, 8, 4096, 3000, F32),
+                                             (32, 8, 4096, 8192, F32), (64, 8, 4096, 700, F32),
+                                             (16, 8, 4096, 257, BF16), (32, 4, 4096, 600, F32),
+                                             (32, 8, 2048, 300, F32)])
+def test_qkv_attention_decode_matches_two_calls(hip, oracle, Hq, Hk, K, pos, qdt):
+    """jh_qkv_attention_decode (the q/k/v product with the prepared norm and the
+    attention in one launch, or the two operators where it does not apply:
+    Hk = 4, K = 2048) against QuantMatvecFused(PRO_NORMED) then AttentionDecode
+    on copies of the same caches: the q/k/v rows, the attention output and the
+    cache rows written must be bit for bit the same; the output also against the
+    oracle's RMSNorm -> QuantMatmul -> q/k norm -> RoPE -> SDPA within 1e-2."""
+    from janis_amd import _lib
+    rng = np.random.default_rng(Hq * 7919 + Hk * 31 + pos + K)
+    Dh, cap = 128, pos + 9
+    scale = Dh ** -0.5
+    q, (w, s, b), h, nw, qn, kn, k_old, v_old, u, st = _qkv_attn_case(hip, rng, pos + 11, Hq, Hk, K, cap, pos)
+    qnd, knd = _put(hip, qn, BF16), _put(hip, kn, BF16)
+    cs = hip.RoPETable(Dh, 1e6, 1.0, pos)
+    step(f"jh_qkv_attention_decode Hq={Hq} Hk={Hk} K={K} pos={pos} qkv={'f32' if qdt == F32 else 'bf16'}")
+    kc1, vc1 = _put(hip, k_old, BF16), _put(hip, v_old, BF16)
+    qkv1 = hip.empty(qdt, 1, (Hq + 2 * Hk) * Dh)
+    got = hip.Floats(hip.QkvAttentionDecode(u, st, 1e-6, w, s, b, 64, 4, qkv1, Hq, Hk, qnd, knd, 1e-6, 1e6, 1.0,
+                                            pos, kc1, vc1, scale, rope_cs=cs, out_dtype=F32))
+    step("the same as two calls")
+    kc2, vc2 = _put(hip, k_old, BF16), _put(hip, v_old, BF16)
+    qkv2 = hip.QuantMatvecFused(u, w, s, b, 64, 4, _lib.JH_PRO_NORMED, eps=1e-6, stats=st, out_dtype=qdt)
+    want2 = hip.Floats(hip.AttentionDecode(qkv2, Hq, Hk, qnd, knd, 1e-6, 1e6, 1.0, pos, kc2, vc2, scale,
+                                           out_dtype=F32, rope_cs=cs))
+    assert np.array_equal(hip.Floats(qkv1), hip.Floats(qkv2))
+    assert np.array_equal(got, want2)
+    assert np.array_equal(hip.Floats(kc1), hip.Floats(kc2)) and np.array_equal(hip.Floats(vc1), hip.Floats(vc2))
+    qkv_o = oracle.quant_matmul(_bf16(oracle.rms_norm(h, nw, 1e-6)), q.w, q.s, q.b, 64)
+    if qdt == BF16:
+        qkv_o = _bf16(qkv_o)
+    want, _, _ = _attention_oracle(oracle, qkv_o, qn, kn, k_old, v_old, Hq, Hk, pos, scale)
+    ok, dd, sc = rel_ok(got, want, 1e-2)
+    assert ok, (dd, sc)
+
+
+def test_qkv_attention_decode_tokens_and_graph_replays(hip, oracle):
+    """Consecutive tokens through one context (each sees the rows the previous
+    launches appended), then the launch captured in a HIP graph and replayed on
+    new inputs with eager work between the replays: every replay equals the
+    eager call bit for bit (the launch's arrival counters are cleared by the
+    launch itself)."""
+    import ctypes
+
+    from janis_amd import _lib
+    rt = hip_runtime()
+    rng = np.random.default_rng(4242)
+    Hq, Hk, K, Dh, cap, pos0 = 32, 8, 4096, 128, 1100, 1021
+    scale = Dh ** -0.5
+    q, (w, s, b), h, nw, qn, kn, k_old, v_old, u, st = _qkv_attn_case(hip, rng, 77, Hq, Hk, K, cap, pos0)
+    qnd, knd = _put(hip, qn, BF16), _put(hip, kn, BF16)
+    kc, vc = _put(hip, k_old, BF16), _put(hip, v_old, BF16)
+    kc2, vc2 = _put(hip, k_old, BF16), _put(hip, v_old, BF16)
+    qkv = hip.empty(F32, 1, (Hq + 2 * Hk) * Dh)
+    for t in range(3):
+        pos = pos0 + t
+        step(f"jh_qkv_attention_decode token {t} pos={pos}")
+        got = hip.Floats(hip.QkvAttentionDecode(u, st, 1e-6, w, s, b, 64, 4, qkv, Hq, Hk, qnd, knd, 1e-6, 1e6, 1.0,
+                                                pos, kc, vc, scale, out_dtype=F32))
+        q2 = hip.QuantMatvecFused(u, w, s, b, 64, 4, _lib.JH_PRO_NORMED, eps=1e-6, stats=st, out_dtype=F32)
+        want = hip.Floats(hip.AttentionDecode(q2, Hq, Hk, qnd, knd, 1e-6, 1e6, 1.0, pos, kc2, vc2, scale,
+                                              out_dtype=F32))
+        assert np.array_equal(got, want), t
+    # graph: the same launch on new norm inputs, replayed
+    pos = pos0 + 3
+    hs = [(2.0 * rng.standard_normal((1, K))).astype(np.float32) for _ in range(3)]
+    h_d = hip.FromFloats(hs[0])
+    nwd = _put(hip, nw, BF16)
+    out = hip.empty(F32, 1, Hq * Dh)
+
+    def call():
+        hip.NormPrepare(h_d, nwd, norm_out=u, stats=st)
+        return hip.QkvAttentionDecode(u, st, 1e-6, w, s, b, 64, 4, qkv, Hq, Hk, qnd, knd, 1e-6, 1e6, 1.0, pos, kc, vc,
+                                      scale, out=out)
+
+    def put(a):
+        hip.Sync()
+        hip._L.jh_h2d(hip._ctx, ctypes.c_void_p(h_d.ptr), a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
+        hip.Sync()
+
+    eager = []
+    for a in hs:
+        put(a)
+        call()
+        eager.append(hip.Floats(out).copy())
+    stream, graph, exe = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    assert rt.hipStreamCreate(ctypes.byref(stream)) == 0
+    try:
+        hip.SetStream(stream.value)
+        step("capture jh_qkv_attention_decode")
+        assert rt.hipStreamBeginCapture(stream, 0) == 0
+        call()
+        assert rt.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+        assert rt.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for rep, i in enumerate((1, 2, 0, 1)):
+            step(f"graph replay {rep} on input {i}")
+            put(hs[i])
+            assert rt.hipGraphLaunch(exe, stream) == 0
+            assert rt.hipStreamSynchronize(stream) == 0
+            assert np.array_equal(hip.Floats(out), eager[i]), (rep, i)
+            hip.Floats(hip.QuantMatvecFused(u, w, s, b, 64, 4, _lib.JH_PRO_NORMED, eps=1e-6, stats=st,
+                                            out_dtype=F32))  # eager work between replays
+    finally:
+        hip.SetStream(None)
+        rt.hipGraphExecDestroy(exe)
+        rt.hipGraphDestroy(graph)
+        rt.hipStreamDestroy(stream)
