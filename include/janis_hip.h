@@ -530,6 +530,25 @@ JH_API int jh_quant_matvec_fused(jh_ctx *ctx, jh_prologue prologue, const void *
 JH_API int jh_norm_prepare(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t d, const void *norm_w,
                     jh_dtype norm_w_dtype, void *norm_out, float *norm_stats);
 
+/* The decode step's entry into the first block, one launch: h = the embedding
+ * row of token ids[0] (QuantEmbedding.Forward, qwen/embed.go:78-83: TakeAxis of
+ * the packed table, its scales and biases, then Dequantize, cpu/cpu_misc.go:
+ * 134-161; zeros for an id outside [0, vocab), as jh_take_rows gives), then
+ * jh_norm_prepare on h with norm_w (the first block's InputNorm), and, when
+ * rope_cs is not NULL, jh_rope_table(rope_dims, rope_base, rope_scale, pos)
+ * into rope_cs. Every output is bit-identical to those separate calls.
+ *   ids      int32 [1], device (the previous step's jh_argmax output)
+ *   w/scales/biases  the [vocab, dims] table (bits 2, 4 or 8)
+ *   h        F32 [dims]; norm_out bf16 [dims]; norm_stats JH_NORM_STATS fp32
+ * No counterpart call in the reference: it fuses the three its decode step makes
+ * (qwen/model.go:294-303 embedding, qwen/block.go:58 InputNorm, and the RoPE
+ * factors every Attention.ForwardCached call evaluates). */
+JH_API int jh_embed_norm_prepare(jh_ctx *ctx, const int32_t *ids, const uint32_t *w, const void *scales,
+                          const void *biases, jh_dtype sb_dtype, int64_t vocab, int64_t dims,
+                          int group_size, int bits, const void *norm_w, jh_dtype norm_w_dtype,
+                          float *h, void *norm_out, float *norm_stats, int rope_dims, float rope_base,
+                          float rope_scale, int64_t pos, float *rope_cs);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,7 +29,7 @@ EXPORTS = [
     "jh_take_rows", "jh_kv_append", "jh_qk_norm_rope_append", "jh_quant_matvec_fused",
     "jh_attention_decode", "jh_rope_table", "jh_norm_prepare", "jh_copy_strided", "jh_scatter_rows",
     "jh_softmax", "jh_mean", "jh_scalar", "jh_check_finite", "jh_attention_decode_noalloc",
-    "jh_qkv_attention_decode",
+    "jh_qkv_attention_decode", "jh_embed_norm_prepare",
 ]
 
 _lib = None
@@ -105,6 +105,8 @@ def load() -> ctypes.CDLL:
                                           f32, f32, p, i64, p, p, i, i64, f32, p, i]
     L.jh_qkv_attention_decode.restype = i
     L.jh_rope_table.argtypes = [c_ctx, i, f32, f32, i64, p, p]
+    L.jh_embed_norm_prepare.argtypes = [c_ctx, p, p, p, p, i, i64, i64, i, i, p, i, p, p, p, i, f32, f32, i64, p]
+    L.jh_embed_norm_prepare.restype = i
     L.jh_quant_matvec_fused.argtypes = [c_ctx, i, p, i, p, i, f32, p, p, p, i, i64, i64, i, i, i, p, p, i, p, p]
     L.jh_norm_prepare.argtypes = [c_ctx, p, i, i64, p, i, p, p]
     L.jh_copy_strided.argtypes = [c_ctx, p, i, i, p, p, p, i, p]

@@ -211,6 +211,69 @@ __global__ __launch_bounds__(256) void norm_prepare_kernel(const void* __restric
         for (int i = gridDim.x + threadIdx.x; i < kNormSlots; i += 256) stats[i] = 0.0f;
 }
 
+// The decode step's first launch: the embedding row of token ids[0] (Dequantize
+// of the row TakeAxis picks, qwen/embed.go:78-83, zero for an id outside the
+// table, as take_rows gives), the first block's split RMSNorm producer half on
+// it, and, from one more block when cs is given, the RoPE factor table at pos.
+// Blocks below nb follow norm_prepare_kernel element for element: h is the
+// value Dequantize stores, the sums of squares run in the same order, so u and
+// the statistics are those of the three separate launches bit for bit.
+template <int BITS>
+__global__ __launch_bounds__(256) void embed_norm_kernel(const int32_t* __restrict__ ids, const uint32_t* __restrict__ W,
+                                                         const void* __restrict__ S, const void* __restrict__ B,
+                                                         int sb_dt, int64_t vocab, int64_t d, int gs,
+                                                         const void* __restrict__ w, int w_dt, float* __restrict__ h,
+                                                         uint16_t* __restrict__ out, float* __restrict__ stats, int nb,
+                                                         int rope_dims, float base, float scale, int64_t pos,
+                                                         float* __restrict__ cs) {
+    constexpr int VPW = 32 / BITS;
+    constexpr uint32_t MASK = (1u << BITS) - 1u;
+    if ((int)blockIdx.x >= nb) {  // the RoPE table, as rope_table_kernel
+        const int half = rope_dims / 2;
+        for (int i = threadIdx.x; i < half; i += 256) {
+            const float inv = (float)pow((double)base, -(double)(2 * i) / (double)rope_dims);
+            const float theta = (float)pos * scale * inv;
+            cs[i] = (float)cos((double)theta);
+            cs[half + i] = (float)sin((double)theta);
+        }
+        return;
+    }
+    __shared__ float red[4];
+    const int32_t id = ids[0];
+    const bool ok = id >= 0 && id < vocab;
+    const int64_t P = d / VPW, G = d / gs;
+    const int64_t row = ok ? (int64_t)id : 0;
+    const int64_t base_i = (int64_t)blockIdx.x * 256 * kPrepPer + threadIdx.x;
+    float xv[kPrepPer], wv[kPrepPer];
+#pragma unroll
+    for (int e = 0; e < kPrepPer; e++) {
+        const int64_t i = base_i + 256 * e;
+        float v = 0.0f;
+        if (i < d && ok) {
+            const uint32_t word = W[row * P + i / VPW];
+            const int64_t g = i / gs;
+            v = unfused_qsb((float)((word >> (BITS * (int)(i % VPW))) & MASK), load_sb(S, row * G + g, sb_dt),
+                            load_sb(B, row * G + g, sb_dt));
+        }
+        xv[e] = v;
+        wv[e] = i < d ? ld_act(w, i, w_dt) : 0.0f;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kPrepPer; e++) {
+        const int64_t i = base_i + 256 * e;
+        ss = fmaf(xv[e], xv[e], ss);
+        if (i < d) {
+            h[i] = xv[e];
+            out[i] = f32_to_bf16(xv[e] * wv[e]);
+        }
+    }
+    ss = block_sum256(ss, red);
+    if (threadIdx.x == 0) stats[blockIdx.x] = ss;
+    if (blockIdx.x == 0)
+        for (int i = nb + threadIdx.x; i < kNormSlots; i += 256) stats[i] = 0.0f;
+}
+
 __global__ __launch_bounds__(256) void norm_apply_kernel(const uint16_t* __restrict__ u, int64_t d,
                                                          const float* __restrict__ stats, float eps,
                                                          uint16_t* __restrict__ out) {
@@ -1151,6 +1214,63 @@ __global__ __launch_bounds__(128) void argmax_final_kernel(const float* __restri
     }
 }
 
+// One launch: argmax_partial_kernel's blocks, then the last block of row r to
+// arrive (counted at sync[r], across all XCDs: agent-scope fences around the
+// count) reduces the row's candidates as argmax_final_kernel does and resets
+// the counter. The result does not depend on arrival order (better() is a
+// total order on (value, index)).
+__global__ __launch_bounds__(256) void argmax_one_kernel(const void* __restrict__ x, int x_dt, int64_t n,
+                                                         float* __restrict__ pv, int64_t* __restrict__ pi,
+                                                         int* __restrict__ sync, int32_t* __restrict__ out) {
+    __shared__ float sv[4];
+    __shared__ int64_t si[4];
+    __shared__ int last;
+    const int64_t r = blockIdx.y;
+    const int64_t chunk = (n + kArgmaxChunks - 1) / kArgmaxChunks;
+    const int64_t lo = blockIdx.x * chunk, hi = min(n, lo + chunk);
+    float best = -__builtin_inff();
+    int64_t idx = n;
+    constexpr int U = 8;
+    for (int64_t i0 = lo + threadIdx.x; i0 < hi; i0 += 256 * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t i = i0 + (int64_t)u * 256;
+            v[u] = i < hi ? ld_act(x, r * n + i, x_dt) : -__builtin_inff();
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (v[u] > best) best = v[u], idx = i0 + (int64_t)u * 256;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) better(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
+    if ((threadIdx.x & 63) == 0) sv[threadIdx.x >> 6] = best, si[threadIdx.x >> 6] = idx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; k++) better(best, idx, sv[k], si[k]);
+        pv[r * kArgmaxChunks + blockIdx.x] = best;
+        pi[r * kArgmaxChunks + blockIdx.x] = idx;
+        __threadfence();  // the candidate is visible device-wide before the arrival
+        last = atomicAdd(sync + r, 1) == kArgmaxChunks - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();  // and every other block's candidate is seen here
+    if (threadIdx.x < kArgmaxChunks) {
+        best = pv[r * kArgmaxChunks + threadIdx.x];
+        idx = pi[r * kArgmaxChunks + threadIdx.x];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) better(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
+        if ((threadIdx.x & 63) == 0) sv[threadIdx.x >> 6] = best, si[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        better(best, idx, sv[1], si[1]);
+        out[r] = idx < n ? (int32_t)idx : 0;
+        sync[r] = 0;
+    }
+}
+
 // ---- row gather and KV append ------------------------------------------------------
 // ---- strided copy with conversion (Slice / Transpose / Concat / Cast / contiguous) --
 // dst = src over `shape`, each side addressed through its own element strides,
@@ -1498,6 +1618,21 @@ Status launch_norm_prepare(const void* x, int x_dt, int64_t d, const void* w, in
     return Status::ok();
 }
 
+Status launch_embed_norm(const int32_t* ids, const QuantMatrix& m, const void* w, int w_dt, float* h, uint16_t* out,
+                         float* stats, int rope_dims, float base, float scale, int64_t pos, float* cs, hipStream_t st) {
+    const int64_t nb = (m.in + 256 * kPrepPer - 1) / (256 * kPrepPer);
+    if (nb > kNormSlots) return Status::fail(JH_ERR_UNSUPPORTED, "embed_norm: row too long");
+    const dim3 grid((unsigned)(nb + (cs ? 1 : 0)));
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, ids, m.w, m.scales, m.biases, m.sb_dtype, m.rows, m.in,
+                           m.group_size, w, w_dt, h, out, stats, (int)nb, rope_dims, base, scale, pos, cs);
+    };
+    if (m.bits == 8) go(embed_norm_kernel<8>);
+    else if (m.bits == 2) go(embed_norm_kernel<2>);
+    else go(embed_norm_kernel<4>);
+    return Status::ok();
+}
+
 Status launch_norm_apply(const uint16_t* u, int64_t d, const float* stats, float eps, uint16_t* out, hipStream_t st) {
     hipLaunchKernelGGL(norm_apply_kernel, dim3(1), dim3(256), 0, st, u, d, stats, eps, out);
     return Status::ok();
@@ -1519,11 +1654,17 @@ Status launch_elementwise(int op, const void* a, int a_dt, const void* b, int b_
 
 size_t argmax_workspace_bytes(int64_t rows) { return (size_t)rows * kArgmaxChunks * (sizeof(float) + sizeof(int64_t)); }
 
-Status launch_argmax(const void* x, int x_dt, int64_t rows, int64_t n, int32_t* out, void* workspace, hipStream_t st) {
+Status launch_argmax(const void* x, int x_dt, int64_t rows, int64_t n, int32_t* out, void* workspace, int* sync,
+                     hipStream_t st) {
     if (rows == 0) return Status::ok();
     if (rows > 65535) return Status::fail(JH_ERR_UNSUPPORTED, "argmax: more than 65535 rows");
     int64_t* pi = static_cast<int64_t*>(workspace);
     float* pv = reinterpret_cast<float*>(pi + rows * kArgmaxChunks);
+    if (sync && rows <= kArgmaxSyncRows) {
+        hipLaunchKernelGGL(argmax_one_kernel, dim3(kArgmaxChunks, (unsigned)rows), dim3(256), 0, st, x, x_dt, n, pv,
+                           pi, sync + kArgmaxSyncSlot, out);
+        return Status::ok();
+    }
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxChunks, (unsigned)rows), dim3(256), 0, st, x, x_dt, n, pv, pi);
     hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)rows), dim3(kArgmaxChunks), 0, st, pv, pi, n, out);
     return Status::ok();

@@ -11,15 +11,6 @@
 namespace jh {
 namespace {
 
-// fl32(fl32(q * s) + b): the product is rounded before the add, as the
-// reference computes it on amd64; contraction into an FMA is switched off here
-// (hipcc contracts by default).
-__device__ __forceinline__ float unfused_qsb(float q, float s, float b) {
-#pragma clang fp contract(off)
-    const float p = q * s;
-    return p + b;
-}
-
 // One thread per packed word of BITS-wide codes (VPW = 32/BITS per word).
 template <int BITS>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict__ W,

@@ -192,6 +192,15 @@ __device__ __forceinline__ float load_sb(const void* p, int64_t i, int dt) {
     return static_cast<const float*>(p)[i];
 }
 
+// fl32(fl32(q * s) + b): the product is rounded before the add, the order the
+// reference's Dequantize computes on amd64 (cpu/cpu_misc.go:134-161);
+// contraction into an FMA is switched off here (hipcc contracts by default).
+__device__ __forceinline__ float unfused_qsb(float q, float s, float b) {
+#pragma clang fp contract(off)
+    const float p = q * s;
+    return p + b;
+}
+
 __device__ __forceinline__ void store_y(void* y, int64_t i, float v, int dt) {
     if (dt == JH_BF16)
         static_cast<uint16_t*>(y)[i] = f32_to_bf16(v);
@@ -301,7 +310,10 @@ Status launch_sdpa(const void* q, int q_dt, const void* k, const void* v, int kv
 Status launch_elementwise(int op, const void* a, int a_dt, const void* b, int b_dt, void* out, int out_dt, int64_t n,
                           hipStream_t st);
 size_t argmax_workspace_bytes(int64_t rows);
-Status launch_argmax(const void* x, int x_dt, int64_t rows, int64_t n, int32_t* out, void* workspace, hipStream_t st);
+// With `sync` (the context's zeroed counters) rows up to kArgmaxSyncRows take
+// one launch (the last block of a row merges its candidates); otherwise two.
+Status launch_argmax(const void* x, int x_dt, int64_t rows, int64_t n, int32_t* out, void* workspace, int* sync,
+                     hipStream_t st);
 Status launch_qk_norm_rope_append(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w,
                                   int w_dt, float eps, float base, float scale, int64_t pos, void* kc, void* vc,
                                   int c_dt, int64_t cap, void* q_out, int q_dt, hipStream_t st);
@@ -317,6 +329,9 @@ constexpr int kAttnSyncSlots = 4096;
 // flags of its blocks at kAttnFlagSlot + 128 x (zero between calls).
 constexpr int kAttnFlagSlot = 1024;
 constexpr int kAttnMaxBlocksPerXcd = 128;
+// jh_argmax's share: the arrival counter of row r at kArgmaxSyncSlot + r for
+// the first kArgmaxSyncRows rows (zero between calls).
+constexpr int kArgmaxSyncSlot = 2048, kArgmaxSyncRows = 2048;
 bool attn_merge_in_launch(int64_t Hk, const int* sync);
 Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt,
                           float eps, float base, float rscale, const float* rope_cs, int64_t pos, void* kc,
@@ -333,6 +348,11 @@ Status launch_qkv_attn(const QuantMatrix& m, const uint16_t* x, float* stats, fl
 // buf: 64 ints of device memory), else 0.
 int probe_xcd_round_robin(int* buf, hipStream_t st);
 Status launch_rope_table(int dims, float base, float scale, int64_t pos, const float* freqs, float* out,
+                         hipStream_t st);
+// Embedding row of ids[0] (4-bit, 2-bit or 8-bit codes) + the split RMSNorm
+// producer half on it (+ the RoPE table at pos when cs is given), one launch.
+Status launch_embed_norm(const int32_t* ids, const QuantMatrix& table, const void* w, int w_dt, float* h,
+                         uint16_t* out, float* stats, int rope_dims, float base, float scale, int64_t pos, float* cs,
                          hipStream_t st);
 constexpr int kMaxCopyDims = 8;
 // dst = src over shape, both through element strides (dst_strides nullptr:

@@ -534,6 +534,27 @@ int jh_norm_prepare(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t d, const
                   op);
 }
 
+int jh_embed_norm_prepare(jh_ctx* c, const int32_t* ids, const uint32_t* w, const void* scales, const void* biases,
+                          jh_dtype sb_dtype, int64_t vocab, int64_t dims, int group_size, int bits, const void* norm_w,
+                          jh_dtype norm_w_dtype, float* h, void* norm_out, float* norm_stats, int rope_dims,
+                          float rope_base, float rope_scale, int64_t pos, float* rope_cs) {
+    if (int r = enter(c)) return r;
+    const char* op = "jh_embed_norm_prepare";
+    if (int r = check_quant(c, op, w, scales, biases, sb_dtype, vocab, dims, group_size, bits)) return r;
+    if (norm_w_dtype != JH_BF16 && norm_w_dtype != JH_F16 && norm_w_dtype != JH_F32)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": norm weight must be bf16, f16 or f32");
+    if (vocab <= 0 || dims <= 0) return fail(c, JH_ERR_INVALID, std::string(op) + ": empty table");
+    if (!ids || !norm_w || !h || !norm_out || !norm_stats)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
+    if (rope_cs && (rope_dims <= 0 || (rope_dims & 1) || rope_dims > 65536 || pos < 0))
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": bad RoPE dims or position");
+    if (int r = check_indices(c, op, ids, 1, vocab, "id")) return r;
+    jh::QuantMatrix m{w, scales, biases, sb_dtype, vocab, dims, group_size, bits};
+    return finish(c, jh::launch_embed_norm(ids, m, norm_w, norm_w_dtype, h, static_cast<uint16_t*>(norm_out),
+                                           norm_stats, rope_dims, rope_base, rope_scale, pos, rope_cs, c->stream),
+                  op);
+}
+
 int jh_gather_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t n_lead,
                            int64_t a_vectors, const uint32_t* w, const void* scales,
                            const void* biases, jh_dtype sb_dtype, int64_t n_experts,
@@ -673,7 +694,7 @@ int jh_argmax(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, int64_t 
     if (rows > 0x7fffffff) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": too many rows");
     if (!x || !out) return fail(c, JH_ERR_INVALID, std::string(op) + ": null pointer");
     if (int r = ensure_workspace(c, jh::argmax_workspace_bytes(rows), op)) return r;
-    return finish(c, jh::launch_argmax(x, x_dtype, rows, n, out, c->ws, c->stream), op);
+    return finish(c, jh::launch_argmax(x, x_dtype, rows, n, out, c->ws, c->attn_sync, c->stream), op);
 }
 
 int jh_qk_norm_rope_append(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t n_heads, int64_t n_kv_heads,

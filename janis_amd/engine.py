@@ -822,6 +822,30 @@ class HipBackend:
         check(self._ctx, self._L.jh_norm_prepare(self._ctx, x.ptr, x.dtype, d, norm.ptr, norm.dtype, u.ptr, st.ptr))
         return u, st
 
+    def EmbedNormPrepare(self, ids: Tensor, w: Tensor, scales: Tensor, biases: Tensor, groupSize: int, bits: int,
+                         norm: Tensor, rope: tuple | None = None) -> tuple:
+        """The decode step's first launch: the embedding row of token ids[0]
+        (QuantEmbedding.Forward, qwen/embed.go:78-83: Dequantize of the TakeAxis
+        rows), NormPrepare on it with norm, and with rope = (dims, base, scale,
+        pos) the RoPETable at pos. Returns (h F32 [1, d], u BF16 [1, d], stats,
+        cs or None), each bit-identical to the separate calls."""
+        if w.dtype != U32 or len(w.shape) != 2:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "EmbedNormPrepare: table is not packed U32 [vocab, P]")
+        ids, w, scales, biases, norm = (self._c(t) for t in (ids, w, scales, biases, norm))
+        if ids.dtype != I32 or ids.numel != 1:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "EmbedNormPrepare: one I32 token id")
+        vocab, d = w.shape[0], w.shape[-1] * 32 // bits
+        if norm.numel != d:
+            raise JanisHipError(_lib.JH_ERR_INVALID, "EmbedNormPrepare: norm weight of the row's length")
+        h, u, st = self.empty(F32, 1, d), self.empty(BF16, 1, d), self.empty(F32, _lib.JH_NORM_STATS)
+        cs = self.empty(F32, int(rope[0])) if rope is not None else None
+        rd, rb, rs, rp = rope if rope is not None else (0, 0.0, 0.0, 0)
+        check(self._ctx, self._L.jh_embed_norm_prepare(
+            self._ctx, ids.ptr, w.ptr, scales.ptr, biases.ptr, self._sb_dtype(scales, biases), vocab, d, groupSize,
+            bits, norm.ptr, norm.dtype, h.ptr, u.ptr, st.ptr, int(rd), float(rb), float(rs), int(rp),
+            cs.ptr if cs is not None else None))
+        return h, u, st, cs
+
     def RoPETable(self, dims: int, base: float, scale: float, pos: int, freqs: Tensor | None = None) -> Tensor:
         """cos and sin of the RoPE angles at pos (cpu/cpu_attn.go:13-34): F32
         [dims] = [cos(theta_0..), sin(theta_0..)]."""

@@ -68,9 +68,11 @@ def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bo
     and the sum of h^2) and the product that reads it (which applies the
     1/rms factor to its output), SiLU*mul in the gate/up product's epilogue,
     the residual adds in the o/down products' epilogues, and the q/k norms,
-    RoPE, KV append and SDPA in one launch, whose split partials are merged
-    inside it (5 launches per layer; a merge launch follows on GPUs that do not
-    deal workgroups to their XCDs round-robin).
+    RoPE, KV append and SDPA in the q/k/v product's launch, whose split
+    partials are merged inside it (4 launches per layer; on GPUs that do not
+    deal workgroups to their XCDs round-robin the product and the attention
+    are separate launches, with a merge launch), and the embedding row, the
+    first norm's producer half and the RoPE factors in one launch.
     fused=False makes the reference's calls one for one (qwen/block.go,
     qwen/attention.go, qwen/mlp.go, qwen/cache.go): separate q/k/v and gate/up
     products on row views of the stacked matrices, Reshape/Transpose views, the
@@ -79,13 +81,14 @@ def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bo
     gs, bits = c.group_size, c.bits
     H, Hq, Hk, Dh, I = c.hidden, c.n_heads, c.n_kv, c.head_dim, c.inter
     NORMED, SWIGLU, RESID_NORM = _lib.JH_PRO_NORMED, _lib.JH_EPI_SWIGLU, _lib.JH_EPI_RESID_NORM
-    # QuantEmbedding.Forward (qwen/embed.go:78-83)
     ew, es, eb = m.embed
-    h = b.Dequantize(b.TakeAxis(ew, token), b.TakeAxis(es, token), b.TakeAxis(eb, token), gs, bits)  # F32 [1, H]
     head = m.lm_head if m.lm_head is not None else m.embed
     if fused:
-        cs = b.RoPETable(Dh, c.theta, 1.0, pos)  # shared by every layer
-        u, st = b.NormPrepare(h, m.layers[0].in_norm)  # the first block's InputNorm, producer half
+        # QuantEmbedding.Forward (qwen/embed.go:78-83), the first block's
+        # InputNorm (producer half) and the RoPE factors shared by every layer,
+        # in one launch
+        h, u, st, cs = b.EmbedNormPrepare(token, ew, es, eb, gs, bits, m.layers[0].in_norm,
+                                          rope=(Dh, c.theta, 1.0, pos))
         qkv_buf = b.empty(F32, 1, (Hq + 2 * Hk) * Dh)
         for li, L in enumerate(m.layers):
             nxt = m.layers[li + 1].in_norm if li + 1 < len(m.layers) else m.norm
@@ -101,6 +104,8 @@ def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bo
         logits = b.QuantMatvecFused(u, *head, gs, bits, NORMED, eps=c.eps, stats=st, out_dtype=F32)
         return logits, b.Argmax(logits)
     # the reference's operator sequence, call for call
+    # QuantEmbedding.Forward (qwen/embed.go:78-83)
+    h = b.Dequantize(b.TakeAxis(ew, token), b.TakeAxis(es, token), b.TakeAxis(eb, token), gs, bits)  # F32 [1, H]
     B, T = 1, 1
     for L in m.layers:
         # Block.ForwardCached (qwen/block.go:58-61): h = x + Attn(InputNorm(x))

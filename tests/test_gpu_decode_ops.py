@@ -147,6 +147,107 @@ def test_argmax(hip, oracle):
     assert list(got) == list(oracle.argmax(x)) == [int(np.argmax(x[0])), 123, 0]
 
 
+def test_argmax_one_launch_rows_and_repeats(hip, oracle):
+    """Up to 2048 rows take the one-launch argmax (the last block of a row
+    merges its candidates and resets the row's counter); more rows the two
+    launches. Repeated calls, NaN rows and rows past the counted ones."""
+    rng = np.random.default_rng(31)
+    for rows, n in ((1, 151936), (7, 5000), (2049, 300)):
+        x = rng.standard_normal((rows, n)).astype(np.float32)
+        x[0, n - 1] = x[0, 1] = 9.0  # tie
+        if rows > 3:
+            x[3] = np.nan
+            x[2, n // 2] = np.inf
+        step(f"jh_argmax rows={rows} n={n} (3 calls)")
+        t = hip.FromFloats(x)
+        want = oracle.argmax(x)
+        for _ in range(3):
+            assert np.array_equal(hip.Ints(hip.Argmax(t)), want)
+
+
+def test_argmax_graph_replays(hip, oracle):
+    """The one-launch argmax captured in a HIP graph and replayed on new logits,
+    with eager argmax calls between the replays (the row counter is reset by
+    the launch itself)."""
+    import ctypes
+
+    rt = hip_runtime()
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal((1, 151936)).astype(np.float32)
+    t = hip.FromFloats(x)
+    other = hip.FromFloats(rng.standard_normal((2, 9000)).astype(np.float32))
+    out = hip.empty(I32, 1)
+
+    def put(a):
+        hip.Sync()
+        hip._L.jh_h2d(hip._ctx, ctypes.c_void_p(t.ptr), a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
+        hip.Sync()
+
+    def call():
+        from janis_amd._lib import check
+        check(hip._ctx, hip._L.jh_argmax(hip._ctx, t.ptr, F32, 1, 151936, out.ptr))
+
+    call()  # eager call before the capture
+    stream, graph, exe = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    assert rt.hipStreamCreate(ctypes.byref(stream)) == 0
+    try:
+        hip.SetStream(stream.value)
+        step("capture jh_argmax")
+        assert rt.hipStreamBeginCapture(stream, 0) == 0
+        call()
+        assert rt.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+        assert rt.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for k in range(4):
+            step(f"argmax graph replay {k}")
+            x2 = rng.standard_normal((1, 151936)).astype(np.float32)
+            x2[0, 1000 * k + 5] = 20.0
+            put(x2)
+            assert rt.hipGraphLaunch(exe, stream) == 0
+            assert rt.hipStreamSynchronize(stream) == 0
+            assert hip.Ints(out)[0] == 1000 * k + 5 == oracle.argmax(x2)[0]
+            hip.Ints(hip.Argmax(other))  # eager work between replays
+    finally:
+        hip.SetStream(None)
+        rt.hipGraphExecDestroy(exe)
+        rt.hipGraphDestroy(graph)
+        rt.hipStreamDestroy(stream)
+
+
+@pytest.mark.parametrize("bits,d,gs,sb", [(4, 4096, 64, BF16), (8, 4096, 64, F32), (2, 1024, 32, BF16),
+                                          (4, 2560, 128, F32)])
+def test_embed_norm_prepare_matches_separate_calls(hip, bits, d, gs, sb):
+    """jh_embed_norm_prepare = TakeAxis x3 + Dequantize, NormPrepare and
+    RoPETable, bit for bit; an id outside the table gives the zero row."""
+    q = synth.quant_linear(40 + bits, 300, d, group_size=gs, bits=bits)
+    w = hip.FromRaw(U32, q.w, *q.w.shape)
+    if sb == F32:
+        s, b = hip.FromFloats(q.s, *q.s.shape), hip.FromFloats(q.b, *q.b.shape)
+    else:
+        s, b = hip.FromBF16Bits(q.s_bits, *q.s_bits.shape), hip.FromBF16Bits(q.b_bits, *q.b_bits.shape)
+    nw = hip.FromBF16Bits(synth.f32_to_bf16_bits((1 + 0.1 * np.random.default_rng(d).standard_normal(d))
+                                                 .astype(np.float32)), d)
+    for tok, pos in ((299, 511), (0, 8191), (17, 0), (300, 3)):
+        step(f"jh_embed_norm_prepare bits={bits} d={d} gs={gs} token={tok} pos={pos}")
+        ids = hip.FromInt32(np.array([tok], np.int32))
+        h, u, st, cs = hip.EmbedNormPrepare(ids, w, s, b, gs, bits, nw, rope=(128, 1e6, 1.0, pos))
+        h2 = hip.Dequantize(hip.TakeAxis(w, ids), hip.TakeAxis(s, ids), hip.TakeAxis(b, ids), gs, bits)
+        u2, st2 = hip.NormPrepare(h2, nw)
+        cs2 = hip.RoPETable(128, 1e6, 1.0, pos)
+        for a, c in ((h, h2), (st, st2), (cs, cs2)):
+            assert np.array_equal(hip.Floats(a).view(np.uint32), hip.Floats(c).view(np.uint32))
+        assert hip.Bytes(u) == hip.Bytes(u2)
+        if tok >= 300:
+            assert not hip.Floats(h).any()
+    _, _, _, none = hip.EmbedNormPrepare(hip.FromInt32(np.array([5], np.int32)), w, s, b, gs, bits, nw)
+    assert none is None
+    hip.SetChecks(True)
+    try:
+        with pytest.raises(JanisHipError):
+            hip.EmbedNormPrepare(hip.FromInt32(np.array([300], np.int32)), w, s, b, gs, bits, nw)
+    finally:
+        hip.SetChecks(False)
+
+
 def test_quant_embedding_rows(hip, oracle):
     """QuantEmbedding.Forward (qwen/embed.go:78-83): TakeAxis of the packed
     words, scales and biases, then Dequantize; bit-exact."""
