@@ -671,6 +671,29 @@ def test_moe_swiglu_one_token(hip, oracle, k, out_dtype, collide):
     assert ok, (d, s_)
 
 
+def test_moe_swiglu_one_token_bad_index(hip, oracle):
+    """One token over 8 slots at the Qwen3-30B-A3B shapes: an expert index
+    outside [0, E) gives the token a NaN row with checks off and an error with
+    checks on; the next call with good indices is the oracle's again."""
+    qs, st = _t1_stacks(hip)
+    idx, sc = synth.route(9450, 1, 128, 8)
+    xb, x = synth.activations(9451, (1, 2048))
+    bad = idx.copy()
+    bad[0, 3] = 128
+    step("jh_moe_swiglu one token, index 128 of 128 experts, checks off")
+    assert np.isnan(_t1_call(hip, st, xb, bad, sc)).all()
+    hip.SetChecks(True)
+    try:
+        with pytest.raises(JanisHipError):
+            _t1_call(hip, st, xb, bad, sc)
+    finally:
+        hip.SetChecks(False)
+    step("jh_moe_swiglu one token after the bad call")
+    got = _t1_call(hip, st, xb, idx, sc)
+    ok, d, s_ = rel_ok(got, oracle.moe_apply(x, *[(q.w, q.s, q.b) for q in qs], idx, sc), BF16_TOL)
+    assert ok, (d, s_)
+
+
 def test_moe_swiglu_one_token_graph_replays(hip, oracle):
     """Captured once into a HIP graph and replayed on new tokens and routes
     (written into the captured buffers between replays): every replay matches
