@@ -1,5 +1,12 @@
 // Prefill GEMM for MLX affine 4-bit weights on gfx950:
-//   Y[M, N] = X[M, K] . W^T,  W dequantized tile by tile into LDS as bf16.
+//   Y[M, N] = X[M, K] . W^T.
+// Three tiles share the MFMA layout below. K divisible by 256 takes a 128-row
+// tile whose waves dequantize their own weight words into B fragments in
+// registers: qmm_dma_kernel for bf16 X (X tiles, weight words and scales staged
+// through LDS rings by loads with an LDS destination, several steps ahead) and
+// qmm_wreg_kernel for fp32 X (weights prefetched in registers, X converted on its
+// way to LDS). Other K take qmm_mfma_kernel, described next, which dequantizes W
+// tile by tile into LDS as bf16.
 //
 // Reference semantics: QuantMatmul with rows > 1 (cpu/cpu_misc.go:378-399),
 // which dequantizes a weight row once (wbuf = q*scale + bias) and dots it with
@@ -584,6 +591,205 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_wreg_kernel(
         }
 }
 
+
+// ---- The same tile with its operands staged in LDS rings ---------------------------
+//
+// Every load of a step — the X tile, the wave's 16 bytes of weight words per lane
+// and, once per super-step, its scales and biases — is a buffer load with an LDS
+// destination, issued A steps before the step that reads it. Nothing in flight
+// holds registers, so the loads get A steps (A+1 LDS slots) to land, where the
+// register tile's weights had about two; and the X tile needs no register
+// staging or LDS stores. The LDS layout, the K permutation, the dequantization
+// and the MFMA order are those of qmm_wreg_kernel, so the two tiles give the
+// same bits.
+//
+// The loads are issued from inline asm with explicit waits: the compiler tracks
+// loads into LDS it issued itself and makes each LDS read wait for all of them
+// (vmcnt(0)), which would drain the ring every step. Loads complete in issue
+// order, so at the top of step t `s_waitcnt vmcnt(n)` with n = the loads issued
+// after step t's own leaves exactly those in flight; any load the compiler adds
+// in between only makes the wait longer, never shorter.
+
+// LDS byte offset of a __shared__ address (the value M0 takes for a load into LDS).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(__attribute__((address_space(3))) const void*)p);
+}
+// 16 bytes per lane into LDS at m0 + 16 * lane (the s_nop covers the M0 write).
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t m0) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(m0) : "memory");
+}
+// 4 bytes per lane into LDS at m0 + 4 * lane.
+__device__ __forceinline__ void lds_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t m0) {
+    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(m0) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Dwords of scales (and of biases) per lane per super-step: SUP/2 elements of
+// the lane's K half are NG groups; 0 when they do not fill whole dwords.
+template <int SBT, int GSL>
+constexpr int dma_sb_dwords() {
+    constexpr int ng = (128 >> GSL) > 0 ? (128 >> GSL) : 1;
+    constexpr int bytes = ng * (SBT == 2 ? 4 : 2);
+    return bytes % 4 == 0 ? bytes / 4 : 0;
+}
+
+// Loads a wave issues after those of step t (t % SPS = u): they were issued at
+// step t - A, and steps t - A + v (v = 1 .. A-1) issue the loads of step t + v:
+// NX X loads, one weight load, and 2·NSB scale/bias loads when t + v starts a
+// super-step. (Step t's own scales were issued no later than its X and weights.)
+template <int A, int NX, int NSB, int SPS>
+constexpr int dma_loads_after(int u) {
+    int n = 0;
+    for (int v = 1; v < A; v++) n += NX + 1 + (((u + v) % SPS) == 0 ? 2 * NSB : 0);
+    return n;
+}
+
+template <bool SPLIT, int SBT, int GSL, int NW, int A>
+__global__ __launch_bounds__(64 * NW, 2) void qmm_dma_kernel(
+    const uint32_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ B,
+    const void* __restrict__ X, void* __restrict__ Y, int y_dt, uint32_t M, uint32_t N, uint32_t K,
+    uint32_t k_per_split, float* __restrict__ acc_out) {
+    constexpr int SUP = 256, SPS = SUP / 64, R = A + 1;
+    static_assert(A >= 1 && A <= SPS, "the scale/bias ring has two super-step slots");
+    constexpr int RBN = 32 * NW;
+    constexpr uint32_t SBB = SBT == 2 ? 4 : 2;
+    constexpr int NSB = dma_sb_dwords<SBT, GSL>();
+    static_assert(NSB >= 1, "scales/biases in whole dwords");
+    constexpr int XQ = RXT / 1024;              // 1 KiB loads per X tile (8 rows each)
+    constexpr int NX = (XQ + NW - 1) / NW;      // X loads per wave per step
+    constexpr int WSLOT = NW * 1024;            // weight words of one step, all waves
+    constexpr int SBW = 2 * NSB * 256;          // one wave's scales + biases of a super-step
+    constexpr int JUNK = NX * NW > XQ ? 1024 : 0;  // target of the filler loads that even out the count
+    __shared__ __attribute__((aligned(16))) uint8_t lds[R * RXT + R * WSLOT + 2 * NW * SBW + JUNK];
+    uint8_t* const xring = lds;
+    uint8_t* const wring = lds + R * RXT;
+    uint8_t* const sbring = wring + R * WSLOT;
+    uint8_t* const junk = sbring + 2 * NW * SBW;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, c32 = lane & 31;
+    const uint32_t m0 = blockIdx.y * RBM, n0 = blockIdx.x * RBN + wave * 32;
+    const uint32_t P = K >> 3, G = K >> GSL;
+    const auto rx = make_rsrc(X, M * K * 2);
+    const auto rw = make_rsrc(W, N * P * 4);
+    const auto rs = make_rsrc(S, N * G * SBB);
+    const auto rb = make_rsrc(B, N * G * SBB);
+    const uint32_t kb = blockIdx.z * k_per_split;
+    const uint32_t ke = min(K, kb + k_per_split);
+    const int nsup = kb < ke ? (int)((ke - kb) / SUP) : 0;
+    const int nsteps = SPS * nsup;
+
+    floatx16 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
+
+    // Super-steps past the last are clamped to it: their loads are repeats into
+    // slots nobody reads, so every step issues the same number of loads.
+    auto ksup = [&](int sup) { return kb + (uint32_t)min(sup, nsup - 1) * SUP; };
+    // The loads of step s into ring slot s % R.
+    auto issue = [&](int s) {
+        const int slot = s % R, t = s % SPS;
+        const uint32_t k0 = ksup(s / SPS);
+        // X: load q is rows 8q .. 8q+7 of the tile; lane -> (row, physical chunk p)
+        // holding logical chunk p ^ ((row/2) % 8) (the swizzle is applied on the source side)
+#pragma unroll
+        for (int i = 0; i < NX; i++) {
+            const int q = wave + NW * i;
+            const int qs = q < XQ ? q : q - XQ;  // a filler repeats a real load into junk
+            const int r = 8 * qs + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+            const uint32_t kc = k0 + (SUP / 2) * (c >> 2) + 32 * t + 8 * (c & 3);
+            lds_load16(rx, ((m0 + r) * K + kc) * 2, lds_addr(q < XQ ? xring + slot * RXT + 1024 * q : junk));
+        }
+        // weights: words 16h + 4t .. +3 of column n0 + c32's super-step segment
+        lds_load16(rw, ((n0 + c32) * P + (k0 >> 3) + 16 * h + 4 * t) * 4,
+                   lds_addr(wring + slot * WSLOT + 1024 * wave));
+        if (t == 0) {  // the super-step's scales and biases
+            uint8_t* const base = sbring + (((s / SPS) & 1) * NW + wave) * SBW;
+            const uint32_t off = ((n0 + c32) * G + ((k0 + (SUP / 2) * h) >> GSL)) * SBB;
+#pragma unroll
+            for (int i = 0; i < NSB; i++) lds_load4(rs, off + 4 * i, lds_addr(base + 256 * i));
+#pragma unroll
+            for (int i = 0; i < NSB; i++) lds_load4(rb, off + 4 * i, lds_addr(base + 256 * (NSB + i)));
+        }
+    };
+    auto compute = [&](int s) {
+        const int slot = s % R, t = s % SPS;
+        const uint8_t* const xs = xring + slot * RXT;
+        const uint4 wq = *reinterpret_cast<const uint4*>(wring + slot * WSLOT + 1024 * wave + 16 * lane);
+        const uint8_t* const sbb = sbring + (((s / SPS) & 1) * NW + wave) * SBW;
+        uint32_t sw[NSB], bw[NSB];
+#pragma unroll
+        for (int i = 0; i < NSB; i++) {
+            sw[i] = *reinterpret_cast<const uint32_t*>(sbb + 256 * i + 4 * lane);
+            bw[i] = *reinterpret_cast<const uint32_t*>(sbb + 256 * (NSB + i) + 4 * lane);
+        }
+        const int e = (32 * t) >> GSL;
+        const float sc = sb_elem<SBT, GSL>(sw, e), bi = sb_elem<SBT, GSL>(bw, e);
+        bf16x8_t a[2][4], bq[2];
+        auto read_a = [&](int k, int buf) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                a[buf][i] = *reinterpret_cast<const bf16x8_t*>(xs + xswz(32 * i + c32, 4 * h + k));
+        };
+        auto deq = [&](int k, int buf) {
+            const uint32_t word = k == 0 ? wq.x : k == 1 ? wq.y : k == 2 ? wq.z : wq.w;
+            bq[buf] = dequant_word(word, sc, bi);
+        };
+        read_a(0, 0);
+        deq(0, 0);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (k < 3) {
+                read_a(k + 1, (k + 1) & 1);
+                deq(k + 1, (k + 1) & 1);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[k & 1][i], bq[k & 1], acc[i], 0, 0, 0);
+        }
+    };
+    if (nsteps > 0) {
+#pragma unroll
+        for (int s = 0; s < A; s++) issue(s);
+        auto step = [&](int t, auto uc) {
+            constexpr int u = decltype(uc)::value;
+            wait_vmem<dma_loads_after<A, NX, NSB, SPS>(u)>();  // this step's loads have landed (this wave's) ...
+            __syncthreads();  // ... and every wave's; slot (t+u-1) % R is free
+            issue(t + u + A);
+            compute(t + u);
+        };
+        for (int t = 0; t < nsteps; t += SPS) {
+            static_assert(SPS == 4, "four steps per super-step");
+            step(t, std::integral_constant<int, 0>{});
+            step(t, std::integral_constant<int, 1>{});
+            step(t, std::integral_constant<int, 2>{});
+            step(t, std::integral_constant<int, 3>{});
+        }
+        wait_vmem<0>();  // no load may still target LDS when the block ends
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t n = n0 + c32;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const uint32_t m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (m < M && n < N) {
+                if constexpr (SPLIT)
+                    acc_out[blockIdx.z * split_stride(M, N) + (size_t)m * N + n] = acc[i][r];
+                else
+                    store_y(Y, (int64_t)m * N + n, acc[i][r], y_dt);
+            }
+        }
+    }
+}
+
 }  // namespace
 
 Status launch_generic(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y,
@@ -591,26 +797,51 @@ Status launch_generic(const QuantMatrix& m, const void* x, int x_dtype, int64_t 
 
 constexpr int kBM = BM, kBN = BN;  // the LDS tile
 
-// How one prefill product is launched. K divisible by 256 takes the W-in-
-// registers tile with 4, 6 or 8 waves (128 x 32·waves of Y per block; two
-// 4-wave blocks or one 6- or 8-wave block per CU) and K split 1, 2, 4 or 8 ways
-// (8 for 4 waves only). Each K range stores its fp32 partial tile, and one
-// pass sums them in order. The pair is the one with the least modelled time:
-// the busiest CU's blocks, each costing a fixed start plus its columns x K
-// super-steps at the CU's measured rate for that wave count, plus a fixed and
-// a per-element cost of the split (partial stores, the summing pass). The
-// constants are a least-squares fit (4.8 % rms) to 320 timed plans of the
-// Qwen3-8B projections (N x K = 12288/6144/4096 x 4096, 4096 x 12288) at
-// M = 128 .. 2048 on MI355X; over those 32 cases the fitted choice took
-// 3079 us against 3075 us for the best plan of each. Other K (multiples of
-// 64) take the LDS tile.
+// How one prefill product is launched. K divisible by 256 takes the 128-row
+// tile (128 x 32·waves of Y per block) with K split 1, 2, 4 or 8 ways; each K
+// range stores its fp32 partial tile, and one pass sums them in order. bf16 X
+// (with scales in whole dwords per lane) takes the LDS-ring tile in one of
+// four shapes: 4 waves with a lead of 1 step (two blocks per CU) or 3 steps
+// (one), 8 waves with a lead of 2 or 3 steps (one block per CU); fp32 X takes
+// the register tile with 4, 6 or 8 waves. The plan is the one with the least
+// modelled time: the busiest CU's blocks, each costing a fixed start plus its
+// columns x K super-steps at the CU's measured rate for that shape, plus a fixed
+// and a per-element cost of the split (partial stores, the summing pass). The
+// constants are least-squares fits to timed plans of the Qwen3-8B projections
+// (N x K = 12288/6144/4096 x 4096, 4096 x 12288) at M = 128 .. 2048 on MI355X:
+// for the LDS-ring tile 7.9 % rms over 280 plans, the fitted choices taking
+// 1471 us summed over the 20 cases against 1442 us for the best plan of each;
+// for the register tile 4.8 % rms over 320 plans, 3079 against 3075 us over 32
+// cases. Other K (multiples of 64) take the LDS tile.
 struct QmmPlan {
     bool wreg;
     int nw;
+    int lead;  // steps of lead of the LDS-ring tile; 0: the register tile
     int64_t split;
     uint32_t k_per_split;
     dim3 grid;
 };
+
+// Modelled microseconds of one LDS-ring plan (see above).
+double qmm_dma_cost(int64_t M, int64_t N, int64_t nsup, int nw, int lead, int64_t split, int num_cus) {
+    constexpr double kSplitFixed = 4.51;  // µs: the summing launch
+    constexpr double kSplitElem = 1.075;  // µs per 10^6 partial sums
+    const int64_t rbn = 32 * nw, mt = (M + RBM - 1) / RBM;
+    const int64_t blocks = ((N + rbn - 1) / rbn) * mt * split;
+    const int64_t per_cu = (blocks + num_cus - 1) / num_cus;
+    const double u = (double)rbn * (double)((nsup + split - 1) / split);
+    double t;
+    if (nw == 4 && lead == 1)  // two blocks per CU: 56.8 column·super-steps per µs, 46.1 alone
+        t = (double)(per_cu / 2) * (2.0 * u / 56.8 + 2.10) + (double)(per_cu % 2) * (u / 46.1 + 2.10);
+    else if (nw == 4)
+        t = (double)per_cu * (u / 55.6 + 3.73);
+    else if (lead == 2)
+        t = (double)per_cu * (u / 65.0 + 2.37);
+    else
+        t = (double)per_cu * (u / 76.8 + 5.69);
+    if (split > 1) t += kSplitFixed + kSplitElem * (double)(M * N * split) * 1e-6;
+    return t;
+}
 
 // Modelled microseconds of one W-in-registers plan (see above).
 double qmm_wreg_cost(int64_t M, int64_t N, int64_t nsup, int nw, int64_t split, int num_cus) {
@@ -634,17 +865,27 @@ double qmm_wreg_cost(int64_t M, int64_t N, int64_t nsup, int nw, int64_t split, 
     return t;
 }
 
-QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus) {
+QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus, bool dma) {
     QmmPlan p{};
     if (m.in % 256 == 0) {
         p.wreg = true;
         const int64_t nsup = m.in / 256;
         double best = 0;
-        for (int nw : {8, 4, 6})
-            for (int64_t split = 1; split <= (nw == 4 ? 8 : 4) && (split == 1 || nsup / split >= 2); split *= 2) {
-                const double t = qmm_wreg_cost(rows, m.rows, nsup, nw, split, num_cus);
-                if (p.nw == 0 || t < best) best = t, p.nw = nw, p.split = split;
-            }
+        if (dma) {
+            static constexpr int kShapes[4][2] = {{8, 3}, {8, 2}, {4, 3}, {4, 1}};  // waves, lead
+            for (const auto& sh : kShapes)
+                for (int64_t split = 1; split <= (sh[0] == 4 ? 8 : 4) && (split == 1 || nsup / split >= 2);
+                     split *= 2) {
+                    const double t = qmm_dma_cost(rows, m.rows, nsup, sh[0], sh[1], split, num_cus);
+                    if (p.nw == 0 || t < best) best = t, p.nw = sh[0], p.lead = sh[1], p.split = split;
+                }
+        } else {
+            for (int nw : {8, 4, 6})
+                for (int64_t split = 1; split <= (nw == 4 ? 8 : 4) && (split == 1 || nsup / split >= 2); split *= 2) {
+                    const double t = qmm_wreg_cost(rows, m.rows, nsup, nw, split, num_cus);
+                    if (p.nw == 0 || t < best) best = t, p.nw = nw, p.split = split;
+                }
+        }
         const int64_t rbn = 32 * p.nw;
         p.k_per_split = (uint32_t)(((nsup + p.split - 1) / p.split) * 256);
         p.grid = dim3((unsigned)((m.rows + rbn - 1) / rbn), (unsigned)((rows + RBM - 1) / RBM), (unsigned)p.split);
@@ -662,6 +903,13 @@ QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus) {
     return p;
 }
 
+// The LDS-ring tile (qmm_dma_kernel) takes bf16 X whenever a lane's scales of a
+// super-step fill whole dwords (group size 32 or 64, or 128 with fp32 scales).
+bool qmm_dma_ok(const QuantMatrix& m, int x_dtype) {
+    const int gl = log2_exact(m.group_size);
+    return x_dtype == JH_BF16 && (gl == 5 || gl == 6 || (gl == 7 && m.sb_dtype == JH_F32));
+}
+
 bool qmm_uses_mfma(const QuantMatrix& m, int64_t rows, int x_dtype) {
     const int gl = log2_exact(m.group_size);
     const int64_t xb = x_dtype == JH_F32 ? 4 : 2;
@@ -672,7 +920,7 @@ bool qmm_uses_mfma(const QuantMatrix& m, int64_t rows, int x_dtype) {
 size_t qmm_workspace_bytes(const QuantMatrix& m, int64_t rows, int x_dtype, int y_dtype, int num_cus) {
     (void)y_dtype;
     if (!qmm_uses_mfma(m, rows, x_dtype)) return 0;
-    const int64_t split = qmm_plan(m, rows, num_cus).split;
+    const int64_t split = qmm_plan(m, rows, num_cus, qmm_dma_ok(m, x_dtype)).split;
     return split == 1 ? 0 : sizeof(float) * (size_t)split * split_stride((uint32_t)rows, (uint32_t)m.rows);
 }
 
@@ -688,6 +936,27 @@ void launch_tile_wreg(const QuantMatrix& m, const void* x, int64_t rows, void* y
         if (gl == 5) go(qmm_wreg_kernel<SPLIT, XF32, SBT, 5, NW, WNF, SUP>);
         else if (gl == 6) go(qmm_wreg_kernel<SPLIT, XF32, SBT, 6, NW, WNF, SUP>);
         else go(qmm_wreg_kernel<SPLIT, XF32, SBT, 7, NW, WNF, SUP>);
+    };
+    if (m.sb_dtype == JH_F32)
+        by_gs(std::integral_constant<int, 2>{});
+    else if (m.sb_dtype == JH_F16)
+        by_gs(std::integral_constant<int, 1>{});
+    else
+        by_gs(std::integral_constant<int, 0>{});
+}
+
+template <int NW, int A, bool SPLIT>
+void launch_tile_dma(const QuantMatrix& m, const void* x, int64_t rows, void* y, int y_dtype, int gl,
+                     uint32_t k_per_split, float* acc, dim3 grid, hipStream_t st) {
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(64 * NW), 0, st, m.w, m.scales, m.biases, x, y, y_dtype,
+                           (uint32_t)rows, (uint32_t)m.rows, (uint32_t)m.in, k_per_split, acc);
+    };
+    auto by_gs = [&](auto sbt) {
+        constexpr int SBT = decltype(sbt)::value;
+        if (gl == 5) go(qmm_dma_kernel<SPLIT, SBT, 5, NW, A>);
+        else if (gl == 6) go(qmm_dma_kernel<SPLIT, SBT, 6, NW, A>);
+        else if constexpr (SBT == 2) go(qmm_dma_kernel<SPLIT, SBT, 7, NW, A>);
     };
     if (m.sb_dtype == JH_F32)
         by_gs(std::integral_constant<int, 2>{});
@@ -716,11 +985,21 @@ Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows
                   int y_dtype, int num_cus, hipStream_t st, void* workspace) {
     if (!qmm_uses_mfma(m, rows, x_dtype)) return launch_generic(m, x, x_dtype, rows, y, y_dtype, num_cus, st);
     const int gl = log2_exact(m.group_size);
-    const QmmPlan p = qmm_plan(m, rows, num_cus);
+    const bool dma = qmm_dma_ok(m, x_dtype);
+    const QmmPlan p = qmm_plan(m, rows, num_cus, dma);
     const bool xf32 = x_dtype == JH_F32;
     auto tile = [&](auto split_c, float* acc) {
         constexpr bool SPLIT = decltype(split_c)::value;
-        if (p.wreg) {
+        if (p.wreg && p.lead > 0) {
+            if (p.nw == 8 && p.lead == 3)
+                launch_tile_dma<8, 3, SPLIT>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+            else if (p.nw == 8)
+                launch_tile_dma<8, 2, SPLIT>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+            else if (p.lead == 3)
+                launch_tile_dma<4, 3, SPLIT>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+            else
+                launch_tile_dma<4, 1, SPLIT>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+        } else if (p.wreg) {
             if (p.nw == 6) {
                 if (xf32) launch_tile_wreg<6, 1, 256, SPLIT, true>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
                 else launch_tile_wreg<6, 1, 256, SPLIT, false>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);

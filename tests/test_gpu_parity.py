@@ -270,20 +270,29 @@ def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,gs,sb,xf32,out_dtype", [
-    (500, 12288, 4096, 64, "bf16", False, BF16),   # 6 waves, K whole, M ragged
-    (640, 8000, 2048, 32, "f16", False, BF16),     # 6 waves, N ragged (8000 = 41.7 tiles of 192)
+    # bf16 x: the LDS-ring tile (waves, steps of lead, K split)
+    (500, 12288, 4096, 64, "bf16", False, BF16),   # 8 waves lead 3, K whole, M ragged
+    (640, 8000, 2048, 32, "f16", False, BF16),     # 8 waves lead 3, N ragged (8000 = 31.25 tiles of 256)
+    (300, 2784, 2048, 64, "bf16", False, BF16),    # 8 waves lead 2, K split 4, bf16 out via the fp32 buffer
+    (128, 12288, 4096, 32, "f32", False, F32),     # 8 waves lead 2, K split 4, 4 dwords of scales per lane
+    (384, 6144, 4096, 64, "f16", False, F32),      # qkv at M=384: 4 waves lead 3, K whole
+    (260, 9000, 4096, 64, "bf16", False, BF16),    # 4 waves lead 3, M ragged
+    (128, 4096, 12288, 64, "f16", False, BF16),    # down at M=128: 4 waves lead 3, K split 8
+    (77, 1000, 4096, 64, "bf16", False, F32),      # 4 waves lead 1, K split 8, M and N ragged
+    (1000, 2000, 1024, 128, "f32", False, BF16),   # group 128 with fp32 scales: 4 waves lead 3
+    (1536, 4096, 12288, 64, "bf16", False, BF16),  # down at M=1536: 8 waves lead 3, K whole
+    # fp32 x: the register tile (waves, K split)
     (1000, 6000, 1024, 128, "f32", True, F32),     # 6 waves, fp32 x and scales
-    (300, 2784, 2048, 64, "bf16", False, BF16),    # 6 waves, K split 4, bf16 out via the fp32 buffer
-    (300, 2784, 2048, 64, "bf16", True, F32),      # 6 waves, K split 4, atomics straight into y
-    (384, 6144, 4096, 64, "f16", False, F32),      # qkv at M=384: 6 waves, K split 2
-    (260, 9000, 4096, 64, "bf16", False, BF16),    # 8 waves, K split 2, M ragged
-    (1536, 4096, 12288, 64, "bf16", False, BF16),  # down at M=1536: 8 waves, K split 4
+    (300, 2784, 2048, 64, "bf16", True, F32),      # 6 waves, K split 4, fp32 out
     (1100, 3000, 2048, 64, "bf16", True, BF16),    # 4 waves, K whole
+    (2048, 4096, 12288, 64, "bf16", True, F32),    # 8 waves, K whole
 ])
 def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
-    """Every tile/split pair the prefill planner picks on a 256-CU MI355X (4/6/8
-    waves, K whole or split, ragged M and N, fp32 x, bf16/f16/fp32 scales and
-    both outputs): the oracle on a random 48x96 block of the output."""
+    """Every tile/split pair the prefill planner picks on a 256-CU MI355X (the
+    LDS-ring tile in its four shapes for bf16 x, the register tile with 4/6/8
+    waves for fp32 x; K whole or split, ragged M and N, bf16/f16/fp32 scales,
+    group sizes 32/64/128 and both outputs): the oracle on a random 48x96 block
+    of the output."""
     q = synth.quant_linear(9000 + m + n, n, k, gs)
     xb, x = synth.activations(9500 + m, (m, k))
     w = hip.FromRaw(U32, q.w, *q.w.shape)
@@ -305,6 +314,34 @@ def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
     want = oracle.quant_matmul(x[rs], q.w[cs], s_np[cs], b_np[cs], gs)
     ok, d, sc = rel_ok(y[np.ix_(rs, cs)], want, BF16_TOL if out_dtype == BF16 else 5e-3)
     assert ok, (d, sc)
+
+
+@pytest.mark.parametrize("m,n,k,gs,sb", [
+    (2048, 12288, 4096, 64, "bf16"),  # LDS ring 8 waves lead 3 / register 8 waves, K whole
+    (300, 2784, 2048, 64, "f16"),     # 8 waves lead 2 / 6 waves, K split 4
+    (1000, 6000, 1024, 32, "bf16"),   # 8 waves lead 2 / 6 waves, K whole, group 32
+    (128, 4096, 12288, 64, "f32"),    # 4 waves lead 3 / 4 waves, K split 8
+    (77, 1000, 4096, 64, "bf16"),     # 4 waves lead 1 / 4 waves, K split 8, ragged
+    (1000, 2000, 1024, 128, "f32"),   # 4 waves lead 3 / 4 waves, group 128
+])
+def test_qmm_bf16_x_matches_fp32_x(hip, m, n, k, gs, sb):
+    """The LDS-ring tile (bf16 x) against the register tile (the same x widened
+    to fp32): the same K permutation, dequantization and MFMA order, so with the
+    same K split (the planner splits these shapes alike for both tiles) the
+    outputs are the same bits."""
+    q = synth.quant_linear(9900 + m + n, n, k, gs)
+    xb, x = synth.activations(9950 + m, (m, k))
+    w = hip.FromRaw(U32, q.w, *q.w.shape)
+    if sb == "bf16":
+        s, b = hip.FromBF16Bits(q.s_bits, *q.s_bits.shape), hip.FromBF16Bits(q.b_bits, *q.b_bits.shape)
+    elif sb == "f16":
+        s, b = hip.FromRaw(F16, q.s.astype(np.float16), *q.s.shape), hip.FromRaw(F16, q.b.astype(np.float16), *q.b.shape)
+    else:
+        s, b = hip.FromFloats(q.s), hip.FromFloats(q.b)
+    step(f"jh_quant_matmul bf16 x vs fp32 x M={m} N={n} K={k} gs={gs} sb={sb}")
+    y1 = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, m, k), w, s, b, True, gs, 4, out_dtype=F32))
+    y2 = hip.Floats(hip.QuantMatmul(hip.FromFloats(x), w, s, b, True, gs, 4, out_dtype=F32))
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32)), float(np.max(np.abs(y1 - y2)))
 
 
 @pytest.mark.parametrize("out_dtype", [BF16, F32])
