@@ -385,10 +385,11 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
             pre[f"{name}_M{m}"] = {"us": round(ms * 1e3, 1), "TFLOP_s": round(fl / (ms * 1e-3) / 1e12, 1),
                                    "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)}
             del g
-        # a few rows (batched decode of several sequences): the multi-row decode
-        # GEMV up to 8 rows (4 for down), HBM-bound on the weights
+        # a few rows (batched decode of several sequences, a short draft to
+        # verify): the multi-row decode GEMV up to 8 rows (4 for down), HBM-bound
+        # on the weights; 16-64 rows take the MFMA tile's 32/64-row blocks
         few = {}
-        for m in ((2, 4, 8) if k == 4096 else (2, 4)):
+        for m in ((2, 4, 8, 16, 32, 64) if k == 4096 else (2, 4, 16, 32, 64)):
             x = bf16((m, k))
             y = bf16((m, n), randn=False)
             g = capture(lambda: [hip.QuantMatmul(x, *c, True, GS, 4, out=y) for c in copies])

@@ -647,7 +647,7 @@ constexpr int dma_loads_after(int u) {
     return n;
 }
 
-template <bool SPLIT, int SBT, int GSL, int NW, int A>
+template <bool SPLIT, int SBT, int GSL, int NW, int A, int RB = RBM>  // RB: rows of X per block, 32 | 64 | 128
 __global__ __launch_bounds__(64 * NW, 2) void qmm_dma_kernel(
     const uint32_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ B,
     const void* __restrict__ X, void* __restrict__ Y, int y_dt, uint32_t M, uint32_t N, uint32_t K,
@@ -658,21 +658,24 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_dma_kernel(
     constexpr uint32_t SBB = SBT == 2 ? 4 : 2;
     constexpr int NSB = dma_sb_dwords<SBT, GSL>();
     static_assert(NSB >= 1, "scales/biases in whole dwords");
-    constexpr int XQ = RXT / 1024;              // 1 KiB loads per X tile (8 rows each)
+    static_assert(RB == 32 || RB == 64 || RB == 128, "rows per block");
+    constexpr int RT = RB / 32;                 // MFMA row tiles per wave
+    constexpr int XT = RB * ROW_BYTES;          // X tile per K step
+    constexpr int XQ = XT / 1024;               // 1 KiB loads per X tile (8 rows each)
     constexpr int NX = (XQ + NW - 1) / NW;      // X loads per wave per step
     constexpr int WSLOT = NW * 1024;            // weight words of one step, all waves
     constexpr int SBW = 2 * NSB * 256;          // one wave's scales + biases of a super-step
     constexpr int JUNK = NX * NW > XQ ? 1024 : 0;  // target of the filler loads that even out the count
-    __shared__ __attribute__((aligned(16))) uint8_t lds[R * RXT + R * WSLOT + 2 * NW * SBW + JUNK];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[R * XT + R * WSLOT + 2 * NW * SBW + JUNK];
     uint8_t* const xring = lds;
-    uint8_t* const wring = lds + R * RXT;
+    uint8_t* const wring = lds + R * XT;
     uint8_t* const sbring = wring + R * WSLOT;
     uint8_t* const junk = sbring + 2 * NW * SBW;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, c32 = lane & 31;
-    const uint32_t m0 = blockIdx.y * RBM, n0 = blockIdx.x * RBN + wave * 32;
+    const uint32_t m0 = blockIdx.y * RB, n0 = blockIdx.x * RBN + wave * 32;
     const uint32_t P = K >> 3, G = K >> GSL;
     const auto rx = make_rsrc(X, M * K * 2);
     const auto rw = make_rsrc(W, N * P * 4);
@@ -683,9 +686,9 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_dma_kernel(
     const int nsup = kb < ke ? (int)((ke - kb) / SUP) : 0;
     const int nsteps = SPS * nsup;
 
-    floatx16 acc[4];
+    floatx16 acc[RT];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < RT; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
 
@@ -704,7 +707,7 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_dma_kernel(
             const int qs = q < XQ ? q : q - XQ;  // a filler repeats a real load into junk
             const int r = 8 * qs + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
             const uint32_t kc = k0 + (SUP / 2) * (c >> 2) + 32 * t + 8 * (c & 3);
-            lds_load16(rx, ((m0 + r) * K + kc) * 2, lds_addr(q < XQ ? xring + slot * RXT + 1024 * q : junk));
+            lds_load16(rx, ((m0 + r) * K + kc) * 2, lds_addr(q < XQ ? xring + slot * XT + 1024 * q : junk));
         }
         // weights: words 16h + 4t .. +3 of column n0 + c32's super-step segment
         lds_load16(rw, ((n0 + c32) * P + (k0 >> 3) + 16 * h + 4 * t) * 4,
@@ -720,7 +723,7 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_dma_kernel(
     };
     auto compute = [&](int s) {
         const int slot = s % R, t = s % SPS;
-        const uint8_t* const xs = xring + slot * RXT;
+        const uint8_t* const xs = xring + slot * XT;
         const uint4 wq = *reinterpret_cast<const uint4*>(wring + slot * WSLOT + 1024 * wave + 16 * lane);
         const uint8_t* const sbb = sbring + (((s / SPS) & 1) * NW + wave) * SBW;
         uint32_t sw[NSB], bw[NSB];
@@ -731,10 +734,10 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_dma_kernel(
         }
         const int e = (32 * t) >> GSL;
         const float sc = sb_elem<SBT, GSL>(sw, e), bi = sb_elem<SBT, GSL>(bw, e);
-        bf16x8_t a[2][4], bq[2];
+        bf16x8_t a[2][RT], bq[2];
         auto read_a = [&](int k, int buf) {
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < RT; i++)
                 a[buf][i] = *reinterpret_cast<const bf16x8_t*>(xs + xswz(32 * i + c32, 4 * h + k));
         };
         auto deq = [&](int k, int buf) {
@@ -750,7 +753,7 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_dma_kernel(
                 deq(k + 1, (k + 1) & 1);
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < RT; i++)
                 acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[k & 1][i], bq[k & 1], acc[i], 0, 0, 0);
         }
     };
@@ -775,7 +778,7 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_dma_kernel(
     }
 
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < RT; i++) {
         const uint32_t n = n0 + c32;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
@@ -817,22 +820,31 @@ struct QmmPlan {
     bool wreg;
     int nw;
     int lead;  // steps of lead of the LDS-ring tile; 0: the register tile
+    int rb;    // rows of X per block (the LDS-ring tile takes 32 or 64 for up to 64 rows)
     int64_t split;
     uint32_t k_per_split;
     dim3 grid;
 };
 
 // Modelled microseconds of one LDS-ring plan (see above).
-double qmm_dma_cost(int64_t M, int64_t N, int64_t nsup, int nw, int lead, int64_t split, int num_cus) {
+double qmm_dma_cost(int64_t M, int64_t N, int64_t nsup, int nw, int lead, int rb, int64_t split, int num_cus) {
     constexpr double kSplitFixed = 4.51;  // µs: the summing launch
     constexpr double kSplitElem = 1.075;  // µs per 10^6 partial sums
-    const int64_t rbn = 32 * nw, mt = (M + RBM - 1) / RBM;
+    const int64_t rbn = 32 * nw, mt = (M + rb - 1) / rb;
     const int64_t blocks = ((N + rbn - 1) / rbn) * mt * split;
     const int64_t per_cu = (blocks + num_cus - 1) / num_cus;
     const double u = (double)rbn * (double)((nsup + split - 1) / split);
+    // two 4-wave blocks share a CU: pairs at the pair rate, a last odd block alone
+    auto pairs = [&](double rate2, double rate1, double start) {
+        return (double)(per_cu / 2) * (2.0 * u / rate2 + start) + (double)(per_cu % 2) * (u / rate1 + start);
+    };
     double t;
-    if (nw == 4 && lead == 1)  // two blocks per CU: 56.8 column·super-steps per µs, 46.1 alone
-        t = (double)(per_cu / 2) * (2.0 * u / 56.8 + 2.10) + (double)(per_cu % 2) * (u / 46.1 + 2.10);
+    if (rb == 32)
+        t = nw == 4 ? pairs(110.5, 104.2, 2.70) : (double)per_cu * (u / 124.9 + 2.60);
+    else if (rb == 64)
+        t = nw == 4 ? pairs(95.2, 82.2, 3.22) : (double)per_cu * (u / 106.2 + 2.99);
+    else if (nw == 4 && lead == 1)
+        t = pairs(56.8, 46.1, 2.10);
     else if (nw == 4)
         t = (double)per_cu * (u / 55.6 + 3.73);
     else if (lead == 2)
@@ -871,14 +883,19 @@ QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus, bool dma) {
         p.wreg = true;
         const int64_t nsup = m.in / 256;
         double best = 0;
+        p.rb = RBM;
         if (dma) {
-            static constexpr int kShapes[4][2] = {{8, 3}, {8, 2}, {4, 3}, {4, 1}};  // waves, lead
-            for (const auto& sh : kShapes)
-                for (int64_t split = 1; split <= (sh[0] == 4 ? 8 : 4) && (split == 1 || nsup / split >= 2);
-                     split *= 2) {
-                    const double t = qmm_dma_cost(rows, m.rows, nsup, sh[0], sh[1], split, num_cus);
-                    if (p.nw == 0 || t < best) best = t, p.nw = sh[0], p.lead = sh[1], p.split = split;
+            // waves, lead, rows per block: 128-row blocks, or 32/64 for up to 64 rows
+            static constexpr int kShapes[4][3] = {{8, 3, 128}, {8, 2, 128}, {4, 3, 128}, {4, 1, 128}};
+            static constexpr int kSmall[4][3] = {{4, 3, 32}, {8, 3, 32}, {4, 2, 64}, {8, 2, 64}};
+            const int(*tab)[3] = rows <= 64 ? kSmall : kShapes;
+            for (int i = 0; i < 4; i++) {
+                const int nw = tab[i][0], lead = tab[i][1], rb = tab[i][2];
+                for (int64_t split = 1; split <= (nw == 4 ? 8 : 4) && (split == 1 || nsup / split >= 2); split *= 2) {
+                    const double t = qmm_dma_cost(rows, m.rows, nsup, nw, lead, rb, split, num_cus);
+                    if (p.nw == 0 || t < best) best = t, p.nw = nw, p.lead = lead, p.rb = rb, p.split = split;
                 }
+            }
         } else {
             for (int nw : {8, 4, 6})
                 for (int64_t split = 1; split <= (nw == 4 ? 8 : 4) && (split == 1 || nsup / split >= 2); split *= 2) {
@@ -888,7 +905,7 @@ QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus, bool dma) {
         }
         const int64_t rbn = 32 * p.nw;
         p.k_per_split = (uint32_t)(((nsup + p.split - 1) / p.split) * 256);
-        p.grid = dim3((unsigned)((m.rows + rbn - 1) / rbn), (unsigned)((rows + RBM - 1) / RBM), (unsigned)p.split);
+        p.grid = dim3((unsigned)((m.rows + rbn - 1) / rbn), (unsigned)((rows + p.rb - 1) / p.rb), (unsigned)p.split);
         return p;
     }
     p.wreg = false;
@@ -945,7 +962,7 @@ void launch_tile_wreg(const QuantMatrix& m, const void* x, int64_t rows, void* y
         by_gs(std::integral_constant<int, 0>{});
 }
 
-template <int NW, int A, bool SPLIT>
+template <int NW, int A, bool SPLIT, int RB = RBM>
 void launch_tile_dma(const QuantMatrix& m, const void* x, int64_t rows, void* y, int y_dtype, int gl,
                      uint32_t k_per_split, float* acc, dim3 grid, hipStream_t st) {
     auto go = [&](auto kern) {
@@ -954,9 +971,9 @@ void launch_tile_dma(const QuantMatrix& m, const void* x, int64_t rows, void* y,
     };
     auto by_gs = [&](auto sbt) {
         constexpr int SBT = decltype(sbt)::value;
-        if (gl == 5) go(qmm_dma_kernel<SPLIT, SBT, 5, NW, A>);
-        else if (gl == 6) go(qmm_dma_kernel<SPLIT, SBT, 6, NW, A>);
-        else if constexpr (SBT == 2) go(qmm_dma_kernel<SPLIT, SBT, 7, NW, A>);
+        if (gl == 5) go(qmm_dma_kernel<SPLIT, SBT, 5, NW, A, RB>);
+        else if (gl == 6) go(qmm_dma_kernel<SPLIT, SBT, 6, NW, A, RB>);
+        else if constexpr (SBT == 2) go(qmm_dma_kernel<SPLIT, SBT, 7, NW, A, RB>);
     };
     if (m.sb_dtype == JH_F32)
         by_gs(std::integral_constant<int, 2>{});
@@ -990,7 +1007,17 @@ Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows
     const bool xf32 = x_dtype == JH_F32;
     auto tile = [&](auto split_c, float* acc) {
         constexpr bool SPLIT = decltype(split_c)::value;
-        if (p.wreg && p.lead > 0) {
+        if (p.wreg && p.lead > 0 && p.rb == 32) {
+            if (p.nw == 8)
+                launch_tile_dma<8, 3, SPLIT, 32>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+            else
+                launch_tile_dma<4, 3, SPLIT, 32>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+        } else if (p.wreg && p.lead > 0 && p.rb == 64) {
+            if (p.nw == 8)
+                launch_tile_dma<8, 2, SPLIT, 64>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+            else
+                launch_tile_dma<4, 2, SPLIT, 64>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+        } else if (p.wreg && p.lead > 0) {
             if (p.nw == 8 && p.lead == 3)
                 launch_tile_dma<8, 3, SPLIT>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
             else if (p.nw == 8)

@@ -281,6 +281,12 @@ def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
     (77, 1000, 4096, 64, "bf16", False, F32),      # 4 waves lead 1, K split 8, M and N ragged
     (1000, 2000, 1024, 128, "f32", False, BF16),   # group 128 with fp32 scales: 4 waves lead 3
     (1536, 4096, 12288, 64, "bf16", False, BF16),  # down at M=1536: 8 waves lead 3, K whole
+    # up to 64 rows of bf16 x: 32- or 64-row blocks of the LDS-ring tile
+    (9, 12288, 4096, 64, "bf16", False, F32),      # 32 rows, 8 waves, K split 4
+    (20, 4096, 12288, 64, "f16", False, BF16),     # 32 rows, 4 waves, K split 8
+    (24, 24576, 4096, 128, "f32", False, F32),     # 32 rows, 4 waves, K whole, group 128
+    (50, 6144, 4096, 32, "bf16", False, F32),      # 64 rows, 4 waves, K split 4, group 32
+    (48, 9000, 4096, 64, "bf16", False, BF16),     # 64 rows, 8 waves, K split 4, N ragged
     # fp32 x: the register tile (waves, K split)
     (1000, 6000, 1024, 128, "f32", True, F32),     # 6 waves, fp32 x and scales
     (300, 2784, 2048, 64, "bf16", True, F32),      # 6 waves, K split 4, fp32 out
@@ -289,10 +295,10 @@ def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
 ])
 def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
     """Every tile/split pair the prefill planner picks on a 256-CU MI355X (the
-    LDS-ring tile in its four shapes for bf16 x, the register tile with 4/6/8
-    waves for fp32 x; K whole or split, ragged M and N, bf16/f16/fp32 scales,
-    group sizes 32/64/128 and both outputs): the oracle on a random 48x96 block
-    of the output."""
+    LDS-ring tile in its four 128-row shapes and its 32/64-row blocks for bf16 x,
+    the register tile with 4/6/8 waves for fp32 x; K whole or split, ragged M
+    and N, bf16/f16/fp32 scales, group sizes 32/64/128 and both outputs): the
+    oracle on a random block of up to 48x96 of the output."""
     q = synth.quant_linear(9000 + m + n, n, k, gs)
     xb, x = synth.activations(9500 + m, (m, k))
     w = hip.FromRaw(U32, q.w, *q.w.shape)
@@ -309,7 +315,7 @@ def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
     step(f"jh_quant_matmul planner M={m} N={n} K={k} gs={gs} sb={sb} xf32={xf32} out={out_dtype}")
     y = hip.Floats(hip.QuantMatmul(xt, w, s, b, True, gs, 4, out_dtype=out_dtype))
     rng = np.random.default_rng(m * 7 + n)
-    rs = np.sort(np.concatenate([rng.choice(m - 1, size=47, replace=False), [m - 1]]))
+    rs = np.sort(np.concatenate([rng.choice(m - 1, size=min(47, m - 1), replace=False), [m - 1]]))
     cs = np.sort(np.concatenate([rng.choice(n - 1, size=95, replace=False), [n - 1]]))
     want = oracle.quant_matmul(x[rs], q.w[cs], s_np[cs], b_np[cs], gs)
     ok, d, sc = rel_ok(y[np.ix_(rs, cs)], want, BF16_TOL if out_dtype == BF16 else 5e-3)
@@ -323,6 +329,11 @@ def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
     (128, 4096, 12288, 64, "f32"),    # 4 waves lead 3 / 4 waves, K split 8
     (77, 1000, 4096, 64, "bf16"),     # 4 waves lead 1 / 4 waves, K split 8, ragged
     (1000, 2000, 1024, 128, "f32"),   # 4 waves lead 3 / 4 waves, group 128
+    (9, 12288, 4096, 64, "bf16"),     # 32-row blocks, 8 waves / 6 waves, K split 4
+    (33, 12288, 4096, 32, "f16"),     # 64-row blocks, 8 waves / 6 waves, K split 4
+    (20, 4096, 12288, 64, "bf16"),    # 32-row blocks, 4 waves / 4 waves, K split 8
+    (60, 4096, 4096, 64, "f32"),      # 64-row blocks, 4 waves / 4 waves, K split 8
+    (40, 3000, 2048, 64, "bf16"),     # 32-row blocks, 4 waves / 4 waves, K split 4, N ragged
 ])
 def test_qmm_bf16_x_matches_fp32_x(hip, m, n, k, gs, sb):
     """The LDS-ring tile (bf16 x) against the register tile (the same x widened
