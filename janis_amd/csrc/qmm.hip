@@ -647,8 +647,8 @@ constexpr int dma_loads_after(int u) {
     return n;
 }
 
-template <bool SPLIT, int SBT, int GSL, int NW, int A, int RB = RBM>  // RB: rows of X per block, 32 | 64 | 128
-__global__ __launch_bounds__(64 * NW, 2) void qmm_dma_kernel(
+template <bool SPLIT, int SBT, int GSL, int NW, int A, int RB = RBM>  // RB: rows of X per block, 32 | 64 | 128 | 256
+__global__ __launch_bounds__(64 * NW, RB == 256 ? 1 : 2) void qmm_dma_kernel(
     const uint32_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ B,
     const void* __restrict__ X, void* __restrict__ Y, int y_dt, uint32_t M, uint32_t N, uint32_t K,
     uint32_t k_per_split, float* __restrict__ acc_out) {
@@ -658,7 +658,7 @@ __global__ __launch_bounds__(64 * NW, 2) void qmm_dma_kernel(
     constexpr uint32_t SBB = SBT == 2 ? 4 : 2;
     constexpr int NSB = dma_sb_dwords<SBT, GSL>();
     static_assert(NSB >= 1, "scales/biases in whole dwords");
-    static_assert(RB == 32 || RB == 64 || RB == 128, "rows per block");
+    static_assert(RB == 32 || RB == 64 || RB == 128 || RB == 256, "rows per block");
     constexpr int RT = RB / 32;                 // MFMA row tiles per wave
     constexpr int XT = RB * ROW_BYTES;          // X tile per K step
     constexpr int XQ = XT / 1024;               // 1 KiB loads per X tile (8 rows each)
@@ -800,27 +800,29 @@ Status launch_generic(const QuantMatrix& m, const void* x, int x_dtype, int64_t 
 
 constexpr int kBM = BM, kBN = BN;  // the LDS tile
 
-// How one prefill product is launched. K divisible by 256 takes the 128-row
-// tile (128 x 32·waves of Y per block) with K split 1, 2, 4 or 8 ways; each K
-// range stores its fp32 partial tile, and one pass sums them in order. bf16 X
-// (with scales in whole dwords per lane) takes the LDS-ring tile in one of
-// four shapes: 4 waves with a lead of 1 step (two blocks per CU) or 3 steps
-// (one), 8 waves with a lead of 2 or 3 steps (one block per CU); fp32 X takes
-// the register tile with 4, 6 or 8 waves. The plan is the one with the least
-// modelled time: the busiest CU's blocks, each costing a fixed start plus its
-// columns x K super-steps at the CU's measured rate for that shape, plus a fixed
-// and a per-element cost of the split (partial stores, the summing pass). The
-// constants are least-squares fits to timed plans of the Qwen3-8B projections
-// (N x K = 12288/6144/4096 x 4096, 4096 x 12288) at M = 128 .. 2048 on MI355X:
-// for the LDS-ring tile 7.9 % rms over 280 plans, the fitted choices taking
-// 1471 us summed over the 20 cases against 1442 us for the best plan of each;
-// for the register tile 4.8 % rms over 320 plans, 3079 against 3075 us over 32
-// cases. Other K (multiples of 64) take the LDS tile.
+// How one prefill product is launched. K divisible by 256 takes a tile of
+// 32·waves columns of Y per block with K split 1, 2, 4 or 8 ways; each K range
+// stores its fp32 partial tile, and one pass sums them in order. bf16 X (with
+// scales in whole dwords per lane) takes the LDS-ring tile: up to 64 rows in
+// 32- or 64-row blocks; beyond, 128-row blocks of 4 waves with a lead of 1 step
+// (two blocks per CU) or 3 steps (one), or of 8 waves with a lead of 2 or 3,
+// and from 256 rows also 256-row blocks of 8 waves with a lead of 1. fp32 X takes
+// the 128-row register tile with 4, 6 or 8 waves. The plan is the one with the
+// least modelled time: the busiest CU's blocks, each costing a fixed start plus
+// its columns x K super-steps at the CU's measured rate for that shape, plus a
+// fixed and a per-element cost of the split (partial stores, the summing
+// pass). The constants are least-squares fits to timed plans of the Qwen3-8B
+// projections (N x K = 12288/6144/4096 x 4096, 4096 x 12288) on MI355X: for the
+// LDS-ring tile at M = 128 .. 2048 7.1 % rms over 616 plans, the fitted choices
+// taking 2407 us summed over 32 cases against 2375 us for the best plan of each
+// (2505 us without the 256-row blocks); at M = 9 .. 64 5.6 % rms, 250.7 against
+// 244.9 us over 16 cases; for the register tile 4.8 % rms over 320 plans, 3079
+// against 3075 us over 32 cases. Other K (multiples of 64) take the LDS tile.
 struct QmmPlan {
     bool wreg;
     int nw;
     int lead;  // steps of lead of the LDS-ring tile; 0: the register tile
-    int rb;    // rows of X per block (the LDS-ring tile takes 32 or 64 for up to 64 rows)
+    int rb;    // rows of X per block (LDS-ring tile: 32 or 64 up to 64 rows, 128 or 256 beyond)
     int64_t split;
     uint32_t k_per_split;
     dim3 grid;
@@ -828,8 +830,9 @@ struct QmmPlan {
 
 // Modelled microseconds of one LDS-ring plan (see above).
 double qmm_dma_cost(int64_t M, int64_t N, int64_t nsup, int nw, int lead, int rb, int64_t split, int num_cus) {
-    constexpr double kSplitFixed = 4.51;  // µs: the summing launch
-    constexpr double kSplitElem = 1.075;  // µs per 10^6 partial sums
+    // the summing launch: fixed µs and µs per 10^6 partial sums (each table's own fit)
+    const double kSplitFixed = rb < 128 ? 4.51 : 4.74;
+    const double kSplitElem = rb < 128 ? 1.075 : 1.154;
     const int64_t rbn = 32 * nw, mt = (M + rb - 1) / rb;
     const int64_t blocks = ((N + rbn - 1) / rbn) * mt * split;
     const int64_t per_cu = (blocks + num_cus - 1) / num_cus;
@@ -843,14 +846,16 @@ double qmm_dma_cost(int64_t M, int64_t N, int64_t nsup, int nw, int lead, int rb
         t = nw == 4 ? pairs(110.5, 104.2, 2.70) : (double)per_cu * (u / 124.9 + 2.60);
     else if (rb == 64)
         t = nw == 4 ? pairs(95.2, 82.2, 3.22) : (double)per_cu * (u / 106.2 + 2.99);
+    else if (rb == 256)
+        t = (double)per_cu * (u / 46.6 + 4.82);
     else if (nw == 4 && lead == 1)
-        t = pairs(56.8, 46.1, 2.10);
+        t = pairs(60.5, 45.5, 0.76);
     else if (nw == 4)
-        t = (double)per_cu * (u / 55.6 + 3.73);
+        t = (double)per_cu * (u / 55.7 + 2.38);
     else if (lead == 2)
-        t = (double)per_cu * (u / 65.0 + 2.37);
+        t = (double)per_cu * (u / 65.4 + 0.78);
     else
-        t = (double)per_cu * (u / 76.8 + 5.69);
+        t = (double)per_cu * (u / 74.9 + 3.61);
     if (split > 1) t += kSplitFixed + kSplitElem * (double)(M * N * split) * 1e-6;
     return t;
 }
@@ -885,11 +890,14 @@ QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus, bool dma) {
         double best = 0;
         p.rb = RBM;
         if (dma) {
-            // waves, lead, rows per block: 128-row blocks, or 32/64 for up to 64 rows
-            static constexpr int kShapes[4][3] = {{8, 3, 128}, {8, 2, 128}, {4, 3, 128}, {4, 1, 128}};
+            // waves, lead, rows per block: 32/64-row blocks up to 64 rows, 128-row
+            // blocks beyond, and 256-row blocks from 256 rows (a lead of 2 at 256 rows was
+            // never the modelled best over the shapes the fit covers)
             static constexpr int kSmall[4][3] = {{4, 3, 32}, {8, 3, 32}, {4, 2, 64}, {8, 2, 64}};
+            static constexpr int kShapes[5][3] = {{8, 3, 128}, {8, 2, 128}, {4, 3, 128}, {4, 1, 128}, {8, 1, 256}};
             const int(*tab)[3] = rows <= 64 ? kSmall : kShapes;
-            for (int i = 0; i < 4; i++) {
+            const int nshapes = rows <= 64 ? 4 : rows >= 256 ? 5 : 4;
+            for (int i = 0; i < nshapes; i++) {
                 const int nw = tab[i][0], lead = tab[i][1], rb = tab[i][2];
                 for (int64_t split = 1; split <= (nw == 4 ? 8 : 4) && (split == 1 || nsup / split >= 2); split *= 2) {
                     const double t = qmm_dma_cost(rows, m.rows, nsup, nw, lead, rb, split, num_cus);
@@ -1007,7 +1015,9 @@ Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows
     const bool xf32 = x_dtype == JH_F32;
     auto tile = [&](auto split_c, float* acc) {
         constexpr bool SPLIT = decltype(split_c)::value;
-        if (p.wreg && p.lead > 0 && p.rb == 32) {
+        if (p.wreg && p.lead > 0 && p.rb == 256) {
+            launch_tile_dma<8, 1, SPLIT, 256>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
+        } else if (p.wreg && p.lead > 0 && p.rb == 32) {
             if (p.nw == 8)
                 launch_tile_dma<8, 3, SPLIT, 32>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
             else

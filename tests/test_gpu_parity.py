@@ -280,7 +280,11 @@ def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
     (128, 4096, 12288, 64, "f16", False, BF16),    # down at M=128: 4 waves lead 3, K split 8
     (77, 1000, 4096, 64, "bf16", False, F32),      # 4 waves lead 1, K split 8, M and N ragged
     (1000, 2000, 1024, 128, "f32", False, BF16),   # group 128 with fp32 scales: 4 waves lead 3
-    (1536, 4096, 12288, 64, "bf16", False, BF16),  # down at M=1536: 8 waves lead 3, K whole
+    (1536, 4096, 12288, 64, "bf16", False, BF16),  # down at M=1536: 256-row blocks, 8 waves lead 1, K split 2
+    (1024, 12288, 4096, 64, "bf16", False, F32),   # 256-row blocks, K whole
+    (768, 4096, 12288, 64, "f16", False, BF16),    # 256-row blocks, K split 4
+    (1300, 6000, 2048, 64, "f32", False, F32),     # 256-row blocks, M ragged (5.08 blocks), fp32 scales
+    (1000, 9000, 4096, 32, "bf16", False, BF16),   # 256-row blocks, N ragged, group 32
     # up to 64 rows of bf16 x: 32- or 64-row blocks of the LDS-ring tile
     (9, 12288, 4096, 64, "bf16", False, F32),      # 32 rows, 8 waves, K split 4
     (20, 4096, 12288, 64, "f16", False, BF16),     # 32 rows, 4 waves, K split 8
@@ -295,7 +299,7 @@ def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
 ])
 def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
     """Every tile/split pair the prefill planner picks on a 256-CU MI355X (the
-    LDS-ring tile in its four 128-row shapes and its 32/64-row blocks for bf16 x,
+    LDS-ring tile in its four 128-row shapes and its 32/64/256-row blocks for bf16 x,
     the register tile with 4/6/8 waves for fp32 x; K whole or split, ragged M
     and N, bf16/f16/fp32 scales, group sizes 32/64/128 and both outputs): the
     oracle on a random block of up to 48x96 of the output."""
@@ -334,6 +338,9 @@ def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
     (20, 4096, 12288, 64, "bf16"),    # 32-row blocks, 4 waves / 4 waves, K split 8
     (60, 4096, 4096, 64, "f32"),      # 64-row blocks, 4 waves / 4 waves, K split 8
     (40, 3000, 2048, 64, "bf16"),     # 32-row blocks, 4 waves / 4 waves, K split 4, N ragged
+    (1024, 12288, 4096, 64, "bf16"),  # 256-row blocks / 6 waves, K whole
+    (1300, 6000, 2048, 32, "f16"),    # 256-row blocks / 6 waves, K whole, M ragged
+    (768, 4096, 12288, 64, "f32"),    # 256-row blocks / 4 waves, K split 4
 ])
 def test_qmm_bf16_x_matches_fp32_x(hip, m, n, k, gs, sb):
     """The LDS-ring tile (bf16 x) against the register tile (the same x widened
