@@ -181,7 +181,10 @@ JH_API int jh_dequantize(jh_ctx *ctx, const uint32_t *w, const void *scales, con
  * run the MFMA prefill GEMM. rows == 0 is a no-op.
  * When the prefill GEMM splits K, its fp32 partial products go to the
  * context's workspace (grown to split * rows * out_features floats) and are
- * added in a fixed order: results are the same bits on every call. */
+ * added in a fixed order: results are the same bits on every call. The GEMM
+ * multiplies x rounded to bf16: fp32 x is first rounded into the workspace
+ * (rows * in_features bf16 more), so fp32 x gives the bits of its bf16
+ * rounding passed as bf16. */
 JH_API int jh_quant_matmul(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t rows, const uint32_t *w,
                     const void *scales, const void *biases, jh_dtype sb_dtype, int64_t out_features,
                     int64_t in_features, int transpose, int group_size, int bits, void *y,

@@ -928,11 +928,26 @@ QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus, bool dma) {
     return p;
 }
 
-// The LDS-ring tile (qmm_dma_kernel) takes bf16 X whenever a lane's scales of a
-// super-step fill whole dwords (group size 32 or 64, or 128 with fp32 scales).
+// The LDS-ring tile (qmm_dma_kernel) takes X whenever a lane's scales of a
+// super-step fill whole dwords (group size 32 or 64, or 128 with fp32 scales);
+// fp32 X is first rounded to bf16 into the workspace (as the register tile
+// rounds it on its way to LDS, so both give the same bits).
 bool qmm_dma_ok(const QuantMatrix& m, int x_dtype) {
+    (void)x_dtype;
     const int gl = log2_exact(m.group_size);
-    return x_dtype == JH_BF16 && (gl == 5 || gl == 6 || (gl == 7 && m.sb_dtype == JH_F32));
+    return gl == 5 || gl == 6 || (gl == 7 && m.sb_dtype == JH_F32);
+}
+
+// Bytes of the bf16 copy of fp32 X in the workspace, rounded up to 256.
+size_t qmm_xconv_bytes(int64_t rows, int64_t in) { return ((size_t)rows * (size_t)in * 2 + 255) & ~(size_t)255; }
+
+// n fp32 values (16-byte aligned, n a multiple of 4) to bf16, round to nearest even.
+__global__ void x_to_bf16_kernel(const float4* __restrict__ x, int64_t n4, uint2* __restrict__ out) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        const float4 v = x[i];
+        out[i] = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+    }
 }
 
 bool qmm_uses_mfma(const QuantMatrix& m, int64_t rows, int x_dtype) {
@@ -945,8 +960,9 @@ bool qmm_uses_mfma(const QuantMatrix& m, int64_t rows, int x_dtype) {
 size_t qmm_workspace_bytes(const QuantMatrix& m, int64_t rows, int x_dtype, int y_dtype, int num_cus) {
     (void)y_dtype;
     if (!qmm_uses_mfma(m, rows, x_dtype)) return 0;
-    const int64_t split = qmm_plan(m, rows, num_cus, qmm_dma_ok(m, x_dtype)).split;
-    return split == 1 ? 0 : sizeof(float) * (size_t)split * split_stride((uint32_t)rows, (uint32_t)m.rows);
+    const QmmPlan p = qmm_plan(m, rows, num_cus, qmm_dma_ok(m, x_dtype));
+    const size_t xconv = p.wreg && p.lead > 0 && x_dtype == JH_F32 ? qmm_xconv_bytes(rows, m.in) : 0;
+    return xconv + (p.split == 1 ? 0 : sizeof(float) * (size_t)p.split * split_stride((uint32_t)rows, (uint32_t)m.rows));
 }
 
 template <int NW, int WNF, int SUP, bool SPLIT, bool XF32>
@@ -1013,6 +1029,16 @@ Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows
     const bool dma = qmm_dma_ok(m, x_dtype);
     const QmmPlan p = qmm_plan(m, rows, num_cus, dma);
     const bool xf32 = x_dtype == JH_F32;
+    char* ws = static_cast<char*>(workspace);
+    if (p.wreg && p.lead > 0 && xf32) {
+        // the LDS-ring tile reads bf16 X: round fp32 X into the workspace first
+        if (!ws) return Status::fail(JH_ERR_INVALID, "qmm: fp32 x needs a workspace");
+        const int64_t n4 = rows * m.in / 4;  // in is a multiple of 256
+        hipLaunchKernelGGL(x_to_bf16_kernel, dim3((unsigned)std::min<int64_t>((n4 + 255) / 256, 4096)), dim3(256), 0,
+                           st, static_cast<const float4*>(x), n4, reinterpret_cast<uint2*>(ws));
+        x = ws;
+        ws += qmm_xconv_bytes(rows, m.in);
+    }
     auto tile = [&](auto split_c, float* acc) {
         constexpr bool SPLIT = decltype(split_c)::value;
         if (p.wreg && p.lead > 0 && p.rb == 256) {
@@ -1058,7 +1084,7 @@ Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows
     }
     // split K: each K range stores its fp32 partial tile into its own slice of
     // the workspace, and one pass adds the slices in order into y
-    float* acc = static_cast<float*>(workspace);
+    float* acc = reinterpret_cast<float*>(ws);
     if (!acc) return Status::fail(JH_ERR_INVALID, "qmm: split-K needs a workspace");
     const int64_t n = rows * m.rows;
     tile(std::true_type{}, acc);

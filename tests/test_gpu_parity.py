@@ -291,18 +291,23 @@ def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
     (24, 24576, 4096, 128, "f32", False, F32),     # 32 rows, 4 waves, K whole, group 128
     (50, 6144, 4096, 32, "bf16", False, F32),      # 64 rows, 4 waves, K split 4, group 32
     (48, 9000, 4096, 64, "bf16", False, BF16),     # 64 rows, 8 waves, K split 4, N ragged
-    # fp32 x: the register tile (waves, K split)
-    (1000, 6000, 1024, 128, "f32", True, F32),     # 6 waves, fp32 x and scales
-    (300, 2784, 2048, 64, "bf16", True, F32),      # 6 waves, K split 4, fp32 out
-    (1100, 3000, 2048, 64, "bf16", True, BF16),    # 4 waves, K whole
-    (2048, 4096, 12288, 64, "bf16", True, F32),    # 8 waves, K whole
+    # fp32 x: rounded to bf16 into the workspace, then the LDS-ring tile
+    (700, 12288, 4096, 64, "bf16", True, BF16),    # 256-row blocks
+    (128, 4096, 12288, 64, "f16", True, F32),      # 4 waves lead 3, K split 8
+    (9, 12288, 4096, 64, "bf16", True, F32),       # 32-row blocks, K split 4
+    # group 128 with bf16/f16 scales (scales in half dwords): the register tile (waves, K split)
+    (1000, 6000, 1024, 128, "bf16", True, F32),    # 6 waves, fp32 x
+    (300, 2784, 2048, 128, "f16", False, F32),     # 6 waves, K split 4
+    (1100, 3000, 2048, 128, "bf16", True, BF16),   # 4 waves, K whole
+    (2048, 4096, 12288, 128, "bf16", False, F32),  # 8 waves, K whole
 ])
 def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
     """Every tile/split pair the prefill planner picks on a 256-CU MI355X (the
-    LDS-ring tile in its four 128-row shapes and its 32/64/256-row blocks for bf16 x,
-    the register tile with 4/6/8 waves for fp32 x; K whole or split, ragged M
-    and N, bf16/f16/fp32 scales, group sizes 32/64/128 and both outputs): the
-    oracle on a random block of up to 48x96 of the output."""
+    LDS-ring tile in its four 128-row shapes and its 32/64/256-row blocks, for
+    bf16 x and for fp32 x rounded into the workspace; the register tile with
+    4/6/8 waves where the scales do not fill whole dwords; K whole or split,
+    ragged M and N, bf16/f16/fp32 scales, group sizes 32/64/128 and both
+    outputs): the oracle on a random block of up to 48x96 of the output."""
     q = synth.quant_linear(9000 + m + n, n, k, gs)
     xb, x = synth.activations(9500 + m, (m, k))
     w = hip.FromRaw(U32, q.w, *q.w.shape)
@@ -327,26 +332,22 @@ def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
 
 
 @pytest.mark.parametrize("m,n,k,gs,sb", [
-    (2048, 12288, 4096, 64, "bf16"),  # LDS ring 8 waves lead 3 / register 8 waves, K whole
-    (300, 2784, 2048, 64, "f16"),     # 8 waves lead 2 / 6 waves, K split 4
-    (1000, 6000, 1024, 32, "bf16"),   # 8 waves lead 2 / 6 waves, K whole, group 32
-    (128, 4096, 12288, 64, "f32"),    # 4 waves lead 3 / 4 waves, K split 8
-    (77, 1000, 4096, 64, "bf16"),     # 4 waves lead 1 / 4 waves, K split 8, ragged
-    (1000, 2000, 1024, 128, "f32"),   # 4 waves lead 3 / 4 waves, group 128
-    (9, 12288, 4096, 64, "bf16"),     # 32-row blocks, 8 waves / 6 waves, K split 4
-    (33, 12288, 4096, 32, "f16"),     # 64-row blocks, 8 waves / 6 waves, K split 4
-    (20, 4096, 12288, 64, "bf16"),    # 32-row blocks, 4 waves / 4 waves, K split 8
-    (60, 4096, 4096, 64, "f32"),      # 64-row blocks, 4 waves / 4 waves, K split 8
-    (40, 3000, 2048, 64, "bf16"),     # 32-row blocks, 4 waves / 4 waves, K split 4, N ragged
-    (1024, 12288, 4096, 64, "bf16"),  # 256-row blocks / 6 waves, K whole
-    (1300, 6000, 2048, 32, "f16"),    # 256-row blocks / 6 waves, K whole, M ragged
-    (768, 4096, 12288, 64, "f32"),    # 256-row blocks / 4 waves, K split 4
+    (2048, 12288, 4096, 64, "bf16"),  # 8 waves lead 3, K whole
+    (300, 2784, 2048, 64, "f16"),     # 8 waves lead 2, K split 4
+    (1000, 6000, 1024, 32, "bf16"),   # 8 waves lead 2, K whole, group 32
+    (128, 4096, 12288, 64, "f32"),    # 4 waves lead 3, K split 8
+    (77, 1000, 4096, 64, "bf16"),     # 4 waves lead 1, K split 8, ragged
+    (1000, 2000, 1024, 128, "f32"),   # 4 waves lead 3, group 128
+    (9, 12288, 4096, 64, "bf16"),     # 32-row blocks, K split 4
+    (33, 12288, 4096, 32, "f16"),     # 64-row blocks, K split 4
+    (1024, 12288, 4096, 64, "bf16"),  # 256-row blocks, K whole
+    (1300, 6000, 2048, 128, "bf16"),  # register tile (group 128, bf16 scales), M ragged
+    (300, 2784, 2048, 128, "f16"),    # register tile, K split 4
 ])
 def test_qmm_bf16_x_matches_fp32_x(hip, m, n, k, gs, sb):
-    """The LDS-ring tile (bf16 x) against the register tile (the same x widened
-    to fp32): the same K permutation, dequantization and MFMA order, so with the
-    same K split (the planner splits these shapes alike for both tiles) the
-    outputs are the same bits."""
+    """bf16 x against the same values widened to fp32 (rounded back to bf16 in
+    the workspace before the LDS-ring tile; with group 128 and bf16/f16 scales,
+    the register tile, which rounds x on its way to LDS): the same bits."""
     q = synth.quant_linear(9900 + m + n, n, k, gs)
     xb, x = synth.activations(9950 + m, (m, k))
     w = hip.FromRaw(U32, q.w, *q.w.shape)
