@@ -2,11 +2,12 @@
 //   Y[M, N] = X[M, K] . W^T.
 // Three tiles share the MFMA layout below. K divisible by 256 takes a 128-row
 // tile whose waves dequantize their own weight words into B fragments in
-// registers: qmm_dma_kernel for bf16 X (X tiles, weight words and scales staged
-// through LDS rings by loads with an LDS destination, several steps ahead) and
-// qmm_wreg_kernel for fp32 X (weights prefetched in registers, X converted on its
-// way to LDS). Other K take qmm_mfma_kernel, described next, which dequantizes W
-// tile by tile into LDS as bf16.
+// registers: qmm_dma_kernel (X tiles, weight words and scales staged through
+// LDS rings by loads with an LDS destination, several steps ahead; fp32 X is
+// rounded to bf16 into the workspace first) and, where a lane's scales of a
+// super-step do not fill whole dwords, qmm_wreg_kernel (weights prefetched in
+// registers, X rounded on its way to LDS). Other K take qmm_mfma_kernel,
+// described next, which dequantizes W tile by tile into LDS as bf16.
 //
 // Reference semantics: QuantMatmul with rows > 1 (cpu/cpu_misc.go:378-399),
 // which dequantizes a weight row once (wbuf = q*scale + bias) and dots it with
@@ -802,11 +803,11 @@ constexpr int kBM = BM, kBN = BN;  // the LDS tile
 
 // How one prefill product is launched. K divisible by 256 takes a tile of
 // 32·waves columns of Y per block with K split 1, 2, 4 or 8 ways; each K range
-// stores its fp32 partial tile, and one pass sums them in order. bf16 X (with
-// scales in whole dwords per lane) takes the LDS-ring tile: up to 64 rows in
+// stores its fp32 partial tile, and one pass sums them in order. With scales in
+// whole dwords per lane, X (fp32 X rounded to bf16 first) takes the LDS-ring tile: up to 64 rows in
 // 32- or 64-row blocks; beyond, 128-row blocks of 4 waves with a lead of 1 step
 // (two blocks per CU) or 3 steps (one), or of 8 waves with a lead of 2 or 3,
-// and from 256 rows also 256-row blocks of 8 waves with a lead of 1. fp32 X takes
+// and from 256 rows also 256-row blocks of 8 waves with a lead of 1. Otherwise
 // the 128-row register tile with 4, 6 or 8 waves. The plan is the one with the
 // least modelled time: the busiest CU's blocks, each costing a fixed start plus
 // its columns x K super-steps at the CU's measured rate for that shape, plus a
