@@ -331,6 +331,34 @@ def test_qmm_planner_tiles(hip, oracle, m, n, k, gs, sb, xf32, out_dtype):
     assert ok, (d, sc)
 
 
+@pytest.mark.parametrize("m,n,k", [
+    (64, 1000, 2048),    # 32-row blocks (two), K split 4, N ragged
+    (63, 5000, 4096),    # one 64-row block with its last row empty
+    (65, 5000, 4096),    # 128-row blocks from 65 rows: 4 waves lead 1, K split 8
+    (129, 5000, 4096),   # two 128-row blocks, the second with one row
+    (257, 12288, 4096),  # three 128-row blocks, the third with one row
+    (769, 12288, 4096),  # four 256-row blocks, the fourth with one row
+])
+def test_qmm_row_block_edges(hip, oracle, m, n, k):
+    """Row counts around the planner's block-size changes (32/64 up to 64
+    rows, 128 beyond, 256 from 256 rows) and blocks holding a single row: the
+    oracle on the rows next to each block edge and the last row and column."""
+    q = synth.quant_linear(9700 + m + n, n, k, 64)
+    xb, x = synth.activations(9750 + m, (m, k))
+    w, s, b = upload_quant(hip, q)
+    step(f"jh_quant_matmul row-block edges M={m} N={n} K={k}")
+    y = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, m, k), w, s, b, True, 64, 4, out_dtype=F32))
+    edges = {0, m - 1}
+    for e in (32, 64, 128, 256, 512, 768):
+        edges.update(r for r in (e - 1, e) if r < m)
+    rs = np.array(sorted(edges))
+    rng = np.random.default_rng(m + n)
+    cs = np.sort(np.concatenate([rng.choice(n - 1, size=63, replace=False), [n - 1]]))
+    want = oracle.quant_matmul(x[rs], q.w[cs], q.s[cs], q.b[cs], 64)
+    ok, d, sc = rel_ok(y[np.ix_(rs, cs)], want, 5e-3)
+    assert ok, (d, sc)
+
+
 @pytest.mark.parametrize("m,n,k,gs,sb", [
     (2048, 12288, 4096, 64, "bf16"),  # 8 waves lead 3, K whole
     (300, 2784, 2048, 64, "f16"),     # 8 waves lead 2, K split 4
