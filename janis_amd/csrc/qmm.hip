@@ -619,6 +619,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t m0) {
     asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(m0) : "memory");
 }
+// The same with a wave-uniform part of the offset in soff; the range check
+// applies to voff, which carries the row, so rows past the buffer still read 0.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint32_t m0) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r),
+                 "s"(__builtin_amdgcn_readfirstlane(soff)), "{m0}"(m0)
+                 : "memory");
+}
 // 4 bytes per lane into LDS at m0 + 4 * lane.
 __device__ __forceinline__ void lds_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t m0) {
     asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(m0) : "memory");
@@ -639,12 +646,13 @@ constexpr int dma_sb_dwords() {
 
 // Loads a wave issues after those of step t (t % SPS = u): they were issued at
 // step t - A, and steps t - A + v (v = 1 .. A-1) issue the loads of step t + v:
-// NX X loads, one weight load, and 2·NSB scale/bias loads when t + v starts a
-// super-step. (Step t's own scales were issued no later than its X and weights.)
+// NX X loads, and when t + v starts a super-step its 4 weight loads and 2·NSB
+// scale/bias loads. (Step t's own weights and scales were issued no later than
+// its X.)
 template <int A, int NX, int NSB, int SPS>
 constexpr int dma_loads_after(int u) {
     int n = 0;
-    for (int v = 1; v < A; v++) n += NX + 1 + (((u + v) % SPS) == 0 ? 2 * NSB : 0);
+    for (int v = 1; v < A; v++) n += NX + (((u + v) % SPS) == 0 ? 4 + 2 * NSB : 0);
     return n;
 }
 
@@ -664,13 +672,13 @@ __global__ __launch_bounds__(64 * NW, RB == 256 ? 1 : 2) void qmm_dma_kernel(
     constexpr int XT = RB * ROW_BYTES;          // X tile per K step
     constexpr int XQ = XT / 1024;               // 1 KiB loads per X tile (8 rows each)
     constexpr int NX = (XQ + NW - 1) / NW;      // X loads per wave per step
-    constexpr int WSLOT = NW * 1024;            // weight words of one step, all waves
+    constexpr int WSLOT = NW * 4096;            // weight words of one super-step, all waves
     constexpr int SBW = 2 * NSB * 256;          // one wave's scales + biases of a super-step
     constexpr int JUNK = NX * NW > XQ ? 1024 : 0;  // target of the filler loads that even out the count
-    __shared__ __attribute__((aligned(16))) uint8_t lds[R * XT + R * WSLOT + 2 * NW * SBW + JUNK];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[R * XT + 2 * WSLOT + 2 * NW * SBW + JUNK];
     uint8_t* const xring = lds;
-    uint8_t* const wring = lds + R * XT;
-    uint8_t* const sbring = wring + R * WSLOT;
+    uint8_t* const wring = lds + R * XT;  // two super-step slots
+    uint8_t* const sbring = wring + 2 * WSLOT;
     uint8_t* const junk = sbring + 2 * NW * SBW;
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -707,13 +715,21 @@ __global__ __launch_bounds__(64 * NW, RB == 256 ? 1 : 2) void qmm_dma_kernel(
             const int q = wave + NW * i;
             const int qs = q < XQ ? q : q - XQ;  // a filler repeats a real load into junk
             const int r = 8 * qs + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
-            const uint32_t kc = k0 + (SUP / 2) * (c >> 2) + 32 * t + 8 * (c & 3);
-            lds_load16(rx, ((m0 + r) * K + kc) * 2, lds_addr(q < XQ ? xring + slot * XT + 1024 * q : junk));
+            const uint32_t kc = (SUP / 2) * (c >> 2) + 8 * (c & 3);
+            lds_load16(rx, ((m0 + r) * K + kc) * 2, (k0 + 32 * t) * 2,
+                       lds_addr(q < XQ ? xring + slot * XT + 1024 * q : junk));
         }
-        // weights: words 16h + 4t .. +3 of column n0 + c32's super-step segment
-        lds_load16(rw, ((n0 + c32) * P + (k0 >> 3) + 16 * h + 4 * t) * 4,
-                   lds_addr(wring + slot * WSLOT + 1024 * wave));
-        if (t == 0) {  // the super-step's scales and biases
+        if (t == 0) {  // the super-step's weights, scales and biases
+            // weights: the 128-byte super-step segments of the wave's 32 columns as
+            // whole lines, load i holding rows 8i .. 8i+7; 16-byte chunk c of row r
+            // sits at position c ^ (r % 8), so that the step's reads (chunk 4h + t
+            // of row c32 by lane (h, c32)) spread over the banks
+            uint8_t* const wbase = wring + ((s / SPS) & 1) * WSLOT + 4096 * wave;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = 8 * i + (lane >> 3), c = (lane & 7) ^ (r & 7);
+                lds_load16(rw, ((n0 + r) * P + 4 * c) * 4, (k0 >> 3) * 4, lds_addr(wbase + 1024 * i));
+            }
             uint8_t* const base = sbring + (((s / SPS) & 1) * NW + wave) * SBW;
             const uint32_t off = ((n0 + c32) * G + ((k0 + (SUP / 2) * h) >> GSL)) * SBB;
 #pragma unroll
@@ -725,7 +741,8 @@ __global__ __launch_bounds__(64 * NW, RB == 256 ? 1 : 2) void qmm_dma_kernel(
     auto compute = [&](int s) {
         const int slot = s % R, t = s % SPS;
         const uint8_t* const xs = xring + slot * XT;
-        const uint4 wq = *reinterpret_cast<const uint4*>(wring + slot * WSLOT + 1024 * wave + 16 * lane);
+        const uint4 wq = *reinterpret_cast<const uint4*>(wring + ((s / SPS) & 1) * WSLOT + 4096 * wave + 128 * c32 +
+                                                          16 * ((4 * h + t) ^ (c32 & 7)));
         const uint8_t* const sbb = sbring + (((s / SPS) & 1) * NW + wave) * SBW;
         uint32_t sw[NSB], bw[NSB];
 #pragma unroll
