@@ -722,12 +722,12 @@ __global__ __launch_bounds__(64 * NW, RB == 256 ? 1 : 2) void qmm_dma_kernel(
         if (t == 0) {  // the super-step's weights, scales and biases
             // weights: the 128-byte super-step segments of the wave's 32 columns as
             // whole lines, load i holding rows 8i .. 8i+7; 16-byte chunk c of row r
-            // sits at position c ^ (r % 8), so that the step's reads (chunk 4h + t
-            // of row c32 by lane (h, c32)) spread over the banks
+            // sits at position c ^ ((r/2) % 8), so that the step's reads (chunk
+            // 4h + t of row c32 by lane (h, c32)) spread over the banks
             uint8_t* const wbase = wring + ((s / SPS) & 1) * WSLOT + 4096 * wave;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int r = 8 * i + (lane >> 3), c = (lane & 7) ^ (r & 7);
+                const int r = 8 * i + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
                 lds_load16(rw, ((n0 + r) * P + 4 * c) * 4, (k0 >> 3) * 4, lds_addr(wbase + 1024 * i));
             }
             uint8_t* const base = sbring + (((s / SPS) & 1) * NW + wave) * SBW;
@@ -742,7 +742,7 @@ __global__ __launch_bounds__(64 * NW, RB == 256 ? 1 : 2) void qmm_dma_kernel(
         const int slot = s % R, t = s % SPS;
         const uint8_t* const xs = xring + slot * XT;
         const uint4 wq = *reinterpret_cast<const uint4*>(wring + ((s / SPS) & 1) * WSLOT + 4096 * wave + 128 * c32 +
-                                                          16 * ((4 * h + t) ^ (c32 & 7)));
+                                                          16 * ((4 * h + t) ^ ((c32 >> 1) & 7)));
         const uint8_t* const sbb = sbring + (((s / SPS) & 1) * NW + wave) * SBW;
         uint32_t sw[NSB], bw[NSB];
 #pragma unroll
