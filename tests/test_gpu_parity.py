@@ -285,6 +285,8 @@ def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
     (768, 4096, 12288, 64, "f16", False, BF16),    # 256-row blocks, K split 4
     (1300, 6000, 2048, 64, "f32", False, F32),     # 256-row blocks, M ragged (5.08 blocks), fp32 scales
     (1000, 9000, 4096, 32, "bf16", False, BF16),   # 256-row blocks, N ragged, group 32
+    (500, 12288, 4096, 32, "f32", False, F32),     # 8 waves lead 3 with 4 dwords of scales per lane: 160 KiB of LDS
+    (1024, 12288, 4096, 32, "f32", False, BF16),   # 256-row blocks with 4 dwords of scales per lane: 160 KiB
     # up to 64 rows of bf16 x: 32- or 64-row blocks of the LDS-ring tile
     (9, 12288, 4096, 64, "bf16", False, F32),      # 32 rows, 8 waves, K split 4
     (20, 4096, 12288, 64, "f16", False, BF16),     # 32 rows, 4 waves, K split 8
