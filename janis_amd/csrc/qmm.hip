@@ -823,17 +823,17 @@ constexpr int kBM = BM, kBN = BN;  // the LDS tile
 // stores its fp32 partial tile, and one pass sums them in order. With scales in
 // whole dwords per lane, X (fp32 X rounded to bf16 first) takes the LDS-ring tile: up to 64 rows in
 // 32- or 64-row blocks; beyond, 128-row blocks of 4 waves with a lead of 1 step
-// (two blocks per CU) or 3 steps (one), or of 8 waves with a lead of 2 or 3,
-// and from 256 rows also 256-row blocks of 8 waves with a lead of 1. Otherwise
+// (two blocks per CU) or 3 steps (one), or of 8 waves with a lead of 3, and
+// from 256 rows also 256-row blocks of 8 waves with a lead of 1. Otherwise
 // the 128-row register tile with 4, 6 or 8 waves. The plan is the one with the
 // least modelled time: the busiest CU's blocks, each costing a fixed start plus
 // its columns x K super-steps at the CU's measured rate for that shape, plus a
 // fixed and a per-element cost of the split (partial stores, the summing
 // pass). The constants are least-squares fits to timed plans of the Qwen3-8B
 // projections (N x K = 12288/6144/4096 x 4096, 4096 x 12288) on MI355X: for the
-// LDS-ring tile at M = 128 .. 2048 7.1 % rms over 616 plans, the fitted choices
-// taking 2407 us summed over 32 cases against 2375 us for the best plan of each
-// (2505 us without the 256-row blocks); at M = 9 .. 64 5.6 % rms, 250.7 against
+// LDS-ring tile at M = 128 .. 2048 6.6 % rms over 532 plans, the fitted choices
+// taking 2364 us summed over 32 cases against 2361 us for the best plan of each
+// (2436 us without the 256-row blocks); at M = 9 .. 64 5.6 % rms, 250.7 against
 // 244.9 us over 16 cases; for the register tile 4.8 % rms over 320 plans, 3079
 // against 3075 us over 32 cases. Other K (multiples of 64) take the LDS tile.
 struct QmmPlan {
@@ -849,8 +849,8 @@ struct QmmPlan {
 // Modelled microseconds of one LDS-ring plan (see above).
 double qmm_dma_cost(int64_t M, int64_t N, int64_t nsup, int nw, int lead, int rb, int64_t split, int num_cus) {
     // the summing launch: fixed µs and µs per 10^6 partial sums (each table's own fit)
-    const double kSplitFixed = rb < 128 ? 4.51 : 4.74;
-    const double kSplitElem = rb < 128 ? 1.075 : 1.154;
+    const double kSplitFixed = rb < 128 ? 4.51 : 3.71;
+    const double kSplitElem = rb < 128 ? 1.075 : 1.017;
     const int64_t rbn = 32 * nw, mt = (M + rb - 1) / rb;
     const int64_t blocks = ((N + rbn - 1) / rbn) * mt * split;
     const int64_t per_cu = (blocks + num_cus - 1) / num_cus;
@@ -865,15 +865,13 @@ double qmm_dma_cost(int64_t M, int64_t N, int64_t nsup, int nw, int lead, int rb
     else if (rb == 64)
         t = nw == 4 ? pairs(95.2, 82.2, 3.22) : (double)per_cu * (u / 106.2 + 2.99);
     else if (rb == 256)
-        t = (double)per_cu * (u / 46.6 + 4.82);
+        t = (double)per_cu * (u / 47.1 + 7.87);
     else if (nw == 4 && lead == 1)
-        t = pairs(60.5, 45.5, 0.76);
+        t = pairs(65.2, 51.3, 3.50);
     else if (nw == 4)
-        t = (double)per_cu * (u / 55.7 + 2.38);
-    else if (lead == 2)
-        t = (double)per_cu * (u / 65.4 + 0.78);
+        t = (double)per_cu * (u / 57.7 + 3.28);
     else
-        t = (double)per_cu * (u / 74.9 + 3.61);
+        t = (double)per_cu * (u / 75.4 + 5.15);
     if (split > 1) t += kSplitFixed + kSplitElem * (double)(M * N * split) * 1e-6;
     return t;
 }
@@ -909,12 +907,12 @@ QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus, bool dma) {
         p.rb = RBM;
         if (dma) {
             // waves, lead, rows per block: 32/64-row blocks up to 64 rows, 128-row
-            // blocks beyond, and 256-row blocks from 256 rows (a lead of 2 at 256 rows was
-            // never the modelled best over the shapes the fit covers)
+            // blocks beyond, and 256-row blocks from 256 rows (8 waves with a lead
+            // of 2 were never the modelled best over the shapes the fit covers)
             static constexpr int kSmall[4][3] = {{4, 3, 32}, {8, 3, 32}, {4, 2, 64}, {8, 2, 64}};
-            static constexpr int kShapes[5][3] = {{8, 3, 128}, {8, 2, 128}, {4, 3, 128}, {4, 1, 128}, {8, 1, 256}};
+            static constexpr int kShapes[4][3] = {{8, 3, 128}, {4, 3, 128}, {4, 1, 128}, {8, 1, 256}};
             const int(*tab)[3] = rows <= 64 ? kSmall : kShapes;
-            const int nshapes = rows <= 64 ? 4 : rows >= 256 ? 5 : 4;
+            const int nshapes = rows <= 64 ? 4 : rows >= 256 ? 4 : 3;
             for (int i = 0; i < nshapes; i++) {
                 const int nw = tab[i][0], lead = tab[i][1], rb = tab[i][2];
                 for (int64_t split = 1; split <= (nw == 4 ? 8 : 4) && (split == 1 || nsup / split >= 2); split *= 2) {
@@ -1072,10 +1070,8 @@ Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows
             else
                 launch_tile_dma<4, 2, SPLIT, 64>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
         } else if (p.wreg && p.lead > 0) {
-            if (p.nw == 8 && p.lead == 3)
+            if (p.nw == 8)
                 launch_tile_dma<8, 3, SPLIT>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
-            else if (p.nw == 8)
-                launch_tile_dma<8, 2, SPLIT>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
             else if (p.lead == 3)
                 launch_tile_dma<4, 3, SPLIT>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st);
             else

@@ -273,12 +273,13 @@ def test_qmm_prefill_shapes(hip, oracle, m, name, n, k):
     # bf16 x: the LDS-ring tile (waves, steps of lead, K split)
     (500, 12288, 4096, 64, "bf16", False, BF16),   # 8 waves lead 3, K whole, M ragged
     (640, 8000, 2048, 32, "f16", False, BF16),     # 8 waves lead 3, N ragged (8000 = 31.25 tiles of 256)
-    (300, 2784, 2048, 64, "bf16", False, BF16),    # 8 waves lead 2, K split 4, bf16 out via the fp32 buffer
-    (128, 12288, 4096, 32, "f32", False, F32),     # 8 waves lead 2, K split 4, 4 dwords of scales per lane
+    (300, 2784, 2048, 64, "bf16", False, BF16),    # 4 waves lead 3, K split 2, bf16 out via the fp32 buffer
+    (128, 12288, 4096, 32, "f32", False, F32),     # 4 waves lead 3, K split 2, 4 dwords of scales per lane
     (384, 6144, 4096, 64, "f16", False, F32),      # qkv at M=384: 4 waves lead 3, K whole
     (260, 9000, 4096, 64, "bf16", False, BF16),    # 4 waves lead 3, M ragged
     (128, 4096, 12288, 64, "f16", False, BF16),    # down at M=128: 4 waves lead 3, K split 8
-    (77, 1000, 4096, 64, "bf16", False, F32),      # 4 waves lead 1, K split 8, M and N ragged
+    (77, 1000, 4096, 64, "bf16", False, F32),      # 4 waves lead 3, K split 8, M and N ragged
+    (96, 6144, 12288, 64, "bf16", False, F32),     # 4 waves lead 1 (two blocks per CU), K split 8
     (1000, 2000, 1024, 128, "f32", False, BF16),   # group 128 with fp32 scales: 4 waves lead 3
     (1536, 4096, 12288, 64, "bf16", False, BF16),  # down at M=1536: 256-row blocks, 8 waves lead 1, K split 2
     (1024, 12288, 4096, 64, "bf16", False, F32),   # 256-row blocks, K whole
@@ -363,10 +364,10 @@ def test_qmm_row_block_edges(hip, oracle, m, n, k):
 
 @pytest.mark.parametrize("m,n,k,gs,sb", [
     (2048, 12288, 4096, 64, "bf16"),  # 8 waves lead 3, K whole
-    (300, 2784, 2048, 64, "f16"),     # 8 waves lead 2, K split 4
-    (1000, 6000, 1024, 32, "bf16"),   # 8 waves lead 2, K whole, group 32
+    (300, 2784, 2048, 64, "f16"),     # 4 waves lead 3, K split 2
+    (1000, 6000, 1024, 32, "bf16"),   # 8 waves lead 3, K whole, group 32
     (128, 4096, 12288, 64, "f32"),    # 4 waves lead 3, K split 8
-    (77, 1000, 4096, 64, "bf16"),     # 4 waves lead 1, K split 8, ragged
+    (96, 6144, 12288, 64, "bf16"),    # 4 waves lead 1, K split 8
     (1000, 2000, 1024, 128, "f32"),   # 4 waves lead 3, group 128
     (9, 12288, 4096, 64, "bf16"),     # 32-row blocks, K split 4
     (33, 12288, 4096, 32, "f16"),     # 64-row blocks, K split 4
