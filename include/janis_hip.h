@@ -61,7 +61,9 @@ enum {
     JH_ERR_UNSUPPORTED = 2, /* valid for the reference, not implemented here */
     JH_ERR_HIP = 3,         /* the HIP runtime reported an error */
     JH_ERR_OOM = 4,         /* device allocation failed */
-    JH_ERR_NONFINITE = 5    /* value checks on (JH_CHECK_VALUES): the result holds NaN/Inf */
+    JH_ERR_NONFINITE = 5,   /* value checks on (JH_CHECK_VALUES): the result holds NaN/Inf */
+    JH_ERR_TIMEOUT = 6      /* a jh_qkv_attention_decode launch gave up waiting for its own blocks
+                               (reported by the next jh_sync / jh_d2h / fused call; see there) */
 };
 
 typedef struct jh_ctx jh_ctx;
@@ -88,8 +90,21 @@ JH_API const char *jh_last_error(const jh_ctx *ctx);
 JH_API int jh_device_info(jh_ctx *ctx, char *name, size_t name_len, int *compute_units);
 
 /* Enqueue on a caller-owned hipStream_t instead of the context's own stream
- * (NULL restores the context's stream). The caller keeps the stream alive. */
+ * (NULL restores the context's stream). The caller keeps the stream alive.
+ * The attention merges inside one launch (jh_attention_decode,
+ * jh_qkv_attention_decode) need workgroups dealt to the 8 XCDs round-robin,
+ * which jh_create checks; a stream whose CU mask leaves any CU out
+ * (hipExtStreamCreateWithCUMask) runs them as separate launches instead. */
 JH_API int jh_set_stream(jh_ctx *ctx, void *hip_stream);
+
+/* Bound on the in-kernel wait of jh_qkv_attention_decode's attention blocks
+ * for the product blocks of their XCD, in polls of the arrival flags (default
+ * 2^22, far beyond a normal wait of about a microsecond). When a wait gives up
+ * the call's attention output is NaN and the next jh_sync / jh_d2h (or fused
+ * call) returns JH_ERR_TIMEOUT and resets the synchronisation state. 0 makes
+ * every wait give up at once: the failure path, for tests. No counterpart in
+ * the reference: a safety bound of this backend's fused launch. */
+JH_API int jh_set_wait_limit(jh_ctx *ctx, int64_t polls);
 
 /* The hipStream_t operators are enqueued on. */
 JH_API void *jh_get_stream(const jh_ctx *ctx);
@@ -122,7 +137,9 @@ JH_API int jh_set_checks(jh_ctx *ctx, int flags);
 JH_API int jh_check_finite(jh_ctx *ctx, const void *x, jh_dtype dtype, int64_t n, int64_t *count,
                            int64_t *first);
 
-/* Waits for every operator enqueued on the context's stream. */
+/* Waits for every operator enqueued on the context's stream. Returns
+ * JH_ERR_TIMEOUT if a jh_qkv_attention_decode launch since the last check gave
+ * up its in-kernel wait (see jh_set_wait_limit); jh_d2h does the same. */
 JH_API int jh_sync(jh_ctx *ctx);
 
 /* Device memory (hipMalloc / hipFree). jh_free(NULL) is a no-op. */
@@ -175,10 +192,14 @@ JH_API int jh_dequantize(jh_ctx *ctx, const uint32_t *w, const void *scales, con
  *   in increasing order, terms rounded then added, zero x terms skipped), so its
  *   fp32 results have the CPU backend's bits; a slow path, off the models' path.
  * x_dtype and y_dtype are JH_BF16 or JH_F32; accumulation is fp32. rows == 1
- * runs the decode GEMV; 2..8 bf16 rows (2..4 for in_features 768, 1536, 3072,
+ * runs the decode GEMV; 2..8 rows (2..4 for in_features 768, 1536, 3072,
  * 6144, 12288 and 16384) run the decode GEMV's tiles with every row's x in
  * registers, so each row's result has the bits of a one-row call; more rows
- * run the MFMA prefill GEMM. rows == 0 is a no-op.
+ * run the MFMA prefill GEMM. rows == 0 is a no-op. fp32 x (the activation type
+ * of the CPU backend, of Dequantize and of the embedding) takes the same tiles:
+ * each lane rounds its part of x to bf16 (nearest even) in registers, so an
+ * fp32-x call has the bits of a bf16-x call on bf16(x). Shapes outside the
+ * tiles run a generic kernel that multiplies fp32 x unrounded.
  * When the prefill GEMM splits K, its fp32 partial products go to the
  * context's workspace (grown to split * rows * out_features floats) and are
  * added in a fixed order: results are the same bits on every call. The GEMM
@@ -236,7 +257,9 @@ JH_API int jh_rope(jh_ctx *ctx, const void *x, jh_dtype x_dtype, int64_t rows, i
  * [B, Hk, kv_capacity, Dh] with the first Lk rows valid (a KV cache, or
  * kv_capacity == Lk for plain tensors); GQA (head h reads kv head h/(Hq/Hk));
  * causal masks keys past (Lk - Lq) + i for query row i. out [B, Hq, Lq, Dh].
- * Lq == 1 with bf16 k/v, Dh == 128 and Hq/Hk in {1,2,4,8} runs split over the
+ * k/v are JH_BF16, JH_F16 (what KVCache.Update's cast makes, qwen/cache.go:
+ * 90-93) or JH_F32. Lq == 1 with bf16 or f16 k/v, Dh == 128 and Hq/Hk in
+ * {1,2,4,8} runs split over the
  * keys (flash-decoding); other shapes a per-row kernel. */
 JH_API int jh_sdpa(jh_ctx *ctx, const void *q, jh_dtype q_dtype, const void *k, const void *v,
             jh_dtype kv_dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t Lq, int64_t Lk,
@@ -281,7 +304,10 @@ JH_API int jh_take_rows(jh_ctx *ctx, const void *table, int64_t row_bytes, int64
 
 /* KV-cache append (the KVAppender capability, engine/backend.go:56-61; the
  * reference KVCache.Update, qwen/cache.go:90): writes k_new/v_new
- * [BH, L, Dh] into rows pos .. pos+L-1 of the caches [BH, capacity, Dh]. */
+ * [BH, L, Dh] into rows pos .. pos+L-1 of the caches [BH, capacity, Dh].
+ * Caches and new rows are JH_BF16, JH_F16 or JH_F32 (converted, nearest even):
+ * KVCache.Update casts f32 keys and values to f16 on a backend that reports
+ * dtypes (qwen/cache.go:90-93). */
 JH_API int jh_kv_append(jh_ctx *ctx, void *k_cache, void *v_cache, jh_dtype cache_dtype, int64_t BH,
                  int64_t capacity, int64_t pos, const void *k_new, const void *v_new,
                  jh_dtype new_dtype, int64_t L, int64_t Dh);
@@ -313,7 +339,7 @@ JH_API int jh_qk_norm_rope_append(jh_ctx *ctx, const void *qkv, jh_dtype qkv_dty
  *   qkv       [(n_heads + 2 n_kv_heads) * 128]: q heads, then k heads, then v heads
  *   rope_cs   NULL, or jh_rope_table(128, rope_base, rope_scale, pos) (the same
  *             factors, computed once for all layers)
- *   caches    bf16 [n_kv_heads, capacity, 128]; pos < capacity
+ *   caches    bf16 or f16 [n_kv_heads, capacity, 128] (cache_dtype); pos < capacity
  *   out       [n_heads * 128] (the input of the o product)
  * head_dim must be 128, n_heads / n_kv_heads 1, 2, 4 or 8. */
 JH_API int jh_attention_decode(jh_ctx *ctx, const void *qkv, jh_dtype qkv_dtype, int64_t n_heads,
@@ -336,8 +362,14 @@ JH_API int jh_attention_decode(jh_ctx *ctx, const void *qkv, jh_dtype qkv_dtype,
  * groups of 64 with bf16 scales, the kv head h's rows are computed on XCD h and
  * its attention follows there in the same launch (workgroups are dealt to the
  * XCDs round-robin; jh_create checks this); any other call runs the two
- * operators. The fused launch keeps all its blocks resident and must not share
- * the GPU's CUs with other long-running kernels (it waits for its own blocks). */
+ * operators. The fused launch's attention blocks wait, inside the kernel, for
+ * the product blocks of their XCD; the launch is sized so that all its blocks
+ * are resident at once, so the wait ends when the GPU's CUs are free for it.
+ * Fused calls on one GPU must therefore be serialised (one stream, or calls
+ * ordered by the caller) and must not run beside kernels that hold the CUs
+ * indefinitely. The wait is bounded (jh_set_wait_limit): a wait that gives up
+ * makes the call's attention output NaN and is reported as JH_ERR_TIMEOUT by
+ * the next jh_sync, jh_d2h or fused call, never silently. */
 JH_API int jh_qkv_attention_decode(jh_ctx *ctx, const void *x, const float *norm_stats, float norm_eps,
                                    const uint32_t *w, const void *scales, const void *biases, jh_dtype sb_dtype,
                                    int64_t in_features, int group_size, int bits, void *qkv,

@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(HERE, "libjanis_hip.so")
 
 # engine.DType (engine/backend.go:11-21)
 F32, F16, BF16, I32, U32, U8 = range(6)
-JH_OK, JH_ERR_INVALID, JH_ERR_UNSUPPORTED, JH_ERR_HIP, JH_ERR_OOM, JH_ERR_NONFINITE = range(6)
+JH_OK, JH_ERR_INVALID, JH_ERR_UNSUPPORTED, JH_ERR_HIP, JH_ERR_OOM, JH_ERR_NONFINITE, JH_ERR_TIMEOUT = range(7)
 JH_CHECK_INDICES, JH_CHECK_VALUES = 1, 2  # jh_set_checks flags
 JH_SCALAR_MUL, JH_SCALAR_ADD = 0, 1  # jh_scalar_op
 JH_OP_ADD, JH_OP_MUL, JH_OP_SILU, JH_OP_SILU_MUL = range(4)  # jh_op
@@ -29,7 +29,7 @@ EXPORTS = [
     "jh_take_rows", "jh_kv_append", "jh_qk_norm_rope_append", "jh_quant_matvec_fused",
     "jh_attention_decode", "jh_rope_table", "jh_norm_prepare", "jh_copy_strided", "jh_scatter_rows",
     "jh_softmax", "jh_mean", "jh_scalar", "jh_check_finite", "jh_attention_decode_noalloc",
-    "jh_qkv_attention_decode", "jh_embed_norm_prepare",
+    "jh_qkv_attention_decode", "jh_embed_norm_prepare", "jh_set_wait_limit",
 ]
 
 _lib = None
@@ -71,6 +71,8 @@ def load() -> ctypes.CDLL:
     L.jh_get_stream.restype = p
     L.jh_set_checks.argtypes = [c_ctx, i]
     L.jh_set_checks.restype = i
+    L.jh_set_wait_limit.argtypes = [c_ctx, ctypes.c_int64]
+    L.jh_set_wait_limit.restype = i
     L.jh_sync.argtypes = [c_ctx]
     L.jh_sync.restype = i
     L.jh_alloc.argtypes = [c_ctx, ctypes.c_size_t, ctypes.POINTER(p)]

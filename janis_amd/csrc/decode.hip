@@ -46,8 +46,39 @@ __device__ __forceinline__ float word_to_f32(uint32_t w, const void* p, int64_t 
 __device__ __forceinline__ void st_act(void* p, int64_t i, float v, int dt) {
     if (dt == JH_BF16)
         static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+    else if (dt == JH_F16)
+        static_cast<uint16_t*>(p)[i] = f32_to_f16(v);
     else
         static_cast<float*>(p)[i] = v;
+}
+
+// A 16-byte row chunk of 8 bf16 or f16 values (a K/V cache row) as fp32.
+template <bool F16>
+__device__ __forceinline__ void unpack8(uint4 r, float (&f)[8]) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if constexpr (F16) {
+            f[2 * q] = f16_to_f32(static_cast<uint16_t>(w[q]));
+            f[2 * q + 1] = f16_to_f32(static_cast<uint16_t>(w[q] >> 16));
+        } else {
+            f[2 * q] = __uint_as_float(w[q] << 16);
+            f[2 * q + 1] = __uint_as_float(w[q] & 0xFFFF0000u);
+        }
+    }
+}
+
+// fp32 -> a cache element (bf16 or f16, nearest even) and back, for the new key
+// and value of a one-token attention, which score as the values the cache holds.
+template <bool F16>
+__device__ __forceinline__ uint16_t to_cache(float v) {
+    if constexpr (F16) return f32_to_f16(v);
+    else return f32_to_bf16(v);
+}
+template <bool F16>
+__device__ __forceinline__ float from_cache(uint16_t h) {
+    if constexpr (F16) return f16_to_f32(h);
+    else return bf16_to_f32(h);
 }
 
 // Sum over a block of 256 threads; every thread gets the total.
@@ -349,7 +380,7 @@ __global__ __launch_bounds__(256) void sdpa_rows_kernel(const void* __restrict__
 constexpr int kDecodeDh = 128;
 
 
-template <int G>
+template <int G, bool KF16>
 __global__ __launch_bounds__(256) void sdpa_decode_split_kernel(const void* __restrict__ q, int q_dt,
                                                                 const uint16_t* __restrict__ k,
                                                                 const uint16_t* __restrict__ v, int Hk,
@@ -393,14 +424,9 @@ __global__ __launch_bounds__(256) void sdpa_decode_split_kernel(const void* __re
             kn = *reinterpret_cast<const uint4*>(k + kbase + (int64_t)(j + 16) * Dh + 8 * kl);
             vn = *reinterpret_cast<const uint4*>(v + kbase + (int64_t)(j + 16) * Dh + 8 * kl);
         }
-        const float kf[8] = {__uint_as_float(kr.x << 16), __uint_as_float(kr.x & 0xFFFF0000u),
-                             __uint_as_float(kr.y << 16), __uint_as_float(kr.y & 0xFFFF0000u),
-                             __uint_as_float(kr.z << 16), __uint_as_float(kr.z & 0xFFFF0000u),
-                             __uint_as_float(kr.w << 16), __uint_as_float(kr.w & 0xFFFF0000u)};
-        const float vf[8] = {__uint_as_float(vr.x << 16), __uint_as_float(vr.x & 0xFFFF0000u),
-                             __uint_as_float(vr.y << 16), __uint_as_float(vr.y & 0xFFFF0000u),
-                             __uint_as_float(vr.z << 16), __uint_as_float(vr.z & 0xFFFF0000u),
-                             __uint_as_float(vr.w << 16), __uint_as_float(vr.w & 0xFFFF0000u)};
+        float kf[8], vf[8];
+        unpack8<KF16>(kr, kf);
+        unpack8<KF16>(vr, vf);
 #pragma unroll
         for (int g = 0; g < G; g++) {
             float s = 0.0f;
@@ -520,7 +546,11 @@ __global__ __launch_bounds__(128 * kMergeGroups) void sdpa_decode_merge_kernel(c
 
 // Per-head RMSNorm of one 128-feature head held as lane i: (a, b) = features
 // (i, i + 64) of a wave, with the lane's weights (w0, w1) = (w[i], w[i + 64]).
+// Contraction into FMAs is off in these helpers: the kernels that share them
+// (the standalone q/k norm + RoPE + append, the one-launch attention) then store
+// the same bits for a new key, which an f16 cache keeps to 11 bits.
 __device__ __forceinline__ void head_rms_norm_w(float& a, float& b, float w0, float w1, float eps) {
+#pragma clang fp contract(off)
     const float ss = wave_sum(fmaf(a, a, b * b));
     const float inv = 1.0f / (float)sqrt((double)(ss / 128.0f + eps));
     a = (a * inv) * w0;
@@ -543,6 +573,7 @@ __device__ __forceinline__ void head_rope_factors(float base, float scale, int64
 }
 
 __device__ __forceinline__ void rotate_pair(float& a, float& b, float c, float sn) {
+#pragma clang fp contract(off)
     const float ra = a * c - b * sn, rb = a * sn + b * c;
     a = ra;
     b = rb;
@@ -643,7 +674,7 @@ struct AttnArgs {
     float eps, base, rscale, scale;
     const float* rope_cs;  // [128]: cos, sin at pos (rope_table_kernel), or nullptr
     int64_t pos;
-    uint16_t* kc;       // bf16 [Hk, cap, 128]
+    uint16_t* kc;       // bf16 or f16 [Hk, cap, 128]
     uint16_t* vc;
     int64_t cap;
     int Hk, nsplit, kps;
@@ -655,6 +686,8 @@ struct AttnArgs {
     int* flags;         // fused q/k/v + attention launch: this XCD's arrival flags, cleared by its
                         // last attention block; nullptr otherwise
     int nflags;
+    int* marker;        // fused launch: this XCD's give-up marker (set when a wait gave up; stays set
+                        // until the host resets it), nullptr otherwise
 };
 
 // Floats of one split's partials in the in-launch merge layout: G x (max, sum,
@@ -666,8 +699,11 @@ static_assert(kDecodeDh == 128, "the in-launch merge maps 64 lanes onto G x 128 
 // One block's share of a one-token attention: split `split` of kv head hk.
 // FUSED (the q/k/v product ran earlier in the same launch, on this XCD): the
 // block's K/V rows are requested first, then wait() returns once the product's
-// rows are all stored, and q/k/v are read device-coherently from the L2.
-template <int G, int U, bool FUSED, class Wait>  // U: keys per slot per load batch
+// rows are all stored (false) or once it gave up (true), and q/k/v are read
+// device-coherently from the L2. When a wait of the XCD gave up (now or in an
+// earlier call the host has not reset), the head's output is NaN and the flags
+// are left as they are for the host to reset.
+template <int G, int U, bool FUSED, bool KF16, class Wait>  // U: keys per slot per load batch; KF16: f16 caches
 __device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, const int hk, Wait wait) {
     constexpr int Dh = 128;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -706,11 +742,12 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, co
         }
     };
     int64_t j0 = j_begin + slot;
+    bool gave_up = false;
     if constexpr (FUSED) {
         // the K/V rows do not depend on the product: in flight while it finishes
         load_rows(kr, kb, j0);
         load_rows(vr, vb, j0);
-        wait();
+        gave_up = wait();
     }
     // q/k/v words (FUSED: bf16 or f32, stored by other CUs of this XCD, read from L2)
     const bool qf32 = a.qkv_dt == JH_F32;
@@ -772,17 +809,17 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, co
         if (kn) head_rms_norm_w(k0, k1, word_to_f32(kvraw[4], kwp, lane, kw_dt),
                                 word_to_f32(kvraw[5], kwp, lane + 64, kw_dt), a.eps);
         rotate_pair(k0, k1, rc, rsn);
-        const uint16_t bk0 = f32_to_bf16(k0), bk1 = f32_to_bf16(k1);
-        const uint16_t bv0 = f32_to_bf16(v0), bv1 = f32_to_bf16(v1);
+        const uint16_t bk0 = to_cache<KF16>(k0), bk1 = to_cache<KF16>(k1);
+        const uint16_t bv0 = to_cache<KF16>(v0), bv1 = to_cache<KF16>(v1);
         const int64_t row = ((int64_t)hk * a.cap + a.pos) * Dh;
         a.kc[row + lane] = bk0;
         a.kc[row + lane + 64] = bk1;
         a.vc[row + lane] = bv0;
         a.vc[row + lane + 64] = bv1;
-        kn_s[lane] = bf16_to_f32(bk0);
-        kn_s[lane + 64] = bf16_to_f32(bk1);
-        vn_s[lane] = bf16_to_f32(bv0);
-        vn_s[lane + 64] = bf16_to_f32(bv1);
+        kn_s[lane] = from_cache<KF16>(bk0);
+        kn_s[lane + 64] = from_cache<KF16>(bk1);
+        vn_s[lane] = from_cache<KF16>(bv0);
+        vn_s[lane + 64] = from_cache<KF16>(bv1);
     }
     __syncthreads();
 
@@ -800,14 +837,6 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, co
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
     }
-    auto unpack = [](uint4 r, float (&f)[8]) {
-        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            f[2 * q] = __uint_as_float(w[q] << 16);
-            f[2 * q + 1] = __uint_as_float(w[q] & 0xFFFF0000u);
-        }
-    };
     // Scores for the batch (keys unpacked one at a time), then the next batch's
     // keys are requested while the softmax and the value sums run, and its
     // values once those are done.
@@ -817,7 +846,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, co
 #pragma unroll
         for (int u = 0; u < U; u++) {
             float kf[8];
-            unpack(kr[u], kf);
+            unpack8<KF16>(kr[u], kf);
             const bool in = j0 + 16 * u < jc_end;
 #pragma unroll
             for (int g = 0; g < G; g++) {
@@ -849,7 +878,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, co
 #pragma unroll
         for (int u = 0; u < U; u++) {
             float vf[8];
-            unpack(vr[u], vf);
+            unpack8<KF16>(vr[u], vf);
 #pragma unroll
             for (int g = 0; g < G; g++)
 #pragma unroll
@@ -917,10 +946,12 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, co
 #pragma unroll
         for (int r = 0; r < PER; r++) {
             const int t = threadIdx.x + 256 * r;
-            if (t < G * Dh) st_act(a.out, (int64_t)hk * G * Dh + t, rA[r] / rL[r], a.out_dt);
+            if (t < G * Dh)
+                st_act(a.out, (int64_t)hk * G * Dh + t, gave_up ? __builtin_nanf("") : rA[r] / rL[r], a.out_dt);
         }
-        // the XCD's only attention block: every block has arrived, the call is over
-        if (FUSED)
+        // the XCD's only attention block: every block has arrived (its wait saw
+        // every flag set), the call is over
+        if (FUSED && !gave_up)
             for (int i = threadIdx.x; i < a.nflags; i += 256) a.flags[i] = 0;
         return;
     }
@@ -971,6 +1002,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, co
     // Reads are device-coherent (sc1): they miss this CU's L1, which could hold a
     // stale copy of a line another CU wrote, and are served by the shared L2.
     const auto hb = make_rsrc(a.part + (int64_t)hk * a.nsplit * REC, (uint32_t)(a.nsplit * REC * 4));
+    // whether any wait of this XCD gave up: its marker was stored before that
+    // block's arrival, so it is in the L2 by now (read with the partials)
+    const int marked = FUSED ? __hip_atomic_load(a.marker, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
     float M = -__builtin_inff(), L = 0.0f, A[VPL];
 #pragma unroll
     for (int e = 0; e < VPL; e++) A[e] = 0.0f;
@@ -1034,26 +1068,27 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, co
                 Lt = fmaf(wl[w][g], c, Lt);
                 At = fmaf(wacc[w][g][d], c, At);
             }
-            st_act(a.out, (int64_t)hk * G * Dh + t, At / Lt, a.out_dt);
+            st_act(a.out, (int64_t)hk * G * Dh + t, marked ? __builtin_nanf("") : At / Lt, a.out_dt);
         }
     }
     if (threadIdx.x == 0) {
         __hip_atomic_store(a.sync + hk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    // every block of the XCD has arrived and every attention block has passed
-    // its wait: the flags start the next call at zero
-    if (FUSED)
+    // every block of the XCD has arrived and every attention block's wait saw
+    // every flag set: the flags start the next call at zero (after a wait that
+    // gave up, a flag may still be set later, so they stay for the host's reset)
+    if (FUSED && !marked)
         for (int i = threadIdx.x; i < a.nflags; i += 256) a.flags[i] = 0;
 }
 
-template <int G, int U>
+template <int G, int U, bool KF16>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
     // 1-D grid with `sync`: block b = 8 t + x runs on XCD x and takes kv head
     // x + 8 (t / nsplit), split t % nsplit
     const int t8 = blockIdx.x >> 3;
     const int split = a.sync ? t8 % a.nsplit : blockIdx.x;
     const int hk = a.sync ? (blockIdx.x & 7) + 8 * (t8 / a.nsplit) : blockIdx.y;
-    attn_body<G, U, false>(a, split, hk, [] {});
+    attn_body<G, U, false, KF16>(a, split, hk, [] { return false; });
 }
 
 // ---- the q/k/v product and the attention of one token in one launch ----------------
@@ -1069,8 +1104,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
 // launch, whose last block clears the flags for the next call.
 // (One arrival counter per XCD, 96 atomics on one L2 line, took 3-11 us to be
 // seen by the pollers on MI355X; per-block flags, about 1 us.) Every block of the grid is resident at once
-// (the launcher sizes the grid to the occupancy), so the wait ends; its bound
-// is a safety net only.
+// (the launcher sizes the grid to the occupancy), so the wait ends. Its bound
+// (`spin` polls) is a safety net that fails loudly: a wait that gives up marks
+// its XCD, the head's output is NaN, the flags are not cleared, and `status`
+// (host memory) is set for the library to report at the next synchronisation,
+// where it resets the flags and markers. A marker left by an earlier call
+// makes this call's heads on that XCD NaN as well.
 struct QkvRows {
     uint32_t qbase, kbase, vbase, g128, nblk, past;
     __device__ uint32_t base(uint32_t blk) const {
@@ -1091,16 +1130,18 @@ struct QkvAttnArgs {
     float norm_eps;
     int gs_log2;
     int bpx;                    // blocks per XCD
+    uint32_t spin;              // polls of the flags before a wait gives up
+    int* markers;               // per XCD give-up markers (device)
+    int* status;                // set to 1 when a wait gives up (host memory the library reads)
 };
 
-constexpr uint32_t kPhaseSpin = 1u << 22;
-
-template <int G, int U>
+template <int G, int U, bool KF16>
 __global__ __launch_bounds__(256) void qkv_attn_kernel(QkvAttnArgs f) {
     const int x = blockIdx.x & 7, t = blockIdx.x >> 3;
     int* flags = f.flags + kAttnMaxBlocksPerXcd * x;
     AttnArgs a = f.a;
     a.flags = flags;
+    a.marker = f.markers + x;
     const int Hq = a.Hk * G;
     const uint32_t rows = (uint32_t)(Hq + 2 * a.Hk) * 128;
     const QkvRows map{(uint32_t)(x * G * 128), (uint32_t)((Hq + x) * 128), (uint32_t)((Hq + a.Hk + x) * 128),
@@ -1116,19 +1157,37 @@ __global__ __launch_bounds__(256) void qkv_attn_kernel(QkvAttnArgs f) {
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(flags + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t >= a.nsplit) return;
-    attn_body<G, U, true>(a, t, x, [&] {
+    attn_body<G, U, true, KF16>(a, t, x, [&]() -> bool {
+        __shared__ int bad;
         // wave 0 reads all the XCD's flags per round (device-scope atomic loads:
         // they miss the L1, and the compiler keeps them in the loop)
         if (threadIdx.x < 64) {
             const int l = threadIdx.x;
-            for (uint32_t n = 0; n < kPhaseSpin; n++) {
+            // a marker an earlier call left (not yet reset by the host)
+            const int stale = __hip_atomic_load(a.marker, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            bool seen = false;
+            for (uint32_t n = 0; n < f.spin; n++) {
                 const int f0 = l < f.bpx ? __hip_atomic_load(flags + l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1;
                 const int f1 =
                     l + 64 < f.bpx ? __hip_atomic_load(flags + l + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1;
-                if (__all(f0 == 1 && f1 == 1)) break;
+                if (__all(f0 == 1 && f1 == 1)) {
+                    seen = true;
+                    break;
+                }
+            }
+            if (l == 0) {
+                bad = !seen || stale != 0;
+                if (!seen) {
+                    // the marker reaches this XCD's L2 before the block's arrival
+                    // (the partial stores' wait covers it); the status word is
+                    // read by the host after the stream's work is done
+                    __hip_atomic_store(a.marker, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(f.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                }
             }
         }
         __syncthreads();
+        return bad != 0;
     });
 }
 
@@ -1391,7 +1450,7 @@ Status launch_rope(const void* x, int x_dt, void* out, int out_dt, int64_t rows,
 
 bool sdpa_decode_ok(int q_dt, int kv_dt, int64_t Hq, int64_t Hk, int64_t Lq, int64_t Dh) {
     const int64_t G = Hk > 0 ? Hq / Hk : 0;
-    return Lq == 1 && Dh == kDecodeDh && kv_dt == JH_BF16 && (G == 1 || G == 2 || G == 4 || G == 8) &&
+    return Lq == 1 && Dh == kDecodeDh && (kv_dt == JH_BF16 || kv_dt == JH_F16) && (G == 1 || G == 2 || G == 4 || G == 8) &&
            (q_dt == JH_BF16 || q_dt == JH_F32);
 }
 
@@ -1427,10 +1486,11 @@ Status launch_sdpa(const void* q, int q_dt, const void* k, const void* v, int kv
             hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, q, q_dt, static_cast<const uint16_t*>(k),
                                static_cast<const uint16_t*>(v), (int)Hk, (int)Lk, (int)kcap, scale, kps, part);
         };
-        if (G == 1) go(sdpa_decode_split_kernel<1>);
-        else if (G == 2) go(sdpa_decode_split_kernel<2>);
-        else if (G == 4) go(sdpa_decode_split_kernel<4>);
-        else go(sdpa_decode_split_kernel<8>);
+        const bool f16 = kv_dt == JH_F16;
+        if (G == 1) f16 ? go(sdpa_decode_split_kernel<1, true>) : go(sdpa_decode_split_kernel<1, false>);
+        else if (G == 2) f16 ? go(sdpa_decode_split_kernel<2, true>) : go(sdpa_decode_split_kernel<2, false>);
+        else if (G == 4) f16 ? go(sdpa_decode_split_kernel<4, true>) : go(sdpa_decode_split_kernel<4, false>);
+        else f16 ? go(sdpa_decode_split_kernel<8, true>) : go(sdpa_decode_split_kernel<8, false>);
         hipLaunchKernelGGL(sdpa_decode_merge_kernel, dim3((unsigned)(B * Hq)), dim3(kDecodeDh * merge_groups(nsplit)), 0, st,
                            part, (int)Hk, G,
                            (int)nsplit, out, out_dt);
@@ -1517,8 +1577,8 @@ bool qkv_attn_ok(const QuantMatrix& m, int64_t Hq, int64_t Hk, const int* sync, 
 
 Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt,
                           float eps, float base, float rscale, const float* rope_cs, int64_t pos, void* kc,
-                          void* vc, int64_t cap, float scale, void* out, int out_dt, void* workspace, int num_cus,
-                          hipStream_t st, int* sync) {
+                          void* vc, int c_dt, int64_t cap, float scale, void* out, int out_dt, void* workspace,
+                          int num_cus, hipStream_t st, int* sync) {
     const int G = Hq / Hk;
     const bool sync_ok = attn_merge_in_launch(Hk, sync);
     const AttnSplit sp = attn_split(Hk, pos, num_cus, sync_ok);
@@ -1538,10 +1598,19 @@ Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const voi
         else
             hipLaunchKernelGGL(k4, grid, dim3(256), 0, st, a);
     };
-    if (G == 1) go(attn_decode_kernel<1, 4>, attn_decode_kernel<1, 8>);
-    else if (G == 2) go(attn_decode_kernel<2, 4>, attn_decode_kernel<2, 8>);
-    else if (G == 4) go(attn_decode_kernel<4, 4>, attn_decode_kernel<4, 8>);
-    else if (G == 8) go(attn_decode_kernel<8, 4>, attn_decode_kernel<8, 8>);
+    auto go_dt = [&](auto b4, auto b8, auto h4, auto h8) { c_dt == JH_F16 ? go(h4, h8) : go(b4, b8); };
+    if (G == 1)
+        go_dt(attn_decode_kernel<1, 4, false>, attn_decode_kernel<1, 8, false>, attn_decode_kernel<1, 4, true>,
+              attn_decode_kernel<1, 8, true>);
+    else if (G == 2)
+        go_dt(attn_decode_kernel<2, 4, false>, attn_decode_kernel<2, 8, false>, attn_decode_kernel<2, 4, true>,
+              attn_decode_kernel<2, 8, true>);
+    else if (G == 4)
+        go_dt(attn_decode_kernel<4, 4, false>, attn_decode_kernel<4, 8, false>, attn_decode_kernel<4, 4, true>,
+              attn_decode_kernel<4, 8, true>);
+    else if (G == 8)
+        go_dt(attn_decode_kernel<8, 4, false>, attn_decode_kernel<8, 8, false>, attn_decode_kernel<8, 4, true>,
+              attn_decode_kernel<8, 8, true>);
     else return Status::fail(JH_ERR_UNSUPPORTED, "attention: n_heads / n_kv_heads must be 1, 2, 4 or 8");
     if (nsplit > 1 && !in_launch)
         hipLaunchKernelGGL(sdpa_decode_merge_kernel, dim3((unsigned)Hq), dim3(kDecodeDh * merge_groups(nsplit)), 0, st,
@@ -1551,8 +1620,9 @@ Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const voi
 
 Status launch_qkv_attn(const QuantMatrix& m, const uint16_t* x, float* stats, float norm_eps, void* qkv, int qkv_dt,
                        int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt, float eps, float base, float rscale,
-                       const float* rope_cs, int64_t pos, void* kc, void* vc, int64_t cap, float scale, void* out,
-                       int out_dt, void* workspace, int num_cus, hipStream_t st, int* sync) {
+                       const float* rope_cs, int64_t pos, void* kc, void* vc, int c_dt, int64_t cap, float scale,
+                       void* out, int out_dt, void* workspace, int num_cus, hipStream_t st, int* sync,
+                       uint32_t spin, int* status) {
     const int G = Hk > 0 ? Hq / Hk : 0;
     if (!qkv_attn_ok(m, Hq, Hk, sync, num_cus)) return Status::fail(JH_ERR_UNSUPPORTED, "qkv_attn: outside the fused launch");
     if (cap > ((int64_t)1 << 23) - 1024) return Status::fail(JH_ERR_UNSUPPORTED, "attention: capacity above 8M tokens");
@@ -1588,13 +1658,24 @@ Status launch_qkv_attn(const QuantMatrix& m, const uint16_t* x, float* stats, fl
         f.norm_eps = norm_eps;
         f.gs_log2 = log2_exact(m.group_size);
         f.bpx = bpx;
+        f.spin = spin;
+        f.markers = sync + kAttnMarkerSlot;
+        f.status = status;
         hipLaunchKernelGGL(kern, dim3((unsigned)(8 * bpx)), dim3(256), 0, st, f);
         return Status::ok();
     };
-    if (G == 1) return go(qkv_attn_kernel<1, 4>, qkv_attn_kernel<1, 8>);
-    if (G == 2) return go(qkv_attn_kernel<2, 4>, qkv_attn_kernel<2, 8>);
-    if (G == 4) return go(qkv_attn_kernel<4, 4>, qkv_attn_kernel<4, 8>);
-    return go(qkv_attn_kernel<8, 4>, qkv_attn_kernel<8, 8>);
+    const bool f16 = c_dt == JH_F16;
+    if (G == 1)
+        return f16 ? go(qkv_attn_kernel<1, 4, true>, qkv_attn_kernel<1, 8, true>)
+                   : go(qkv_attn_kernel<1, 4, false>, qkv_attn_kernel<1, 8, false>);
+    if (G == 2)
+        return f16 ? go(qkv_attn_kernel<2, 4, true>, qkv_attn_kernel<2, 8, true>)
+                   : go(qkv_attn_kernel<2, 4, false>, qkv_attn_kernel<2, 8, false>);
+    if (G == 4)
+        return f16 ? go(qkv_attn_kernel<4, 4, true>, qkv_attn_kernel<4, 8, true>)
+                   : go(qkv_attn_kernel<4, 4, false>, qkv_attn_kernel<4, 8, false>);
+    return f16 ? go(qkv_attn_kernel<8, 4, true>, qkv_attn_kernel<8, 8, true>)
+               : go(qkv_attn_kernel<8, 4, false>, qkv_attn_kernel<8, 8, false>);
 }
 
 int probe_xcd_round_robin(int* buf, hipStream_t st) {

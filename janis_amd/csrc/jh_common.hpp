@@ -35,6 +35,11 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
+// float -> IEEE half, round to nearest even (the hardware conversion).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // Raw buffer resources (gfx9 descriptor word 3 = 0x00020000: 32-bit dwords,
@@ -257,12 +262,12 @@ Status launch_norm_prepare(const void* x, int x_dt, int64_t d, const void* w, in
                            hipStream_t st);
 // out = bf16(u / sqrt(sum(stats) / d + eps)).
 Status launch_norm_apply(const uint16_t* u, int64_t d, const float* stats, float eps, uint16_t* out, hipStream_t st);
-// A few bf16 x rows (2..kQmvRowsMax, fewer for long rows) through the decode
+// A few bf16 or fp32 x rows (2..kQmvRowsMax, fewer for long rows) through the decode
 // tiles, the weights read once per launch of 2, 4 or 8 rows.
 constexpr int64_t kQmvRowsMax = 8;
 bool qmv_rows_ok(const QuantMatrix& m, int64_t rows, int x_dtype);
-Status launch_qmv_rows(const QuantMatrix& m, const void* x, int64_t rows, void* y, int y_dtype, int num_cus,
-                       hipStream_t st);
+Status launch_qmv_rows(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y, int y_dtype,
+                       int num_cus, hipStream_t st);
 Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y,
                   int y_dtype, int num_cus, hipStream_t st, void* workspace);
 // fp32 accumulation buffer a split-K prefill needs (0 when none).
@@ -324,7 +329,7 @@ size_t attn_decode_workspace_bytes(int64_t Hq, int64_t Hk, int64_t pos, int num_
 // partials be merged inside the attention launch when the GPU deals workgroups
 // to its 8 XCDs round-robin (probe_xcd_round_robin) and the kv heads are a
 // multiple of 8; otherwise a merge launch follows.
-constexpr int kAttnSyncSlots = 4096;
+constexpr int kAttnSyncSlots = 4096 + 64;
 // The fused q/k/v + attention launch's share of them: per XCD x, the arrival
 // flags of its blocks at kAttnFlagSlot + 128 x (zero between calls).
 constexpr int kAttnFlagSlot = 1024;
@@ -332,18 +337,25 @@ constexpr int kAttnMaxBlocksPerXcd = 128;
 // jh_argmax's share: the arrival counter of row r at kArgmaxSyncSlot + r for
 // the first kArgmaxSyncRows rows (zero between calls).
 constexpr int kArgmaxSyncSlot = 2048, kArgmaxSyncRows = 2048;
+// The fused launch's give-up markers, one per XCD (zero until a wait gives up;
+// reset by the host, see jh_sync).
+constexpr int kAttnMarkerSlot = 4096;
+// Polls of the arrival flags before a fused launch's wait gives up (the default
+// of jh_set_wait_limit).
+constexpr uint32_t kDefaultWaitPolls = 1u << 22;
 bool attn_merge_in_launch(int64_t Hk, const int* sync);
 Status launch_attn_decode(const void* qkv, int qkv_dt, int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt,
                           float eps, float base, float rscale, const float* rope_cs, int64_t pos, void* kc,
-                          void* vc, int64_t cap, float scale, void* out, int out_dt, void* workspace, int num_cus,
-                          hipStream_t st, int* sync);
+                          void* vc, int c_dt, int64_t cap, float scale, void* out, int out_dt, void* workspace,
+                          int num_cus, hipStream_t st, int* sync);
 // The q/k/v product (JH_PRO_NORMED prologue, bf16 or f32 out) and the attention of one
 // token in one launch (decode.hip); JH_ERR_UNSUPPORTED outside qkv_attn_ok.
 bool qkv_attn_ok(const QuantMatrix& m, int64_t Hq, int64_t Hk, const int* sync, int num_cus);
 Status launch_qkv_attn(const QuantMatrix& m, const uint16_t* x, float* stats, float norm_eps, void* qkv, int qkv_dt,
                        int Hq, int Hk, const void* qn_w, const void* kn_w, int w_dt, float eps, float base, float rscale,
-                       const float* rope_cs, int64_t pos, void* kc, void* vc, int64_t cap, float scale, void* out,
-                       int out_dt, void* workspace, int num_cus, hipStream_t st, int* sync);
+                       const float* rope_cs, int64_t pos, void* kc, void* vc, int c_dt, int64_t cap, float scale,
+                       void* out, int out_dt, void* workspace, int num_cus, hipStream_t st, int* sync,
+                       uint32_t spin, int* status);
 // 8 when block b of a launch runs on XCD b % 8 (checked on a 64-block launch;
 // buf: 64 ints of device memory), else 0.
 int probe_xcd_round_robin(int* buf, hipStream_t st);

@@ -31,12 +31,13 @@ namespace {
 // and split into (128 + q) bf16 pairs once and applied to every row's x, so
 // the weights stream from HBM once for all rows. The lanes, words, dot order
 // and reductions are those of qmv_bf16x_kernel with the same tile, so row m of
-// y has the bits a one-row call on x[m] gives. bf16 x and y rows of N (bf16 or
-// fp32); rows past `rows` read as zero and are not stored.
-template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int MR>
+// y has the bits a one-row call on x[m] gives. x rows of bf16 (XF32: fp32,
+// rounded to bf16 in registers as the one-row tile does) and y rows of N (bf16
+// or fp32); rows past `rows` read as zero and are not stored.
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int MR, bool XF32>
 __global__ __launch_bounds__(256) void qmv_rows_kernel(
     const uint32_t* __restrict__ W, const uint16_t* __restrict__ S, const uint16_t* __restrict__ B,
-    const uint16_t* __restrict__ X, void* Y, int y_dt, uint32_t N, int gs_log2, int rows) {
+    const void* __restrict__ X, void* Y, int y_dt, uint32_t N, int gs_log2, int rows) {
     constexpr int SLICES = 64 / LPR;
     constexpr int RGROUPS = 4 / KSPLIT;
     constexpr uint32_t PK = 4 * LPR * ITERS;
@@ -52,7 +53,8 @@ __global__ __launch_bounds__(256) void qmv_rows_kernel(
     const auto rw = make_rsrc(W, N * P * 4);
     const auto rs = make_rsrc(S, N * G * 2);
     const auto rb = make_rsrc(B, N * G * 2);
-    const auto rx = make_rsrc(X, (uint32_t)rows * K * 2);
+    constexpr uint32_t XB = XF32 ? 4 : 2;  // bytes per x element
+    const auto rx = make_rsrc(X, (uint32_t)rows * K * XB);
     __shared__ float red[(KSPLIT > 1) ? (KSPLIT - 1) * RGROUPS * SLICES * RPW * MR : 1];
 
     uint32_t gi[ITERS], wo[ITERS];
@@ -68,12 +70,24 @@ __global__ __launch_bounds__(256) void qmv_rows_kernel(
     for (int m = 0; m < MR; m++)
 #pragma unroll
         for (int it = 0; it < ITERS; it++) {
-            const uint32_t off = (m * K + 8 * wo[it]) * 2;
+            const uint32_t off = (m * K + 8 * wo[it]) * XB;
             float sum = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16 * j, 0, 0);
-                sum += pair_up(make_uint4(v.x, v.y, v.z, v.w), &xp[m][it][4 * j]);
+                uint4 xb;
+                if constexpr (XF32) {
+                    const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 32 * j, 0, 0);
+                    const u32x4_t b = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 32 * j + 16, 0, 0);
+                    auto cvt2 = [](uint32_t u, uint32_t v) {
+                        return (uint32_t)f32_to_bf16_hw(__uint_as_float(u)) |
+                               ((uint32_t)f32_to_bf16_hw(__uint_as_float(v)) << 16);
+                    };
+                    xb = make_uint4(cvt2(a.x, a.y), cvt2(a.z, a.w), cvt2(b.x, b.y), cvt2(b.z, b.w));
+                } else {
+                    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16 * j, 0, 0);
+                    xb = make_uint4(v.x, v.y, v.z, v.w);
+                }
+                sum += pair_up(xb, &xp[m][it][4 * j]);
             }
             xs[m][it] = sum;
         }
@@ -288,7 +302,7 @@ template <int LPR, int ITERS, int RPW, int KSPLIT, int PRO, int EPI, int BITS, i
 bool tile_bits(const QuantMatrix& m, const void* x, void* y, int y_dtype, int gl, int num_cus, hipStream_t st,
                const QmvFusion& fu) {
     if (m.sb_dtype == JH_F16) {
-        if constexpr (PRO == PRO_NONE && EPI == EPI_STORE)
+        if constexpr ((PRO == PRO_NONE || PRO == PRO_XF32) && EPI == EPI_STORE)
             return run_fast_sb<LPR, ITERS, RPW, KSPLIT, true, PRO, EPI, BITS, BPC>(m, x, y, y_dtype, gl, num_cus, st,
                                                                                  fu)
                        .code == JH_OK;
@@ -379,6 +393,10 @@ Status launch_qmv(const QuantMatrix& m, const void* x, int x_dtype, void* y, int
                   int num_cus, hipStream_t st) {
     if (x_dtype == JH_BF16 && launch_tiles<PRO_NONE, EPI_STORE>(m, x, y, y_dtype, num_cus, st, QmvFusion{}))
         return Status::ok();
+    // fp32 x (the CPU backend's activation type): the same tiles, x rounded to
+    // bf16 in registers
+    if (x_dtype == JH_F32 && launch_tiles<PRO_XF32, EPI_STORE>(m, x, y, y_dtype, num_cus, st, QmvFusion{}))
+        return Status::ok();
     return launch_generic(m, x, x_dtype, 1, y, y_dtype, num_cus, st);
 }
 
@@ -391,11 +409,12 @@ namespace {
 template <int ITERS>
 constexpr int rows_mr() { return ITERS == 1 ? 8 : (ITERS == 2 ? 4 : 2); }
 
-template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int MR>
-Status run_rows_mr(const QuantMatrix& m, const uint16_t* x, int64_t rows, void* y, int y_dtype, int gl,
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, int MR, bool XF32>
+Status run_rows_mr(const QuantMatrix& m, const void* x, int64_t rows, void* y, int y_dtype, int gl,
                    int num_cus, hipStream_t st) {
     constexpr int64_t rows_per_block = (4 / KSPLIT) * (64 / LPR) * RPW;
-    auto kern = qmv_rows_kernel<LPR, ITERS, RPW, KSPLIT, SB_F16, MR>;
+    constexpr size_t xsz = XF32 ? 4 : 2;
+    auto kern = qmv_rows_kernel<LPR, ITERS, RPW, KSPLIT, SB_F16, MR, XF32>;
     static int per_cu = 0;  // resident blocks per CU, asked once per instantiation
     if (per_cu == 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) != hipSuccess || per_cu < 1))
         per_cu = 1;
@@ -406,7 +425,8 @@ Status run_rows_mr(const QuantMatrix& m, const uint16_t* x, int64_t rows, void* 
         const int n = (int)std::min<int64_t>(MR, rows - r0);
         hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, st, m.w,
                            static_cast<const uint16_t*>(m.scales), static_cast<const uint16_t*>(m.biases),
-                           x + r0 * m.in, static_cast<char*>(y) + (size_t)r0 * m.rows * ysz, y_dtype,
+                           static_cast<const char*>(x) + (size_t)r0 * m.in * xsz,
+                           static_cast<char*>(y) + (size_t)r0 * m.rows * ysz, y_dtype,
                            (uint32_t)m.rows, gl, n);
     }
     return Status::ok();
@@ -414,15 +434,28 @@ Status run_rows_mr(const QuantMatrix& m, const uint16_t* x, int64_t rows, void* 
 
 // The kernel computes all MR rows whatever the count, so the smallest of 2, 4
 // and 8 rows per launch that covers the call (up to the tile's limit) is used.
-template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16>
-Status run_rows(const QuantMatrix& m, const uint16_t* x, int64_t rows, void* y, int y_dtype, int gl, int num_cus,
+template <int LPR, int ITERS, int RPW, int KSPLIT, bool SB_F16, bool XF32>
+Status run_rows(const QuantMatrix& m, const void* x, int64_t rows, void* y, int y_dtype, int gl, int num_cus,
                 hipStream_t st) {
     constexpr int MRMAX = rows_mr<ITERS>();
     if constexpr (MRMAX >= 8)
-        if (rows > 4) return run_rows_mr<LPR, ITERS, RPW, KSPLIT, SB_F16, 8>(m, x, rows, y, y_dtype, gl, num_cus, st);
+        if (rows > 4)
+            return run_rows_mr<LPR, ITERS, RPW, KSPLIT, SB_F16, 8, XF32>(m, x, rows, y, y_dtype, gl, num_cus, st);
     if constexpr (MRMAX >= 4)
-        if (rows > 2) return run_rows_mr<LPR, ITERS, RPW, KSPLIT, SB_F16, 4>(m, x, rows, y, y_dtype, gl, num_cus, st);
-    return run_rows_mr<LPR, ITERS, RPW, KSPLIT, SB_F16, 2>(m, x, rows, y, y_dtype, gl, num_cus, st);
+        if (rows > 2)
+            return run_rows_mr<LPR, ITERS, RPW, KSPLIT, SB_F16, 4, XF32>(m, x, rows, y, y_dtype, gl, num_cus, st);
+    return run_rows_mr<LPR, ITERS, RPW, KSPLIT, SB_F16, 2, XF32>(m, x, rows, y, y_dtype, gl, num_cus, st);
+}
+
+template <int LPR, int ITERS, int RPW, int KSPLIT>
+Status run_rows_dt(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y, int y_dtype, int gl,
+                   int num_cus, hipStream_t st) {
+    const bool f16 = m.sb_dtype == JH_F16;
+    if (x_dtype == JH_F32)
+        return f16 ? run_rows<LPR, ITERS, RPW, KSPLIT, true, true>(m, x, rows, y, y_dtype, gl, num_cus, st)
+                   : run_rows<LPR, ITERS, RPW, KSPLIT, false, true>(m, x, rows, y, y_dtype, gl, num_cus, st);
+    return f16 ? run_rows<LPR, ITERS, RPW, KSPLIT, true, false>(m, x, rows, y, y_dtype, gl, num_cus, st)
+               : run_rows<LPR, ITERS, RPW, KSPLIT, false, false>(m, x, rows, y, y_dtype, gl, num_cus, st);
 }
 
 // 16-byte weight loads per lane and row of the multi-row tile for a 4-bit row
@@ -445,20 +478,18 @@ int tile_iters(int64_t row_words) {
 // down 4096 x 12288 at 4 rows 20.9 against 32.2, at 8 rows 42.2). Only row
 // lengths with a case in launch_qmv_rows are accepted (tile_iters > 0).
 bool qmv_rows_ok(const QuantMatrix& m, int64_t rows, int x_dtype) {
-    if (x_dtype != JH_BF16 || m.bits != 4 || rows < 2 || !qmv_fast_shape(m) || rows * m.in * 2 >= ((int64_t)1 << 31))
+    if ((x_dtype != JH_BF16 && x_dtype != JH_F32) || m.bits != 4 || rows < 2 || !qmv_fast_shape(m) ||
+        rows * m.in * 4 >= ((int64_t)1 << 31))
         return false;
     const int it = tile_iters(row_words(m));
     return it > 0 && rows <= (it >= 3 ? 4 : kQmvRowsMax);
 }
 
-Status launch_qmv_rows(const QuantMatrix& m, const void* x, int64_t rows, void* y, int y_dtype, int num_cus,
-                       hipStream_t st) {
-    if (!qmv_rows_ok(m, rows, JH_BF16)) return Status::fail(JH_ERR_UNSUPPORTED, "qmv_rows: shape outside the tiles");
+Status launch_qmv_rows(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y, int y_dtype,
+                       int num_cus, hipStream_t st) {
+    if (!qmv_rows_ok(m, rows, x_dtype)) return Status::fail(JH_ERR_UNSUPPORTED, "qmv_rows: shape outside the tiles");
     const int gl = log2_exact(m.group_size);
-    const uint16_t* xb = static_cast<const uint16_t*>(x);
-#define JH_ROWS(L, I, R, KS)                                                                   \
-    return m.sb_dtype == JH_F16 ? run_rows<L, I, R, KS, true>(m, xb, rows, y, y_dtype, gl, num_cus, st) \
-                                : run_rows<L, I, R, KS, false>(m, xb, rows, y, y_dtype, gl, num_cus, st)
+#define JH_ROWS(L, I, R, KS) return run_rows_dt<L, I, R, KS>(m, x, x_dtype, rows, y, y_dtype, gl, num_cus, st)
     // Each case keeps the one-row tile's lanes per row (L), loads per lane (I)
     // and K split (KS) for that row length, so a row's reduction order -- and
     // its bits -- are those of a one-row call; only the rows per slice (R) may

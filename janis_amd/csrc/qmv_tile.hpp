@@ -95,11 +95,15 @@ __device__ __forceinline__ void store_rows(void* Y, int y_dt, uint32_t row0, uin
 //                sum of h^2 in kNormSlots partials: each wave sums its share of
 //                the partials (loaded ahead of the weights), and the epilogue
 //                scales as PRO_RMSNORM does, so x costs what a plain one does.
+//   PRO_XF32     x is fp32 [K] (the activation type of the CPU backend and of
+//                Dequantize): each lane rounds its part of x to bf16 (nearest
+//                even) in registers and the tile runs as PRO_NONE on it, so the
+//                result has the bits of a bf16-x call on bf16(x).
 //   EPI_RESID_NORM  EPI_RESID, plus the next norm's input: nout[row] =
 //                bf16(y * nw[row]) and, per block, the sum of y^2 over its rows
 //                in stats[blockIdx.x] (grid <= kNormSlots; block 0 zeroes the
 //                unused slots). Fixed order: deterministic.
-enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_NORMED = 3 };
+enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_NORMED = 3, PRO_XF32 = 4 };
 constexpr int kProSiluMul = 2;  // x = [gate | up]: composed from separate launches
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_RESID_NORM = 3 };
 
@@ -217,6 +221,8 @@ __device__ __forceinline__ void qmv_tile(
     constexpr int XW = PRO == PRO_RMSNORM ? 8 : (int)EPW / 2;  // 16-byte chunks of them
     uint4 xraw[ITERS][XW];
     uint4 xaux[ITERS][4];  // norm weights (PRO_RMSNORM)
+    constexpr int XF = PRO == PRO_XF32 ? (int)EPW : 1;  // PRO_XF32: fp32 x, 16-byte chunks
+    uint4 xf32[ITERS][XF];
 #pragma unroll
     for (int it = 0; it < ITERS; it++) {
         const uint32_t e0 = EPW * wo[it];
@@ -224,6 +230,10 @@ __device__ __forceinline__ void qmv_tile(
             const uint4* xv = reinterpret_cast<const uint4*>(static_cast<const float*>(Xv) + e0);
 #pragma unroll
             for (int j = 0; j < 8; j++) xraw[it][j] = xv[j];
+        } else if constexpr (PRO == PRO_XF32) {
+            const uint4* xv = reinterpret_cast<const uint4*>(static_cast<const float*>(Xv) + e0);
+#pragma unroll
+            for (int j = 0; j < XF; j++) xf32[it][j] = xv[j];
         } else {
             const uint4* xv = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(Xv) + e0);
 #pragma unroll
@@ -263,6 +273,19 @@ __device__ __forceinline__ void qmv_tile(
         if constexpr (KSPLIT > 1)
             if (lane == 0) ssq[wv_id] = ss_part;
     }
+    if constexpr (PRO == PRO_XF32) {
+        // fp32 x to bf16 pairs (nearest even), in the layout a bf16 x loads as
+        auto cvt2 = [](uint32_t a, uint32_t b) {
+            return (uint32_t)f32_to_bf16_hw(__uint_as_float(a)) | ((uint32_t)f32_to_bf16_hw(__uint_as_float(b)) << 16);
+        };
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+#pragma unroll
+            for (int j = 0; j < XW; j++) {
+                const uint4 a = xf32[it][2 * j], b = xf32[it][2 * j + 1];
+                xraw[it][j] = make_uint4(cvt2(a.x, a.y), cvt2(a.z, a.w), cvt2(b.x, b.y), cvt2(b.z, b.w));
+            }
+    }
     float xs8[ITERS];  // 8-bit: the sum of the real inputs
     if constexpr (BITS == 8) {
         // word j of a 16-byte chunk holds elements 4j..4j+3: its virtual input is
@@ -284,7 +307,7 @@ __device__ __forceinline__ void qmv_tile(
             for (int j = 0; j < 4; j++) xin[it][j] = make_uint4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
             xs8[it] = sum;
         }
-    } else if constexpr (PRO == PRO_NONE || PRO == PRO_NORMED) {
+    } else if constexpr (PRO == PRO_NONE || PRO == PRO_NORMED || PRO == PRO_XF32) {
 #pragma unroll
         for (int it = 0; it < ITERS; it++)
 #pragma unroll

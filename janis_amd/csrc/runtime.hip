@@ -34,6 +34,13 @@ struct jh_ctx {
     // ints, zero between calls), or nullptr when the GPU does not deal
     // workgroups to its XCDs round-robin: then the merge is a second launch.
     int* attn_sync = nullptr;
+    // The stream operators are enqueued on keeps the round-robin placement the
+    // in-launch merges rely on (false for a stream restricted to some CUs).
+    bool stream_xcd_ok = true;
+    // Set by a fused launch whose in-kernel wait gave up (host memory the kernel
+    // writes); read after every synchronisation (jh_sync, jh_d2h).
+    int* wait_status = nullptr;
+    uint32_t wait_polls = jh::kDefaultWaitPolls;
 };
 
 namespace {
@@ -148,9 +155,39 @@ int check_quant(jh_ctx* c, const char* op, const uint32_t* w, const void* s, con
     return JH_OK;
 }
 
+// The in-launch merge counters, when the context's stream keeps the
+// round-robin workgroup placement (else nullptr: merges are launches of their own).
+int* xcd_sync(const jh_ctx* c) { return c->stream_xcd_ok ? c->attn_sync : nullptr; }
+
+// After the stream's work is done: a fused launch whose in-kernel wait gave up
+// left its status word set. Its heads' outputs are NaN; the flags and markers it
+// left are reset here (the stream is idle) and the failure is reported.
+int check_wait_status(jh_ctx* c, const char* op) {
+    if (!c->wait_status || !*reinterpret_cast<volatile int*>(c->wait_status)) return JH_OK;
+    *reinterpret_cast<volatile int*>(c->wait_status) = 0;
+    if (c->attn_sync) {
+        hipError_t e = hipMemsetAsync(c->attn_sync, 0, jh::kAttnSyncSlots * sizeof(int), c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "resetting the in-launch synchronisation state");
+    }
+    return fail(c, JH_ERR_TIMEOUT,
+                std::string(op) + ": a jh_qkv_attention_decode launch gave up waiting for its own blocks (were "
+                                  "other kernels holding the GPU's CUs?); the attention outputs of that call and of "
+                                  "the fused calls after it on this context until now are NaN. The synchronisation "
+                                  "state was reset: the next call runs normally.");
+}
+
 int check_act_dtype(jh_ctx* c, const char* op, const char* what, int dt) {
     if (dt != JH_BF16 && dt != JH_F32)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": " + what + " must be bf16 or f32");
+    return JH_OK;
+}
+
+// KV caches and the rows appended to them may also be f16 (KVCache.Update casts
+// f32 keys and values to f16 on a backend that reports dtypes, qwen/cache.go:90-93).
+int check_float_dtype(jh_ctx* c, const char* op, const char* what, int dt) {
+    if (dt != JH_BF16 && dt != JH_F32 && dt != JH_F16)
+        return fail(c, JH_ERR_INVALID, std::string(op) + ": " + what + " must be bf16, f16 or f32");
     return JH_OK;
 }
 
@@ -236,7 +273,8 @@ int check_attention(jh_ctx* c, const char* op, const void* qkv, jh_dtype qkv_dty
     if (int r = check_act_dtype(c, op, "qkv", qkv_dtype)) return r;
     if (int r = check_act_dtype(c, op, "out", out_dtype)) return r;
     if (head_dim != 128) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": head_dim must be 128");
-    if (cache_dtype != JH_BF16) return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": the caches must be bf16");
+    if (cache_dtype != JH_BF16 && cache_dtype != JH_F16)
+        return fail(c, JH_ERR_UNSUPPORTED, std::string(op) + ": the caches must be bf16 or f16");
     if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads || n_heads > 65536)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": bad head counts");
     const int64_t G = n_heads / n_kv_heads;
@@ -312,6 +350,17 @@ int jh_create(int device, jh_ctx** out) {
         (void)hipGetLastError();
         c->attn_sync = nullptr;
     }
+    // the fused launch's give-up status, in host memory so that reading it after
+    // a synchronisation costs no copy (a failure only disables the fused launch)
+    if (c->attn_sync) {
+        void* st = nullptr;
+        if (hipHostMalloc(&st, 64, hipHostMallocDefault) == hipSuccess) {
+            std::memset(st, 0, 64);
+            c->wait_status = static_cast<int*>(st);
+        } else {
+            (void)hipGetLastError();
+        }
+    }
     std::snprintf(c->name, sizeof(c->name), "%s (%s, %d CUs)", prop.name, prop.gcnArchName, c->num_cus);
     *out = c;
     return JH_OK;
@@ -326,6 +375,7 @@ void jh_destroy(jh_ctx* c) {
     for (void* p : c->retired) (void)hipFree(p);
     if (c->check_buf) (void)hipFree(c->check_buf);
     if (c->attn_sync) (void)hipFree(c->attn_sync);
+    if (c->wait_status) (void)hipHostFree(c->wait_status);
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     delete c;
 }
@@ -345,6 +395,29 @@ int jh_device_info(jh_ctx* c, char* name, size_t name_len, int* compute_units) {
 int jh_set_stream(jh_ctx* c, void* s) {
     if (int r = enter(c)) return r;
     c->stream = s ? static_cast<hipStream_t>(s) : c->own_stream;
+    // The in-launch merges rely on workgroups being dealt to the XCDs
+    // round-robin, which jh_create checked on the context's own stream; a stream
+    // restricted to a subset of the CUs (hipExtStreamCreateWithCUMask) breaks
+    // it, so such a stream runs the merges as launches of their own.
+    c->stream_xcd_ok = true;
+    if (c->stream != c->own_stream) {
+        std::vector<uint32_t> mask((size_t)(c->num_cus + 31) / 32, 0u);
+        if (hipExtStreamGetCUMask(c->stream, (uint32_t)mask.size(), mask.data()) != hipSuccess) {
+            (void)hipGetLastError();
+            c->stream_xcd_ok = false;
+        } else {
+            for (int cu = 0; cu < c->num_cus; cu++)
+                if (!((mask[(size_t)cu / 32] >> (cu % 32)) & 1u)) c->stream_xcd_ok = false;
+        }
+    }
+    return JH_OK;
+}
+
+int jh_set_wait_limit(jh_ctx* c, int64_t polls) {
+    if (int r = enter(c)) return r;
+    if (polls < 0 || polls > 0x7fffffff)
+        return fail(c, JH_ERR_INVALID, "jh_set_wait_limit: polls must be in [0, 2^31)");
+    c->wait_polls = (uint32_t)polls;
     return JH_OK;
 }
 
@@ -374,7 +447,7 @@ int jh_check_finite(jh_ctx* c, const void* x, jh_dtype dtype, int64_t n, int64_t
 int jh_sync(jh_ctx* c) {
     if (int r = enter(c)) return r;
     JH_HIP(c, hipStreamSynchronize(c->stream));
-    return JH_OK;
+    return check_wait_status(c, "jh_sync");
 }
 
 int jh_alloc(jh_ctx* c, size_t bytes, void** out) {
@@ -413,7 +486,7 @@ int jh_d2h(jh_ctx* c, void* dst, const void* src, size_t bytes) {
     if (!dst || !src) return fail(c, JH_ERR_INVALID, "jh_d2h: null pointer");
     JH_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
     JH_HIP(c, hipStreamSynchronize(c->stream));
-    return JH_OK;
+    return check_wait_status(c, "jh_d2h");
 }
 
 int jh_dequantize(jh_ctx* c, const uint32_t* w, const void* scales, const void* biases,
@@ -462,7 +535,7 @@ int jh_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, co
     if (rows == 1)
         r = finish(c, jh::launch_qmv(m, x, x_dtype, y, y_dtype, c->num_cus, c->stream), "qmv");
     else if (jh::qmv_rows_ok(m, rows, x_dtype))
-        r = finish(c, jh::launch_qmv_rows(m, x, rows, y, y_dtype, c->num_cus, c->stream), "qmv_rows");
+        r = finish(c, jh::launch_qmv_rows(m, x, x_dtype, rows, y, y_dtype, c->num_cus, c->stream), "qmv_rows");
     else {
         const size_t need = jh::qmm_workspace_bytes(m, rows, x_dtype, y_dtype, c->num_cus);
         if (need)
@@ -648,7 +721,7 @@ int jh_sdpa(jh_ctx* c, const void* q, jh_dtype q_dtype, const void* k, const voi
     if (int r = enter(c)) return r;
     const char* op = "jh_sdpa";
     if (int r = check_act_dtype(c, op, "q", q_dtype)) return r;
-    if (int r = check_act_dtype(c, op, "k/v", kv_dtype)) return r;
+    if (int r = check_float_dtype(c, op, "k/v", kv_dtype)) return r;
     if (int r = check_act_dtype(c, op, "out", out_dtype)) return r;
     if (B < 0 || Hq <= 0 || Hk <= 0 || Hq % Hk || Lq < 0 || Lk < 0 || kv_capacity < Lk || Dh <= 0)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": bad shape (Hq must be a multiple of Hk, capacity >= Lk)");
@@ -704,7 +777,7 @@ int jh_qk_norm_rope_append(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64
     if (int r = enter(c)) return r;
     const char* op = "jh_qk_norm_rope_append";
     if (int r = check_act_dtype(c, op, "qkv", qkv_dtype)) return r;
-    if (int r = check_act_dtype(c, op, "cache", cache_dtype)) return r;
+    if (int r = check_float_dtype(c, op, "cache", cache_dtype)) return r;
     if (int r = check_act_dtype(c, op, "q_out", q_out_dtype)) return r;
     if (w_dtype != JH_BF16 && w_dtype != JH_F16 && w_dtype != JH_F32)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": norm weights must be bf16, f16 or f32");
@@ -744,8 +817,8 @@ int jh_attention_decode(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, int64_t 
         if (int r = ensure_workspace(c, need, op)) return r;
     if (int r = finish(c, jh::launch_attn_decode(qkv, qkv_dtype, (int)n_heads, (int)n_kv_heads, q_norm_w, k_norm_w,
                                                  w_dtype, eps, rope_base, rope_scale, rope_cs, pos, k_cache, v_cache,
-                                                 capacity, scale, out, out_dtype, c->ws, c->num_cus, c->stream,
-                                                 c->attn_sync),
+                                                 cache_dtype, capacity, scale, out, out_dtype, c->ws, c->num_cus,
+                                                 c->stream, xcd_sync(c)),
                        op))
         return r;
     return check_values(c, op, out, out_dtype, n_heads * head_dim);
@@ -774,12 +847,15 @@ int jh_qkv_attention_decode(jh_ctx* c, const void* x, const float* norm_stats, f
     const size_t need = jh::attn_decode_workspace_bytes(n_heads, n_kv_heads, pos, c->num_cus);
     if (need)
         if (int r = ensure_workspace(c, need, op)) return r;
-    if (jh::qkv_attn_ok(m, n_heads, n_kv_heads, c->attn_sync, c->num_cus)) {
+    if (c->wait_status && jh::qkv_attn_ok(m, n_heads, n_kv_heads, xcd_sync(c), c->num_cus)) {
+        // an earlier fused call's wait that gave up is reported as soon as the
+        // host can see it
+        if (int r = check_wait_status(c, op)) return r;
         const jh::Status st = jh::launch_qkv_attn(m, static_cast<const uint16_t*>(x), const_cast<float*>(norm_stats),
                                                   norm_eps, qkv, (int)qkv_dtype, (int)n_heads, (int)n_kv_heads,
                                                   q_norm_w, k_norm_w, w_dtype, eps, rope_base, rope_scale, rope_cs, pos,
-                                                  k_cache, v_cache, capacity, scale, out, out_dtype, c->ws, c->num_cus,
-                                                  c->stream, c->attn_sync);
+                                                  k_cache, v_cache, cache_dtype, capacity, scale, out, out_dtype, c->ws,
+                                                  c->num_cus, c->stream, xcd_sync(c), c->wait_polls, c->wait_status);
         if (st.code != JH_ERR_UNSUPPORTED) {
             if (int r = finish(c, st, op)) return r;
             return check_values(c, op, out, out_dtype, n_heads * head_dim);
@@ -814,11 +890,13 @@ int jh_attention_decode_noalloc(jh_ctx* c, const void* qkv, jh_dtype qkv_dtype, 
                                                "-byte scratch (use jh_attention_decode)");
     // every split block writes all of its partials before the merge reads them,
     // so the scratch needs no clearing
-    return finish(c, jh::launch_attn_decode(qkv, qkv_dtype, (int)n_heads, (int)n_kv_heads, q_norm_w, k_norm_w,
-                                            w_dtype, eps, rope_base, rope_scale, rope_cs, pos, k_cache, v_cache,
-                                            capacity, scale, out, out_dtype, c->scratch, c->num_cus, c->stream,
-                                            c->attn_sync),
-                  op);
+    if (int r = finish(c, jh::launch_attn_decode(qkv, qkv_dtype, (int)n_heads, (int)n_kv_heads, q_norm_w, k_norm_w,
+                                                 w_dtype, eps, rope_base, rope_scale, rope_cs, pos, k_cache, v_cache,
+                                                 cache_dtype, capacity, scale, out, out_dtype, c->scratch, c->num_cus,
+                                                 c->stream, xcd_sync(c)),
+                       op))
+        return r;
+    return check_values(c, op, out, out_dtype, n_heads * head_dim);
 }
 
 int jh_copy_strided(jh_ctx* c, const void* src, jh_dtype src_dtype, int ndim, const int64_t* shape,
@@ -896,8 +974,8 @@ int jh_kv_append(jh_ctx* c, void* k_cache, void* v_cache, jh_dtype cache_dtype, 
                  int64_t pos, const void* k_new, const void* v_new, jh_dtype new_dtype, int64_t L, int64_t Dh) {
     if (int r = enter(c)) return r;
     const char* op = "jh_kv_append";
-    if (int r = check_act_dtype(c, op, "cache", cache_dtype)) return r;
-    if (int r = check_act_dtype(c, op, "new rows", new_dtype)) return r;
+    if (int r = check_float_dtype(c, op, "cache", cache_dtype)) return r;
+    if (int r = check_float_dtype(c, op, "new rows", new_dtype)) return r;
     if (BH < 0 || capacity < 0 || pos < 0 || L < 0 || Dh <= 0 || pos + L > capacity)
         return fail(c, JH_ERR_INVALID, std::string(op) + ": rows " + std::to_string(pos) + ".." +
                                            std::to_string(pos + L) + " do not fit capacity " + std::to_string(capacity));

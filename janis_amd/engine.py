@@ -160,6 +160,57 @@ class HipBackend:
     def Sync(self) -> None:
         check(self._ctx, self._L.jh_sync(self._ctx))
 
+    def Eval(self, *ts) -> None:
+        """engine.Backend.Eval (engine/backend.go:168): operators run as they are
+        called, so forcing evaluation is waiting for the stream (the Qwen session
+        and the MoE block call it, qwen/session.go:319, qwen/moe.go:632, 652)."""
+        self.Sync()
+
+    def SetWaitLimit(self, polls: int) -> None:
+        """jh_set_wait_limit: polls of the fused q/k/v + attention launch's
+        in-kernel wait before it gives up (0: at once, for tests of the failure
+        path, reported as JH_ERR_TIMEOUT by the next Sync)."""
+        check(self._ctx, self._L.jh_set_wait_limit(self._ctx, int(polls)))
+
+    # -- engine.Backend methods off this backend's path ------------------------------
+    # The interface's other operators (engine/backend.go:180-248) serve models
+    # outside the Qwen3 decode path (Gemma, Whisper, Qwen3.5's GatedDeltaNet);
+    # they exist so the type satisfies the interface and fail loudly, as the
+    # ggml backend does for its own gaps.
+    def _unsupported(self, name: str):
+        raise JanisHipError(_lib.JH_ERR_UNSUPPORTED, f"{name}: not in this backend (engine/backend.go; "
+                                                     f"off the quantized-linear decode path)")
+
+    def MatMul(self, a: Tensor, b: Tensor) -> Tensor:
+        self._unsupported("MatMul")
+
+    def LayerNorm(self, x: Tensor, weight: Tensor, bias: Tensor, eps: float) -> Tensor:
+        self._unsupported("LayerNorm")
+
+    def Erf(self, x: Tensor) -> Tensor:
+        self._unsupported("Erf")
+
+    def Tanh(self, x: Tensor) -> Tensor:
+        self._unsupported("Tanh")
+
+    def Exp(self, x: Tensor) -> Tensor:
+        self._unsupported("Exp")
+
+    def Sigmoid(self, x: Tensor) -> Tensor:
+        self._unsupported("Sigmoid")
+
+    def Softplus(self, x: Tensor) -> Tensor:
+        self._unsupported("Softplus")
+
+    def Conv1dDepthwise(self, x: Tensor, w: Tensor) -> Tensor:
+        self._unsupported("Conv1dDepthwise")
+
+    def GatedDeltaScan(self, q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, state: Tensor) -> tuple:
+        self._unsupported("GatedDeltaScan")
+
+    def Gelu(self, x: Tensor) -> Tensor:
+        self._unsupported("Gelu")
+
     def SetStream(self, stream_handle: int | None) -> None:
         """Enqueue on a caller's hipStream_t (e.g. torch.cuda.current_stream().cuda_stream)."""
         check(self._ctx, self._L.jh_set_stream(self._ctx, ctypes.c_void_p(stream_handle or 0)))

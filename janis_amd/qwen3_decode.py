@@ -18,7 +18,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _lib
-from .engine import BF16, F32, I32, HipBackend, Tensor
+from .engine import BF16, F16, F32, I32, HipBackend, Tensor
 
 
 @dataclass
@@ -74,9 +74,11 @@ def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bo
     are separate launches, with a merge launch), and the embedding row, the
     first norm's producer half and the RoPE factors in one launch.
     fused=False makes the reference's calls one for one (qwen/block.go,
-    qwen/attention.go, qwen/mlp.go, qwen/cache.go): separate q/k/v and gate/up
-    products on row views of the stacked matrices, Reshape/Transpose views, the
-    KVAppender, SDPA over the cache views."""
+    qwen/attention.go, qwen/mlp.go, qwen/cache.go), with engine.Backend's own
+    parameters only: separate q/k/v and gate/up products on row views of the
+    stacked matrices, Reshape/Transpose views, KVCache.Update's F16 cast and the
+    KVAppender, SDPA over the cache views. Its activations are F32 (Dequantize's
+    dtype, kept by every operator), as unchanged janis model code makes them."""
     c = m.cfg
     gs, bits = c.group_size, c.bits
     H, Hq, Hk, Dh, I = c.hidden, c.n_heads, c.n_kv, c.head_dim, c.inter
@@ -103,40 +105,57 @@ def decode_step(b: HipBackend, m: Qwen3Model, token: Tensor, pos: int, fused: bo
                                norm_out=u)
         logits = b.QuantMatvecFused(u, *head, gs, bits, NORMED, eps=c.eps, stats=st, out_dtype=F32)
         return logits, b.Argmax(logits)
-    # the reference's operator sequence, call for call
-    # QuantEmbedding.Forward (qwen/embed.go:78-83)
-    h = b.Dequantize(b.TakeAxis(ew, token), b.TakeAxis(es, token), b.TakeAxis(eb, token), gs, bits)  # F32 [1, H]
+    # The reference's operator sequence, call for call, with the dtype flow its
+    # unchanged model code produces on this backend: every result takes its
+    # input's dtype, so the F32 row Dequantize returns keeps the activations
+    # F32 throughout (the products' fp32 x takes the same decode tiles, rounded
+    # to bf16 in registers), and KVCache.Update casts the F32 keys and values to
+    # F16 because this backend is a RawReader (qwen/cache.go:90-93).
+    # QuantEmbedding.Forward (qwen/embed.go:78-83), forwardCachedT's reshape
+    # (qwen/model.go:294-303)
     B, T = 1, 1
+    h = b.Reshape(b.Dequantize(b.TakeAxis(ew, token, 0), b.TakeAxis(es, token, 0), b.TakeAxis(eb, token, 0), gs,
+                               bits), B, T, H)
     for L in m.layers:
         # Block.ForwardCached (qwen/block.go:58-61): h = x + Attn(InputNorm(x))
-        x = b.Reshape(h, B, T, H)
-        xn = b.RMSNorm(x, L.in_norm, c.eps, out_dtype=BF16)
+        x = h
+        xn = b.RMSNorm(x, L.in_norm, c.eps)
         # Attention.ForwardCached (qwen/attention.go:98-128)
         wq, wk, wv = (_linear_rows(b, L.qkv, r0, n) for r0, n in ((0, Hq * Dh), (Hq * Dh, Hk * Dh),
                                                                     ((Hq + Hk) * Dh, Hk * Dh)))
-        q = b.Reshape(b.QuantMatmul(xn, *wq, True, gs, bits, out_dtype=F32), B, T, Hq, Dh)
-        k = b.Reshape(b.QuantMatmul(xn, *wk, True, gs, bits, out_dtype=F32), B, T, Hk, Dh)
+        q = b.Reshape(b.QuantMatmul(xn, *wq, True, gs, bits), B, T, Hq, Dh)
+        k = b.Reshape(b.QuantMatmul(xn, *wk, True, gs, bits), B, T, Hk, Dh)
         q, k = b.RMSNorm(q, L.q_norm, c.eps), b.RMSNorm(k, L.k_norm, c.eps)
         q, k = b.Transpose(q, 0, 2, 1, 3), b.Transpose(k, 0, 2, 1, 3)
-        v = b.Transpose(b.Reshape(b.QuantMatmul(xn, *wv, True, gs, bits, out_dtype=F32), B, T, Hk, Dh), 0, 2, 1, 3)
+        v = b.Transpose(b.Reshape(b.QuantMatmul(xn, *wv, True, gs, bits), B, T, Hk, Dh), 0, 2, 1, 3)
         q = b.RoPE(q, Dh, False, c.theta, 1.0, pos)
         k = b.RoPE(k, Dh, False, c.theta, 1.0, pos)
-        # KVCache.Update through engine.KVAppender (qwen/cache.go:90-98); the
-        # model's caches are the spare-room buffers, their first pos rows the views
-        _, kview = b.AppendKV(L.k_cache, b.Slice(L.k_cache, 2, 0, pos), pos, k)
-        _, vview = b.AppendKV(L.v_cache, b.Slice(L.v_cache, 2, 0, pos), pos, v)
-        att = b.SDPA(q, kview, vview, Dh ** -0.5, T > 1, out_dtype=BF16)
+        k, v = kv_cache_update(b, L, pos, k, v)
+        att = b.SDPA(q, k, v, Dh ** -0.5, T > 1)
         att = b.Reshape(b.Transpose(att, 0, 2, 1, 3), B, T, Hq * Dh)
-        h = b.Add(x, b.QuantMatmul(att, *_linear_rows(b, L.o, 0, H), True, gs, bits, out_dtype=F32))
+        h = b.Add(x, b.QuantMatmul(att, *_linear_rows(b, L.o, 0, H), True, gs, bits))
         # MLP.Forward (qwen/mlp.go:32-36) on PostNorm(h), and the second residual add
-        xn = b.RMSNorm(h, L.post_norm, c.eps, out_dtype=BF16)
-        gate = b.SiLU(b.QuantMatmul(xn, *_linear_rows(b, L.gate_up, 0, I), True, gs, bits, out_dtype=BF16))
-        up = b.QuantMatmul(xn, *_linear_rows(b, L.gate_up, I, I), True, gs, bits, out_dtype=BF16)
-        h = b.Add(h, b.QuantMatmul(b.Mul(gate, up), *_linear_rows(b, L.down, 0, H), True, gs, bits, out_dtype=F32))
-    # forwardCachedT's last position, final norm, head (qwen/model.go:294-303)
-    hn = b.RMSNorm(b.Slice(h, 1, T - 1, T), m.norm, c.eps, out_dtype=BF16)
-    logits = b.Reshape(b.QuantMatmul(hn, *head, True, gs, bits, out_dtype=F32), 1, -1)
-    return logits, b.Argmax(logits)
+        xn = b.RMSNorm(h, L.post_norm, c.eps)
+        gate = b.SiLU(b.QuantMatmul(xn, *_linear_rows(b, L.gate_up, 0, I), True, gs, bits))
+        up = b.QuantMatmul(xn, *_linear_rows(b, L.gate_up, I, I), True, gs, bits)
+        h = b.Add(h, b.QuantMatmul(b.Mul(gate, up), *_linear_rows(b, L.down, 0, H), True, gs, bits))
+    # forwardCachedT's final norm, last position, head (qwen/model.go:294-303, 271-276)
+    h = b.Slice(b.RMSNorm(h, m.norm, c.eps), 1, T - 1, T)
+    logits = b.QuantMatmul(h, *head, True, gs, bits)
+    return b.Reshape(logits, 1, -1), b.Argmax(logits, -1)
+
+
+def kv_cache_update(b: HipBackend, L: Qwen3Layer, n: int, k: Tensor, v: Tensor) -> tuple:
+    """KVCache.Update (qwen/cache.go:90-98) on this backend: it is an
+    engine.RawReader, so F32 keys and values are cast to F16 first; then
+    KVAppender.AppendKV writes them at token n of the layer's spare-room buffers
+    (the model's caches; their first n tokens are the current views) and the
+    views of the first n + L tokens come back."""
+    if b.DTypeOf(k) == F32:
+        k, v = b.Cast(k, F16), b.Cast(v, F16)
+    _, kview = b.AppendKV(L.k_cache, b.Slice(L.k_cache, 2, 0, n), n, k)
+    _, vview = b.AppendKV(L.v_cache, b.Slice(L.v_cache, 2, 0, n), n, v)
+    return kview, vview
 
 
 def _linear_rows(b: HipBackend, lin: tuple, r0: int, n: int) -> tuple:
@@ -145,10 +164,12 @@ def _linear_rows(b: HipBackend, lin: tuple, r0: int, n: int) -> tuple:
     return tuple(b.Slice(t, 0, r0, r0 + n) for t in lin)
 
 
-def random_model(b: HipBackend, cfg: Qwen3Config, capacity: int, seed: int = 0, torch=None, dev=None):
+def random_model(b: HipBackend, cfg: Qwen3Config, capacity: int, seed: int = 0, torch=None, dev=None,
+                 cache_dtype: int = BF16):
     """Random-init weights of the architecture (codes uniform 0..15, scales
     |N(0,1)|*0.02, biases -8*scale + N(0, 1e-3), norm weights 1 + N(0, 0.05))
-    and zeroed bf16 caches of `capacity` rows. With torch given, everything is
+    and zeroed caches of `capacity` rows (bf16, or f16: the dtype
+    KVCache.Update's cast gives F32 keys on this backend). With torch given, everything is
     generated on the device (the 8B model in seconds); otherwise with numpy from
     janis_amd.synth and uploaded (small models). Returns (model, host copies or
     None)."""
@@ -182,9 +203,10 @@ def random_model(b: HipBackend, cfg: Qwen3Config, capacity: int, seed: int = 0, 
 
     def cache():
         if torch is not None:
-            t = torch.zeros((1, Hk, capacity, Dh), dtype=torch.bfloat16, device=dev)
-            return b.Wrap(t.data_ptr(), tuple(t.shape), BF16, keep=t)
-        return b.FromBF16Bits(np.zeros((1, Hk, capacity, Dh), np.uint16), 1, Hk, capacity, Dh)
+            t = torch.zeros((1, Hk, capacity, Dh), dtype=torch.bfloat16 if cache_dtype == BF16 else torch.float16,
+                            device=dev)
+            return b.Wrap(t.data_ptr(), tuple(t.shape), cache_dtype, keep=t)
+        return b.FromRaw(cache_dtype, np.zeros((1, Hk, capacity, Dh), np.uint16), 1, Hk, capacity, Dh)
 
     m = Qwen3Model(cfg, qlin("embed", cfg.vocab, H))
     for l in range(cfg.layers):

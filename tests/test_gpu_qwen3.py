@@ -3,18 +3,41 @@ size the oracle finishes in seconds) against the same step composed from the
 oracle's operators, following qwen/model.go:294-303, qwen/block.go:58-61,
 qwen/attention.go:98-128 and qwen/mlp.go:32-36.
 
-The GPU feeds bf16 inputs to the quantized products and keeps a bf16 KV cache;
-the oracle is fp32 throughout, so logits are held to 3e-2 of max|logit| and the
-greedy token to equality whenever the oracle's top-2 margin exceeds that bar.
-Both sides are fed the same tokens (the GPU's choice) so a near-tie cannot make
-the trajectories diverge.
+The GPU feeds bf16 inputs to the quantized products (fp32 activations are
+rounded to bf16 in the products' registers) and keeps a bf16 or f16 KV cache;
+the oracle is fp32 throughout, so logits are held to TOL of max|logit|, and the
+GPU's greedy token must be one the oracle scores within TOL * max|logit| of its
+own best. Both sides are fed the same tokens (the GPU's choice) so a near-tie
+cannot make the trajectories diverge. The unfused step is the reference's call
+sequence with its dtype flow (F32 activations, KVCache.Update's F16 cast), the
+fused one the backend's fused operators.
 """
 import numpy as np
 import pytest
 
-from janis_amd.engine import F32
+from janis_amd.engine import BF16, F16, F32
 from janis_amd.qwen3_decode import Qwen3Config, decode_step, random_model
 from tests.conftest import rel_ok, step
+
+# The north star's bar (relOK, ggml/ggml_test.go:56-65) for the random model,
+# where max|diff| / max|logit| measured on MI355X is 1.1e-3 .. 1.9e-3. The
+# tiny MLX checkpoint is more sensitive to the bf16 rounding of the products'
+# inputs: rounding only those in the oracle's own composition moves its logits
+# by 5.0e-3 (untied) and 7.0e-3 (tied) of max, and the GPU's fused step, which
+# also rounds the cache rows and the attention output, measured 1.12e-2 and
+# 1.43e-2; its bar is 3e-2.
+TOL = 1e-2
+TOL_CHECKPOINT = 3e-2
+
+
+def check_logits(got, want, nxt_id, what, tol=TOL):
+    """The logits within tol * max|want| of the oracle's, and the greedy token
+    one whose oracle logit is within tol * max|want| of the oracle's best."""
+    ok, d, sc = rel_ok(got, want, tol)
+    print(f"  {what}: max|diff| {d:.4g} of max|logit| {sc:.4g} ({d / sc:.2e})", flush=True)
+    assert ok, (what, d, sc)
+    assert nxt_id == int(np.argmax(got)), what
+    assert want[nxt_id] >= want.max() - tol * sc, (what, nxt_id, int(np.argmax(want)))
 
 pytestmark = pytest.mark.gpu
 
@@ -49,26 +72,22 @@ def _oracle_step(o, cfg, host, token, pos, kc, vc):
     return o.quant_matmul(hn, w.w, w.s, w.b, gs)[0]
 
 
-@pytest.mark.parametrize("fused", [True, False])
-def test_qwen3_small_decode_matches_oracle(hip, oracle, fused):
+@pytest.mark.parametrize("fused,cache_dt", [(True, BF16), (True, F16), (False, F16), (False, BF16)])
+def test_qwen3_small_decode_matches_oracle(hip, oracle, fused, cache_dt):
     cfg = Qwen3Config(hidden=512, inter=1024, n_heads=4, n_kv=2, head_dim=128, vocab=1000, layers=2)
     cap, steps = 32, 6
-    m, host = random_model(hip, cfg, cap, seed=5)
+    m, host = random_model(hip, cfg, cap, seed=5, cache_dtype=cache_dt)
     kc = [np.zeros((1, cfg.n_kv, cap, cfg.head_dim), np.float32) for _ in range(cfg.layers)]
     vc = [np.zeros((1, cfg.n_kv, cap, cfg.head_dim), np.float32) for _ in range(cfg.layers)]
     token = 17
+    cname = "bf16" if cache_dt == BF16 else "f16"
     for pos in range(steps):
-        step(f"qwen3 small decode fused={fused} pos={pos} token={token}")
+        step(f"qwen3 small decode fused={fused} cache={cname} pos={pos} token={token}")
         logits, nxt = decode_step(hip, m, hip.FromInt32(np.array([token], np.int32)), pos, fused=fused)
-        got = hip.Floats(logits)[0]
+        got = hip.Floats(logits).reshape(-1)
         want = _oracle_step(oracle, cfg, host, token, pos, kc, vc)
-        ok, d, sc = rel_ok(got, want, 3e-2)
-        assert ok, (pos, d, sc)
-        g = int(hip.Ints(nxt)[0])
-        assert g == int(np.argmax(got))
-        top2 = np.sort(want)[-2:]
-        if top2[1] - top2[0] > 3e-2 * sc:
-            assert g == int(np.argmax(want)), (pos, g, int(np.argmax(want)))
+        g = int(hip.Ints(nxt).reshape(-1)[0])
+        check_logits(got, want, g, f"fused={fused} cache={cname} pos={pos}")
         token = g
 
 
@@ -111,6 +130,5 @@ def test_loaded_mlx_checkpoint_decodes_like_the_oracle(hip, oracle, tmp_path, ti
         logits, nxt = decode_step(hip, m, hip.FromInt32(np.array([token], np.int32)), pos)
         got = hip.Floats(logits)[0]
         want = _oracle_step(oracle, cfg, host, token, pos, kc, vc)
-        ok, d_, sc = rel_ok(got, want, 3e-2)
-        assert ok, (pos, d_, sc)
         token = int(hip.Ints(nxt)[0])
+        check_logits(got, want, token, f"checkpoint tie={tie} pos={pos}", TOL_CHECKPOINT)

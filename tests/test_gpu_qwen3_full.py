@@ -8,20 +8,24 @@ qwen/block.go:58-61, qwen/attention.go:98-128, qwen/mlp.go:32-36).
 
 The weights are generated once on the device and copied to the host for the
 oracle (4.3 GB), so both sides read the same bits. The GPU feeds bf16 inputs
-to the products and keeps bf16 caches; the oracle is fp32 throughout, so the
-logits are held to 3e-2 of max|logit| (36 layers of bf16 rounding of the
-products' inputs) and the greedy token to equality whenever the oracle's
-top-2 margin exceeds that bar.
+to the products (fp32 activations rounded in registers) and keeps bf16 or f16
+caches; the oracle is fp32 throughout. The logits are held to TOL of
+max|logit| and the GPU's greedy token must be one the oracle scores within
+TOL * max|logit| of its best. The unfused case is the reference's own call
+sequence and dtype flow: F32 activations from Dequantize on, and the f16
+caches KVCache.Update's cast makes on this backend (qwen/cache.go:90-93).
 """
 import numpy as np
 import pytest
 
+from janis_amd.engine import F16
 from janis_amd.qwen3_decode import Qwen3Config, decode_step, random_model
 from tests.conftest import rel_ok, step
 
 pytestmark = pytest.mark.gpu
 
-TOL = 3e-2
+# the north star's bar (relOK, ggml/ggml_test.go:56-65)
+TOL = 1e-2
 
 
 class _Q:
@@ -63,9 +67,30 @@ def full_model(hip):
     torch.cuda.empty_cache()
 
 
+def _with_f16_caches(hip, m, ctx):
+    """The same model with f16 caches of ctx + 8 rows holding the bf16 caches'
+    first ctx rows (converted), as a copy of the model's layer list."""
+    import copy
+
+    import torch
+
+    m2 = copy.copy(m)
+    m2.layers = []
+    for L in m.layers:
+        L2 = copy.copy(L)
+        for name in ("k_cache", "v_cache"):
+            src = getattr(L, name)._keep
+            t = torch.zeros((1, src.shape[1], ctx + 8, src.shape[3]), dtype=torch.float16, device=src.device)
+            t[:, :, :ctx] = src[:, :, :ctx].to(torch.float16)
+            setattr(L2, name, hip.Wrap(t.data_ptr(), tuple(t.shape), F16, keep=t))
+        m2.layers.append(L2)
+    torch.cuda.synchronize()
+    return m2
+
+
 def _oracle_step(o, cfg, host, m, token, pos):
     """The step composed from the pinned oracle operators; the cache rows
-    before pos are read from the GPU's bf16 caches, the row at pos is the
+    before pos are read from the GPU's caches, the row at pos is the
     oracle's own key and value."""
     gs, eps = cfg.group_size, cfg.eps
     Hq, Hk, Dh, I = cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.inter
@@ -98,21 +123,25 @@ def _oracle_step(o, cfg, host, m, token, pos):
     return o.quant_matmul(hn, w.w, w.s, w.b, gs)[0]
 
 
-@pytest.mark.parametrize("ctx,fused", [(512, True), (512, False), (8192, True)])
-def test_qwen3_8b_full_decode_step(hip, oracle, full_model, ctx, fused):
+@pytest.mark.parametrize("ctx,fused,cache", [(512, True, "bf16"), (512, False, "bf16"), (512, False, "f16"),
+                                             (512, True, "f16"), (8192, True, "bf16")])
+def test_qwen3_8b_full_decode_step(hip, oracle, full_model, ctx, fused, cache):
     cfg, m, host = full_model
     token = 1234
-    step(f"oracle: full Qwen3-8B step at ctx {ctx}")
+    if cache == "f16":
+        step(f"f16 copies of the caches' first {ctx} rows")
+        m = _with_f16_caches(hip, m, ctx)
+    step(f"oracle: full Qwen3-8B step at ctx {ctx} (cache {cache})")
     want = _oracle_step(oracle, cfg, host, m, token, ctx)
-    step(f"GPU: full Qwen3-8B decode step at ctx {ctx} fused={fused}")
+    step(f"GPU: full Qwen3-8B decode step at ctx {ctx} fused={fused} cache={cache}")
     logits, nxt = decode_step(hip, m, hip.FromInt32(np.array([token], np.int32)), ctx, fused=fused)
-    got = hip.Floats(logits)[0]
+    got = hip.Floats(logits).reshape(-1)
     assert got.shape == (cfg.vocab,) and np.isfinite(got).all()
     ok, d, sc = rel_ok(got, want, TOL)
-    print(f"  ctx {ctx} fused={fused}: max|diff| {d:.4g} of max|logit| {sc:.4g} ({d / sc:.2e})", flush=True)
+    print(f"  ctx {ctx} fused={fused} cache={cache}: max|diff| {d:.4g} of max|logit| {sc:.4g} ({d / sc:.2e})",
+          flush=True)
     assert ok, (d, sc)
-    g = int(hip.Ints(nxt)[0])
+    g = int(hip.Ints(nxt).reshape(-1)[0])
     assert g == int(np.argmax(got))
-    top2 = np.sort(want)[-2:]
-    if top2[1] - top2[0] > TOL * sc:
-        assert g == int(np.argmax(want)), (g, int(np.argmax(want)))
+    # the GPU's greedy token is one the oracle scores within TOL of its best
+    assert want[g] >= want.max() - TOL * sc, (g, int(np.argmax(want)), float(want.max() - want[g]))
