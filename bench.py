@@ -74,6 +74,9 @@ def main() -> int:
                     help="profiling workload: only the roofline kernel's graph (36 layers x q/k/v, o, gate+up), "
                          "warmup + steps replays, the same graph bench.py times for `roofline`; prints one line "
                          "to stderr")
+    ap.add_argument("--f32-workload", action="store_true",
+                    help="eager launches for rocprofv3: one token of the config-1 linears with fp32 x (the "
+                         "activation dtype of the reference's unchanged model code), then the same with bf16 x")
     ap.add_argument("--moe-workload", type=int, default=0, metavar="T",
                     help="eager launches for rocprofv3: the config-3 expert MLP (jh_moe_swiglu, Qwen3-30B-A3B "
                          "experts, top-8) at T tokens over 4 layers' expert stacks, 3 passes")
@@ -86,7 +89,7 @@ def main() -> int:
 
     import torch
 
-    from janis_amd.engine import BF16, I32, U32, HipBackend
+    from janis_amd.engine import BF16, F32, I32, U32, HipBackend
 
     dev = torch.device("cuda:0")
     torch.manual_seed(1234)
@@ -117,6 +120,17 @@ def main() -> int:
     x_h, x_attn, x_ffn = bf16((1, HIDDEN)), bf16((1, HIDDEN)), bf16((1, INTER))
     ys = {name: bf16((1, n), randn=False) for name, (n, k) in shapes.items()}
     y_head = bf16((1, VOCAB), randn=False)
+
+    def f32(shape, randn=True):
+        t = torch.randn(shape, device=dev) if randn else torch.empty(shape, device=dev)
+        return hip.Wrap(t.data_ptr(), shape, F32, keep=t)
+
+    # fp32 activations, the dtype janis's unchanged model code hands the products
+    # (Dequantize returns F32 and every operator keeps its input's dtype)
+    xin32 = {"qkv": f32((1, HIDDEN)), "o": f32((1, HIDDEN)), "gate_up": None, "down": f32((1, INTER))}
+    xin32["gate_up"] = xin32["qkv"]
+    ys32 = {name: f32((1, n), randn=False) for name, (n, k) in shapes.items()}
+    y_head32 = f32((1, VOCAB), randn=False)
     torch.cuda.synchronize()
     log(f"weights ready in {time.time() - t0:.1f}s")
     xin = {"qkv": x_h, "o": x_attn, "gate_up": x_h, "down": x_ffn}
@@ -130,6 +144,12 @@ def main() -> int:
             for name in ("qkv", "o", "gate_up", "down"):
                 launch(name, L[name], xin[name], ys[name])
         launch("lm_head", head, x_h, y_head)
+
+    def sequence_f32():
+        for L in layers:
+            for name in ("qkv", "o", "gate_up", "down"):
+                launch(name, L[name], xin32[name], ys32[name])
+        launch("lm_head", head, xin32["qkv"], y_head32)
 
     bytes_layer = sum(qbytes(n, k) for n, k in shapes.values())
     bytes_token = LAYERS * bytes_layer + qbytes(VOCAB, HIDDEN)
@@ -184,6 +204,15 @@ def main() -> int:
             launch("lm_head", head, x_h, y_head)
         torch.cuda.synchronize()
         log("shapes workload done")
+        hip.Close()
+        return 0
+
+    if args.f32_workload:
+        hip.SetStream(torch.cuda.current_stream().cuda_stream)
+        sequence_f32()
+        sequence()
+        torch.cuda.synchronize()
+        log("f32 workload done")
         hip.Close()
         return 0
 
@@ -255,6 +284,16 @@ def main() -> int:
     gbs = bytes_token / (ms_step * 1e-3) / 1e9
     tok_s = 1000.0 / ms_step
     log(f"sequence: {ms_step * 1e3:.1f} us/token, {gbs:.0f} GB/s, {tok_s:.0f} tok/s")
+    # the same token with fp32 x and fp32 y (x rounded to bf16 in the tiles' registers)
+    g_f32 = capture(sequence_f32)
+    ms_f32 = time_graph(g_f32, args.steps, args.warmup)
+    del g_f32
+    bytes_f32 = bytes_token + LAYERS * sum(2 * (n + k) for n, k in shapes.values()) + 2 * (VOCAB + HIDDEN)
+    f32_line = {"us_per_token": round(ms_f32 * 1e3, 1), "tok_s": round(1000.0 / ms_f32, 1),
+                "GB_s": round(bytes_f32 / (ms_f32 * 1e-3) / 1e9, 1), "vs_bf16_x": round(ms_step / ms_f32, 4),
+                "note": "config 1 with fp32 x and y (the dtype flow of the reference's unchanged model code); "
+                        "algorithmic bytes count the 4-byte x and y"}
+    log("sequence, fp32 x:", f32_line)
 
     # ---- per shape, rotating through the 36 layer copies (defeats the 256 MB cache) -------
     per_shape = {}
@@ -326,7 +365,8 @@ def main() -> int:
                 "launches_per_step": n_dom, "avg_launch_us": round(ms_dom * 1e3 / n_dom, 3),
                 "algorithmic_bytes_per_launch": bytes_dom // n_dom}
 
-    extra = {"per_shape": per_shape, "per_shape_8bit": per_shape_8, "launches_per_token": n_launch,
+    extra = {"config1_f32_x": f32_line, "per_shape": per_shape, "per_shape_8bit": per_shape_8,
+             "launches_per_token": n_launch,
              "bytes_per_token": bytes_token, "hbm_measured": floors["hbm"],
              "read_floors": floors["floors"]}
 
@@ -515,6 +555,36 @@ def decode_step_figures(hip, torch, dev, capture, time_graph, args, contexts=(51
                             "GB_s": round((weights + kv) / (ms * 1e-3) / 1e9, 1), "kv_bytes": kv,
                             "launches_per_token": launches}
         del g
+    # The reference's own call sequence (qwen/block.go, qwen/attention.go,
+    # qwen/mlp.go, qwen/cache.go: one engine call per operator, F32 activations,
+    # KVCache.Update's cast to F16 caches) at the smallest context, in a graph:
+    # what unchanged janis model code gets through the plain binding.
+    import copy
+
+    from janis_amd.engine import F16
+    ctx = min(contexts)
+    m16 = copy.copy(m)
+    m16.layers = []
+    for L in m.layers:
+        L2 = copy.copy(L)
+        for name in ("k_cache", "v_cache"):
+            t = getattr(L, name)._keep[:, :, :ctx + 8].to(torch.float16).contiguous()
+            setattr(L2, name, hip.Wrap(t.data_ptr(), tuple(t.shape), F16, keep=t))
+        m16.layers.append(L2)
+    torch.cuda.synchronize()
+
+    def ref_calls():
+        with hip.use_arena(arena):
+            decode_step(hip, m16, tt, ctx, fused=False)
+    g = capture(ref_calls, keep=True)
+    launches = graph_kernel_nodes(g.raw_cuda_graph())
+    ms = time_graph(g, max(5, args.steps // 4), 3)
+    kv = cfg.layers * 2 * Hk * (ctx + 1) * Dh * 2
+    res[f"ctx{ctx}_reference_calls_f32_f16cache"] = {
+        "us_per_token": round(ms * 1e3, 1), "tok_s": round(1000.0 / ms, 1),
+        "GB_s": round((weights + kv) / (ms * 1e-3) / 1e9, 1), "launches_per_token": launches,
+        "note": "decode_step(fused=False): the reference's operator calls one by one with its dtype flow"}
+    del g, m16
     log("decode step:", res)
     del m, arena
     torch.cuda.empty_cache()

@@ -66,31 +66,54 @@ __global__ __launch_bounds__(256) void qmv_rows_kernel(
     // every row's part of x as (x_p, x_{p+4}) pairs, and its group sums
     uint32_t xp[MR][ITERS][16];
     float xs[MR][ITERS];
+    if constexpr (XF32) {
+        // fp32 rows: each wave reads its K part of a row with consecutive lanes
+        // on consecutive 16 bytes, rounds it to bf16 (nearest even) into LDS and
+        // takes its runs from there (as the one-row tile does), row after row
+        constexpr uint32_t XE = 8 * PK;  // elements of a wave's K part
+        constexpr int XC = (int)((XE / 4 + 63) / 64);
+        __shared__ uint2 xstage[4 * (XE / 4)];
+        uint2* xw = xstage + wv_id * (XE / 4);
+        auto cvt2 = [](uint32_t u, uint32_t v) {
+            return (uint32_t)f32_to_bf16_hw(__uint_as_float(u)) | ((uint32_t)f32_to_bf16_hw(__uint_as_float(v)) << 16);
+        };
 #pragma unroll
-    for (int m = 0; m < MR; m++)
+        for (int m = 0; m < MR; m++) {
+            const uint32_t base = (m * K + ks * XE) * 4;
+            u32x4_t c4[XC];
 #pragma unroll
-        for (int it = 0; it < ITERS; it++) {
-            const uint32_t off = (m * K + 8 * wo[it]) * XB;
-            float sum = 0.0f;
+            for (int c = 0; c < XC; c++)
+                c4[c] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + (uint32_t)(c * 64 + lane) * 16, 0, 0);
+            if (m > 0) __syncthreads();  // the previous row's runs are read
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                uint4 xb;
-                if constexpr (XF32) {
-                    const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 32 * j, 0, 0);
-                    const u32x4_t b = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 32 * j + 16, 0, 0);
-                    auto cvt2 = [](uint32_t u, uint32_t v) {
-                        return (uint32_t)f32_to_bf16_hw(__uint_as_float(u)) |
-                               ((uint32_t)f32_to_bf16_hw(__uint_as_float(v)) << 16);
-                    };
-                    xb = make_uint4(cvt2(a.x, a.y), cvt2(a.z, a.w), cvt2(b.x, b.y), cvt2(b.z, b.w));
-                } else {
-                    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16 * j, 0, 0);
-                    xb = make_uint4(v.x, v.y, v.z, v.w);
-                }
-                sum += pair_up(xb, &xp[m][it][4 * j]);
+            for (int c = 0; c < XC; c++)
+                if ((uint32_t)(c * 64 + lane) < XE / 4)
+                    xw[c * 64 + lane] = make_uint2(cvt2(c4[c].x, c4[c].y), cvt2(c4[c].z, c4[c].w));
+            __syncthreads();
+#pragma unroll
+            for (int it = 0; it < ITERS; it++) {
+                const uint4* src = reinterpret_cast<const uint4*>(xw + (8 * (wo[it] - ks * PK)) / 4);
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; j++) sum += pair_up(src[j], &xp[m][it][4 * j]);
+                xs[m][it] = sum;
             }
-            xs[m][it] = sum;
         }
+    } else {
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+#pragma unroll
+            for (int it = 0; it < ITERS; it++) {
+                const uint32_t off = (m * K + 8 * wo[it]) * 2;
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16 * j, 0, 0);
+                    sum += pair_up(make_uint4(v.x, v.y, v.z, v.w), &xp[m][it][4 * j]);
+                }
+                xs[m][it] = sum;
+            }
+    }
 
     const uint32_t lane_row = rg * ROWS_PER_WAVE + (uint32_t)slice * RPW;
     for (uint32_t bbase = blockIdx.x * ROWS_PER_BLOCK; bbase < N; bbase += gridDim.x * ROWS_PER_BLOCK) {

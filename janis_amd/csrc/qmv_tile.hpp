@@ -96,9 +96,14 @@ __device__ __forceinline__ void store_rows(void* Y, int y_dt, uint32_t row0, uin
 //                the partials (loaded ahead of the weights), and the epilogue
 //                scales as PRO_RMSNORM does, so x costs what a plain one does.
 //   PRO_XF32     x is fp32 [K] (the activation type of the CPU backend and of
-//                Dequantize): each lane rounds its part of x to bf16 (nearest
-//                even) in registers and the tile runs as PRO_NONE on it, so the
-//                result has the bits of a bf16-x call on bf16(x).
+//                Dequantize), rounded to bf16 (nearest even) and then used as
+//                PRO_NONE uses its x, so the result has the bits of a bf16-x
+//                call on bf16(x). A lane's 32-element run is 128 bytes of fp32:
+//                read lane by lane that is 8 loads with a 128-byte lane stride
+//                (4x the cache lines of the bf16 loads). Instead each wave reads
+//                its K part with consecutive lanes on consecutive 16 bytes,
+//                rounds it to bf16 into LDS, and every lane takes its run from
+//                there, as it would from a bf16 x.
 //   EPI_RESID_NORM  EPI_RESID, plus the next norm's input: nout[row] =
 //                bf16(y * nw[row]) and, per block, the sum of y^2 over its rows
 //                in stats[blockIdx.x] (grid <= kNormSlots; block 0 zeroes the
@@ -221,8 +226,20 @@ __device__ __forceinline__ void qmv_tile(
     constexpr int XW = PRO == PRO_RMSNORM ? 8 : (int)EPW / 2;  // 16-byte chunks of them
     uint4 xraw[ITERS][XW];
     uint4 xaux[ITERS][4];  // norm weights (PRO_RMSNORM)
-    constexpr int XF = PRO == PRO_XF32 ? (int)EPW : 1;  // PRO_XF32: fp32 x, 16-byte chunks
-    uint4 xf32[ITERS][XF];
+    // PRO_XF32: the wave's K part of x (EPW * PK elements) in 16-byte chunks,
+    // chunk c read by lane c % 64, and its bf16 copy in LDS (one region per wave)
+    constexpr uint32_t XE = EPW * PK;                            // fp32 elements of a wave's K part
+    constexpr int XC = PRO == PRO_XF32 ? (int)((XE / 4 + 63) / 64) : 1;  // chunks per lane
+    uint4 xf32[XC];
+    __shared__ uint2 xstage[PRO == PRO_XF32 ? 4 * (XE / 4) : 1];  // 4 waves x XE bf16
+    if constexpr (PRO == PRO_XF32) {
+        const auto rxf = make_rsrc(static_cast<const float*>(Xv) + ks * XE, XE * 4);
+#pragma unroll
+        for (int c = 0; c < XC; c++) {
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rxf, (uint32_t)(c * 64 + lane) * 16, 0, 0);
+            xf32[c] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+    }
 #pragma unroll
     for (int it = 0; it < ITERS; it++) {
         const uint32_t e0 = EPW * wo[it];
@@ -231,9 +248,7 @@ __device__ __forceinline__ void qmv_tile(
 #pragma unroll
             for (int j = 0; j < 8; j++) xraw[it][j] = xv[j];
         } else if constexpr (PRO == PRO_XF32) {
-            const uint4* xv = reinterpret_cast<const uint4*>(static_cast<const float*>(Xv) + e0);
-#pragma unroll
-            for (int j = 0; j < XF; j++) xf32[it][j] = xv[j];
+            // taken from LDS after the weights are requested
         } else {
             const uint4* xv = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(Xv) + e0);
 #pragma unroll
@@ -274,17 +289,23 @@ __device__ __forceinline__ void qmv_tile(
             if (lane == 0) ssq[wv_id] = ss_part;
     }
     if constexpr (PRO == PRO_XF32) {
-        // fp32 x to bf16 pairs (nearest even), in the layout a bf16 x loads as
+        // fp32 chunks to bf16 (nearest even) in the wave's LDS region, then each
+        // lane's runs in the layout a bf16 x loads as
         auto cvt2 = [](uint32_t a, uint32_t b) {
             return (uint32_t)f32_to_bf16_hw(__uint_as_float(a)) | ((uint32_t)f32_to_bf16_hw(__uint_as_float(b)) << 16);
         };
+        uint2* xw = xstage + wv_id * (XE / 4);
 #pragma unroll
-        for (int it = 0; it < ITERS; it++)
+        for (int c = 0; c < XC; c++)
+            if ((uint32_t)(c * 64 + lane) < XE / 4)
+                xw[c * 64 + lane] = make_uint2(cvt2(xf32[c].x, xf32[c].y), cvt2(xf32[c].z, xf32[c].w));
+        __syncthreads();
 #pragma unroll
-            for (int j = 0; j < XW; j++) {
-                const uint4 a = xf32[it][2 * j], b = xf32[it][2 * j + 1];
-                xraw[it][j] = make_uint4(cvt2(a.x, a.y), cvt2(a.z, a.w), cvt2(b.x, b.y), cvt2(b.z, b.w));
-            }
+        for (int it = 0; it < ITERS; it++) {
+            const uint4* src = reinterpret_cast<const uint4*>(xw + (EPW * (wo[it] - ks * PK)) / 4);
+#pragma unroll
+            for (int j = 0; j < XW; j++) xraw[it][j] = src[j];
+        }
     }
     float xs8[ITERS];  // 8-bit: the sum of the real inputs
     if constexpr (BITS == 8) {
