@@ -386,6 +386,10 @@ __device__ __forceinline__ void store_out(void* y, int dt, int64_t i, float v) {
 // order. Out is written once (fp32 or bf16), so nothing clears it first, and
 // the order is fixed. A token with an expert index outside [0, E) gets NaN.
 // Rows per block = (64 / LPR) * RPW; K (the down's in_features) = 32 * LPR * ITERS.
+// The h rows and the scores do not depend on the expert indices: they are
+// requested together with the indices, ahead of the weights, so the only
+// dependent round trip is index -> weights (when a lane's h chunks fit in
+// registers, SPW * ITERS <= 6; longer rows load them slot by slot as before).
 template <int LPR, int ITERS, int RPW, bool SB_F16, int SPW>
 __global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeArgs a, void* __restrict__ out, int out_dt) {
     constexpr int NW = 4;
@@ -405,12 +409,37 @@ __global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeArgs a, void* 
     for (int it = 0; it < ITERS; it++) wo[it] = it * 4 * LPR + 4 * sl;
     int64_t es[SPW];
     bool bad = false;
+    int32_t eraw[SPW];
+#pragma unroll
+    for (int j = 0; j < SPW; j++) {
+        const int64_t k = (int64_t)w * SPW + j;
+        eraw[j] = k < a.k_slots ? a.idx[t * a.k_slots + k] : -1;
+    }
+    // the slots' h chunks and scores, in flight with the indices
+    constexpr bool PRELOAD = SPW * ITERS <= 6;
+    uint4 xh[PRELOAD ? SPW : 1][PRELOAD ? ITERS : 1][4];
+    float score[SPW];
+#pragma unroll
+    for (int j = 0; j < SPW; j++) {
+        const int64_t k = (int64_t)w * SPW + j;
+        const int64_t pair = t * a.k_slots + (k < a.k_slots ? k : 0);
+        score[j] = a.scores[pair];
+        if constexpr (PRELOAD) {
+            const uint16_t* xr = a.x + pair * K;
+#pragma unroll
+            for (int it = 0; it < ITERS; it++) {
+                const uint4* xv = reinterpret_cast<const uint4*>(xr + 8 * wo[it]);
+#pragma unroll
+                for (int q = 0; q < 4; q++) xh[j][it][q] = xv[q];
+            }
+        }
+    }
 #pragma unroll
     for (int j = 0; j < SPW; j++) {
         const int64_t k = (int64_t)w * SPW + j;
         es[j] = -1;
         if (k < a.k_slots) {
-            const int64_t e = a.idx[t * a.k_slots + k];
+            const int64_t e = eraw[j];
             if (e < 0 || e >= a.E) bad = true;
             else es[j] = e;
         }
@@ -455,9 +484,14 @@ __global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeArgs a, void* 
         for (int r = 0; r < RPW; r++) part[r] = 0.0f;
 #pragma unroll
         for (int it = 0; it < ITERS; it++) {
-            const uint4* xv = reinterpret_cast<const uint4*>(xr + 8 * wo[it]);
+            uint4 x0, x1, x2, x3;
+            if constexpr (PRELOAD) {
+                x0 = xh[j][it][0], x1 = xh[j][it][1], x2 = xh[j][it][2], x3 = xh[j][it][3];
+            } else {
+                const uint4* xv = reinterpret_cast<const uint4*>(xr + 8 * wo[it]);
+                x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
+            }
             uint32_t xp[16];
-            const uint4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
             const float xs = (pair_up(x0, &xp[0]) + pair_up(x1, &xp[4])) + (pair_up(x2, &xp[8]) + pair_up(x3, &xp[12]));
 #pragma unroll
             for (int r = 0; r < RPW; r++) {
@@ -472,9 +506,8 @@ __global__ __launch_bounds__(256) void moe_down_combine_kernel(MoeArgs a, void* 
                 part[r] = fmaf(fmaf(-kCodeOffset, sc, bi), xs, part[r]);
             }
         }
-        const float score = a.scores[pair];
 #pragma unroll
-        for (int r = 0; r < RPW; r++) acc[r] += score * slice_sum_last<LPR>(part[r]);
+        for (int r = 0; r < RPW; r++) acc[r] += score[j] * slice_sum_last<LPR>(part[r]);
     }
     if (sl == LPR - 1)
 #pragma unroll
