@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # WRITE_SIZE over `bench.py --pmc-workload`, each scaled by what the counter reads
 # for a 256 MiB copy in the same run (FETCH_SIZE x2.0, WRITE_SIZE x1.0). Re-measure
 # after changing the kernel; the summary sits in profiles/.
-DOMINANT_TRAFFIC_BYTES = 26916846
+DOMINANT_TRAFFIC_BYTES = 26918717
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 HIDDEN, INTER, VOCAB, LAYERS, GS = 4096, 12288, 151936, 36, 64
 
@@ -80,6 +80,10 @@ def main() -> int:
     ap.add_argument("--moe-workload", type=int, default=0, metavar="T",
                     help="eager launches for rocprofv3: the config-3 expert MLP (jh_moe_swiglu, Qwen3-30B-A3B "
                          "experts, top-8) at T tokens over 4 layers' expert stacks, 3 passes")
+    ap.add_argument("--ceiling-workload", action="store_true",
+                    help="profiling workload: the launch-ceiling measurements only (empty-kernel graph nodes, "
+                         "re-reads after a 1 GiB read of other memory, the 2 GiB read and 1 GiB copy); prints "
+                         "them to stderr")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this backend is measured on one GPU; --gpus N > 1 is not "
@@ -184,6 +188,12 @@ def main() -> int:
         e1.record(st)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps  # ms per replay
+
+    if args.ceiling_workload:
+        res = memory_floors(torch, dev, capture, time_graph, {})
+        log("ceiling workload:", json.dumps(res))
+        hip.Close()
+        return 0
 
     if args.decode_step:
         res = decode_step_figures(hip, torch, dev, capture, time_graph, args, contexts=(args.decode_step,))
@@ -368,7 +378,7 @@ def main() -> int:
     extra = {"config1_f32_x": f32_line, "per_shape": per_shape, "per_shape_8bit": per_shape_8,
              "launches_per_token": n_launch,
              "bytes_per_token": bytes_token, "hbm_measured": floors["hbm"],
-             "read_floors": floors["floors"]}
+             "read_floors": floors["floors"], "launch_ceiling": floors["ceiling"]}
 
     if not args.quick:
         extra.update(prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args))
@@ -415,7 +425,8 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
     # prefill: gate_up 4096->12288 and down 12288->4096 at M in {128, 512, 2048}
     pre = {}
     for name, (n, k) in {"gate_up": (12288, 4096), "down": (4096, 12288)}.items():
-        copies = [qweight(n, k) for _ in range(4)]
+        # 24 copies (680 MB) rotated, more than the 256 MB memory-side cache holds
+        copies = [qweight(n, k) for _ in range(24)]
         for m in (128, 512, 2048):
             x = bf16((m, k))
             y = bf16((m, n), randn=False)
@@ -445,7 +456,9 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
     # MoE: Qwen3-30B-A3B experts (E=128, hidden 2048, inter 768), top-8
     E, H, I, K = 128, 2048, 768, 8
     moe = {}
-    nl = 8  # rotate 8 layers of experts (8 x 340 MB) to defeat the cache
+    # 32 layers of expert stacks (32 x 340 MB) rotated: even batch 1 (8 experts,
+    # 21 MB per layer) then touches 680 MB, more than the 256 MB memory-side cache
+    nl = 32
     stacks = [{"gate": qweight(I, H, (E,)), "up": qweight(I, H, (E,)), "down": qweight(H, I, (E,))}
               for _ in range(nl)]
     for T in (1, 16):
@@ -607,7 +620,9 @@ def memory_floors(torch, dev, capture, time_graph, sizes):
     L.jhb_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                            ctypes.c_void_p]
     L.jhb_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
-    L.jhb_read.restype = L.jhb_copy.restype = ctypes.c_int
+    L.jhb_read_cached.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    L.jhb_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    L.jhb_read.restype = L.jhb_copy.restype = L.jhb_read_cached.restype = L.jhb_empty.restype = ctypes.c_int
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     pool_bytes = 2 << 30
     pool = torch.empty(pool_bytes, dtype=torch.uint8, device=dev).fill_(7)
@@ -634,6 +649,7 @@ def memory_floors(torch, dev, capture, time_graph, sizes):
                     best = (ms, bpc, unroll)
         floors[name] = {"bytes": nb, "us": round(best[0] * 1e3, 2), "GB_s": round(nb / (best[0] * 1e-3) / 1e9, 1),
                         "blocks_per_cu": best[1], "loads_in_flight_per_lane": best[2], "launches_timed": n}
+    ceiling = ceiling_figures(torch, L, pool, sink, capture, time_graph, cus)
     # whole-buffer read and copy
     g = capture(lambda: reads(pool_bytes, 4 * cus, 8, 1))
     ms_read = time_graph(g, 10, 3)
@@ -654,7 +670,69 @@ def memory_floors(torch, dev, capture, time_graph, sizes):
            "note": "1 GiB device copy (read + write bytes / time) and a 2 GiB read, one launch each, "
                    "janis_amd/csrc/bench_kernels.hip; the roofline's peak stays the 8 TB/s specification"}
     log("hbm measured:", hbm, "read floors:", floors)
-    return {"hbm": hbm, "floors": floors}
+    return {"hbm": hbm, "floors": floors, "ceiling": ceiling}
+
+
+def ceiling_figures(torch, L, pool, sink, capture, time_graph, cus):
+    """What bounds one launch per linear, measured with bench.py's own kernels:
+    - graph_node_us: a graph of 64 dependent launches of an empty kernel (1 and
+      256 blocks), time per launch -- the fixed cost each extra kernel adds;
+    - reread: a buffer of S bytes read three times in a row right after a 1 GiB
+      read of other memory (which leaves none of it in the 256 MB memory-side
+      cache): the first two reads with one cache policy (non-temporal, as the
+      decode products load weights, or the default), the third non-temporal.
+      Events around each launch, median of 5 rounds. A second or third read
+      faster than the first means that cache served it."""
+    st = torch.cuda.current_stream().cuda_stream
+
+    def chk(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: {rc}")
+
+    nodes = {}
+    for blocks in (1, 256):
+        g = capture(lambda blocks=blocks: [chk(L.jhb_empty(blocks, torch.cuda.current_stream().cuda_stream), "jhb_empty")
+                                           for _ in range(64)])
+        nodes[f"blocks_{blocks}"] = round(time_graph(g, 20, 5) * 1e3 / 64, 3)
+        del g
+    base = pool.data_ptr()
+    flush_off = 1 << 30
+
+    def read(off, nb, nt):
+        if nt:
+            chk(L.jhb_read(base + off, nb, sink.data_ptr(), 4 * cus, 8, st), "jhb_read")
+        else:
+            chk(L.jhb_read_cached(base + off, nb, sink.data_ptr(), 4 * cus, st), "jhb_read_cached")
+
+    reread = {}
+    for mb in (48, 160):
+        nb = mb << 20
+        for nt in (True, False):
+            t1, t2, t3 = [], [], []
+            for _ in range(5):
+                read(flush_off, 1 << 30, True)
+                read(flush_off, 1 << 30, False)
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+                ev[0].record()
+                read(0, nb, nt)
+                ev[1].record()
+                read(0, nb, nt)
+                ev[2].record()
+                read(0, nb, True)
+                ev[3].record()
+                torch.cuda.synchronize()
+                t1.append(ev[0].elapsed_time(ev[1]) * 1e3)
+                t2.append(ev[1].elapsed_time(ev[2]) * 1e3)
+                t3.append(ev[2].elapsed_time(ev[3]) * 1e3)
+            med = [sorted(t)[2] for t in (t1, t2, t3)]
+            reread[f"{mb}MB_{'nt' if nt else 'default'}"] = {
+                "first_us": round(med[0], 2), "second_us": round(med[1], 2), "third_nt_us": round(med[2], 2),
+                "first_TB_s": round(nb / med[0] / 1e6, 2), "third_TB_s": round(nb / med[2] / 1e6, 2)}
+    out = {"graph_node_us": nodes, "reread": reread,
+           "note": "empty-kernel graph nodes; re-reads after a 1 GiB read of other memory "
+                   "(janis_amd/csrc/bench_kernels.hip)"}
+    log("ceiling:", out)
+    return out
 
 
 def host_info() -> dict:

@@ -2,7 +2,10 @@
 // backend's C ABI): a plain streaming read and a copy of device memory. They do
 // nothing but move bytes, so their time for a given byte count is the floor a
 // decode product reading that many bytes in one launch can reach, and the copy
-// gives the device's measured bandwidth beside the 8 TB/s specification.
+// gives the device's measured bandwidth beside the 8 TB/s specification. An
+// empty kernel gives the fixed cost of one node of a HIP graph, and the read
+// with the default cache policy (the decode products' weight loads are
+// non-temporal) shows whether the memory-side cache serves a re-read.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -15,7 +18,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // any is used (the way the decode tiles issue a pass's weight loads), and
 // strides over the buffer by the grid. The loaded words are folded into one
 // value that is stored only if it equals a constant, so the loads stay.
-template <int UNROLL>
+template <int UNROLL, bool NT = true>
 __global__ __launch_bounds__(256) void read_kernel(const u32x4* __restrict__ src, int64_t n16,
                                                    uint32_t* __restrict__ sink) {
     u32x4 acc = {0u, 0u, 0u, 0u};
@@ -25,7 +28,10 @@ __global__ __launch_bounds__(256) void read_kernel(const u32x4* __restrict__ src
 #pragma unroll
         for (int u = 0; u < UNROLL; u++) {
             const int64_t i = base + (int64_t)u * 256;
-            v[u] = i < n16 ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+            if constexpr (NT)
+                v[u] = i < n16 ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+            else
+                v[u] = i < n16 ? src[i] : u32x4{0u, 0u, 0u, 0u};
         }
 #pragma unroll
         for (int u = 0; u < UNROLL; u++) acc ^= v[u];
@@ -52,6 +58,8 @@ __global__ __launch_bounds__(256) void copy_kernel(u32x4* __restrict__ dst, cons
     }
 }
 
+__global__ void empty_kernel() {}
+
 }  // namespace
 
 extern "C" {
@@ -70,6 +78,22 @@ __attribute__((visibility("default"))) int jhb_read(const void* src, int64_t byt
     else if (unroll == 8) hipLaunchKernelGGL(read_kernel<8>, dim3(blocks), dim3(256), 0, st, s, n16, k);
     else if (unroll == 16) hipLaunchKernelGGL(read_kernel<16>, dim3(blocks), dim3(256), 0, st, s, n16, k);
     else return (int)hipErrorInvalidValue;
+    return (int)hipGetLastError();
+}
+
+// jhb_read with the default cache policy (8 loads per lane in flight).
+__attribute__((visibility("default"))) int jhb_read_cached(const void* src, int64_t bytes, void* sink, int blocks,
+                                                           void* stream) {
+    if (bytes <= 0 || (bytes & 15) || ((uintptr_t)src & 15) || blocks <= 0) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL((read_kernel<8, false>), dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const u32x4*>(src), bytes / 16, static_cast<uint32_t*>(sink));
+    return (int)hipGetLastError();
+}
+
+// One launch of an empty kernel with `blocks` blocks of 64 threads.
+__attribute__((visibility("default"))) int jhb_empty(int blocks, void* stream) {
+    if (blocks <= 0) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(64), 0, static_cast<hipStream_t>(stream));
     return (int)hipGetLastError();
 }
 
