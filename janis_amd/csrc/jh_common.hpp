@@ -262,16 +262,27 @@ Status launch_norm_prepare(const void* x, int x_dt, int64_t d, const void* w, in
                            hipStream_t st);
 // out = bf16(u / sqrt(sum(stats) / d + eps)).
 Status launch_norm_apply(const uint16_t* u, int64_t d, const float* stats, float eps, uint16_t* out, hipStream_t st);
+// What a launch that waits for other blocks of its own grid needs: zeroed
+// counters (nullptr: no such launch), the poll bound and the host-visible
+// status word a wait that gives up sets.
+struct InLaunchSync {
+    int* counters;
+    uint32_t spin;
+    int* status;
+};
 // A few bf16 or fp32 x rows (2..kQmvRowsMax, fewer for long rows) through the decode
 // tiles, the weights read once per launch of 2, 4 or 8 rows.
 constexpr int64_t kQmvRowsMax = 8;
 bool qmv_rows_ok(const QuantMatrix& m, int64_t rows, int x_dtype);
 Status launch_qmv_rows(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y, int y_dtype,
                        int num_cus, hipStream_t st);
+// `sync.counters` (the kQmmSyncSlot share, or nullptr) lets the split-K partial
+// tiles be added inside the product's launch (see qmm.hip).
 Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y,
-                  int y_dtype, int num_cus, hipStream_t st, void* workspace);
+                  int y_dtype, int num_cus, hipStream_t st, void* workspace, InLaunchSync sync = {});
 // fp32 accumulation buffer a split-K prefill needs (0 when none).
-size_t qmm_workspace_bytes(const QuantMatrix& m, int64_t rows, int x_dtype, int y_dtype, int num_cus);
+size_t qmm_workspace_bytes(const QuantMatrix& m, int64_t rows, int x_dtype, int y_dtype, int num_cus,
+                           bool in_launch = false);
 
 struct GatherArgs {
     QuantMatrix m;        // one expert's shape; w/scales/biases point at expert 0
@@ -329,7 +340,7 @@ size_t attn_decode_workspace_bytes(int64_t Hq, int64_t Hk, int64_t pos, int num_
 // partials be merged inside the attention launch when the GPU deals workgroups
 // to its 8 XCDs round-robin (probe_xcd_round_robin) and the kv heads are a
 // multiple of 8; otherwise a merge launch follows.
-constexpr int kAttnSyncSlots = 4096 + 64;
+constexpr int kAttnSyncSlots = 4096 + 64 + 32 * 512;
 // The fused q/k/v + attention launch's share of them: per XCD x, the arrival
 // flags of its blocks at kAttnFlagSlot + 128 x (zero between calls).
 constexpr int kAttnFlagSlot = 1024;
@@ -340,6 +351,10 @@ constexpr int kArgmaxSyncSlot = 2048, kArgmaxSyncRows = 2048;
 // The fused launch's give-up markers, one per XCD (zero until a wait gives up;
 // reset by the host, see jh_sync).
 constexpr int kAttnMarkerSlot = 4096;
+// The split-K prefill product's share: the arrival counter of output tile t at
+// kQmmSyncSlot + 32 t (one 128-byte line each) for kQmmSyncTiles tiles (zero
+// between calls).
+constexpr int kQmmSyncSlot = 4096 + 64, kQmmSyncTiles = 512;
 // Polls of the arrival flags before a fused launch's wait gives up (the default
 // of jh_set_wait_limit).
 constexpr uint32_t kDefaultWaitPolls = 1u << 22;

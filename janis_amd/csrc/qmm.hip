@@ -29,7 +29,9 @@
 //   A[i = l % 32][k = 8*(l/32) .. +8]  and  B[k = 8*(l/32) .. +8][j = l % 32],
 // and accumulator register r of lane l holds D[8*(r/4) + 4*(l/32) + r%4][l % 32].
 // When the tile grid is too small to fill the GPU, K is split over blockIdx.z:
-// each K range stores its fp32 partial tile and one pass adds them in order.
+// each K range stores its fp32 partial tile and one pass adds them in order --
+// inside the product's launch when its blocks are all resident at once
+// (qmm_dma_kernel, INL), else a summing launch.
 #include "jh_common.hpp"
 
 namespace jh {
@@ -656,11 +658,65 @@ constexpr int dma_loads_after(int u) {
     return n;
 }
 
-template <bool SPLIT, int SBT, int GSL, int NW, int A, int RB = RBM>  // RB: rows of X per block, 32 | 64 | 128 | 256
+// The split-K partial tiles added inside the product's launch (INL): the S
+// blocks of one output tile (blockIdx.z = 0 .. S-1) run on one XCD (the grid's
+// x·y is a multiple of 8 and the GPU deals blocks to its 8 XCDs round-robin)
+// and all blocks of the grid are resident at once (at most one per CU). Each
+// stores its partial tile, counts its arrival in the tile's counter in the
+// XCD's L2, waits until all S have arrived, then adds rows z·RB/S .. of the S
+// partials (device-coherent loads from the L2) in split order -- the summing
+// launch's order, so the same bits -- and stores them into Y. A second count
+// per block tells the last one to reset the counter for the next call. The
+// wait is bounded: a block that gives up stores NaN for its rows and sets the
+// status word the library reports at the next synchronisation.
+template <int S, int RB, int RBN, int NT>
+__device__ __forceinline__ void split_tile_sum(const float* acc_out, size_t ss, void* Y, int y_dt, uint32_t M,
+                                               uint32_t N, uint32_t mb, uint32_t nb, bool gave_up) {
+    constexpr int C4 = RBN / 4, Q = RB / (8 * S);  // float4 items per thread
+    static_assert(Q >= 1 && (RB / S) * C4 == Q * NT, "rows per share x columns / threads");
+    const auto rp = make_rsrc(acc_out, (uint32_t)(S * ss * 4));
+    const int tid = threadIdx.x;
+    u32x4_t v[Q][S];
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int idx = tid + NT * q;
+        const uint32_t m = mb + idx / C4, n = nb + 4 * (idx % C4);
+        const bool in = m < M && n < N;
+#pragma unroll
+        for (int s = 0; s < S; s++)
+            v[q][s] = in ? __builtin_amdgcn_raw_buffer_load_b128(rp, (uint32_t)((s * ss + (size_t)m * N + n) * 4), 0,
+                                                                 kAuxSc1)
+                         : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int idx = tid + NT * q;
+        const uint32_t m = mb + idx / C4, n = nb + 4 * (idx % C4);
+        if (m >= M || n >= N) continue;
+        float4 a = make_float4(__uint_as_float(v[q][0].x), __uint_as_float(v[q][0].y), __uint_as_float(v[q][0].z),
+                               __uint_as_float(v[q][0].w));
+#pragma unroll
+        for (int s = 1; s < S; s++) {
+            a.x += __uint_as_float(v[q][s].x), a.y += __uint_as_float(v[q][s].y);
+            a.z += __uint_as_float(v[q][s].z), a.w += __uint_as_float(v[q][s].w);
+        }
+        if (gave_up) a = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+        const size_t o = (size_t)m * N + n;
+        if (y_dt == JH_F32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(Y) + o) = a;
+        } else {
+            const uint32_t lo = (uint32_t)f32_to_bf16_hw(a.x) | ((uint32_t)f32_to_bf16_hw(a.y) << 16);
+            const uint32_t hi = (uint32_t)f32_to_bf16_hw(a.z) | ((uint32_t)f32_to_bf16_hw(a.w) << 16);
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(Y) + o) = make_uint2(lo, hi);
+        }
+    }
+}
+
+template <bool SPLIT, int SBT, int GSL, int NW, int A, int RB = RBM, bool INL = false>  // RB: rows of X per block, 32 | 64 | 128 | 256
 __global__ __launch_bounds__(64 * NW, RB == 256 ? 1 : 2) void qmm_dma_kernel(
     const uint32_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ B,
     const void* __restrict__ X, void* __restrict__ Y, int y_dt, uint32_t M, uint32_t N, uint32_t K,
-    uint32_t k_per_split, float* __restrict__ acc_out) {
+    uint32_t k_per_split, float* __restrict__ acc_out, InLaunchSync sy) {
     constexpr int SUP = 256, SPS = SUP / 64, R = A + 1;
     static_assert(A >= 1 && A <= SPS, "the scale/bias ring has two super-step slots");
     constexpr int RBN = 32 * NW;
@@ -809,6 +865,41 @@ __global__ __launch_bounds__(64 * NW, RB == 256 ? 1 : 2) void qmm_dma_kernel(
             }
         }
     }
+    if constexpr (INL) {
+        static_assert(SPLIT && RB <= 128, "in-launch sums of split tiles of up to 128 rows");
+        // the block's partial stores are in the XCD's L2 (they write through the
+        // CU's L1) before its arrival is counted
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const int nsplit = (int)gridDim.z;
+        int* const cnt = sy.counters + 32 * (blockIdx.x + gridDim.x * blockIdx.y);
+        // the rings are idle now (every wave is past its last step and its loads
+        // have landed): their first word carries the wait's outcome
+        int& gave_up_s = *reinterpret_cast<int*>(lds);
+        if (tid == 0) {
+            __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            bool seen = false;
+            for (uint32_t n = 0; n < sy.spin; n++)
+                if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= nsplit) {
+                    seen = true;
+                    break;
+                }
+            if (!seen) __hip_atomic_store(sy.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            gave_up_s = !seen;
+        }
+        __syncthreads();
+        const bool gave_up = gave_up_s != 0;
+        const size_t ss = split_stride(M, N);
+        const uint32_t nb = blockIdx.x * RBN;
+        const uint32_t mb = blockIdx.y * RB + blockIdx.z * (uint32_t)(RB / nsplit);
+        if (nsplit == 2) split_tile_sum<2, RB, RBN, 64 * NW>(acc_out, ss, Y, y_dt, M, N, mb, nb, gave_up);
+        else if (nsplit == 4) split_tile_sum<4, RB, RBN, 64 * NW>(acc_out, ss, Y, y_dt, M, N, mb, nb, gave_up);
+        else if constexpr (RB >= 64) split_tile_sum<8, RB, RBN, 64 * NW>(acc_out, ss, Y, y_dt, M, N, mb, nb, gave_up);
+        // every thread's partial loads have returned (their sums are stored)
+        __syncthreads();
+        if (tid == 0 && __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 2 * nsplit - 1)
+            __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 }  // namespace
@@ -842,9 +933,22 @@ struct QmmPlan {
     int lead;  // steps of lead of the LDS-ring tile; 0: the register tile
     int rb;    // rows of X per block (LDS-ring tile: 32 or 64 up to 64 rows, 128 or 256 beyond)
     int64_t split;
+    bool inl;  // the split's partial tiles are added inside the launch
     uint32_t k_per_split;
     dim3 grid;
 };
+
+// Whether an LDS-ring plan's split partials can be added inside its launch:
+// 128-row blocks, every block resident at once (at most one per CU), the S
+// blocks of a tile on one XCD (x·y a multiple of 8), a counter per tile, each
+// block's share a whole number of 4-column items per thread, and the partials
+// within a buffer resource's 2 GiB.
+bool qmm_inl_fits(int64_t M, int64_t N, int nw, int rb, int64_t split, int num_cus) {
+    if (rb != 128 || split < 2 || split > 8 || N % 4 != 0) return false;
+    const int64_t rbn = 32 * nw, tiles = ((N + rbn - 1) / rbn) * ((M + rb - 1) / rb);
+    return tiles % 8 == 0 && tiles <= kQmmSyncTiles && tiles * split <= num_cus / 8 * 8 &&
+           (size_t)split * split_stride((uint32_t)M, (uint32_t)N) * 4 < ((size_t)1 << 31);
+}
 
 // Modelled microseconds of one LDS-ring plan (see above).
 double qmm_dma_cost(int64_t M, int64_t N, int64_t nsup, int nw, int lead, int rb, int64_t split, int num_cus) {
@@ -898,7 +1002,7 @@ double qmm_wreg_cost(int64_t M, int64_t N, int64_t nsup, int nw, int64_t split, 
     return t;
 }
 
-QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus, bool dma) {
+QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus, bool dma, bool inl_ok = false) {
     QmmPlan p{};
     if (m.in % 256 == 0) {
         p.wreg = true;
@@ -920,6 +1024,13 @@ QmmPlan qmm_plan(const QuantMatrix& m, int64_t rows, int num_cus, bool dma) {
                     if (p.nw == 0 || t < best) best = t, p.nw = nw, p.lead = lead, p.rb = rb, p.split = split;
                 }
             }
+            // a 4-wave plan's partials of a 4- or 8-way split are added inside its
+            // launch where they can be: timed on MI355X against the summing launch
+            // for the Qwen3-8B projections at M = 65 .. 512, 0.1 to 5.4 us faster for
+            // every plan the model picks (o_proj at M = 128: 15.4 against 20.8 us);
+            // 2-way splits came out within +-0.8 us and 8-wave blocks up to 3.7 us
+            // slower, so they keep the summing launch
+            p.inl = inl_ok && p.nw == 4 && p.split >= 4 && qmm_inl_fits(rows, m.rows, p.nw, p.rb, p.split, num_cus);
         } else {
             for (int nw : {8, 4, 6})
                 for (int64_t split = 1; split <= (nw == 4 ? 8 : 4) && (split == 1 || nsup / split >= 2); split *= 2) {
@@ -973,10 +1084,11 @@ bool qmm_uses_mfma(const QuantMatrix& m, int64_t rows, int x_dtype) {
            (m.rows + 256) * (m.in / 2) < ((int64_t)1 << 31) && (rows + 512) * m.in * xb < ((int64_t)1 << 31);
 }
 
-size_t qmm_workspace_bytes(const QuantMatrix& m, int64_t rows, int x_dtype, int y_dtype, int num_cus) {
+size_t qmm_workspace_bytes(const QuantMatrix& m, int64_t rows, int x_dtype, int y_dtype, int num_cus,
+                           bool in_launch) {
     (void)y_dtype;
     if (!qmm_uses_mfma(m, rows, x_dtype)) return 0;
-    const QmmPlan p = qmm_plan(m, rows, num_cus, qmm_dma_ok(m, x_dtype));
+    const QmmPlan p = qmm_plan(m, rows, num_cus, qmm_dma_ok(m, x_dtype), in_launch);
     const size_t xconv = p.wreg && p.lead > 0 && x_dtype == JH_F32 ? qmm_xconv_bytes(rows, m.in) : 0;
     return xconv + (p.split == 1 ? 0 : sizeof(float) * (size_t)p.split * split_stride((uint32_t)rows, (uint32_t)m.rows));
 }
@@ -1002,18 +1114,18 @@ void launch_tile_wreg(const QuantMatrix& m, const void* x, int64_t rows, void* y
         by_gs(std::integral_constant<int, 0>{});
 }
 
-template <int NW, int A, bool SPLIT, int RB = RBM>
+template <int NW, int A, bool SPLIT, int RB = RBM, bool INL = false>
 void launch_tile_dma(const QuantMatrix& m, const void* x, int64_t rows, void* y, int y_dtype, int gl,
-                     uint32_t k_per_split, float* acc, dim3 grid, hipStream_t st) {
+                     uint32_t k_per_split, float* acc, dim3 grid, hipStream_t st, InLaunchSync sy = {}) {
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, grid, dim3(64 * NW), 0, st, m.w, m.scales, m.biases, x, y, y_dtype,
-                           (uint32_t)rows, (uint32_t)m.rows, (uint32_t)m.in, k_per_split, acc);
+                           (uint32_t)rows, (uint32_t)m.rows, (uint32_t)m.in, k_per_split, acc, sy);
     };
     auto by_gs = [&](auto sbt) {
         constexpr int SBT = decltype(sbt)::value;
-        if (gl == 5) go(qmm_dma_kernel<SPLIT, SBT, 5, NW, A, RB>);
-        else if (gl == 6) go(qmm_dma_kernel<SPLIT, SBT, 6, NW, A, RB>);
-        else if constexpr (SBT == 2) go(qmm_dma_kernel<SPLIT, SBT, 7, NW, A, RB>);
+        if (gl == 5) go(qmm_dma_kernel<SPLIT, SBT, 5, NW, A, RB, INL>);
+        else if (gl == 6) go(qmm_dma_kernel<SPLIT, SBT, 6, NW, A, RB, INL>);
+        else if constexpr (SBT == 2) go(qmm_dma_kernel<SPLIT, SBT, 7, NW, A, RB, INL>);
     };
     if (m.sb_dtype == JH_F32)
         by_gs(std::integral_constant<int, 2>{});
@@ -1039,11 +1151,11 @@ void launch_tile(const QuantMatrix& m, const void* x, int64_t rows, void* y, int
 }
 
 Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y,
-                  int y_dtype, int num_cus, hipStream_t st, void* workspace) {
+                  int y_dtype, int num_cus, hipStream_t st, void* workspace, InLaunchSync sync) {
     if (!qmm_uses_mfma(m, rows, x_dtype)) return launch_generic(m, x, x_dtype, rows, y, y_dtype, num_cus, st);
     const int gl = log2_exact(m.group_size);
     const bool dma = qmm_dma_ok(m, x_dtype);
-    const QmmPlan p = qmm_plan(m, rows, num_cus, dma);
+    const QmmPlan p = qmm_plan(m, rows, num_cus, dma, sync.counters != nullptr);
     const bool xf32 = x_dtype == JH_F32;
     char* ws = static_cast<char*>(workspace);
     if (p.wreg && p.lead > 0 && xf32) {
@@ -1097,10 +1209,19 @@ Status launch_qmm(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows
         return Status::ok();
     }
     // split K: each K range stores its fp32 partial tile into its own slice of
-    // the workspace, and one pass adds the slices in order into y
+    // the workspace, and the slices are added in order into y, inside the launch
+    // or by a pass of its own
     float* acc = reinterpret_cast<float*>(ws);
     if (!acc) return Status::fail(JH_ERR_INVALID, "qmm: split-K needs a workspace");
     const int64_t n = rows * m.rows;
+    if (p.inl && (reinterpret_cast<uintptr_t>(y) & (y_dtype == JH_F32 ? 15 : 7)) == 0) {
+        // (qmm_inl_fits holds for the plan; y takes whole 4-column items)
+        if (p.lead == 3)
+            launch_tile_dma<4, 3, true, 128, true>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st, sync);
+        else
+            launch_tile_dma<4, 1, true, 128, true>(m, x, rows, y, y_dtype, gl, p.k_per_split, acc, p.grid, st, sync);
+        return Status::ok();
+    }
     tile(std::true_type{}, acc);
     hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)std::min<int64_t>((n / 4 + 255) / 256 + 1, 4096)), dim3(256),
                        0, st, acc, (int)p.split, n, y, y_dtype);

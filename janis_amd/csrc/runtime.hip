@@ -159,6 +159,14 @@ int check_quant(jh_ctx* c, const char* op, const uint32_t* w, const void* s, con
 // round-robin workgroup placement (else nullptr: merges are launches of their own).
 int* xcd_sync(const jh_ctx* c) { return c->stream_xcd_ok ? c->attn_sync : nullptr; }
 
+// What a split-K prefill product needs to add its partial tiles inside its own
+// launch (counters nullptr: a summing launch follows instead).
+jh::InLaunchSync qmm_sync(const jh_ctx* c) {
+    int* sync = xcd_sync(c);
+    if (!sync || !c->wait_status) return {};
+    return {sync + jh::kQmmSyncSlot, c->wait_polls, c->wait_status};
+}
+
 // After the stream's work is done: a fused launch whose in-kernel wait gave up
 // left its status word set. Its heads' outputs are NaN; the flags and markers it
 // left are reset here (the stream is idle) and the failure is reported.
@@ -171,10 +179,11 @@ int check_wait_status(jh_ctx* c, const char* op) {
         if (e != hipSuccess) return hip_fail(c, e, "resetting the in-launch synchronisation state");
     }
     return fail(c, JH_ERR_TIMEOUT,
-                std::string(op) + ": a jh_qkv_attention_decode launch gave up waiting for its own blocks (were "
-                                  "other kernels holding the GPU's CUs?); the attention outputs of that call and of "
-                                  "the fused calls after it on this context until now are NaN. The synchronisation "
-                                  "state was reset: the next call runs normally.");
+                std::string(op) + ": a launch that waits for its own blocks (jh_qkv_attention_decode, or a "
+                                  "split-K jh_quant_matmul) gave up waiting (were other kernels holding the GPU's "
+                                  "CUs?); the outputs it could not finish are NaN (attention heads of that call and "
+                                  "of the fused calls after it on this context until now; rows of the product). The "
+                                  "synchronisation state was reset: the next call runs normally.");
 }
 
 int check_act_dtype(jh_ctx* c, const char* op, const char* what, int dt) {
@@ -537,10 +546,13 @@ int jh_quant_matmul(jh_ctx* c, const void* x, jh_dtype x_dtype, int64_t rows, co
     else if (jh::qmv_rows_ok(m, rows, x_dtype))
         r = finish(c, jh::launch_qmv_rows(m, x, x_dtype, rows, y, y_dtype, c->num_cus, c->stream), "qmv_rows");
     else {
-        const size_t need = jh::qmm_workspace_bytes(m, rows, x_dtype, y_dtype, c->num_cus);
+        const jh::InLaunchSync sy = qmm_sync(c);
+        if (sy.counters)
+            if (int e = check_wait_status(c, op)) return e;
+        const size_t need = jh::qmm_workspace_bytes(m, rows, x_dtype, y_dtype, c->num_cus, sy.counters != nullptr);
         if (need)
             if (int e = ensure_workspace(c, need, op)) return e;
-        r = finish(c, jh::launch_qmm(m, x, x_dtype, rows, y, y_dtype, c->num_cus, c->stream, c->ws), "qmm");
+        r = finish(c, jh::launch_qmm(m, x, x_dtype, rows, y, y_dtype, c->num_cus, c->stream, c->ws, sy), "qmm");
     }
     if (r) return r;
     return check_values(c, op, y, y_dtype, rows * out_features);

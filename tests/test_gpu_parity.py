@@ -422,6 +422,52 @@ def test_qmm_split_k_is_deterministic(hip, out_dtype):
         assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,n,k,out_dtype", [
+    (128, 4096, 4096, BF16),    # o_proj: 4 waves, K split 8, 32 tiles x 8 blocks
+    (128, 6144, 4096, F32),     # q/k/v: K split 4
+    (96, 4096, 12288, BF16),    # down_proj: K split 8, rows 96..127 of the tile empty
+    (200, 4096, 4096, F32),     # two row tiles, the second ragged: K split 4
+])
+def test_qmm_split_sums_in_launch(hip, oracle, m, n, k, out_dtype):
+    """Plans whose split partial tiles are added inside the product's launch
+    (every block resident, a tile's splits on one XCD): the oracle on a random
+    block of the output, identical bits on a repeat; then, with a wait bound of 0
+    polls (jh_set_wait_limit), every block gives up its wait at once (each kernel
+    still exits normally): the output is all NaN, the next synchronisation
+    reports JH_ERR_TIMEOUT and resets the counters, and the next call with the
+    default bound has the first call's bits."""
+    from janis_amd import _lib
+
+    q = synth.quant_linear(61 + m + n, n, k)
+    xb, x = synth.activations(62 + m, (m, k))
+    w, s, b = upload_quant(hip, q)
+    xt = hip.FromBF16Bits(xb, m, k)
+    step(f"jh_quant_matmul in-launch split sums M={m} N={n} K={k} out={out_dtype}")
+    y0 = hip.Floats(hip.QuantMatmul(xt, w, s, b, True, 64, 4, out_dtype=out_dtype))
+    rng = np.random.default_rng(m + n + k)
+    rs = np.sort(np.concatenate([rng.choice(m - 1, size=min(31, m - 1), replace=False), [m - 1]]))
+    cs = np.sort(np.concatenate([rng.choice(n - 1, size=63, replace=False), [n - 1]]))
+    want = oracle.quant_matmul(x[rs], q.w[cs], q.s[cs], q.b[cs], 64)
+    ok, d, sc = rel_ok(y0[np.ix_(rs, cs)], want, BF16_TOL if out_dtype == BF16 else 5e-3)
+    assert ok, (d, sc)
+    y1 = hip.Floats(hip.QuantMatmul(xt, w, s, b, True, 64, 4, out_dtype=out_dtype))
+    assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
+    try:
+        hip.SetWaitLimit(0)
+        step("the same call with a wait bound of 0 polls")
+        yn = hip.QuantMatmul(xt, w, s, b, True, 64, 4, out_dtype=out_dtype)
+        with pytest.raises(JanisHipError) as ei:
+            hip.Sync()
+        assert ei.value.code == _lib.JH_ERR_TIMEOUT, str(ei.value)
+        assert np.isnan(hip.Floats(yn)).all()
+        hip.Sync()  # reported once, then reset
+    finally:
+        hip.SetWaitLimit(1 << 22)
+    step("the next call, default bound")
+    y2 = hip.Floats(hip.QuantMatmul(xt, w, s, b, True, 64, 4, out_dtype=out_dtype))
+    assert np.array_equal(y0.view(np.uint32), y2.view(np.uint32))
+
+
 @pytest.mark.parametrize("rows,n,k", [(128, 12288, 4096), (4, 4096, 4096)])
 def test_quant_matmul_graph_replays(hip, oracle, rows, n, k):
     """Captured once into a HIP graph (after one eager call, which sizes the
