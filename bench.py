@@ -61,6 +61,9 @@ def main() -> int:
     ap.add_argument("--decode-step", type=int, default=0, metavar="CTX",
                     help="profiling workload: only the config-4 decode step at context CTX (graph "
                          "replays, warmup + steps); prints one line to stderr")
+    ap.add_argument("--fused-only", action="store_true",
+                    help="with --decode-step: skip the reference's unfused call sequence (profiles of the fused "
+                         "step alone)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="eager launches for rocprofv3 --pmc: a 256 MiB copy (counter calibration), "
                          "then one pass of the dominant kernel's launches; prints nothing else")
@@ -568,6 +571,11 @@ def decode_step_figures(hip, torch, dev, capture, time_graph, args, contexts=(51
                             "GB_s": round((weights + kv) / (ms * 1e-3) / 1e9, 1), "kv_bytes": kv,
                             "launches_per_token": launches}
         del g
+    if getattr(args, "fused_only", False):
+        log("decode step:", res)
+        del m, arena
+        torch.cuda.empty_cache()
+        return {"qwen3_8b_decode_step": res}
     # The reference's own call sequence (qwen/block.go, qwen/attention.go,
     # qwen/mlp.go, qwen/cache.go: one engine call per operator, F32 activations,
     # KVCache.Update's cast to F16 caches) at the smallest context, in a graph:
