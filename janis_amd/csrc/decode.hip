@@ -990,7 +990,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, co
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(a.sync + hk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+        last = __hip_atomic_fetch_add(a.sync + hk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                a.nsplit - 1;
     __syncthreads();
     if (!last) return;
@@ -1072,7 +1072,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int split, co
         }
     }
     if (threadIdx.x == 0) {
-        __hip_atomic_store(a.sync + hk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_store(a.sync + hk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // every block of the XCD has arrived and every attention block's wait saw
     // every flag set: the flags start the next call at zero (after a wait that
