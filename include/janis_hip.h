@@ -62,8 +62,9 @@ enum {
     JH_ERR_HIP = 3,         /* the HIP runtime reported an error */
     JH_ERR_OOM = 4,         /* device allocation failed */
     JH_ERR_NONFINITE = 5,   /* value checks on (JH_CHECK_VALUES): the result holds NaN/Inf */
-    JH_ERR_TIMEOUT = 6      /* a jh_qkv_attention_decode launch gave up waiting for its own blocks
-                               (reported by the next jh_sync / jh_d2h / fused call; see there) */
+    JH_ERR_TIMEOUT = 6      /* a launch that waits for its own blocks (jh_qkv_attention_decode, a
+                               split-K jh_quant_matmul) gave up (reported by the next jh_sync /
+                               jh_d2h / fused call / split-K call; see jh_set_wait_limit) */
 };
 
 typedef struct jh_ctx jh_ctx;
@@ -91,19 +92,23 @@ JH_API int jh_device_info(jh_ctx *ctx, char *name, size_t name_len, int *compute
 
 /* Enqueue on a caller-owned hipStream_t instead of the context's own stream
  * (NULL restores the context's stream). The caller keeps the stream alive.
- * The attention merges inside one launch (jh_attention_decode,
- * jh_qkv_attention_decode) need workgroups dealt to the 8 XCDs round-robin,
- * which jh_create checks; a stream whose CU mask leaves any CU out
+ * The exchanges inside one launch (the attention merges of
+ * jh_attention_decode and jh_qkv_attention_decode, the split-K sums of
+ * jh_quant_matmul's prefill product) need workgroups dealt to the 8 XCDs
+ * round-robin, which jh_create checks; a stream whose CU mask leaves any CU out
  * (hipExtStreamCreateWithCUMask) runs them as separate launches instead. */
 JH_API int jh_set_stream(jh_ctx *ctx, void *hip_stream);
 
-/* Bound on the in-kernel wait of jh_qkv_attention_decode's attention blocks
- * for the product blocks of their XCD, in polls of the arrival flags (default
- * 2^22, far beyond a normal wait of about a microsecond). When a wait gives up
- * the call's attention output is NaN and the next jh_sync / jh_d2h (or fused
- * call) returns JH_ERR_TIMEOUT and resets the synchronisation state. 0 makes
- * every wait give up at once: the failure path, for tests. No counterpart in
- * the reference: a safety bound of this backend's fused launch. */
+/* Bound on the in-kernel waits, in polls: of jh_qkv_attention_decode's
+ * attention blocks for the product blocks of their XCD, and of a split-K
+ * prefill product's blocks for the other K splits of their output tile
+ * (default 2^22, far beyond a normal wait of about a microsecond). When a wait
+ * gives up, the outputs it guards are NaN (the call's attention output; the
+ * product's rows of that block) and the next jh_sync / jh_d2h (or fused or
+ * split-K call) returns JH_ERR_TIMEOUT and resets the synchronisation state.
+ * 0 makes every wait give up at once: the failure path, for tests. No
+ * counterpart in the reference: a safety bound of this backend's launches that
+ * wait for their own blocks. */
 JH_API int jh_set_wait_limit(jh_ctx *ctx, int64_t polls);
 
 /* The hipStream_t operators are enqueued on. */
@@ -138,8 +143,8 @@ JH_API int jh_check_finite(jh_ctx *ctx, const void *x, jh_dtype dtype, int64_t n
                            int64_t *first);
 
 /* Waits for every operator enqueued on the context's stream. Returns
- * JH_ERR_TIMEOUT if a jh_qkv_attention_decode launch since the last check gave
- * up its in-kernel wait (see jh_set_wait_limit); jh_d2h does the same. */
+ * JH_ERR_TIMEOUT if a launch since the last check gave up its in-kernel wait
+ * (see jh_set_wait_limit); jh_d2h does the same. */
 JH_API int jh_sync(jh_ctx *ctx);
 
 /* Device memory (hipMalloc / hipFree). jh_free(NULL) is a no-op. */
@@ -202,7 +207,11 @@ JH_API int jh_dequantize(jh_ctx *ctx, const uint32_t *w, const void *scales, con
  * tiles run a generic kernel that multiplies fp32 x unrounded.
  * When the prefill GEMM splits K, its fp32 partial products go to the
  * context's workspace (grown to split * rows * out_features floats) and are
- * added in a fixed order: results are the same bits on every call. The GEMM
+ * added in a fixed order: results are the same bits on every call. Where the
+ * product's blocks all fit on the GPU at once, the sums are made inside its
+ * launch, whose blocks then wait for each other (bounded: jh_set_wait_limit);
+ * split-K calls on one GPU must then be serialised and not run beside kernels
+ * that hold its CUs, as for jh_qkv_attention_decode. The GEMM
  * multiplies x rounded to bf16: fp32 x is first rounded into the workspace
  * (rows * in_features bf16 more), so fp32 x gives the bits of its bf16
  * rounding passed as bf16. */
