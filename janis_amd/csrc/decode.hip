@@ -1191,11 +1191,13 @@ __global__ __launch_bounds__(256) void qkv_attn_kernel(QkvAttnArgs f) {
     });
 }
 
-// Workgroup -> XCD placement: out[b] = the XCD (XCC id) block b runs on.
+// Workgroup -> XCD placement: out[b] = the XCD (XCC id) block b runs on, b the
+// block's index in dispatch order (x fastest, then y, then z).
 __global__ __launch_bounds__(64) void xcc_probe_kernel(int* out) {
     unsigned x;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
-    if (threadIdx.x == 0) out[blockIdx.x] = (int)(x & 0xFu);
+    const unsigned b = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    if (threadIdx.x == 0) out[b] = (int)(x & 0xFu);
 }
 
 // ---- elementwise -----------------------------------------------------------------
@@ -1679,14 +1681,17 @@ Status launch_qkv_attn(const QuantMatrix& m, const uint16_t* x, float* stats, fl
 }
 
 int probe_xcd_round_robin(int* buf, hipStream_t st) {
+    // a 1-D grid (the attention launches) and a 3-D one (the split-K product:
+    // x by columns, y by rows, z by K split)
     constexpr int kBlocks = 64;
     hipLaunchKernelGGL(xcc_probe_kernel, dim3(kBlocks), dim3(64), 0, st, buf);
-    int h[kBlocks];
+    hipLaunchKernelGGL(xcc_probe_kernel, dim3(4, 2, 8), dim3(64), 0, st, buf + kBlocks);
+    int h[2 * kBlocks];
     if (hipMemcpyAsync(h, buf, sizeof h, hipMemcpyDeviceToHost, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
         (void)hipGetLastError();
         return 0;
     }
-    for (int b = 0; b < kBlocks; b++)
+    for (int b = 0; b < 2 * kBlocks; b++)
         if (h[b] != b % 8) return 0;
     return 8;
 }
