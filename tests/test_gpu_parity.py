@@ -427,6 +427,8 @@ def test_qmm_split_k_is_deterministic(hip, out_dtype):
     (128, 6144, 4096, F32),     # q/k/v: K split 4
     (96, 4096, 12288, BF16),    # down_proj: K split 8, rows 96..127 of the tile empty
     (200, 4096, 4096, F32),     # two row tiles, the second ragged: K split 4
+    (100, 4000, 4096, BF16),    # N ragged (the last column tile 32 wide): K split 8
+    (130, 2000, 4096, F32),     # M and N ragged (a row tile of 2 rows): K split 8
 ])
 def test_qmm_split_sums_in_launch(hip, oracle, m, n, k, out_dtype):
     """Plans whose split partial tiles are added inside the product's launch
