@@ -630,7 +630,10 @@ def memory_floors(torch, dev, capture, time_graph, sizes):
     L.jhb_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
     L.jhb_read_cached.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     L.jhb_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    L.jhb_barriers.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint,
+                               ctypes.c_void_p, ctypes.c_void_p]
     L.jhb_read.restype = L.jhb_copy.restype = L.jhb_read_cached.restype = L.jhb_empty.restype = ctypes.c_int
+    L.jhb_barriers.restype = ctypes.c_int
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     pool_bytes = 2 << 30
     pool = torch.empty(pool_bytes, dtype=torch.uint8, device=dev).fill_(7)
@@ -685,6 +688,10 @@ def ceiling_figures(torch, L, pool, sink, capture, time_graph, cus):
     """What bounds one launch per linear, measured with bench.py's own kernels:
     - graph_node_us: a graph of 64 dependent launches of an empty kernel (1 and
       256 blocks), time per launch -- the fixed cost each extra kernel adds;
+    - grid_barrier_us: a grid-wide barrier inside one launch (one block per CU,
+      a counter in memory; relaxed, and with release/acquire ordering, which is
+      what a persistent kernel needs between dependent stages on different
+      XCDs), time per barrier;
     - reread: a buffer of S bytes read three times in a row right after a 1 GiB
       read of other memory (which leaves none of it in the 256 MB memory-side
       cache): the first two reads with one cache policy (non-temporal, as the
@@ -736,9 +743,31 @@ def ceiling_figures(torch, L, pool, sink, capture, time_graph, cus):
             reread[f"{mb}MB_{'nt' if nt else 'default'}"] = {
                 "first_us": round(med[0], 2), "second_us": round(med[1], 2), "third_nt_us": round(med[2], 2),
                 "first_TB_s": round(nb / med[0] / 1e6, 2), "third_TB_s": round(nb / med[2] / 1e6, 2)}
-    out = {"graph_node_us": nodes, "reread": reread,
-           "note": "empty-kernel graph nodes; re-reads after a 1 GiB read of other memory "
-                   "(janis_amd/csrc/bench_kernels.hip)"}
+    # grid-wide barriers inside one launch (one 64-thread block per CU): the
+    # per-stage synchronisation a persistent kernel would pay instead of a graph
+    # node; time per barrier = (64-round launch - 1-round launch) / 63, median of 5
+    cnt = torch.zeros(16, dtype=torch.int32, device=pool.device)
+    barrier = {}
+    for ordered in (0, 1):
+        per = []
+        failed = False
+        for _ in range(5):
+            ts = []
+            for rounds in (1, 64):
+                cnt.zero_()
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+                ev[0].record()
+                chk(L.jhb_barriers(cnt.data_ptr(), cus, rounds, ordered, 1 << 22, cnt.data_ptr() + 32, st),
+                    "jhb_barriers")
+                ev[1].record()
+                torch.cuda.synchronize()
+                failed |= int(cnt[8].item()) != 0
+                ts.append(ev[0].elapsed_time(ev[1]) * 1e3)
+            per.append((ts[1] - ts[0]) / 63)
+        barrier["acq_rel" if ordered else "relaxed"] = None if failed else round(sorted(per)[2], 3)
+    out = {"graph_node_us": nodes, "grid_barrier_us": barrier, "reread": reread,
+           "note": "empty-kernel graph nodes; grid-wide barriers inside one launch (one block per CU); "
+                   "re-reads after a 1 GiB read of other memory (janis_amd/csrc/bench_kernels.hip)"}
     log("ceiling:", out)
     return out
 

@@ -60,6 +60,42 @@ __global__ __launch_bounds__(256) void copy_kernel(u32x4* __restrict__ dst, cons
 
 __global__ void empty_kernel() {}
 
+// `rounds` grid-wide barriers in one launch: in each round every block adds 1
+// to a counter (agent scope) and polls it until the round's blocks have all
+// arrived -- the synchronisation a persistent kernel running dependent stages
+// pays per stage. ORDERED: release on the add and acquire on the polls (what
+// makes one stage's global writes visible to the next stage on other XCDs);
+// otherwise relaxed (the atomic round trips alone). The grid must be resident
+// at once (one 64-thread block per CU); the polls are bounded, and a block
+// that gives up sets *failed and stops.
+template <bool ORDERED>
+__global__ __launch_bounds__(64) void barrier_kernel(unsigned* counter, int rounds, unsigned spin, unsigned* failed) {
+    __shared__ int stop;
+    if (threadIdx.x == 0) stop = 0;
+    __syncthreads();
+    for (int r = 1; r <= rounds && !stop; r++) {
+        if (threadIdx.x == 0) {
+            if constexpr (ORDERED)
+                __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            else
+                __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned target = (unsigned)r * gridDim.x;
+            unsigned n = 0;
+            for (;;) {
+                const unsigned v = ORDERED ? __hip_atomic_load(counter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT)
+                                           : __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (v >= target) break;
+                if (++n > spin) {
+                    __hip_atomic_fetch_or(failed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    stop = 1;
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -94,6 +130,21 @@ __attribute__((visibility("default"))) int jhb_read_cached(const void* src, int6
 __attribute__((visibility("default"))) int jhb_empty(int blocks, void* stream) {
     if (blocks <= 0) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(64), 0, static_cast<hipStream_t>(stream));
+    return (int)hipGetLastError();
+}
+
+// One launch of `blocks` 64-thread blocks passing `rounds` grid-wide barriers
+// on *counter (which must be 0; it ends at rounds * blocks), ordered
+// (release/acquire) or relaxed; *failed is set if a block gave up waiting
+// (after `spin` polls). blocks must not exceed the CU count.
+__attribute__((visibility("default"))) int jhb_barriers(void* counter, int blocks, int rounds, int ordered,
+                                                        unsigned spin, void* failed, void* stream) {
+    if (!counter || !failed || blocks <= 0 || rounds < 0) return (int)hipErrorInvalidValue;
+    auto st = static_cast<hipStream_t>(stream);
+    auto c = static_cast<unsigned*>(counter);
+    auto f = static_cast<unsigned*>(failed);
+    if (ordered) hipLaunchKernelGGL(barrier_kernel<true>, dim3(blocks), dim3(64), 0, st, c, rounds, spin, f);
+    else hipLaunchKernelGGL(barrier_kernel<false>, dim3(blocks), dim3(64), 0, st, c, rounds, spin, f);
     return (int)hipGetLastError();
 }
 
