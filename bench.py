@@ -308,28 +308,33 @@ def main() -> int:
                         "algorithmic bytes count the 4-byte x and y"}
     log("sequence, fp32 x:", f32_line)
 
-    # ---- per shape, rotating through the 36 layer copies (defeats the 256 MB cache) -------
+    # ---- per shape, rotating at least 64 distinct copies and 600 MB (the 256 MB ----------
+    # memory-side cache cannot hold them): the 36 layers' copies plus fresh ones
+    def n_rotate(n, k):
+        return max(64, -(-600_000_000 // qbytes(n, k)))
+
     per_shape = {}
     for name, (n, k) in shapes.items():
-        g = capture(lambda name=name: [launch(name, L[name], xin[name], ys[name]) for L in layers])
-        ms = time_graph(g, max(5, args.steps // 2), 3) / LAYERS
+        ws = [L[name] for L in layers] + [qweight(n, k) for _ in range(n_rotate(n, k) - LAYERS)]
+        g = capture(lambda name=name, ws=ws: [launch(name, w, xin[name], ys[name]) for w in ws])
+        ms = time_graph(g, max(5, args.steps // 2), 3) / len(ws)
         per_shape[name] = {"N": n, "K": k, "us": round(ms * 1e3, 2),
-                           "GB_s": round(qbytes(n, k) / (ms * 1e-3) / 1e9, 1)}
-        del g
+                           "GB_s": round(qbytes(n, k) / (ms * 1e-3) / 1e9, 1), "copies_rotated": len(ws)}
+        del g, ws
     g = capture(lambda: launch("lm_head", head, x_h, y_head))
     ms = time_graph(g, max(5, args.steps // 2), 3)
     per_shape["lm_head"] = {"N": VOCAB, "K": HIDDEN, "us": round(ms * 1e3, 2),
                             "GB_s": round(qbytes(VOCAB, HIDDEN) / (ms * 1e-3) / 1e9, 1)}
     del g
     # q_proj and k_proj / v_proj as the reference's separate linears (config 1 times
-    # each shape separately), 36 copies each
+    # each shape separately), rotated the same way
     for name, (n, k) in {"q_proj": (HIDDEN, HIDDEN), "k_proj": (1024, HIDDEN)}.items():
-        copies = [qweight(n, k) for _ in range(LAYERS)]
+        copies = [qweight(n, k) for _ in range(n_rotate(n, k))]
         yq = bf16((1, n), randn=False)
         g = capture(lambda copies=copies, yq=yq: [hip.QuantMatmul(x_h, *c, True, GS, 4, out=yq) for c in copies])
-        ms = time_graph(g, max(5, args.steps // 2), 3) / LAYERS
+        ms = time_graph(g, max(5, args.steps // 2), 3) / len(copies)
         per_shape[name] = {"N": n, "K": k, "us": round(ms * 1e3, 2),
-                           "GB_s": round(qbytes(n, k) / (ms * 1e-3) / 1e9, 1)}
+                           "GB_s": round(qbytes(n, k) / (ms * 1e-3) / 1e9, 1), "copies_rotated": len(copies)}
         if name == "k_proj":
             per_shape[name]["note"] = "v_proj has the same shape"
         del g, copies
@@ -341,20 +346,20 @@ def main() -> int:
         v["vs_floor"] = round(v["us"] / f["us"], 3)
     log("per shape:", per_shape)
 
-    # ---- the same shapes with 8-bit codes (MLX's other affine width), 8 copies each -----
+    # ---- the same shapes with 8-bit codes (MLX's other affine width), rotated as above --
     per_shape_8 = {}
     for name, (n, k) in shapes.items():
-        copies = [qweight(n, k, bits=8) for _ in range(8)]
+        copies = [qweight(n, k, bits=8) for _ in range(max(64, -(-600_000_000 // qbytes(n, k, 8))))]
         g = capture(lambda name=name, copies=copies: [
             hip.QuantMatmul(xin[name], w, s_, b_, True, GS, 8, out=ys[name]) for (w, s_, b_) in copies])
         ms = time_graph(g, max(5, args.steps // 2), 3) / len(copies)
         per_shape_8[name] = {"N": n, "K": k, "us": round(ms * 1e3, 2),
-                             "GB_s": round(qbytes(n, k, 8) / (ms * 1e-3) / 1e9, 1)}
+                             "GB_s": round(qbytes(n, k, 8) / (ms * 1e-3) / 1e9, 1), "copies_rotated": len(copies)}
         del g, copies
     torch.cuda.synchronize()
     log("per shape, 8-bit:", per_shape_8)
 
-    # ---- dominant kernel: the K=4096 GEMV tile (qkv, o, gate_up; 74% of the step) -------
+    # ---- dominant kernel: the K=4096 GEMV tile (qkv, o, gate_up; ~69% of the step) -----
     # Events bracket a graph of exactly that kernel's launches, back to back, in the
     # sequence's order; achieved = their algorithmic bytes / their time per launch.
     dom_names = ("qkv", "o", "gate_up")
@@ -617,7 +622,8 @@ def memory_floors(torch, dev, capture, time_graph, sizes):
     a 1 GiB device copy and a 2 GiB read (the device's bandwidth beside the 8 TB/s
     specification), and for each byte count in `sizes` the fastest single launch that
     only reads that many bytes -- a graph of launches over distinct windows of a 2 GiB
-    buffer (no window re-read while in the 256 MB last-level cache), best of 1/2/4
+    buffer (at least 64 windows and 600 MB where the buffer holds them, so the 256 MB
+    memory-side cache cannot serve them), best of 1/2/4
     blocks per CU and 4/8/16 loads per lane in flight. That is the floor a decode
     product of those bytes can reach in one launch."""
     import ctypes
@@ -649,7 +655,7 @@ def memory_floors(torch, dev, capture, time_graph, sizes):
     floors = {}
     for name, nbytes in sizes.items():
         nb = (int(nbytes) + 255) // 256 * 256
-        n = max(1, min(36, pool_bytes // nb))
+        n = max(1, min(pool_bytes // nb, max(64, -(-600_000_000 // nb))))
         best = None
         for bpc in (1, 2, 4):
             for unroll in (4, 8, 16):
