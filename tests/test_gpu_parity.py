@@ -470,13 +470,15 @@ def test_qmm_split_sums_in_launch(hip, oracle, m, n, k, out_dtype):
     assert np.array_equal(y0.view(np.uint32), y2.view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,n,k", [(128, 12288, 4096), (4, 4096, 4096)])
+@pytest.mark.parametrize("rows,n,k", [(128, 12288, 4096), (128, 4096, 4096), (4, 4096, 4096)])
 def test_quant_matmul_graph_replays(hip, oracle, rows, n, k):
     """Captured once into a HIP graph (after one eager call, which sizes the
     workspace) and replayed on new x written into the captured buffer: every
-    replay matches the eager call on the same x bit for bit. 128 rows take the
-    K-split prefill tile (partial tiles, then the ordered sum, no fill), 4 rows
-    the multi-row decode tile."""
+    replay matches the eager call on the same x bit for bit. 128 x 12288 rows
+    take the K-split prefill tile with the summing launch (partial tiles, then
+    the ordered sum, no fill), 128 x 4096 the 8-way split with the sums inside
+    the launch (its counters back at zero after every replay), 4 rows the
+    multi-row decode tile."""
     import ctypes
 
     rt = hip_runtime()
