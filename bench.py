@@ -158,6 +158,11 @@ def main() -> int:
                 launch(name, L[name], xin32[name], ys32[name])
         launch("lm_head", head, xin32["qkv"], y_head32)
 
+    def token_stages():
+        # the weight bytes (codes, bf16 scales and biases) of each launch of the token, in order
+        return [int(0.5625 * n * k) for _ in range(LAYERS) for n, k in shapes.values()] + \
+            [int(0.5625 * VOCAB * HIDDEN)]
+
     bytes_layer = sum(qbytes(n, k) for n, k in shapes.values())
     bytes_token = LAYERS * bytes_layer + qbytes(VOCAB, HIDDEN)
     n_launch = LAYERS * 4 + 1
@@ -193,7 +198,7 @@ def main() -> int:
         return e0.elapsed_time(e1) / steps  # ms per replay
 
     if args.ceiling_workload:
-        res = memory_floors(torch, dev, capture, time_graph, {})
+        res = memory_floors(torch, dev, capture, time_graph, {}, token_stages())
         log("ceiling workload:", json.dumps(res))
         hip.Close()
         return 0
@@ -339,7 +344,8 @@ def main() -> int:
             per_shape[name]["note"] = "v_proj has the same shape"
         del g, copies
     # the plain-read floor of each shape's bytes (one launch reading them, nothing else)
-    floors = memory_floors(torch, dev, capture, time_graph, {nm: qbytes(v["N"], v["K"]) for nm, v in per_shape.items()})
+    floors = memory_floors(torch, dev, capture, time_graph, {nm: qbytes(v["N"], v["K"]) for nm, v in per_shape.items()},
+                           token_stages())
     for nm, v in per_shape.items():
         f = floors["floors"][nm]
         v["floor_us"] = f["us"]
@@ -617,7 +623,7 @@ def decode_step_figures(hip, torch, dev, capture, time_graph, args, contexts=(51
     return {"qwen3_8b_decode_step": res}
 
 
-def memory_floors(torch, dev, capture, time_graph, sizes):
+def memory_floors(torch, dev, capture, time_graph, sizes, stages):
     """Measured HBM figures from bench.py's own kernels (janis_amd/libjanis_bench.so):
     a 1 GiB device copy and a 2 GiB read (the device's bandwidth beside the 8 TB/s
     specification), and for each byte count in `sizes` the fastest single launch that
@@ -625,7 +631,8 @@ def memory_floors(torch, dev, capture, time_graph, sizes):
     buffer (at least 64 windows and 600 MB where the buffer holds them, so the 256 MB
     memory-side cache cannot serve them), best of 1/2/4
     blocks per CU and 4/8/16 loads per lane in flight. That is the floor a decode
-    product of those bytes can reach in one launch."""
+    product of those bytes can reach in one launch. `stages`: the byte counts of a
+    token's launches in order, for the chained-read figure of ceiling_figures."""
     import ctypes
 
     from janis_amd import build as jb
@@ -640,6 +647,9 @@ def memory_floors(torch, dev, capture, time_graph, sizes):
                                ctypes.c_void_p, ctypes.c_void_p]
     L.jhb_read.restype = L.jhb_copy.restype = L.jhb_read_cached.restype = L.jhb_empty.restype = ctypes.c_int
     L.jhb_barriers.restype = ctypes.c_int
+    L.jhb_chain_read.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_uint, ctypes.c_void_p,
+                                 ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    L.jhb_chain_read.restype = ctypes.c_int
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     pool_bytes = 2 << 30
     pool = torch.empty(pool_bytes, dtype=torch.uint8, device=dev).fill_(7)
@@ -666,7 +676,7 @@ def memory_floors(torch, dev, capture, time_graph, sizes):
                     best = (ms, bpc, unroll)
         floors[name] = {"bytes": nb, "us": round(best[0] * 1e3, 2), "GB_s": round(nb / (best[0] * 1e-3) / 1e9, 1),
                         "blocks_per_cu": best[1], "loads_in_flight_per_lane": best[2], "launches_timed": n}
-    ceiling = ceiling_figures(torch, L, pool, sink, capture, time_graph, cus)
+    ceiling = ceiling_figures(torch, L, pool, sink, capture, time_graph, cus, stages)
     # whole-buffer read and copy
     g = capture(lambda: reads(pool_bytes, 4 * cus, 8, 1))
     ms_read = time_graph(g, 10, 3)
@@ -690,7 +700,7 @@ def memory_floors(torch, dev, capture, time_graph, sizes):
     return {"hbm": hbm, "floors": floors, "ceiling": ceiling}
 
 
-def ceiling_figures(torch, L, pool, sink, capture, time_graph, cus):
+def ceiling_figures(torch, L, pool, sink, capture, time_graph, cus, stages):
     """What bounds one launch per linear, measured with bench.py's own kernels:
     - graph_node_us: a graph of 64 dependent launches of an empty kernel (1 and
       256 blocks), time per launch -- the fixed cost each extra kernel adds;
@@ -703,7 +713,14 @@ def ceiling_figures(torch, L, pool, sink, capture, time_graph, cus):
       cache): the first two reads with one cache policy (non-temporal, as the
       decode products load weights, or the default), the third non-temporal.
       Events around each launch, median of 5 rounds. A second or third read
-      faster than the first means that cache served it."""
+      faster than the first means that cache served it;
+    - chained_read: a token's weight bytes (`stages`, each launch's bytes in
+      order, laid out one after another in a buffer of their total) read as a
+      graph of one read launch per stage (4 blocks per CU, 8 loads per lane in
+      flight), against one persistent launch that reads every stage with a
+      grid-wide barrier between stages and the next stage's first loads issued
+      before each wait (one 512-thread block per CU, 8 or 16 loads per lane);
+      median of 5."""
     st = torch.cuda.current_stream().cuda_stream
 
     def chk(rc, what):
@@ -771,11 +788,54 @@ def ceiling_figures(torch, L, pool, sink, capture, time_graph, cus):
                 ts.append(ev[0].elapsed_time(ev[1]) * 1e3)
             per.append((ts[1] - ts[0]) / 63)
         barrier["acq_rel" if ordered else "relaxed"] = None if failed else round(sorted(per)[2], 3)
-    out = {"graph_node_us": nodes, "grid_barrier_us": barrier, "reread": reread,
+    chained = chained_read(torch, L, sink, capture, time_graph, cus, stages, chk) if stages else None
+    out = {"graph_node_us": nodes, "grid_barrier_us": barrier, "reread": reread, "chained_read": chained,
            "note": "empty-kernel graph nodes; grid-wide barriers inside one launch (one block per CU); "
-                   "re-reads after a 1 GiB read of other memory (janis_amd/csrc/bench_kernels.hip)"}
+                   "re-reads after a 1 GiB read of other memory; a token's reads as one launch per stage "
+                   "and as one persistent launch (janis_amd/csrc/bench_kernels.hip)"}
     log("ceiling:", out)
     return out
+
+
+def chained_read(torch, L, sink, capture, time_graph, cus, stages, chk):
+    """The `chained_read` figure of ceiling_figures."""
+    import numpy as np
+
+    sizes = [(int(b) + 255) // 256 * 256 for b in stages]
+    offs = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    total = int(sum(sizes))
+    buf = torch.empty(total, dtype=torch.uint8, device=sink.device)
+    base = buf.data_ptr()
+    tab = torch.tensor([[base + int(o), n // 16] for o, n in zip(offs, sizes)], dtype=torch.int64, device=sink.device)
+
+    def graph_of_reads():
+        st = torch.cuda.current_stream().cuda_stream
+        for o, n in zip(offs, sizes):
+            chk(L.jhb_read(base + int(o), n, sink.data_ptr(), 4 * cus, 8, st), "jhb_read")
+
+    g = capture(graph_of_reads)
+    per_stage_us = sorted(time_graph(g, 5, 2) * 1e3 for _ in range(5))[2]
+    del g
+    ctr = torch.zeros(256, dtype=torch.int32, device=sink.device)
+    chain = {}
+    for unroll in (8, 16):
+        ts, failed = [], False
+        for _ in range(6):
+            ctr.zero_()
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record()
+            chk(L.jhb_chain_read(tab.data_ptr(), len(sizes), ctr.data_ptr(), 1 << 20, ctr.data_ptr() + 512,
+                                 sink.data_ptr(), cus, unroll, torch.cuda.current_stream().cuda_stream),
+                "jhb_chain_read")
+            ev[1].record()
+            torch.cuda.synchronize()
+            failed |= int(ctr[128].item()) != 0
+            ts.append(ev[0].elapsed_time(ev[1]) * 1e3)
+        chain[f"unroll_{unroll}_us"] = None if failed else round(sorted(ts[1:])[2], 1)
+    del buf, tab
+    torch.cuda.empty_cache()
+    return {"stages": len(sizes), "bytes": total, "launch_per_stage_us": round(per_stage_us, 1),
+            "launch_per_stage_TB_s": round(total / per_stage_us / 1e6, 3), "persistent_launch_us": chain}
 
 
 def host_info() -> dict:

@@ -5,7 +5,9 @@
 // gives the device's measured bandwidth beside the 8 TB/s specification. An
 // empty kernel gives the fixed cost of one node of a HIP graph, and the read
 // with the default cache policy (the decode products' weight loads are
-// non-temporal) shows whether the memory-side cache serves a re-read.
+// non-temporal) shows whether the memory-side cache serves a re-read. The
+// chained read is the alternative to one launch per stage: every stage of a
+// token's reads in one persistent launch, a grid-wide barrier between stages.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -96,6 +98,95 @@ __global__ __launch_bounds__(64) void barrier_kernel(unsigned* counter, int roun
     }
 }
 
+// One stage of a chained read: a range of 16-byte units.
+struct ChainStage {
+    const u32x4* p;
+    int64_t n16;
+};
+
+// The stages in order in one launch of one 512-thread block per CU, each read
+// as read_kernel reads it (UNROLL loads per lane per step, non-temporal),
+// with a grid-wide barrier between stages -- what a persistent kernel chaining
+// dependent products would pay per stage in place of a graph node. The barrier
+// counts arrivals in 8 counters (block b in counter b % 8, the XCD it runs on;
+// 64 bytes apart), polled by 8 lanes of wave 0; before waiting, every lane
+// requests the first step of the next stage, which does not depend on the
+// barrier (as a product's weights do not depend on its input). The grid must
+// be resident at once; the polls are bounded, and a block that gives up sets
+// *failed and stops.
+template <int UNROLL>
+__global__ __launch_bounds__(512) void chain_read_kernel(const ChainStage* __restrict__ st, int nst,
+                                                         unsigned* ctr, unsigned spin, unsigned* failed,
+                                                         uint32_t* __restrict__ sink) {
+    constexpr int T = 512;
+    __shared__ int stop;
+    const int tid = threadIdx.x;
+    const unsigned nb = gridDim.x;
+    const int64_t step = (int64_t)nb * T * UNROLL;
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    u32x4 v[UNROLL];
+    bool have = false;  // v holds the first step of the current stage
+    for (int s = 0; s < nst; s++) {
+        const u32x4* p = st[s].p;
+        const int64_t n16 = st[s].n16;
+        int64_t b0 = (int64_t)blockIdx.x * T * UNROLL + tid;
+        if (have) {
+#pragma unroll
+            for (int u = 0; u < UNROLL; u++) acc ^= v[u];
+            b0 += step;
+            have = false;
+        }
+        for (; b0 < n16; b0 += step) {
+#pragma unroll
+            for (int u = 0; u < UNROLL; u++) {
+                const int64_t i = b0 + (int64_t)u * T;
+                v[u] = i < n16 ? __builtin_nontemporal_load(p + i) : u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < UNROLL; u++) acc ^= v[u];
+        }
+        if (s + 1 == nst) break;
+        __syncthreads();
+        if (tid == 0) {
+            stop = 0;
+            __hip_atomic_fetch_add(ctr + 16 * (blockIdx.x & 7), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        {
+            const u32x4* q = st[s + 1].p;
+            const int64_t m16 = st[s + 1].n16;
+            const int64_t c0 = (int64_t)blockIdx.x * T * UNROLL + tid;
+            if (c0 < m16) {
+#pragma unroll
+                for (int u = 0; u < UNROLL; u++) {
+                    const int64_t i = c0 + (int64_t)u * T;
+                    v[u] = i < m16 ? __builtin_nontemporal_load(q + i) : u32x4{0u, 0u, 0u, 0u};
+                }
+                have = true;
+            }
+        }
+        if (tid < 64) {
+            // counter j holds the arrivals of blocks j, j + 8, ...: (nb + 7 - j) / 8 per stage
+            const unsigned target = (unsigned)(s + 1) * ((nb + 7 - (unsigned)(tid & 7)) / 8);
+            bool seen = false;
+            for (unsigned n = 0; n < spin; n++) {
+                const unsigned c =
+                    tid < 8 ? __hip_atomic_load(ctr + 16 * tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : target;
+                if (__all(c >= target)) {
+                    seen = true;
+                    break;
+                }
+            }
+            if (!seen && tid == 0) {
+                __hip_atomic_fetch_or(failed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                stop = 1;
+            }
+        }
+        __syncthreads();
+        if (stop) break;
+    }
+    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9e3779b9u) sink[0] = acc.x;
+}
+
 }  // namespace
 
 extern "C" {
@@ -155,6 +246,25 @@ __attribute__((visibility("default"))) int jhb_copy(void* dst, const void* src, 
         return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(copy_kernel<4>, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                        static_cast<u32x4*>(dst), static_cast<const u32x4*>(src), bytes / 16);
+    return (int)hipGetLastError();
+}
+
+// The chained read: `nst` stages {pointer (16-byte aligned), units of 16
+// bytes} at `stages` (device memory), one 512-thread block per CU (`blocks`),
+// `unroll` (8 or 16) loads per lane per step; `ctr` = 8 counters 64 bytes
+// apart, zero before the launch. Returns 0, or the HIP error code.
+__attribute__((visibility("default"))) int jhb_chain_read(const void* stages, int nst, void* ctr, unsigned spin,
+                                                          void* failed, void* sink, int blocks, int unroll,
+                                                          void* stream) {
+    if (nst <= 0 || blocks <= 0) return (int)hipErrorInvalidValue;
+    auto st = static_cast<hipStream_t>(stream);
+    auto S = static_cast<const ChainStage*>(stages);
+    auto c = static_cast<unsigned*>(ctr);
+    auto f = static_cast<unsigned*>(failed);
+    auto k = static_cast<uint32_t*>(sink);
+    if (unroll == 8) hipLaunchKernelGGL(chain_read_kernel<8>, dim3(blocks), dim3(512), 0, st, S, nst, c, spin, f, k);
+    else if (unroll == 16) hipLaunchKernelGGL(chain_read_kernel<16>, dim3(blocks), dim3(512), 0, st, S, nst, c, spin, f, k);
+    else return (int)hipErrorInvalidValue;
     return (int)hipGetLastError();
 }
 
