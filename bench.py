@@ -717,10 +717,12 @@ def ceiling_figures(torch, L, pool, sink, capture, time_graph, cus, stages):
     - chained_read: a token's weight bytes (`stages`, each launch's bytes in
       order, laid out one after another in a buffer of their total) read as a
       graph of one read launch per stage (4 blocks per CU, 8 loads per lane in
-      flight), against one persistent launch that reads every stage with a
-      grid-wide barrier between stages and the next stage's first loads issued
-      before each wait (one 512-thread block per CU, 8 or 16 loads per lane);
-      median of 5."""
+      flight), against one persistent launch that reads every stage (an even
+      share per block) with a grid-wide barrier between stages -- per-block
+      arrival flags, one per 128-byte line -- and the next stage's first loads
+      issued before each wait (one 512- or 1024-thread block per CU, 8 loads
+      per lane), and against that launch with the whole token as one stage (its
+      streaming rate without barriers); median of 5."""
     st = torch.cuda.current_stream().cuda_stream
 
     def chk(rc, what):
@@ -816,23 +818,30 @@ def chained_read(torch, L, sink, capture, time_graph, cus, stages, chk):
     g = capture(graph_of_reads)
     per_stage_us = sorted(time_graph(g, 5, 2) * 1e3 for _ in range(5))[2]
     del g
-    ctr = torch.zeros(256, dtype=torch.int32, device=sink.device)
-    chain = {}
-    for unroll in (8, 16):
+    one = torch.tensor([[base, total // 16]], dtype=torch.int64, device=sink.device)
+    flags = torch.zeros(32 * cus + 64, dtype=torch.int32, device=sink.device)
+    fail_off = 32 * cus
+
+    def chain_us(t, n, threads):
         ts, failed = [], False
         for _ in range(6):
-            ctr.zero_()
+            flags.zero_()
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
             ev[0].record()
-            chk(L.jhb_chain_read(tab.data_ptr(), len(sizes), ctr.data_ptr(), 1 << 20, ctr.data_ptr() + 512,
-                                 sink.data_ptr(), cus, unroll, torch.cuda.current_stream().cuda_stream),
+            chk(L.jhb_chain_read(t.data_ptr(), n, flags.data_ptr(), 1 << 20, flags.data_ptr() + 4 * fail_off,
+                                 sink.data_ptr(), cus, threads, torch.cuda.current_stream().cuda_stream),
                 "jhb_chain_read")
             ev[1].record()
             torch.cuda.synchronize()
-            failed |= int(ctr[128].item()) != 0
+            failed |= int(flags[fail_off].item()) != 0
             ts.append(ev[0].elapsed_time(ev[1]) * 1e3)
-        chain[f"unroll_{unroll}_us"] = None if failed else round(sorted(ts[1:])[2], 1)
-    del buf, tab
+        return None if failed else round(sorted(ts[1:])[2], 1)
+
+    chain = {}
+    for threads in (512, 1024):
+        chain[f"threads_{threads}"] = {"stages_us": chain_us(tab, len(sizes), threads),
+                                       "one_stage_us": chain_us(one, 1, threads)}
+    del buf, tab, one, flags
     torch.cuda.empty_cache()
     return {"stages": len(sizes), "bytes": total, "launch_per_stage_us": round(per_stage_us, 1),
             "launch_per_stage_TB_s": round(total / per_stage_us / 1e6, 3), "persistent_launch_us": chain}

@@ -104,43 +104,44 @@ struct ChainStage {
     int64_t n16;
 };
 
-// The stages in order in one launch of one 512-thread block per CU, each read
-// as read_kernel reads it (UNROLL loads per lane per step, non-temporal),
-// with a grid-wide barrier between stages -- what a persistent kernel chaining
-// dependent products would pay per stage in place of a graph node. The barrier
-// counts arrivals in 8 counters (block b in counter b % 8, the XCD it runs on;
-// 64 bytes apart), polled by 8 lanes of wave 0; before waiting, every lane
-// requests the first step of the next stage, which does not depend on the
+// The stages in order in one launch of one T-thread block per CU -- what a
+// persistent kernel chaining dependent products would pay per stage in place
+// of a graph node. Block b reads units [n16 b / nb, n16 (b+1) / nb) of every
+// stage (UNROLL non-temporal loads per lane per step), then stores the stage
+// number + 1 into its own arrival flag (one flag per 128-byte line: flags
+// sharing a line made the barrier several times slower) and wave 0 polls every
+// block's flag until all have arrived; before waiting, every lane requests the
+// first step of its part of the next stage, which does not depend on the
 // barrier (as a product's weights do not depend on its input). The grid must
 // be resident at once; the polls are bounded, and a block that gives up sets
 // *failed and stops.
-template <int UNROLL>
-__global__ __launch_bounds__(512) void chain_read_kernel(const ChainStage* __restrict__ st, int nst,
-                                                         unsigned* ctr, unsigned spin, unsigned* failed,
-                                                         uint32_t* __restrict__ sink) {
-    constexpr int T = 512;
+template <int T, int UNROLL>
+__global__ __launch_bounds__(T) void chain_read_kernel(const ChainStage* __restrict__ st, int nst,
+                                                       unsigned* flags, unsigned spin, unsigned* failed,
+                                                       uint32_t* __restrict__ sink) {
+    constexpr int PAD = 32;  // words between flags
     __shared__ int stop;
     const int tid = threadIdx.x;
     const unsigned nb = gridDim.x;
-    const int64_t step = (int64_t)nb * T * UNROLL;
     u32x4 acc = {0u, 0u, 0u, 0u};
     u32x4 v[UNROLL];
     bool have = false;  // v holds the first step of the current stage
     for (int s = 0; s < nst; s++) {
         const u32x4* p = st[s].p;
         const int64_t n16 = st[s].n16;
-        int64_t b0 = (int64_t)blockIdx.x * T * UNROLL + tid;
+        const int64_t hi = n16 * (blockIdx.x + 1) / nb;
+        int64_t b0 = n16 * blockIdx.x / nb + tid;
         if (have) {
 #pragma unroll
             for (int u = 0; u < UNROLL; u++) acc ^= v[u];
-            b0 += step;
+            b0 += (int64_t)T * UNROLL;
             have = false;
         }
-        for (; b0 < n16; b0 += step) {
+        for (; b0 < hi; b0 += (int64_t)T * UNROLL) {
 #pragma unroll
             for (int u = 0; u < UNROLL; u++) {
                 const int64_t i = b0 + (int64_t)u * T;
-                v[u] = i < n16 ? __builtin_nontemporal_load(p + i) : u32x4{0u, 0u, 0u, 0u};
+                v[u] = i < hi ? __builtin_nontemporal_load(p + i) : u32x4{0u, 0u, 0u, 0u};
             }
 #pragma unroll
             for (int u = 0; u < UNROLL; u++) acc ^= v[u];
@@ -149,29 +150,27 @@ __global__ __launch_bounds__(512) void chain_read_kernel(const ChainStage* __res
         __syncthreads();
         if (tid == 0) {
             stop = 0;
-            __hip_atomic_fetch_add(ctr + 16 * (blockIdx.x & 7), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(flags + blockIdx.x * PAD, (unsigned)(s + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         {
             const u32x4* q = st[s + 1].p;
             const int64_t m16 = st[s + 1].n16;
-            const int64_t c0 = (int64_t)blockIdx.x * T * UNROLL + tid;
-            if (c0 < m16) {
+            const int64_t c0 = m16 * blockIdx.x / nb + tid, h2 = m16 * (blockIdx.x + 1) / nb;
 #pragma unroll
-                for (int u = 0; u < UNROLL; u++) {
-                    const int64_t i = c0 + (int64_t)u * T;
-                    v[u] = i < m16 ? __builtin_nontemporal_load(q + i) : u32x4{0u, 0u, 0u, 0u};
-                }
-                have = true;
+            for (int u = 0; u < UNROLL; u++) {
+                const int64_t i = c0 + (int64_t)u * T;
+                v[u] = i < h2 ? __builtin_nontemporal_load(q + i) : u32x4{0u, 0u, 0u, 0u};
             }
+            have = true;
         }
         if (tid < 64) {
-            // counter j holds the arrivals of blocks j, j + 8, ...: (nb + 7 - j) / 8 per stage
-            const unsigned target = (unsigned)(s + 1) * ((nb + 7 - (unsigned)(tid & 7)) / 8);
+            const unsigned target = (unsigned)(s + 1);
             bool seen = false;
             for (unsigned n = 0; n < spin; n++) {
-                const unsigned c =
-                    tid < 8 ? __hip_atomic_load(ctr + 16 * tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : target;
-                if (__all(c >= target)) {
+                bool ok = true;
+                for (unsigned j = tid; j < nb; j += 64)
+                    ok &= __hip_atomic_load(flags + j * PAD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target;
+                if (__all(ok)) {
                     seen = true;
                     break;
                 }
@@ -250,21 +249,24 @@ __attribute__((visibility("default"))) int jhb_copy(void* dst, const void* src, 
 }
 
 // The chained read: `nst` stages {pointer (16-byte aligned), units of 16
-// bytes} at `stages` (device memory), one 512-thread block per CU (`blocks`),
-// `unroll` (8 or 16) loads per lane per step; `ctr` = 8 counters 64 bytes
-// apart, zero before the launch. Returns 0, or the HIP error code.
-__attribute__((visibility("default"))) int jhb_chain_read(const void* stages, int nst, void* ctr, unsigned spin,
-                                                          void* failed, void* sink, int blocks, int unroll,
+// bytes} at `stages` (device memory), `blocks` blocks (one per CU) of
+// `threads` (512 or 1024) threads, 8 loads per lane per step; `flags` =
+// blocks x 32 words, zero before the launch. Returns 0, or the HIP error code.
+__attribute__((visibility("default"))) int jhb_chain_read(const void* stages, int nst, void* flags, unsigned spin,
+                                                          void* failed, void* sink, int blocks, int threads,
                                                           void* stream) {
     if (nst <= 0 || blocks <= 0) return (int)hipErrorInvalidValue;
     auto st = static_cast<hipStream_t>(stream);
     auto S = static_cast<const ChainStage*>(stages);
-    auto c = static_cast<unsigned*>(ctr);
-    auto f = static_cast<unsigned*>(failed);
+    auto f = static_cast<unsigned*>(flags);
+    auto fl = static_cast<unsigned*>(failed);
     auto k = static_cast<uint32_t*>(sink);
-    if (unroll == 8) hipLaunchKernelGGL(chain_read_kernel<8>, dim3(blocks), dim3(512), 0, st, S, nst, c, spin, f, k);
-    else if (unroll == 16) hipLaunchKernelGGL(chain_read_kernel<16>, dim3(blocks), dim3(512), 0, st, S, nst, c, spin, f, k);
-    else return (int)hipErrorInvalidValue;
+    if (threads == 512)
+        hipLaunchKernelGGL((chain_read_kernel<512, 8>), dim3(blocks), dim3(512), 0, st, S, nst, f, spin, fl, k);
+    else if (threads == 1024)
+        hipLaunchKernelGGL((chain_read_kernel<1024, 8>), dim3(blocks), dim3(1024), 0, st, S, nst, f, spin, fl, k);
+    else
+        return (int)hipErrorInvalidValue;
     return (int)hipGetLastError();
 }
 
