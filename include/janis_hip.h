@@ -197,10 +197,14 @@ JH_API int jh_dequantize(jh_ctx *ctx, const uint32_t *w, const void *scales, con
  *   in increasing order, terms rounded then added, zero x terms skipped), so its
  *   fp32 results have the CPU backend's bits; a slow path, off the models' path.
  * x_dtype and y_dtype are JH_BF16 or JH_F32; accumulation is fp32. rows == 1
- * runs the decode GEMV; 2..8 rows (2..4 for in_features 768, 1536, 3072,
- * 6144, 12288 and 16384) run the decode GEMV's tiles with every row's x in
- * registers, so each row's result has the bits of a one-row call; more rows
- * run the MFMA prefill GEMM. rows == 0 is a no-op. fp32 x (the activation type
+ * runs the decode GEMV; a few rows run the decode GEMV's tiles with every
+ * row's x in registers, so each row's result has the bits of a one-row call:
+ * 2 rows always; 3..4 rows, except for in_features 768, 1536, 3072, 6144,
+ * 12288 and 16384, where 3..4 rows take the tiles only from in_features 1536
+ * with fewer than 2^24 weights (out_features x in_features); 5..8 rows with
+ * in_features >= 1024 and fewer than 2^24 weights (where those tiles are the
+ * faster path on MI355X). Other row counts run the MFMA prefill GEMM. rows == 0
+ * is a no-op. fp32 x (the activation type
  * of the CPU backend, of Dequantize and of the embedding) takes the same tiles:
  * each lane rounds its part of x to bf16 (nearest even) in registers, so an
  * fp32-x call has the bits of a bf16-x call on bf16(x). Shapes outside the

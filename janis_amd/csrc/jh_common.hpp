@@ -270,8 +270,9 @@ struct InLaunchSync {
     uint32_t spin;
     int* status;
 };
-// A few bf16 or fp32 x rows (2..kQmvRowsMax, fewer for long rows) through the decode
-// tiles, the weights read once per launch of 2, 4 or 8 rows.
+// A few bf16 or fp32 x rows (2..kQmvRowsMax; qmv_rows_ok says which calls, by
+// rows, row length and matrix size) through the decode tiles, the weights read
+// once per launch of 2, 4 or 8 rows.
 constexpr int64_t kQmvRowsMax = 8;
 bool qmv_rows_ok(const QuantMatrix& m, int64_t rows, int x_dtype);
 Status launch_qmv_rows(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y, int y_dtype,

@@ -495,17 +495,34 @@ int tile_iters(int64_t row_words) {
 
 }  // namespace
 
-// Up to 8 rows (4 for tiles whose lanes hold 96 or 128 elements of each row):
-// beyond that the prefill GEMM is faster (measured on MI355X for the Qwen3-8B
-// shapes: gate/up 12288 x 4096 at 8 rows 23.5 us against 28.4 for the GEMM;
-// down 4096 x 12288 at 4 rows 20.9 against 32.2, at 8 rows 42.2). Only row
-// lengths with a case in launch_qmv_rows are accepted (tile_iters > 0).
+// Which few-row calls the multi-row tile takes, and which go to the prefill
+// GEMM, from graph-replay timings on MI355X over weight copies that do not fit
+// the memory-side cache. The tile reads the weights once and does all the rows'
+// dot products in VALU, so it wins while the matrix is small and loses on large
+// ones once the rows multiply its arithmetic:
+//  * 2 rows: always the tile;
+//  * 3-4 rows: the tile for 16-byte-load tiles (K = 256..8192 in this table);
+//    for tiles whose lanes hold 96 or 128 elements of a row only from K = 1536
+//    and below 16M weights (4096 x 1536 at 4 rows 9.4 us against 10.6 for the
+//    GEMM, 1024 x 3072 9.3 against 9.4; 2048 x 768 9.1 against 6.7, 4096 x
+//    6144 14.7 against 11.9, 4096 x 12288 22.3 against 15.9);
+//  * 5-8 rows: the tile from K = 1024 below 16M weights (1024 x 4096 at 5 rows
+//    7.6 against 9.3 us, 8192 x 1024 7.3 against 8.2), the GEMM from 16M
+//    weights (4096 x 4096 at 8 rows 11.7 against 10.6, 12288 x 4096 23.3
+//    against 17.8, 24576 x 4096 40.7 against 24.8) and at K = 512 (4096 x 512
+//    6.9 against 5.6).
+// Only row lengths with a case in launch_qmv_rows are accepted (tile_iters > 0).
 bool qmv_rows_ok(const QuantMatrix& m, int64_t rows, int x_dtype) {
     if ((x_dtype != JH_BF16 && x_dtype != JH_F32) || m.bits != 4 || rows < 2 || !qmv_fast_shape(m) ||
         rows * m.in * 4 >= ((int64_t)1 << 31))
         return false;
     const int it = tile_iters(row_words(m));
-    return it > 0 && rows <= (it >= 3 ? 4 : kQmvRowsMax);
+    if (it == 0 || rows > kQmvRowsMax) return false;
+    if (rows == 2) return true;
+    constexpr int64_t kSmallWeights = (int64_t)1 << 24;
+    const bool small = m.rows * m.in < kSmallWeights;
+    if (it >= 3) return rows <= 4 && small && m.in >= 1536;
+    return rows <= 4 || (small && m.in >= 1024);
 }
 
 Status launch_qmv_rows(const QuantMatrix& m, const void* x, int x_dtype, int64_t rows, void* y, int y_dtype,

@@ -78,11 +78,12 @@ def test_f32_x_takes_the_tiles(hip, oracle, n, k, gs, bits, sb):
     assert ok, (d, sc)
 
 
-@pytest.mark.parametrize("n,k,rows,sb", [(4096, 4096, 2, "bf16"), (4096, 4096, 7, "f16"), (4096, 12288, 3, "bf16"),
+@pytest.mark.parametrize("n,k,rows,sb", [(4096, 4096, 2, "bf16"), (2048, 4096, 7, "f16"), (1300, 12288, 3, "bf16"),
                                          (1000, 24576, 2, "bf16"), (24576, 4096, 4, "bf16")])
 def test_f32_x_rows_match_one_row_calls(hip, oracle, n, k, rows, sb):
-    """2..8 fp32 rows through the multi-row tile: each row has the bits of a
-    one-row fp32 call and of the bf16 multi-row call on bf16(x)."""
+    """fp32 rows the multi-row tile takes (2 rows; up to 8 below 2^24 weights):
+    each row has the bits of a one-row fp32 call and of the bf16 multi-row call
+    on bf16(x)."""
     gs = 64
     q = synth.quant_linear(22000 + n + k, n, k, gs)
     (w, s, b), s_np, b_np = _weights(hip, q, sb)

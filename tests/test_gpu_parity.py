@@ -222,29 +222,29 @@ def _rows_weights(seed, n, k, gs):
 
 
 @pytest.mark.parametrize("n,k,rows,gs,sb", [
-    (4096, 4096, 8, 64, "bf16"),    # 8 rows per launch
-    (4096, 4096, 5, 64, "bf16"),    # 8 rows per launch, 5 used
+    (2048, 4096, 8, 64, "bf16"),    # 8 rows per launch (below 2^24 weights)
+    (1024, 4096, 5, 64, "bf16"),    # 8 rows per launch, 5 used
     (4096, 4096, 3, 64, "f16"),     # 4 rows per launch, 3 used
     (1000, 12288, 4, 64, "bf16"),   # 2 rows per launch, two launches, ragged N
     (1000, 12288, 3, 64, "bf16"),   # two launches, the second with one row
     (4096, 12288, 2, 64, "bf16"),   # down_proj's own shape: the one-row call takes the pipelined
-    (4096, 12288, 3, 64, "bf16"),   #   <32,3,1,4> tile (N >= 2048), the rows kernel <32,3,2,4>
-    (4096, 12288, 4, 64, "f16"),
+    (4096, 12288, 2, 64, "f16"),    #   <32,3,1,4> tile (N >= 2048), the rows kernel <32,3,2,4>
+    (1300, 12288, 3, 64, "bf16"),
     (257, 8192, 3, 32, "f16"),      # 4 rows per launch
     (300, 2048, 7, 128, "bf16"),
     (33, 768, 2, 64, "bf16"),
     (70, 3072, 3, 64, "f16"),
     (100, 16384, 4, 64, "bf16"),
     (1000, 24576, 2, 64, "bf16"),   # the 64-lane 3-load tile (one launch)
-    (1000, 24576, 4, 64, "f16"),    # two launches of 2 rows
+    (600, 24576, 4, 64, "f16"),     # two launches of 2 rows
     (151936, 4096, 2, 64, "bf16"),  # lm_head: the one-row call's 64-lane, 2-way split
-    (151936, 4096, 5, 64, "bf16"),
-    (151936, 4096, 8, 64, "bf16"),
+    (151936, 4096, 3, 64, "bf16"),
+    (151936, 4096, 4, 64, "bf16"),
 ])
 def test_qmv_rows_match_one_row_calls(hip, oracle, n, k, rows, gs, sb):
-    """2..8 rows (2..4 for long rows) take the decode tiles with every row's x
-    in registers: each row of y has the bits of a one-row call on that row
-    (fp32 out), and the bf16 output is within the bar of the oracle."""
+    """The few-row calls the decode tiles take (every row's x in registers):
+    each row of y has the bits of a one-row call on that row (fp32 out), and
+    the bf16 output is within the bar of the oracle."""
     q = _rows_weights(12000 + n + k, n, k, gs)
     xb, x = synth.activations(13000 + rows, (rows, k))
     w = hip.FromRaw(U32, q.w, *q.w.shape)
@@ -262,6 +262,31 @@ def test_qmv_rows_match_one_row_calls(hip, oracle, n, k, rows, gs, sb):
     y16 = hip.Floats(hip.QuantMatmul(hip.FromBF16Bits(xb, rows, k), w, s, b, True, gs, 4))
     cs = np.sort(np.random.default_rng(n).choice(n, size=min(n, 96), replace=False))
     ok, d, sc = rel_ok(y16[:, cs], oracle.quant_matmul(x, q.w[cs], s_np[cs], b_np[cs], gs), BF16_TOL)
+    assert ok, (d, sc)
+
+
+@pytest.mark.parametrize("n,k,rows,xdt", [
+    (4096, 4096, 8, "bf16"),    # 2^24 weights: 5..8 rows go to the GEMM
+    (12288, 4096, 5, "bf16"),
+    (24576, 4096, 6, "f32"),
+    (4096, 512, 7, "bf16"),     # K = 512: the GEMM at 5..8 rows
+    (4096, 12288, 3, "bf16"),   # long rows from 2^24 weights: 3..4 rows go to the GEMM
+    (2048, 768, 4, "f32"),      # K = 768: the GEMM at 3..4 rows
+])
+def test_few_rows_on_the_gemm(hip, oracle, n, k, rows, xdt):
+    """The few-row calls outside the decode tiles' rule take the MFMA product
+    (where it is the faster path): within the bar of the oracle, for bf16 and
+    fp32 x, and the same bits on a repeated call."""
+    q = _rows_weights(15000 + n + k, n, k, 64)
+    xb, x = synth.activations(16000 + rows, (rows, k))
+    w, s, b = upload_quant(hip, q)
+    step(f"jh_quant_matmul rows={rows} N={n} K={k} x={xdt} (few rows on the GEMM)")
+    xt = hip.FromBF16Bits(xb, rows, k) if xdt == "bf16" else hip.FromFloats(x.astype(np.float32), rows, k)
+    y1 = hip.Floats(hip.QuantMatmul(xt, w, s, b, True, 64, 4))
+    y2 = hip.Floats(hip.QuantMatmul(xt, w, s, b, True, 64, 4))
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    cs = np.sort(np.random.default_rng(n + rows).choice(n, size=min(n, 96), replace=False))
+    ok, d, sc = rel_ok(y1[:, cs], oracle.quant_matmul(x, q.w[cs], q.s[cs], q.b[cs], 64), BF16_TOL)
     assert ok, (d, sc)
 
 
