@@ -451,8 +451,9 @@ def prefill_and_moe(hip, torch, dev, qweight, bf16, capture, time_graph, args):
                                    "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)}
             del g
         # a few rows (batched decode of several sequences, a short draft to
-        # verify): the multi-row decode GEMV up to 8 rows (4 for down), HBM-bound
-        # on the weights; 16-64 rows take the MFMA tile's 32/64-row blocks
+        # verify): on these matrices (2^24 weights and more) the multi-row decode
+        # GEMV takes 2..4 rows (2 for down), HBM-bound on the weights, and the
+        # MFMA tile's 32/64-row blocks the rest
         few = {}
         for m in ((2, 4, 8, 16, 32, 64) if k == 4096 else (2, 4, 16, 32, 64)):
             x = bf16((m, k))
