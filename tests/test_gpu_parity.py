@@ -240,6 +240,9 @@ def _rows_weights(seed, n, k, gs):
     (151936, 4096, 2, 64, "bf16"),  # lm_head: the one-row call's 64-lane, 2-way split
     (151936, 4096, 3, 64, "bf16"),
     (151936, 4096, 4, 64, "bf16"),
+    (4095, 4096, 6, 64, "bf16"),    # just under 2^24 weights: 5..8 rows stay on the tile
+    (2048, 1024, 5, 64, "bf16"),    # K = 1024, the smallest row length that keeps 5..8 rows
+    (4096, 1536, 4, 64, "f16"),     # long-row tile from K = 1536 below 2^24 weights
 ])
 def test_qmv_rows_match_one_row_calls(hip, oracle, n, k, rows, gs, sb):
     """The few-row calls the decode tiles take (every row's x in registers):
