@@ -498,7 +498,7 @@ def test_qmm_split_sums_in_launch(hip, oracle, m, n, k, out_dtype):
     assert np.array_equal(y0.view(np.uint32), y2.view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,n,k", [(128, 12288, 4096), (128, 4096, 4096), (4, 4096, 4096)])
+@pytest.mark.parametrize("rows,n,k", [(128, 12288, 4096), (128, 4096, 4096), (4, 4096, 4096), (8, 12288, 4096)])
 def test_quant_matmul_graph_replays(hip, oracle, rows, n, k):
     """Captured once into a HIP graph (after one eager call, which sizes the
     workspace) and replayed on new x written into the captured buffer: every
@@ -506,7 +506,8 @@ def test_quant_matmul_graph_replays(hip, oracle, rows, n, k):
     take the K-split prefill tile with the summing launch (partial tiles, then
     the ordered sum, no fill), 128 x 4096 the 8-way split with the sums inside
     the launch (its counters back at zero after every replay), 4 rows the
-    multi-row decode tile."""
+    multi-row decode tile, 8 rows of a 2^24-weight-plus matrix the GEMM's
+    32-row blocks."""
     import ctypes
 
     rt = hip_runtime()
