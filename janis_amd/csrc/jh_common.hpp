@@ -146,7 +146,8 @@ __device__ __forceinline__ float wave_max(float v) { return rows4_max(row16_redu
 // word into its even and odd codes (one per byte) and v_perm_b32 builds the bf16
 // pairs (128 + q_p, 128 + q_{p+4}); v_dot2_f32_bf16 multiplies them with the
 // input pairs (x_p, x_{p+4}) and accumulates in fp32. The 128 is removed per
-// group through the input sum:
+// group through the input sum, either inside the dot product (the decode tiles
+// start it from -128*sum(x)) or after it:
 //   scale*sum(x*(128+q)) + (bias - 128*scale)*sum(x) = scale*sum(x*q) + bias*sum(x).
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 constexpr uint32_t kBf16Bytes = 0x43434343u;  // 0x43 = high byte of bf16(128.0)

@@ -16,9 +16,10 @@
 //    word into its even and odd codes (one per byte) and v_perm_b32 assembles
 //    the pairs (128 + q_p, 128 + q_{p+4}). v_dot2_f32_bf16 multiplies a pair
 //    with the bf16 pair (x_p, x_{p+4}) and accumulates in fp32, so 8 codes cost
-//    7 integer ops and 4 dot2. The constant 128 is removed per group through
-//    the x-sum that the factorisation needs anyway:
-//      scale*sum(x*(128+q)) + (bias - 128*scale)*sum(x) = scale*sum(x*q) + bias*sum(x).
+//    7 integer ops and 4 dot2. The constant 128 is removed through the x-sum
+//    that the factorisation needs anyway: each dot product starts from
+//    -128*sum(x), so it ends at sum(x*(128+q)) - 128*sum(x) = sum(x*q), and a
+//    group costs two fma beyond it: scale*dot + bias*sum(x).
 //  * Partial sums are reduced across the slice with cross-lane adds; the
 //    slice's first lane writes y (fp32 or bf16).
 #include "qmv_tile.hpp"
@@ -141,10 +142,9 @@ __global__ __launch_bounds__(256) void qmv_rows_kernel(
             for (int it = 0; it < ITERS; it++) {
                 const float sc = SB_F16 ? f16_to_f32(sh[r][it]) : bf16_to_f32(sh[r][it]);
                 const float bi = SB_F16 ? f16_to_f32(bh[r][it]) : bf16_to_f32(bh[r][it]);
-                const float bo = fmaf(-kCodeOffset, sc, bi);
-                float d[MR];
+                float d[MR];  // from -128 * sum(x), as the one-row tile starts them
 #pragma unroll
-                for (int m = 0; m < MR; m++) d[m] = 0.0f;
+                for (int m = 0; m < MR; m++) d[m] = -kCodeOffset * xs[m][it];
                 const uint32_t words[4] = {wv[r][it].x, wv[r][it].y, wv[r][it].z, wv[r][it].w};
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void qmv_rows_kernel(
 #pragma unroll
                 for (int m = 0; m < MR; m++) {
                     part[m * RPW + r] = fmaf(sc, d[m], part[m * RPW + r]);
-                    part[m * RPW + r] = fmaf(bo, xs[m][it], part[m * RPW + r]);
+                    part[m * RPW + r] = fmaf(bi, xs[m][it], part[m * RPW + r]);
                 }
             }
         slice_sums_last<LPR, MR * RPW>(part);

@@ -372,6 +372,11 @@ __device__ __forceinline__ void qmv_tile(
         for (int j = 0; j < 4; j++) sum += pair_up(xin[it][j], &xp[it][4 * j]);
         xs[it] = BITS == 8 ? xs8[it] : sum;
     }
+    // every row's dot product starts from -OFF * sum(x), so the codes' offset
+    // cancels inside it and a row's group term is scale * dot + bias * sum(x)
+    float xo[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; it++) xo[it] = -OFF * xs[it];
 
     // one pass: the rows of bbase from register set Q
     auto pass = [&](auto bufc, uint32_t bbase) {
@@ -385,13 +390,13 @@ __device__ __forceinline__ void qmv_tile(
             for (int it = 0; it < ITERS; it++) {
                 const float sc = SB_F16 ? f16_to_f32(sh[Q][r][it]) : bf16_to_f32(sh[Q][r][it]);
                 const float bi = SB_F16 ? f16_to_f32(bh[Q][r][it]) : bf16_to_f32(bh[Q][r][it]);
-                float d = 0.0f;
+                float d = xo[it];
                 d = word_dot(wv[Q][r][it].x, &xp[it][0], d);
                 d = word_dot(wv[Q][r][it].y, &xp[it][4], d);
                 d = word_dot(wv[Q][r][it].z, &xp[it][8], d);
                 d = word_dot(wv[Q][r][it].w, &xp[it][12], d);
                 part[r] = fmaf(sc, d, part[r]);
-                part[r] = fmaf(fmaf(-OFF, sc, bi), xs[it], part[r]);
+                part[r] = fmaf(bi, xs[it], part[r]);
             }
         }
         slice_sums_last<LPR, RPW>(part);
