@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # WRITE_SIZE over `bench.py --pmc-workload`, each scaled by what the counter reads
 # for a 256 MiB copy in the same run (FETCH_SIZE x2.0, WRITE_SIZE x1.0). Re-measure
 # after changing the kernel; the summary sits in profiles/.
-DOMINANT_TRAFFIC_BYTES = 26918717
+DOMINANT_TRAFFIC_BYTES = 26917793
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 HIDDEN, INTER, VOCAB, LAYERS, GS = 4096, 12288, 151936, 36, 64
 
